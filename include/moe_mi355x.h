@@ -1,0 +1,128 @@
+/*
+ * moe_mi355x.h — C ABI of the MI355X (gfx950) quantised MoE-layer library, libmoe_mi355x.so.
+ *
+ * The reference (Tigerly1/moe-lab) has no native FFI: its drop-in boundary is the Python "variant"
+ * module contract (reference README.md:141-158, moelab/mlx_backend.py:3-8, moelab/torch_backend.py:3-5):
+ *     prepare(w_gate, w_up, w_down) -> state;  run(state, x, idx, wts, act) -> y;  dequant(state)
+ * plus run_slots (moelab/variants/mlx/metal_q4_moe.py:49-51) and the fused router tail topk_norm
+ * (moelab/router.py:71-80). Each entry point below replaces the GPU work behind one of those calls;
+ * the Python variant modules in moe-lab_amd/variants/ bind them with ctypes.
+ *
+ * Conventions (all entry points):
+ *   - every pointer is a device pointer (HBM), except the moe_experts_t descriptor itself, which
+ *     lives in host memory and is read during the call only;
+ *   - all work is enqueued on `stream` (a hipStream_t, passed as void*; NULL = default stream) and
+ *     is asynchronous; nothing allocates device memory and nothing synchronises the host;
+ *   - outputs and workspace are caller-allocated; sizes come from the *_workspace_bytes queries;
+ *   - return 0 on success, a negative MOE_ERR_* code on invalid arguments (checked before any
+ *     launch; mirrors the reference's shape asserts, e.g. metal_q4_moe.py:34) or launch failure;
+ *   - reentrant: no global mutable state; calls that share a workspace must be stream-ordered.
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* return codes */
+#define MOE_OK 0
+#define MOE_ERR_ARG (-1)       /* shape, size or pointer argument invalid */
+#define MOE_ERR_DTYPE (-2)     /* activation dtype or weight format not supported by this entry */
+#define MOE_ERR_WORKSPACE (-3) /* workspace missing or smaller than *_workspace_bytes */
+#define MOE_ERR_LAUNCH (-4)    /* the HIP runtime refused a launch */
+#define MOE_ERR_ALIGN (-5)     /* a pointer is not 16-byte aligned */
+
+/* activation / logits dtypes */
+#define MOE_DTYPE_BF16 0
+#define MOE_DTYPE_F16 1
+#define MOE_DTYPE_F32 2
+
+/* weight formats (reference state layouts: metal_q4_decode_v4.py:161-169, metal_mxfp4_moe.py:448-455) */
+#define MOE_FMT_INT4_G64 0 /* codes u32 [E,N,K/8] (8 nibbles, low first), scales/biases bf16 [E,N,K/64] */
+#define MOE_FMT_MXFP4 1    /* codes u32 [E,N,K/8] (8 E2M1 nibbles, low first), scales u8 E8M0 [E,N,K/32] */
+
+/* GLU activations (reference metal_q4_decode_v4.py:36-41, metal_mxfp4_gptoss.py:36-43) */
+#define MOE_ACT_SWIGLU 0      /* silu(g) * u */
+#define MOE_ACT_GEGLU 1       /* tanh-GELU(g) * u (Gemma-4) */
+#define MOE_ACT_GPTOSS 2      /* g = min(g,7), u = clip(u,-7,7), g * sigmoid(1.702 g) * (u + 1) */
+
+/* expert-path selection for moe_experts_run */
+#define MOE_PATH_AUTO 0       /* T == 1 -> per-slot GEMV; T > 1 -> grouped expert tiles */
+#define MOE_PATH_SLOTS 1      /* per-slot GEMV over all T*k slots, no grouping (the stock-style gather) */
+#define MOE_PATH_GROUPED 2    /* grouped expert tiles: each selected expert's weights read once */
+
+/* One projection of all E experts: N output rows, K inputs. */
+typedef struct {
+    const void* codes;   /* u32 words [E, N, K/8] */
+    const void* scales;  /* int4: bf16 [E, N, K/64]; mxfp4: u8 [E, N, K/32] */
+    const void* biases;  /* int4: bf16 [E, N, K/64]; mxfp4: unused (NULL) */
+    const float* bias;   /* optional additive row bias fp32 [E, N] (gpt-oss), NULL if none */
+} moe_proj_t;
+
+/* Expert weights: gate/up [E, F, d], down [E, d, F]. */
+typedef struct {
+    int32_t fmt;         /* MOE_FMT_* */
+    int32_t E, d, F;
+    moe_proj_t gate, up, down;
+} moe_experts_t;
+
+/*
+ * Fused router: gate GEMV + router tail.
+ * Replaces the stock gate GEMV self.gate(x) (reference e2e.py:57-59) followed by router.topk_norm
+ * (reference moelab/router.py:71-80; semantics router.py:1-12).
+ *   x [T, d] bf16, wr [E, d] bf16, bias [E] fp32 or NULL
+ *   logits [T, E] fp32 out: x . wr^T (+ bias), fp32, fixed reduction order (see the kernel source)
+ *   idx [T, k] int32, wts [T, k] fp32 out; norm = 1: softmax over the top-k logits (= renormalised
+ *   softmax), norm = 0: full-softmax probabilities (DeepSeek-V2 greedy); weights are multiplied by scale.
+ *   Ties: lowest expert id. NaN logits count as -inf. Limits: E <= 1024, 1 <= k <= min(E, 32), d % 8 == 0.
+ *   counters: int32 [moe_router_counter_count(T)], zero before the first call; every call leaves it zero.
+ */
+int moe_router(const void* x, const void* wr, const float* bias, int T, int d, int E, int k, int norm, float scale,
+               float* logits, int32_t* idx, float* wts, int32_t* counters, void* stream);
+int moe_router_counter_count(int T);
+
+/*
+ * Router tail on given logits: reference moelab/router.py:71-80 topk_norm(logits, k, norm).
+ *   logits [T, E] of dtype MOE_DTYPE_*; idx [T, k] int32, wts [T, k] fp32 out.
+ */
+int moe_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
+             void* stream);
+
+/*
+ * Slot grouping: slots p = t*k + j sorted stably by expert (reference metal_q4_tiles_v2.py:362-373 MAP
+ * kernel order; closed form of reference triton_fused_moe.py:56-70 align()).
+ *   idx [n] int32 in; counts [E], offsets [E+1], sorted [n], active [E], meta [2] int32 out.
+ *   meta[0] = number of experts with count > 0 (listed ascending in active[0..meta[0]) , rest -1);
+ *   meta[1] = number of slots whose id is outside [0, E) (they join no group).
+ */
+int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted, int32_t* active,
+              int32_t* meta, void* stream);
+
+/*
+ * Expert part of the layer: reference variant run(state, x, idx, wts, act) (metal_q4_moe.py:54-64,
+ * metal_mxfp4_moe.py:474-512, metal_mxfp4_gptoss.py:129-167):
+ *   y[t] = residual[t] + sum_j wts[t,j] * ( down_e( act(gate_e x_t + bg_e, up_e x_t + bu_e) ) + bd_e ),
+ *   e = idx[t,j]; residual optional (NULL = 0).
+ *   x, y, residual [T, d] of dtype x_dtype; idx [T, k] int32; wts [T, k] fp32.
+ *   path: MOE_PATH_*; nored = 1 writes the unweighted per-slot outputs y[T*k, d] instead (reference
+ *   run_slots / NORED, metal_q4_moe.py:49-51; per-slot path only, residual must be NULL).
+ *   Accumulation in fp32; the GLU output h is stored in x_dtype, as in the reference kernels.
+ *   Requirements: d % 64 == 0 and F % 64 == 0; x, y, codes 16-byte aligned.
+ *   workspace: moe_experts_workspace_bytes(...) bytes, any content.
+ */
+int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T,
+                    int k, int act, int path, int nored, void* y, const void* residual, void* workspace,
+                    size_t workspace_bytes, void* stream);
+size_t moe_experts_workspace_bytes(const moe_experts_t* w, int T, int k, int path);
+
+/* Library version and build target, for logs. */
+const char* moe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_MI355X_H */

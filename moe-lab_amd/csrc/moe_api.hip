@@ -1,0 +1,146 @@
+// C ABI of libmoe_mi355x.so (declarations and contract in include/moe_mi355x.h).
+// Validates arguments before any launch, carves the caller's workspace and dispatches to the kernels.
+#include <stdint.h>
+
+#include "moe_internal.h"
+
+namespace {
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int resolve_path(int path, int T) {
+    if (path == MOE_PATH_AUTO) return T == 1 ? MOE_PATH_SLOTS : MOE_PATH_GROUPED;
+    return path;
+}
+
+struct Layout {
+    size_t h, yp, counts, offsets, sorted, active, meta, total;
+};
+
+Layout layout(const moe_experts_t* w, int T, int k, int path) {
+    Layout L{};
+    const size_t nslots = (size_t)T * k;
+    size_t off = 0;
+    L.h = off;
+    off += align_up(nslots * (size_t)w->F * 2);
+    if (resolve_path(path, T) == MOE_PATH_GROUPED) {
+        L.yp = off;
+        off += align_up(nslots * (size_t)w->d * 4);
+        L.counts = off;
+        off += align_up((size_t)w->E * 4);
+        L.offsets = off;
+        off += align_up((size_t)(w->E + 1) * 4);
+        L.sorted = off;
+        off += align_up(nslots * 4);
+        L.active = off;
+        off += align_up((size_t)w->E * 4);
+        L.meta = off;
+        off += align_up(2 * 4);
+    }
+    L.total = off;
+    return L;
+}
+
+int check_proj(const moe_proj_t& p, int fmt) {
+    if (!p.codes || !p.scales) return MOE_ERR_ARG;
+    if (fmt == MOE_FMT_INT4_G64 && !p.biases) return MOE_ERR_ARG;
+    if (!aligned16(p.codes)) return MOE_ERR_ALIGN;
+    return MOE_OK;
+}
+
+int check_experts(const moe_experts_t* w) {
+    if (!w) return MOE_ERR_ARG;
+    if (w->fmt != MOE_FMT_INT4_G64 && w->fmt != MOE_FMT_MXFP4) return MOE_ERR_DTYPE;
+    if (w->E < 1 || w->d < 1 || w->F < 1) return MOE_ERR_ARG;
+    const int g = w->fmt == MOE_FMT_INT4_G64 ? 64 : 32;
+    if (w->d % 64 || w->F % 64 || w->d % g || w->F % g) return MOE_ERR_ARG;
+    int rc;
+    if ((rc = check_proj(w->gate, w->fmt)) || (rc = check_proj(w->up, w->fmt)) || (rc = check_proj(w->down, w->fmt)))
+        return rc;
+    return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* moe_version(void) { return "moe_mi355x 0.1 (gfx950, wave64)"; }
+
+int moe_router_counter_count(int T) { return T < 1 ? 1 : moe::router_counter_slots(T); }
+
+int moe_router(const void* x, const void* wr, const float* bias, int T, int d, int E, int k, int norm, float scale,
+               float* logits, int32_t* idx, float* wts, int32_t* counters, void* stream) {
+    if (T < 0 || d < 8 || d % 8 || E < 1 || E > 1024 || k < 1 || k > E || k > 32) return MOE_ERR_ARG;
+    if (T == 0) return MOE_OK;
+    if (!x || !wr || !logits || !idx || !wts || !counters) return MOE_ERR_ARG;
+    if (!aligned16(x) || !aligned16(wr)) return MOE_ERR_ALIGN;
+    return moe::launch_router((const uint16_t*)x, (const uint16_t*)wr, bias, T, d, E, k, norm, scale, logits, idx, wts,
+                              counters, (hipStream_t)stream);
+}
+
+int moe_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
+             void* stream) {
+    if (T < 0 || E < 1 || E > 1024 || k < 1 || k > E || k > 32) return MOE_ERR_ARG;
+    if (T == 0) return MOE_OK;
+    if (!logits || !idx || !wts) return MOE_ERR_ARG;
+    return moe::launch_topk(logits, dtype, T, E, k, norm, scale, idx, wts, (hipStream_t)stream);
+}
+
+int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted, int32_t* active,
+              int32_t* meta, void* stream) {
+    if (n < 0 || E < 1 || E > 8192) return MOE_ERR_ARG;
+    if (!counts || !offsets || !active || !meta || (n > 0 && (!idx || !sorted))) return MOE_ERR_ARG;
+    return moe::launch_group(idx, n, E, counts, offsets, sorted, active, meta, (hipStream_t)stream);
+}
+
+size_t moe_experts_workspace_bytes(const moe_experts_t* w, int T, int k, int path) {
+    if (!w || T < 0 || k < 1) return 0;
+    return layout(w, T, k, path).total;
+}
+
+int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T,
+                    int k, int act, int path, int nored, void* y, const void* residual, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+    int rc = check_experts(w);
+    if (rc) return rc;
+    if (T < 0 || k < 1 || act < 0 || act > 2 || path < 0 || path > 2) return MOE_ERR_ARG;
+    if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;
+    const int rpath = resolve_path(path, T);
+    if (nored && (rpath != MOE_PATH_SLOTS || residual)) return MOE_ERR_ARG;
+    if (T == 0) return MOE_OK;
+    if (!x || !idx || !wts || !y) return MOE_ERR_ARG;
+    if (!aligned16(x) || !aligned16(y) || (residual && !aligned16(residual))) return MOE_ERR_ALIGN;
+    const Layout L = layout(w, T, k, path);
+    if (!workspace || workspace_bytes < L.total) return MOE_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return MOE_ERR_ALIGN;
+    char* ws = (char*)workspace;
+    moe::ExpertsArgs a{};
+    a.w = w;
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.idx = idx;
+    a.wts = wts;
+    a.T = T;
+    a.k = k;
+    a.act = act;
+    a.nored = nored;
+    a.y = y;
+    a.residual = residual;
+    a.h = ws + L.h;
+    a.st = (hipStream_t)stream;
+    if (rpath == MOE_PATH_GROUPED) {
+        a.yp = (float*)(ws + L.yp);
+        a.grp.counts = (int32_t*)(ws + L.counts);
+        a.grp.offsets = (int32_t*)(ws + L.offsets);
+        a.grp.sorted = (int32_t*)(ws + L.sorted);
+        a.grp.active = (int32_t*)(ws + L.active);
+        a.grp.meta = (int32_t*)(ws + L.meta);
+    }
+    if (w->fmt == MOE_FMT_INT4_G64)
+        return rpath == MOE_PATH_GROUPED ? moe::run_int4_grouped(a) : moe::run_int4_slots(a);
+    return rpath == MOE_PATH_GROUPED ? moe::run_mxfp4_grouped(a) : moe::run_mxfp4_slots(a);
+}
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+// Shared device helpers for the gfx950 MoE kernels (wave64, CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MOE_WAVE 64
+
+typedef __bf16 moe_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 moe_f16x2 __attribute__((ext_vector_type(2)));
+
+namespace moe {
+
+// ------------------------------------------------------------------------------------ bf16 / fp32
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// a.x*b.x + a.y*b.y + c with bf16 pairs packed in 32-bit words (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(moe_bf16x2, a), __builtin_bit_cast(moe_bf16x2, b), c,
+                                           false);
+}
+
+// Two 4-bit codes of one word -> a bf16 pair holding (128 + q_i, 128 + q_{i+4}): the code lands in the
+// low mantissa bits of 128.0 (bf16 0x4300), whose ulp is exactly 1. Nibble i sits at bits 4i..4i+3 and
+// nibble i+4 at bits 16+4i.., so one shift + mask + or decodes two weights.
+__device__ __forceinline__ uint32_t q4pair_bf16(uint32_t word, int i) {
+    return ((word >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
+}
+#define MOE_Q4_OFFSET 128.0f
+
+// Activation pairs matching q4pair_bf16's element order: for word j of a 32-element chunk the pair for
+// nibble i is (x[8j+i], x[8j+i+4]). xw are the 16 words holding 32 consecutive bf16 (low half = even).
+__device__ __forceinline__ void pair_x32(const uint32_t xw[16], uint32_t xp[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t a = xw[4 * j + 0], b = xw[4 * j + 1], c = xw[4 * j + 2], d = xw[4 * j + 3];
+        xp[4 * j + 0] = (a & 0xffffu) | (c << 16);          // (x0, x4)
+        xp[4 * j + 1] = (a >> 16) | (c & 0xffff0000u);      // (x1, x5)
+        xp[4 * j + 2] = (b & 0xffffu) | (d << 16);          // (x2, x6)
+        xp[4 * j + 3] = (b >> 16) | (d & 0xffff0000u);      // (x3, x7)
+    }
+}
+
+// sum over 32 bf16 held as 16 words (any pairing)
+__device__ __forceinline__ float sum_x32(const uint32_t xw[16]) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s = dot2_bf16(xw[i], 0x3f803f80u, s);
+    return s;
+}
+
+// sum_k (128 + q_k) * x_k over one 16-byte chunk of 32 codes against paired activations
+__device__ __forceinline__ float dot_q4x32(uint4 w, const uint32_t xp[16]) {
+    float acc = 0.f;
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = dot2_bf16(q4pair_bf16(ws[j], i), xp[4 * j + i], acc);
+    return acc;
+}
+
+__device__ __forceinline__ void load_x32(const uint16_t* p, uint32_t xw[16]) {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint4 v = q[i];
+        xw[4 * i + 0] = v.x;
+        xw[4 * i + 1] = v.y;
+        xw[4 * i + 2] = v.z;
+        xw[4 * i + 3] = v.w;
+    }
+}
+
+// ------------------------------------------------------------------------------------ wave reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, MOE_WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, MOE_WAVE));
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        uint32_t o = __shfl_xor(v, s, MOE_WAVE);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+// sum within aligned groups of G lanes (G a power of two <= 64); every lane of the group gets the sum
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int s = G / 2; s >= 1; s >>= 1) v += __shfl_xor(v, s, MOE_WAVE);
+    return v;
+}
+
+// ------------------------------------------------------------------------------------ activations
+// act 0: SiLU(g) * u; 1: tanh-GELU(g) * u; 2: gpt-oss clamped SwiGLU, g = min(g, 7), u = clip(u, -7, 7),
+// g * sigmoid(1.702 g) * (u + 1).
+template <int ACT>
+__device__ __forceinline__ float glu(float g, float u) {
+    if (ACT == 0) return g / (1.f + expf(-g)) * u;
+    if (ACT == 1) return 0.5f * g * (1.f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g))) * u;
+    g = fminf(g, 7.f);
+    u = fminf(fmaxf(u, -7.f), 7.f);
+    return g / (1.f + expf(-1.702f * g)) * (u + 1.f);
+}
+
+}  // namespace moe

@@ -1,0 +1,52 @@
+// Internal launcher interface shared by the kernel translation units and the C-ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moe_mi355x.h"
+
+namespace moe {
+
+// router / grouping (moe_router.hip)
+int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
+                  float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st);
+int router_counter_slots(int T);
+int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
+                hipStream_t st);
+int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
+                 int32_t* active, int32_t* meta, hipStream_t st);
+
+// grouping scratch inside an experts workspace
+struct GroupBufs {
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* sorted;
+    int32_t* active;
+    int32_t* meta;
+};
+
+struct ExpertsArgs {
+    const moe_experts_t* w;
+    const void* x;
+    int x_dtype;
+    const int32_t* idx;
+    const float* wts;
+    int T, k, act, nored;
+    void* y;
+    const void* residual;
+    void* h;        // [T*k, F] activation-dtype scratch
+    float* yp;      // [T*k, d] fp32 scratch (grouped path)
+    GroupBufs grp;  // grouped path
+    hipStream_t st;
+};
+
+// int4 g64 expert kernels (moe_int4.hip)
+int run_int4_slots(const ExpertsArgs& a);
+int run_int4_grouped(const ExpertsArgs& a);
+// MXFP4 expert kernels (moe_mxfp4.hip)
+int run_mxfp4_slots(const ExpertsArgs& a);
+int run_mxfp4_grouped(const ExpertsArgs& a);
+// combine (moe_int4.hip): y[t] = residual[t] + sum_j yp[t*k + j]
+int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int x_dtype, hipStream_t st);
+
+}  // namespace moe

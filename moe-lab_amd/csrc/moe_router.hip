@@ -1,0 +1,281 @@
+// Router and slot grouping kernels for gfx950.
+//
+// router_logits_topk: logits[t, e] = x[t] . Wr[e] (+ b[e]) in fp32, one wave per (expert, token group),
+// then the last block to finish a token group runs the router tail (top-k, softmax) for its tokens.
+// The logit reduction order is fixed (lane l takes 8-element chunks l, l+64, ... with fused
+// multiply-adds in element order; the 64 lane partials are combined by an xor butterfly 32..1; the bias
+// is added last), so a CPU restatement reproduces every logit bit for bit and top-k ids match exactly.
+//
+// Router tail semantics follow reference moelab/router.py:1-66: NaN counts as -inf, k rounds of arg-max
+// with the lowest expert id winning ties, fewer than k finite logits -> lowest unused ids with weight 0,
+// norm: softmax over the top-k logits, !norm: full-softmax probabilities; weights times `scale`.
+//
+// group_slots: stable grouping of the T*k slots by expert (reference metal_q4_tiles_v2.py:362-373 lists a
+// tile's slots in ascending slot id; closed form = stable argsort, reference triton_fused_moe.py:56-70).
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+constexpr int ROUTER_WAVES = 4;   // waves per block = experts per block
+constexpr int ROUTER_TPW = 4;     // tokens per wave (the Wr row chunk is reused across them)
+constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024
+
+template <bool ATOMIC_LOAD>
+__device__ __forceinline__ float load_logit(const float* p) {
+    if (ATOMIC_LOAD) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+
+template <typename LT>
+__device__ __forceinline__ float to_f32(LT v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return bf16_to_f32(v); }
+template <>
+__device__ __forceinline__ float to_f32<_Float16>(_Float16 v) { return (float)v; }
+
+// One wave: router tail for one token. `lg(e)` yields logit e as fp32. Writes idx[k], wts[k].
+template <typename F>
+__device__ void wave_topk(F lg, int E, int k, int norm, float scale, int32_t* idx, float* wts) {
+    const int lane = threadIdx.x & 63;
+    const int J = (E + 63) / 64;
+    float v[TOPK_MAX_J];
+#pragma unroll
+    for (int j = 0; j < TOPK_MAX_J; ++j) {
+        const int e = j * 64 + lane;
+        float l = (j < J && e < E) ? lg(e) : -INFINITY;
+        v[j] = __builtin_isnan(l) ? -INFINITY : l;
+    }
+    float m0 = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < TOPK_MAX_J; ++j) m0 = fmaxf(m0, v[j]);
+    m0 = wave_max(m0);
+    float den = 0.f;
+    if (!norm) {
+#pragma unroll
+        for (int j = 0; j < TOPK_MAX_J; ++j) den += (v[j] == -INFINITY) ? 0.f : expf(v[j] - m0);
+        den = wave_sum(den);
+    }
+    float myv = -INFINITY;   // lane r < k holds round r's value and id
+    uint32_t myi = 0;
+    float top0 = -INFINITY;
+    for (int r = 0; r < k; ++r) {
+        float b = -INFINITY;
+        uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = 0; j < TOPK_MAX_J; ++j)
+            if (v[j] > b) { b = v[j]; bi = (uint32_t)(j * 64 + lane); }
+        float m = wave_max(b);
+        uint32_t sel = wave_min_u32(b == m ? bi : 0xFFFFFFFFu);
+        if (sel == 0xFFFFFFFFu) {   // no finite candidate left: lowest id not chosen yet, weight 0
+            sel = 0;
+            while (__ballot(lane < r && myi == sel) != 0ull) ++sel;
+            m = -INFINITY;
+        } else if ((int)(sel & 63u) == lane) {
+#pragma unroll
+            for (int j = 0; j < TOPK_MAX_J; ++j)
+                if (j == (int)(sel >> 6)) v[j] = -INFINITY;
+        }
+        if (r == 0) top0 = m;
+        if (lane == r) { myv = m; myi = sel; }
+    }
+    float s;
+    if (norm) s = wave_sum(lane < k ? expf(myv - top0) : 0.f);
+    else s = den;
+    const float off = norm ? top0 : m0;
+    if (lane < k) {
+        idx[lane] = (int32_t)myi;
+        wts[lane] = expf(myv - off) / s * scale;
+    }
+}
+
+// grid (ceil(E / ROUTER_WAVES), ceil(T / ROUTER_TPW)), block 64 * ROUTER_WAVES.
+// counters[ty] must be 0 on entry; the last block of token group ty resets it to 0.
+__global__ void __launch_bounds__(64 * ROUTER_WAVES)
+router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, const float* __restrict__ bias,
+                   int T, int d, int E, int k, int norm, float scale, float* __restrict__ logits,
+                   int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* __restrict__ counters) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int e = blockIdx.x * ROUTER_WAVES + wave;
+    const int t0 = blockIdx.y * ROUTER_TPW;
+    const int nt = min(ROUTER_TPW, T - t0);
+    const int nchunk = d >> 3;
+    if (e < E) {
+        float acc[ROUTER_TPW];
+#pragma unroll
+        for (int i = 0; i < ROUTER_TPW; ++i) acc[i] = 0.f;
+        const uint4* wrow = reinterpret_cast<const uint4*>(wr + (size_t)e * d);
+        for (int c = lane; c < nchunk; c += 64) {
+            const uint4 w = wrow[c];
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int i = 0; i < ROUTER_TPW; ++i) {
+                if (i < nt) {
+                    const uint4 xv = reinterpret_cast<const uint4*>(x + (size_t)(t0 + i) * d)[c];
+                    const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+                    float a = acc[i];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        a = __builtin_fmaf(bf16lo(xx[q]), bf16lo(ww[q]), a);
+                        a = __builtin_fmaf(bf16hi(xx[q]), bf16hi(ww[q]), a);
+                    }
+                    acc[i] = a;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < ROUTER_TPW; ++i) {
+            float a = acc[i];
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) a = a + __shfl_xor(a, s, 64);
+            if (bias) a = a + bias[e];
+            if (lane == 0 && i < nt) logits[(size_t)(t0 + i) * E + e] = a;
+        }
+    }
+    // last block of this token group runs the tail
+    __shared__ int s_last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = atomicAdd(&counters[blockIdx.y], 1);
+        s_last = (old == (int)gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    if (wave < nt) {
+        const int t = t0 + wave;
+        const float* lrow = logits + (size_t)t * E;
+        wave_topk([&](int ee) { return load_logit<true>(lrow + ee); }, E, k, norm, scale, idx + (size_t)t * k,
+                  wts + (size_t)t * k);
+    }
+    if (threadIdx.x == 0) counters[blockIdx.y] = 0;
+}
+
+// Router tail on given logits [T, E] (fp32, bf16 or fp16): one wave per token.
+template <typename LT>
+__global__ void __launch_bounds__(256)
+topk_kernel(const LT* __restrict__ logits, int T, int E, int k, int norm, float scale, int32_t* __restrict__ idx,
+            float* __restrict__ wts) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const LT* lrow = logits + (size_t)t * E;
+    wave_topk([&](int ee) { return to_f32<LT>(lrow[ee]); }, E, k, norm, scale, idx + (size_t)t * k,
+              wts + (size_t)t * k);
+}
+
+// Stable slot grouping by expert, one block of 256 threads. Slots p = t*k + j with ids outside [0, E)
+// are left out of every group (they contribute nothing) and counted in meta[1].
+// Outputs: counts[E], offsets[E+1], sorted[n] (valid part: offsets[E] entries), active[E] (first meta[0]
+// entries: experts with count > 0, ascending), meta[0] = number of active experts, meta[1] = bad ids.
+__global__ void __launch_bounds__(256)
+group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+            int32_t* __restrict__ sorted, int32_t* __restrict__ active, int32_t* __restrict__ meta) {
+    extern __shared__ int32_t sm[];   // cnt[E], cursor[E]
+    int32_t* cnt = sm;
+    int32_t* cursor = sm + E;
+    __shared__ int32_t s_bad;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += 256) cnt[e] = 0;
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+    for (int p = tid; p < n; p += 256) {
+        const int e = idx[p];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+        else atomicAdd(&s_bad, 1);
+    }
+    __syncthreads();
+    if (tid < 64) {   // wave 0: exclusive scan of counts and the active list, in chunks of 64 experts
+        const int lane = tid;
+        int run = 0, run_act = 0;
+        for (int base = 0; base < E; base += 64) {
+            const int e = base + lane;
+            const int c = e < E ? cnt[e] : 0;
+            // inclusive wave scan of c and of (c > 0)
+            int inc = c, act = c > 0 ? 1 : 0;
+#pragma unroll
+            for (int s = 1; s < 64; s <<= 1) {
+                const int o = __shfl_up(inc, s, 64);
+                const int oa = __shfl_up(act, s, 64);
+                if (lane >= s) { inc += o; act += oa; }
+            }
+            if (e < E) {
+                const int excl = run + inc - c;
+                offsets[e] = excl;
+                cursor[e] = excl;
+                counts[e] = c;
+                if (c > 0) active[run_act + act - 1] = e;
+            }
+            run += __shfl(inc, 63, 64);
+            run_act += __shfl(act, 63, 64);
+        }
+        if (lane == 0) {
+            offsets[E] = run;
+            meta[0] = run_act;
+            meta[1] = s_bad;
+        }
+        for (int a = run_act + lane; a < E; a += 64) active[a] = -1;
+    }
+    __syncthreads();
+    if (tid < 64) {   // wave 0: stable placement, 64 slots per step in ascending order
+        const int lane = tid;
+        int nbits = 0;
+        while ((1 << nbits) < E) ++nbits;
+        const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        for (int base = 0; base < n; base += 64) {
+            const int p = base + lane;
+            int e = p < n ? idx[p] : -1;
+            const bool ok = (e >= 0 && e < E);
+            // lanes holding the same valid expert: match on every bit of e
+            uint64_t peers = __ballot(ok);
+            for (int b = 0; b < nbits; ++b) {
+                const bool bit = ok && ((e >> b) & 1);
+                const uint64_t m = __ballot(bit);
+                peers &= bit ? m : ~m;
+            }
+            int pos = 0;
+            if (ok) pos = cursor[e] + __popcll(peers & lt_mask);
+            __builtin_amdgcn_wave_barrier();
+            if (ok) {
+                sorted[pos] = p;
+                if ((peers & lt_mask) == 0ull) cursor[e] += __popcll(peers);   // lowest lane of the group
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------ host launchers
+int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
+                  float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st) {
+    dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, (T + ROUTER_TPW - 1) / ROUTER_TPW);
+    router_logits_topk<<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, k, norm, scale, logits, idx, wts,
+                                                            counters);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+int router_counter_slots(int T) { return (T + ROUTER_TPW - 1) / ROUTER_TPW; }
+
+int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
+                hipStream_t st) {
+    dim3 grid((T + 3) / 4);
+    if (dtype == MOE_DTYPE_F32)
+        topk_kernel<float><<<grid, 256, 0, st>>>((const float*)logits, T, E, k, norm, scale, idx, wts);
+    else if (dtype == MOE_DTYPE_BF16)
+        topk_kernel<uint16_t><<<grid, 256, 0, st>>>((const uint16_t*)logits, T, E, k, norm, scale, idx, wts);
+    else if (dtype == MOE_DTYPE_F16)
+        topk_kernel<_Float16><<<grid, 256, 0, st>>>((const _Float16*)logits, T, E, k, norm, scale, idx, wts);
+    else
+        return MOE_ERR_DTYPE;
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
+                 int32_t* active, int32_t* meta, hipStream_t st) {
+    group_slots<<<1, 256, 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted, active, meta);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+}  // namespace moe

@@ -1,0 +1,68 @@
+"""Production dispatcher, int4 affine g64 MoE experts on MI355X (gfx950 HIP kernels).
+
+Same variant contract and dispatch shape as the reference's production int4 dispatcher
+(reference moelab/variants/mlx/metal_q4_moe.py:1-64):
+    T == 1                  -> per-slot GEMV: gate+up+GLU fused, down + k-reduction fused (2 launches)
+    T > 1, custom_wins(...) -> grouped expert tiles: each selected expert's rows are read once and
+                               applied to all of its slots (group, gate/up, down, combine)
+    otherwise               -> gather_moe (module attribute, monkeypatchable like the reference's)
+prepare / dequant keep the reference's state layout (mx.quantize affine, group 64), so `dequant(state)`
+gives the weights the fp32 reference uses.
+"""
+import torch
+
+from .. import _lib, formats
+from ..experts import dims, run_experts
+from ..fallback import gather_moe  # noqa: F401  (module attribute the dispatcher calls; tests patch it)
+
+META = {"name": "hip_q4_moe", "description": "gfx950 HIP: per-slot GEMV at T=1, grouped expert tiles at T>1"}
+BITS, GS = 4, 64
+MODE = "affine"
+W_BITS = BITS + 32 / GS
+
+
+def prepare(w_gate, w_up, w_down):
+    """Dense weights gate/up [E, F, d], down [E, d, F] (any float dtype, on the GPU) -> packed state."""
+    E, f, d = w_gate.shape
+    assert d % 64 == 0 and f % 64 == 0, "d, f must be multiples of 64"
+    s = {n: formats.quantize_int4(w.contiguous()) for n, w in (("g", w_gate), ("u", w_up), ("d", w_down))}
+    s["fmt"] = "int4"
+    return s
+
+
+def state_from_packed(g, u, d, bg=None, bu=None, bd=None):
+    """State from already-packed (codes, scales, biases) triples, e.g. a checkpoint or synthetic weights."""
+    s = {"g": tuple(g), "u": tuple(u), "d": tuple(d), "fmt": "int4"}
+    for n, b in (("bg", bg), ("bu", bu), ("bd", bd)):
+        if b is not None:
+            s[n] = b.to(torch.float32).contiguous()
+    return s
+
+
+def dequant(s):
+    return tuple(formats.dequant_int4(*s[n], group_size=GS) for n in ("g", "u", "d"))
+
+
+def custom_wins(T, k, E, D, F):
+    """Load policy (reference metal_q4_moe.py:42-46): grouped tiles up to load = T*k/E of 24 for large
+    experts (D*F >= 1.5 * 2^20), 8 otherwise; above it the fallback runs."""
+    load = T * k / E
+    return load <= (24 if D * F >= 3 << 19 else 8)
+
+
+def run_slots(s, x, idx, act=0):
+    """T = 1 per-slot expert outputs [k, D], unweighted (reference metal_q4_moe.py:49-51)."""
+    ones = torch.ones(idx.shape, dtype=torch.float32, device=x.device)
+    return run_experts(s, x, idx, ones, act=act, path=_lib.PATH_SLOTS, nored=True)
+
+
+def run(s, x, idx, wts, act=0, residual=None):
+    """act: 0 = SwiGLU, 1 = GeGLU (tanh-GELU), 2 = gpt-oss clamped SwiGLU. residual: optional [T, D]
+    added to the output inside the last kernel (y = residual + moe(x))."""
+    T, k = idx.shape
+    if T == 1:
+        return run_experts(s, x, idx, wts, act=act, path=_lib.PATH_SLOTS, residual=residual)
+    E, D, F = dims(s)
+    if not custom_wins(T, k, E, D, F):
+        return gather_moe(s, x, idx, wts, GS, BITS, act=act, residual=residual)
+    return run_experts(s, x, idx, wts, act=act, path=_lib.PATH_GROUPED, residual=residual)

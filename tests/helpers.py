@@ -1,0 +1,50 @@
+"""Shared test helpers: move packed GPU states to the CPU oracle, run the oracle reference."""
+import numpy as np
+import torch
+
+import __graft_entry__
+
+orc = __graft_entry__.load_oracle()
+
+TOL_MAXABS_RMS = 1e-2   # max |y - y_ref| <= 1e-2 * RMS(y_ref)  (fp32 accumulation, bf16 h and y)
+
+
+def np_u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def np_words(t):
+    return t.detach().cpu().contiguous().numpy().view(np.uint32)
+
+
+def deq(state, name, experts=None):
+    """Oracle dequantisation (fp64) of projection `name` of a packed state, optionally only `experts`."""
+    p = state[name]
+    sel = (lambda t: t) if experts is None else (lambda t: t[experts])  # noqa: E731
+    if state.get("fmt", "int4") == "int4":
+        return orc.dequant_int4(np_words(sel(p[0])), np_u16(sel(p[1])), np_u16(sel(p[2])))
+    return orc.dequant_mxfp4(np_words(sel(p[0])), sel(p[1]).cpu().numpy())
+
+
+class LazyExperts:
+    """e -> dequantised [N, K] weights of one expert (keeps the oracle's memory bounded at full sizes)."""
+
+    def __init__(self, state, name):
+        self.state, self.name = state, name
+
+    def __call__(self, e):
+        return deq(self.state, self.name, experts=[int(e)])[0]
+
+
+def oracle_y(state, x, idx, wts, act=0):
+    xs = orc.bf16_bits_to_f32(np_u16(x)) if x.dtype == torch.bfloat16 else x.float().cpu().numpy()
+    b = {n: state[n].cpu().numpy().astype(np.float64) for n in ("bg", "bu", "bd") if n in state}
+    return orc.moe_reference(xs, LazyExperts(state, "g"), LazyExperts(state, "u"), LazyExperts(state, "d"),
+                             idx.cpu().numpy(), wts.cpu().numpy(), act, b.get("bg"), b.get("bu"), b.get("bd"))
+
+
+def assert_close(y, y_ref, tol=TOL_MAXABS_RMS, what=""):
+    err = orc.error_metrics(y.float().cpu().numpy(), y_ref)
+    assert err["finite"], (what, err)
+    assert err["max_abs"] <= tol * err["rms_ref"] + 1e-30, (what, err)
+    return err

@@ -1,0 +1,84 @@
+"""The C-ABI library loads, exports every entry point include/moe_mi355x.h declares, and rejects
+invalid arguments before touching the GPU (host-side checks only; no kernel runs here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "moe_mi355x.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(moe_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_header_declares_the_api():
+    fns = declared_functions()
+    for n in ("moe_router", "moe_topk", "moe_group", "moe_experts_run", "moe_experts_workspace_bytes"):
+        assert n in fns, fns
+
+
+def test_library_exports_every_declared_symbol():
+    from moelab_amd import _lib
+    L = _lib.lib()
+    for n in declared_functions():
+        assert hasattr(L, n), n
+    assert set(_lib.EXPORTS) <= set(declared_functions())
+    assert b"gfx950" in L.moe_version()
+
+
+def _desc(E=8, d=128, F=128, fmt=0):
+    from moelab_amd import _lib
+    fake = ctypes.c_void_p(4096)   # never dereferenced: argument checks return before any launch
+    p = _lib.Proj(fake, fake, fake, None)
+    return _lib.Experts(fmt, E, d, F, p, p, p)
+
+
+def test_workspace_query_host_only():
+    from moelab_amd import _lib
+    L = _lib.lib()
+    w = _desc(E=128, d=2048, F=768)
+    slots = L.moe_experts_workspace_bytes(w, 1, 8, _lib.PATH_SLOTS)
+    assert slots >= 8 * 768 * 2
+    grouped = L.moe_experts_workspace_bytes(w, 32, 8, _lib.PATH_GROUPED)
+    assert grouped >= 256 * 768 * 2 + 256 * 2048 * 4
+
+
+@pytest.mark.parametrize("case,rc", [("d_not_64", -1), ("bad_fmt", -2), ("bad_act", -1), ("no_ws", -3),
+                                     ("bad_dtype", -2), ("nored_grouped", -1), ("misaligned", -5)])
+def test_argument_errors_before_launch(case, rc):
+    from moelab_amd import _lib
+    L = _lib.lib()
+    w = _desc()
+    x = ctypes.c_void_p(4096)
+    act, dtype, path, nored, ws, wsb = 0, 0, 0, 0, ctypes.c_void_p(8192), 1 << 30
+    if case == "d_not_64":
+        w = _desc(d=96)
+    elif case == "bad_fmt":
+        w = _desc(fmt=7)
+    elif case == "bad_act":
+        act = 9
+    elif case == "no_ws":
+        ws, wsb = None, 0
+    elif case == "bad_dtype":
+        dtype = 5
+    elif case == "nored_grouped":
+        path, nored = _lib.PATH_GROUPED, 1
+    elif case == "misaligned":
+        x = ctypes.c_void_p(4097)
+    got = L.moe_experts_run(w, x, dtype, x, x, 4, 2, act, path, nored, ctypes.c_void_p(4096), None, ws, wsb, None)
+    assert got == rc
+
+
+def test_router_argument_errors():
+    from moelab_amd import _lib
+    L = _lib.lib()
+    p = ctypes.c_void_p(4096)
+    assert L.moe_router(p, p, None, 1, 2048, 2048, 8, 1, 1.0, p, p, p, p, None) == -1   # E > 1024
+    assert L.moe_router(p, p, None, 1, 2048, 128, 33, 1, 1.0, p, p, p, p, None) == -1   # k > 32
+    assert L.moe_topk(p, 0, 1, 16, 17, 1, 1.0, p, p, None) == -1                        # k > E
+    assert L.moe_group(p, 4, 0, p, p, p, p, p, None) == -1                              # E < 1
