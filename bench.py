@@ -1,0 +1,264 @@
+"""Benchmark: quantised MoE layer on one MI355X (BASELINE metric: MoE layer us/call + weight-byte GB/s
+vs HBM peak at T=1 and T=32).
+
+Workload: Qwen3-30B-A3B-shape int4 g64 SwiGLU MoE layer, d=2048, F=768, E=128, k=8,
+T=1, over 48 independently seeded layers (16.3 GB of packed experts, far beyond the 256 MB Infinity
+Cache). A step is one token through the 48 layers: x <- x + moe_l(x) for l = 0..47, captured once in a
+HIP graph and replayed. `value` is expert weight-byte GB/s of that chain: the packed bytes of the unique
+selected experts of all 48 layers divided by the step time, the reference's `run(state, x, idx, wts)`
+contract (routing precomputed per layer, reference mlx_backend.py:91-117). The same chain with the
+fused router inside each layer is reported as `with_router`. BASELINE config 3 (T=32, uniform and
+Zipf(1.1) routing) reports the grouped expert path against the per-slot stock-style gather.
+
+roofline: the dominant kernel at T=1 is the gate/up GEMV (2/3 of the weight bytes). Its average launch
+duration is measured with HIP events on the stream it runs on, around graph replays of 48 gate/up-only
+launches; achieved = algorithmic bytes per launch (k unique experts x gate+up packed bytes) / duration.
+
+cpu_baseline: the reference's CPU torch path (torch_loop, reference variants/cuda/torch_loop.py:11-17)
+on dequantised fp32 weights of the selected experts, timed on this host for a bounded sample of layers.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+import __graft_entry__  # noqa: E402
+
+METRIC = "MoE layer µs/call + weight-byte GB/s vs HBM peak at T=1 and T=32"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def graph_of(fn):
+    """Capture fn() (a chain of launches on the current stream) into a HIP graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()   # eager warm-up on the capture stream (allocations happen here, not in the graph)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    return g, out
+
+
+def time_graph(g, steps, warmup):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(steps):
+        g.replay()
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / 1e3 / steps   # seconds per replay
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU-baseline sample (0: skip)")
+    ap.add_argument("--no-t32", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one MI355X: the expert path is single-GPU (expert "
+                                   "parallel sharding is described in DESIGN.md, not launched); run with --gpus 1"}))
+        sys.exit(2)
+
+    __graft_entry__.load_package()
+    from moelab_amd import _lib, roofline, router
+    from moelab_amd.experts import run_experts
+    from moelab_amd.problem import baseline_int4_layer, baseline_x, zipf_bias
+    from moelab_amd.shapes import SHAPES
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    sh = SHAPES["qwen3-30b-a3b"]
+    L = args.layers
+    per_expert = roofline.expert_bytes(sh.d, sh.f, "int4")
+    log(f"library {_lib.lib().moe_version().decode()} on {torch.cuda.get_device_name(0)}; building {L} layers")
+    t0 = time.time()
+    layers = [baseline_int4_layer(sh, seed=1000 + l, device=dev) for l in range(L)]
+    torch.cuda.synchronize()
+    log(f"layers ready in {time.time() - t0:.1f}s ({L * 3 * per_expert / 1e9:.2f} GB packed experts)")
+
+    # one workspace for every graph below (graphs keep raw pointers into it)
+    desc_probe = layers[0]
+    from moelab_amd.experts import _desc
+    need = max(_lib.lib().moe_experts_workspace_bytes(_desc(desc_probe), T, sh.k, p)
+               for T in (1, 32, 64) for p in (_lib.PATH_SLOTS, _lib.PATH_GROUPED))
+    _lib.workspace(dev, need)
+
+    # ------------------------------------------------------------------ T = 1: experts-only chain
+    x1 = baseline_x(1, sh.d, seed=0, device=dev)
+    routes1 = [router.route(x1, ly["wr"], sh.k) for ly in layers]
+    U1 = [int(torch.unique(r[0]).numel()) for r in routes1]
+    bytes1 = sum(U1) * per_expert
+
+    def chain_t1():
+        x = x1.clone()
+        for ly, (idx, wts) in zip(layers, routes1):
+            x = run_experts(ly, x, idx, wts, path=_lib.PATH_SLOTS, residual=x)
+        return x
+
+    def chain_t1_router():
+        x = x1.clone()
+        for ly in layers:
+            idx, wts = router.route(x, ly["wr"], sh.k)
+            x = run_experts(ly, x, idx, wts, path=_lib.PATH_SLOTS, residual=x)
+        return x
+
+    def gate_up_only():
+        for ly, (idx, wts) in zip(layers, routes1):
+            run_experts(ly, x1, idx, wts, path=_lib.PATH_SLOTS, stages=_lib.STAGE_GATE_UP)
+
+    def down_only():
+        for ly, (idx, wts) in zip(layers, routes1):
+            run_experts(ly, x1, idx, wts, path=_lib.PATH_SLOTS, stages=_lib.STAGE_DOWN)
+
+    g1, _ = graph_of(chain_t1)
+    t_step = time_graph(g1, args.steps, args.warmup)
+    log(f"T=1 experts chain: {t_step * 1e6 / L:.2f} us/layer, {bytes1 / t_step / 1e9:.0f} GB/s")
+    g1r, _ = graph_of(chain_t1_router)
+    t_step_r = time_graph(g1r, args.steps, args.warmup)
+    log(f"T=1 with router: {t_step_r * 1e6 / L:.2f} us/layer")
+    ggu, _ = graph_of(gate_up_only)
+    t_gu = time_graph(ggu, args.steps, args.warmup) / L
+    gdn, _ = graph_of(down_only)
+    t_dn = time_graph(gdn, args.steps, args.warmup) / L
+    gu_bytes = sh.k * 2 * sh.f * sh.d * roofline.W_BITS["int4"] / 8
+    dn_bytes = sh.k * sh.d * sh.f * roofline.W_BITS["int4"] / 8
+    log(f"gate/up kernel {t_gu * 1e6:.2f} us ({gu_bytes / t_gu / 1e9:.0f} GB/s), down kernel {t_dn * 1e6:.2f} us "
+        f"({dn_bytes / t_dn / 1e9:.0f} GB/s)")
+
+    # ------------------------------------------------------------------ T = 32: grouped vs per-slot
+    t32 = {}
+    if not args.no_t32:
+        for dist in ("uniform", "zipf"):
+            T = 32
+            x32 = baseline_x(T, sh.d, seed=32, device=dev)
+            bias = torch.from_numpy(zipf_bias(sh.E, 1.1, seed=3)).to(dev) if dist == "zipf" else None
+            routes = [router.route(x32, ly["wr"], sh.k, bias=bias) for ly in layers]
+            U = [int(torch.unique(r[0]).numel()) for r in routes]
+
+            def chain(path):
+                def f():
+                    x = x32.clone()
+                    for ly, (idx, wts) in zip(layers, routes):
+                        x = run_experts(ly, x, idx, wts, path=path, residual=x)
+                    return x
+                return f
+            res = {}
+            for name, path in (("grouped", _lib.PATH_GROUPED), ("per_slot", _lib.PATH_SLOTS)):
+                g, _ = graph_of(chain(path))
+                t = time_graph(g, max(5, args.steps // 5), max(2, args.warmup // 5))
+                res[name] = t
+                del g
+            ub = sum(U) * per_expert
+            t32[dist] = {
+                "us_per_layer_grouped": res["grouped"] * 1e6 / L,
+                "us_per_layer_per_slot": res["per_slot"] * 1e6 / L,
+                "speedup_per_token": res["per_slot"] / res["grouped"],
+                "unique_experts_mean": float(np.mean(U)),
+                "weight_GBps_grouped": ub / res["grouped"] / 1e9,
+                "slot_weight_GBps_per_slot": L * T * sh.k * per_expert / res["per_slot"] / 1e9,
+            }
+            log(f"T=32 {dist}: grouped {t32[dist]['us_per_layer_grouped']:.1f} us/layer, per-slot "
+                f"{t32[dist]['us_per_layer_per_slot']:.1f} us/layer, speedup {t32[dist]['speedup_per_token']:.2f}x, "
+                f"U={t32[dist]['unique_experts_mean']:.1f}")
+
+    # ------------------------------------------------------------------ CPU baseline (bounded sample)
+    cpu = None
+    if args.cpu_layers > 0:
+        cpu = cpu_baseline(layers[:args.cpu_layers], routes1[:args.cpu_layers], x1, sh)
+        log(f"CPU baseline: {cpu['value']:.1f} us/layer on {cpu['cores']} threads")
+
+    value = bytes1 / t_step / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "qwen3-30b-a3b int4-g64 SwiGLU MoE layer, T=1, 48 seeded layers (BASELINE config 2)",
+                   "d": sh.d, "F": sh.f, "E": sh.E, "k": sh.k, "T": 1, "layers": L,
+                   "weights": "int4 affine g64 (bf16 scale+bias), decoded exactly to bf16 operands",
+                   "accumulation": "fp32", "parallelism": "single GPU"},
+        "us_per_layer": round(t_step * 1e6 / L, 3),
+        "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "weight_bytes_per_step": bytes1,
+        "with_router": {"us_per_layer": round(t_step_r * 1e6 / L, 3),
+                        "weight_GBps": round(bytes1 / t_step_r / 1e9, 2)},
+        "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3)},
+        "t32": t32,
+        "roofline": {"bound": "hbm", "kernel": "q4_gate_up_slots (T=1 gate/up GEMV + SwiGLU)",
+                     "achieved": round(gu_bytes / t_gu / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_bytes / t_gu / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": gu_bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(layers, routes, x, sh):
+    """torch_loop (the reference's CPU torch path) on fp32 dense weights of the selected experts only."""
+    from moelab_amd import formats
+    orc = __graft_entry__.load_oracle()
+    cores = torch.get_num_threads()
+    xs = x.float().cpu()
+    dense = []
+    for ly, (idx, wts) in zip(layers, routes):
+        sel = sorted(set(idx.flatten().tolist()))
+        w = {}
+        for n in ("g", "u", "d"):
+            codes, sc, bi = ly[n]
+            w[n] = {e: formats.dequant_int4(codes[e], sc[e], bi[e]).cpu() for e in sel}
+        dense.append((w, idx.cpu().long(), wts.cpu()))
+
+    def once():
+        y = xs
+        for w, idx, wts in dense:
+            y = y + orc.torch_loop(w["g"], w["u"], w["d"], y, idx, wts)
+        return y
+    once()
+    t0 = time.perf_counter()
+    reps = 0
+    while time.perf_counter() - t0 < 10.0 and reps < 2000:
+        once()
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps / len(dense)
+    return {"value": round(dt * 1e6, 2), "unit": "us/layer (T=1, expert path)", "cores": cores, "kind": "port",
+            "sample": f"{len(dense)} Qwen3 int4 layers at T=1 (k=8 experts each, dequantised to fp32), "
+                      f"{reps} reps of the residual chain, ~10 s",
+            "weight_GBps_equiv": round(sh.k * roofline_bytes(sh) / dt / 1e9, 2)}
+
+
+def roofline_bytes(sh):
+    from moelab_amd import roofline
+    return roofline.expert_bytes(sh.d, sh.f, "int4")
+
+
+if __name__ == "__main__":
+    main()

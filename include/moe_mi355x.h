@@ -107,17 +107,34 @@ int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offset
  * metal_mxfp4_moe.py:474-512, metal_mxfp4_gptoss.py:129-167):
  *   y[t] = residual[t] + sum_j wts[t,j] * ( down_e( act(gate_e x_t + bg_e, up_e x_t + bu_e) ) + bd_e ),
  *   e = idx[t,j]; residual optional (NULL = 0).
- *   x, y, residual [T, d] of dtype x_dtype; idx [T, k] int32; wts [T, k] fp32.
+ *   x [T, d] of x_dtype (MOE_DTYPE_BF16); y and residual [T, d] of y_dtype (MOE_DTYPE_BF16 as the
+ *   reference returns x.dtype, or MOE_DTYPE_F32 for the unrounded result); idx [T, k] int32; wts [T, k] fp32.
  *   path: MOE_PATH_*; nored = 1 writes the unweighted per-slot outputs y[T*k, d] instead (reference
  *   run_slots / NORED, metal_q4_moe.py:49-51; per-slot path only, residual must be NULL).
- *   Accumulation in fp32; the GLU output h is stored in x_dtype, as in the reference kernels.
+ *   Accumulation in fp32; the GLU output h is kept between the two launches as an unevaluated sum of two
+ *   bf16 planes (about 16 significant bits, where the reference kernels store it in x.dtype).
  *   Requirements: d % 64 == 0 and F % 64 == 0; x, y, codes 16-byte aligned.
  *   workspace: moe_experts_workspace_bytes(...) bytes, any content.
  */
 int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T,
-                    int k, int act, int path, int nored, void* y, const void* residual, void* workspace,
+                    int k, int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                     size_t workspace_bytes, void* stream);
 size_t moe_experts_workspace_bytes(const moe_experts_t* w, int T, int k, int path);
+
+/*
+ * The same call split at the one data dependency inside it, the GLU output h held in the workspace.
+ * The reference dispatches these as separate kernels as well (metal_q4_decode_v4.py:177-184 _k1 gate_up,
+ * _k2 down). stages = MOE_STAGE_GATE_UP: grouping (grouped path) + gate/up + GLU, h into the workspace;
+ * MOE_STAGE_DOWN: down projection + combine from the h a previous GATE_UP call with the same arguments
+ * left in the same workspace (stream-ordered); MOE_STAGE_ALL = both = moe_experts_run. Lets a caller
+ * interleave other work between the two stages, or time each stage on its own stream.
+ */
+#define MOE_STAGE_GATE_UP 1
+#define MOE_STAGE_DOWN 2
+#define MOE_STAGE_ALL 3
+int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,
+                           int T, int k, int act, int path, int nored, void* y, int y_dtype, const void* residual,
+                           void* workspace, size_t workspace_bytes, int stages, void* stream);
 
 /* Library version and build target, for logs. */
 const char* moe_version(void);

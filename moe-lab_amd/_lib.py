@@ -20,7 +20,8 @@ PATH_AUTO, PATH_SLOTS, PATH_GROUPED = 0, 1, 2
 ACT_SWIGLU, ACT_GEGLU, ACT_GPTOSS = 0, 1, 2
 
 EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
-           "moe_experts_workspace_bytes", "moe_version")
+           "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_version")
+STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 3
 
 _ERRORS = {
     MOE_ERR_ARG: "invalid argument (shape, size or pointer)",
@@ -61,11 +62,14 @@ def lib():
         L.moe_router_counter_count.argtypes = [i]
         L.moe_topk.argtypes = [vp, i, i, i, i, i, f, vp, vp, vp]
         L.moe_group.argtypes = [vp, i, i, vp, vp, vp, vp, vp, vp]
-        L.moe_experts_run.argtypes = [ctypes.POINTER(Experts), vp, i, vp, vp, i, i, i, i, i, vp, vp, vp, sz, vp]
+        L.moe_experts_run.argtypes = [ctypes.POINTER(Experts), vp, i, vp, vp, i, i, i, i, i, vp, i, vp, vp, sz, vp]
+        L.moe_experts_run_stages.argtypes = [ctypes.POINTER(Experts), vp, i, vp, vp, i, i, i, i, i, vp, i, vp, vp,
+                                             sz, i, vp]
         L.moe_experts_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i, i, i]
         L.moe_experts_workspace_bytes.restype = sz
         L.moe_version.restype = ctypes.c_char_p
-        for n in ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run"):
+        for n in ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
+                  "moe_experts_run_stages"):
             getattr(L, n).restype = ctypes.c_int
         _lib = L
     return _lib

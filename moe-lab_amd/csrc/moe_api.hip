@@ -24,7 +24,7 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
     const size_t nslots = (size_t)T * k;
     size_t off = 0;
     L.h = off;
-    off += align_up(nslots * (size_t)w->F * 2);
+    off += align_up(nslots * (size_t)w->F * 2) * 2;   // hi and lo planes
     if (resolve_path(path, T) == MOE_PATH_GROUPED) {
         L.yp = off;
         off += align_up(nslots * (size_t)w->d * 4);
@@ -101,12 +101,21 @@ size_t moe_experts_workspace_bytes(const moe_experts_t* w, int T, int k, int pat
 }
 
 int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T,
-                    int k, int act, int path, int nored, void* y, const void* residual, void* workspace,
+                    int k, int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                     size_t workspace_bytes, void* stream) {
+    return moe_experts_run_stages(w, x, x_dtype, idx, wts, T, k, act, path, nored, y, y_dtype, residual, workspace,
+                                  workspace_bytes, MOE_STAGE_ALL, stream);
+}
+
+int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,
+                           int T, int k, int act, int path, int nored, void* y, int y_dtype, const void* residual,
+                           void* workspace, size_t workspace_bytes, int stages, void* stream) {
+    if (stages < 1 || stages > MOE_STAGE_ALL) return MOE_ERR_ARG;
     int rc = check_experts(w);
     if (rc) return rc;
     if (T < 0 || k < 1 || act < 0 || act > 2 || path < 0 || path > 2) return MOE_ERR_ARG;
     if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;
+    if (y_dtype != MOE_DTYPE_BF16 && y_dtype != MOE_DTYPE_F32) return MOE_ERR_DTYPE;
     const int rpath = resolve_path(path, T);
     if (nored && (rpath != MOE_PATH_SLOTS || residual)) return MOE_ERR_ARG;
     if (T == 0) return MOE_OK;
@@ -127,9 +136,12 @@ int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const in
     a.act = act;
     a.nored = nored;
     a.y = y;
+    a.y32 = y_dtype == MOE_DTYPE_F32;
     a.residual = residual;
-    a.h = ws + L.h;
+    a.hhi = (uint16_t*)(ws + L.h);
+    a.hlo = a.hhi + align_up((size_t)T * k * w->F * 2) / 2;
     a.st = (hipStream_t)stream;
+    a.stages = stages;
     if (rpath == MOE_PATH_GROUPED) {
         a.yp = (float*)(ws + L.yp);
         a.grp.counts = (int32_t*)(ws + L.counts);

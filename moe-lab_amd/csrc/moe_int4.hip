@@ -8,6 +8,10 @@
 //   sum_k (s q_k + b) x_k = s * sum_k (128 + q_k) x_k + (b - 128 s) * sum_k x_k      (per 32-chunk)
 // Products of bf16 pairs are exact in fp32; accumulation is fp32.
 //
+// The GLU output h is kept at fp32 precision as two bf16 planes, h = hi + lo (hi = bf16(h), lo = bf16(h - hi),
+// |h - hi - lo| <= 2^-18 |h|), so the down projection runs on v_dot2_f32_bf16 twice per pair instead of
+// losing 2^-9 of h to a bf16 store.
+//
 // Per-slot path (T == 1, and the stock-style per-slot gather at T > 1; reference metal_q4_decode_v4.py):
 //   q4_gate_up_slots: one wave per RW rows of one slot; lanes stride over 16-byte chunks of the rows,
 //                     gate and up rows of the same index are read together so SwiGLU runs in-wave.
@@ -31,6 +35,40 @@ __device__ __forceinline__ float q4_fold(float acc, float s, float b, float dot,
     return __builtin_fmaf(s, dot, __builtin_fmaf(beff, xsum, acc));
 }
 
+// store h as hi/lo bf16 planes
+__device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t i, float v) {
+    const uint16_t hi = f32_to_bf16(v);
+    hhi[i] = hi;
+    hlo[i] = f32_to_bf16(v - bf16_to_f32(hi));
+}
+
+// one 32-element chunk of h (both planes) against decoded codes: returns sum (128+q) h, and sum h in *hs
+__device__ __forceinline__ float dot_h32(const uint32_t qp[16], const uint16_t* hhi, const uint16_t* hlo, float* hs) {
+    uint32_t hw[16], hp[16];
+    load_x32(hhi, hw);
+    pair_x32(hw, hp);
+    float s = sum_x32(hw);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2_bf16(qp[i], hp[i], acc);
+    load_x32(hlo, hw);
+    pair_x32(hw, hp);
+    s += sum_x32(hw);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2_bf16(qp[i], hp[i], acc);
+    *hs = s;
+    return acc;
+}
+
+// output store in the caller's dtype (bf16 or fp32)
+__device__ __forceinline__ void store_y(void* y, size_t i, float v, int y32) {
+    if (y32) reinterpret_cast<float*>(y)[i] = v;
+    else reinterpret_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
+}
+__device__ __forceinline__ float load_y(const void* y, size_t i, int y32) {
+    return y32 ? reinterpret_cast<const float*>(y)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
+}
+
 __device__ __forceinline__ void decode_q4x32(uint4 w, uint32_t qp[16]) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -47,13 +85,14 @@ __device__ __forceinline__ float dot_pairs16(const uint32_t qp[16], const uint32
 }
 
 // ------------------------------------------------------------------------------ per-slot gate / up
-// grid (ceil(F / (GU_WAVES*RW)), T*k), block 64*GU_WAVES. h [T*k, F] bf16.
+// grid (ceil(F / (GU_WAVES*RW)), T*k), block 64*GU_WAVES. h planes [T*k, F].
 template <int RW, int ACT>
 __global__ void __launch_bounds__(64 * GU_WAVES)
 q4_gate_up_slots(const uint16_t* __restrict__ x, const uint32_t* __restrict__ gq, const uint16_t* __restrict__ gs,
                  const uint16_t* __restrict__ gb, const uint32_t* __restrict__ uq, const uint16_t* __restrict__ us,
                  const uint16_t* __restrict__ ub, const float* __restrict__ bg, const float* __restrict__ bu,
-                 const int32_t* __restrict__ idx, int k, int d, int F, int E, uint16_t* __restrict__ h) {
+                 const int32_t* __restrict__ idx, int k, int d, int F, int E, uint16_t* __restrict__ hhi,
+                 uint16_t* __restrict__ hlo) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int slot = blockIdx.y;
     const int row0 = (blockIdx.x * GU_WAVES + wave) * RW;
@@ -110,20 +149,20 @@ q4_gate_up_slots(const uint16_t* __restrict__ x, const uint32_t* __restrict__ gq
                 if (bu) u += bu[(size_t)e * F + n];
                 hv = glu<ACT>(g, u);
             }
-            h[(size_t)slot * F + n] = f32_to_bf16(hv);
+            store_h(hhi, hlo, (size_t)slot * F + n, hv);
         }
     }
 }
 
 // ------------------------------------------------------------------------------------ per-slot down
 // grid (ceil(D / RPW), T), block 64*DN_WAVES; RPW = 64 / LPR rows per block, the 4 waves split the k slots.
-// y [T, D] (or [T*k, D] unweighted when nored).
+// y [T, D] (or [T*k, D] unweighted when nored), fp32 when y32 else bf16; resid has y's dtype.
 template <int LPR>
 __global__ void __launch_bounds__(64 * DN_WAVES)
-q4_down_slots(const uint16_t* __restrict__ h, const uint32_t* __restrict__ dq, const uint16_t* __restrict__ ds,
-              const uint16_t* __restrict__ db, const float* __restrict__ bd, const int32_t* __restrict__ idx,
-              const float* __restrict__ wts, int k, int D, int F, int E, int nored, const uint16_t* __restrict__ resid,
-              uint16_t* __restrict__ y) {
+q4_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint32_t* __restrict__ dq,
+              const uint16_t* __restrict__ ds, const uint16_t* __restrict__ db, const float* __restrict__ bd,
+              const int32_t* __restrict__ idx, const float* __restrict__ wts, int k, int D, int F, int E, int nored,
+              int y32, const void* __restrict__ resid, void* __restrict__ y) {
     constexpr int RPW = 64 / LPR;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = blockIdx.y;
@@ -137,12 +176,12 @@ q4_down_slots(const uint16_t* __restrict__ h, const uint32_t* __restrict__ dq, c
         const int slot = t * k + j;
         const int e = idx[slot];
         if ((unsigned)e >= (unsigned)E) {
-            if (nored && psub == 0 && row_ok) y[(size_t)slot * D + n] = 0;
+            if (nored && psub == 0 && row_ok) store_y(y, (size_t)slot * D + n, 0.f, y32);
             continue;
         }
         const size_t row = (size_t)e * D + nn;
         const uint4* wrow = reinterpret_cast<const uint4*>(dq + row * wpr);
-        const uint16_t* hr = h + (size_t)slot * F;
+        const size_t hoff = (size_t)slot * F;
         float acc = 0.f;
         for (int p0 = psub; p0 < cpr; p0 += 4 * LPR) {
             uint4 wv[4];
@@ -158,17 +197,18 @@ q4_down_slots(const uint16_t* __restrict__ h, const uint32_t* __restrict__ dq, c
             for (int i = 0; i < 4; ++i) {
                 const int p = p0 + i * LPR;
                 if (p < cpr) {
-                    uint32_t hw[16], hp[16];
-                    load_x32(hr + p * 32, hw);
-                    pair_x32(hw, hp);
-                    acc = q4_fold(acc, s[i], z[i], dot_q4x32(wv[i], hp), sum_x32(hw));
+                    uint32_t qp[16];
+                    decode_q4x32(wv[i], qp);
+                    float hs;
+                    const float dd = dot_h32(qp, hhi + hoff + p * 32, hlo + hoff + p * 32, &hs);
+                    acc = q4_fold(acc, s[i], z[i], dd, hs);
                 }
             }
         }
         acc = group_sum<LPR>(acc);
         if (bd) acc += bd[(size_t)e * D + nn];
         if (nored) {
-            if (psub == 0 && row_ok) y[(size_t)slot * D + n] = f32_to_bf16(acc);
+            if (psub == 0 && row_ok) store_y(y, (size_t)slot * D + n, acc, y32);
         } else {
             yacc = __builtin_fmaf(wts[slot], acc, yacc);
         }
@@ -183,8 +223,9 @@ q4_down_slots(const uint16_t* __restrict__ h, const uint32_t* __restrict__ dq, c
             float v = red[0][lane];
 #pragma unroll
             for (int w = 1; w < DN_WAVES; ++w) v += red[w][lane];
-            if (resid) v += bf16_to_f32(resid[(size_t)t * D + n2]);
-            y[(size_t)t * D + n2] = f32_to_bf16(v);
+            const size_t o = (size_t)t * D + n2;
+            if (resid) v += load_y(resid, o, y32);
+            store_y(y, o, v, y32);
         }
     }
 }
@@ -199,7 +240,8 @@ q4_gate_up_grouped(const uint16_t* __restrict__ x, const uint32_t* __restrict__ 
                    const uint16_t* __restrict__ ub, const float* __restrict__ bg, const float* __restrict__ bu,
                    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
                    const int32_t* __restrict__ sorted, const int32_t* __restrict__ active,
-                   const int32_t* __restrict__ meta, int k, int d, int F, uint16_t* __restrict__ h) {
+                   const int32_t* __restrict__ meta, int k, int d, int F, uint16_t* __restrict__ hhi,
+                   uint16_t* __restrict__ hlo) {
     const int a = blockIdx.y;
     if (a >= meta[0]) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -277,7 +319,7 @@ q4_gate_up_grouped(const uint16_t* __restrict__ x, const uint32_t* __restrict__ 
 #pragma unroll
                 for (int q = 0; q < NB; ++q)
                     if (q == i) s_i = slot[q];
-                h[(size_t)s_i * F + n] = f32_to_bf16(glu<ACT>(g, u));
+                store_h(hhi, hlo, (size_t)s_i * F + n, glu<ACT>(g, u));
             }
         }
     }
@@ -288,11 +330,12 @@ q4_gate_up_grouped(const uint16_t* __restrict__ x, const uint32_t* __restrict__ 
 // yp [T*k, D] fp32: yp[slot] = wts[slot] * (W_d h[slot] + bd).
 template <int LPR, int NB>
 __global__ void __launch_bounds__(64 * DN_WAVES)
-q4_down_grouped(const uint16_t* __restrict__ h, const uint32_t* __restrict__ dq, const uint16_t* __restrict__ ds,
-                const uint16_t* __restrict__ db, const float* __restrict__ bd, const float* __restrict__ wts,
-                const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-                const int32_t* __restrict__ sorted, const int32_t* __restrict__ active,
-                const int32_t* __restrict__ meta, int D, int F, float* __restrict__ yp) {
+q4_down_grouped(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint32_t* __restrict__ dq,
+                const uint16_t* __restrict__ ds, const uint16_t* __restrict__ db, const float* __restrict__ bd,
+                const float* __restrict__ wts, const int32_t* __restrict__ counts,
+                const int32_t* __restrict__ offsets, const int32_t* __restrict__ sorted,
+                const int32_t* __restrict__ active, const int32_t* __restrict__ meta, int D, int F,
+                float* __restrict__ yp) {
     constexpr int RPW = 64 / LPR;
     const int a = blockIdx.y;
     if (a >= meta[0]) return;
@@ -333,10 +376,10 @@ q4_down_grouped(const uint16_t* __restrict__ h, const uint32_t* __restrict__ dq,
                     decode_q4x32(wv[q], qp);
 #pragma unroll
                     for (int i = 0; i < NB; ++i) {
-                        uint32_t hw[16], hp[16];
-                        load_x32(h + (size_t)slot[i] * F + p * 32, hw);
-                        pair_x32(hw, hp);
-                        acc[i] = q4_fold(acc[i], s[q], z[q], dot_pairs16(qp, hp), sum_x32(hw));
+                        float hs;
+                        const size_t ho = (size_t)slot[i] * F + p * 32;
+                        const float dd = dot_h32(qp, hhi + ho, hlo + ho, &hs);
+                        acc[i] = q4_fold(acc[i], s[q], z[q], dd, hs);
                     }
                 }
             }
@@ -352,10 +395,10 @@ q4_down_grouped(const uint16_t* __restrict__ h, const uint32_t* __restrict__ dq,
 }
 
 // ------------------------------------------------------------------------------------------ combine
-// y[t, n] = residual[t, n] + sum_j yp[t*k + j, n], 4 outputs per thread (D % 4 == 0).
+// y[t, n] = residual[t, n] + sum_j yp[t*k + j, n], 4 outputs per thread (D % 4 == 0); y, resid bf16 or fp32.
 __global__ void __launch_bounds__(256)
-q4_combine(const float* __restrict__ yp, const uint16_t* __restrict__ resid, uint16_t* __restrict__ y, int T, int k,
-           int D) {
+moe_combine(const float* __restrict__ yp, const void* __restrict__ resid, void* __restrict__ y, int T, int k, int D,
+            int y32) {
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total4 = (size_t)T * D / 4;
     if (i4 >= total4) return;
@@ -366,14 +409,22 @@ q4_combine(const float* __restrict__ yp, const uint16_t* __restrict__ resid, uin
         const float4 v = reinterpret_cast<const float4*>(yp + ((size_t)t * k + j) * D + n)[0];
         acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
     }
+    if (y32) {
+        if (resid) {
+            const float4 r = reinterpret_cast<const float4*>(resid)[i4];
+            acc.x += r.x; acc.y += r.y; acc.z += r.z; acc.w += r.w;
+        }
+        reinterpret_cast<float4*>(y)[i4] = acc;
+        return;
+    }
     if (resid) {
-        const uint2 r = reinterpret_cast<const uint2*>(resid + i)[0];
+        const uint2 r = reinterpret_cast<const uint2*>(resid)[i4];
         acc.x += bf16lo(r.x); acc.y += bf16hi(r.x); acc.z += bf16lo(r.y); acc.w += bf16hi(r.y);
     }
     uint2 o;
     o.x = (uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16);
     o.y = (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16);
-    reinterpret_cast<uint2*>(y + i)[0] = o;
+    reinterpret_cast<uint2*>(y)[i4] = o;
 }
 
 // ------------------------------------------------------------------------------------ host side
@@ -385,7 +436,7 @@ static int pick_lpr(int cpr) {
 }
 
 template <int ACT>
-static void launch_gu_slots(const ExpertsArgs& a, int RW, dim3 grid, hipStream_t st) {
+static void launch_gu_slots(const ExpertsArgs& a, int RW, dim3 grid) {
     const moe_experts_t* w = a.w;
     auto* x = (const uint16_t*)a.x;
     auto* gq = (const uint32_t*)w->gate.codes;
@@ -394,13 +445,14 @@ static void launch_gu_slots(const ExpertsArgs& a, int RW, dim3 grid, hipStream_t
     auto* uq = (const uint32_t*)w->up.codes;
     auto* us = (const uint16_t*)w->up.scales;
     auto* ub = (const uint16_t*)w->up.biases;
-    auto* h = (uint16_t*)a.h;
     if (RW == 4)
-        q4_gate_up_slots<4, ACT><<<grid, 64 * GU_WAVES, 0, st>>>(x, gq, gs, gb, uq, us, ub, w->gate.bias, w->up.bias,
-                                                                a.idx, a.k, w->d, w->F, w->E, h);
+        q4_gate_up_slots<4, ACT><<<grid, 64 * GU_WAVES, 0, a.st>>>(x, gq, gs, gb, uq, us, ub, w->gate.bias,
+                                                                  w->up.bias, a.idx, a.k, w->d, w->F, w->E, a.hhi,
+                                                                  a.hlo);
     else
-        q4_gate_up_slots<2, ACT><<<grid, 64 * GU_WAVES, 0, st>>>(x, gq, gs, gb, uq, us, ub, w->gate.bias, w->up.bias,
-                                                                a.idx, a.k, w->d, w->F, w->E, h);
+        q4_gate_up_slots<2, ACT><<<grid, 64 * GU_WAVES, 0, a.st>>>(x, gq, gs, gb, uq, us, ub, w->gate.bias,
+                                                                  w->up.bias, a.idx, a.k, w->d, w->F, w->E, a.hhi,
+                                                                  a.hlo);
 }
 
 int run_int4_slots(const ExpertsArgs& a) {
@@ -409,24 +461,24 @@ int run_int4_slots(const ExpertsArgs& a) {
     const int nslots = a.T * a.k;
     // gate/up: RW rows per wave; fewer rows per wave when the launch would be short of waves
     const int RW = ((long)nslots * F / 4 >= 1024) ? 4 : 2;
-    dim3 g1((F + GU_WAVES * RW - 1) / (GU_WAVES * RW), nslots);
-    if (a.act == 0) launch_gu_slots<0>(a, RW, g1, a.st);
-    else if (a.act == 1) launch_gu_slots<1>(a, RW, g1, a.st);
-    else launch_gu_slots<2>(a, RW, g1, a.st);
-    if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+    if (a.stages & 1) {
+        dim3 g1((F + GU_WAVES * RW - 1) / (GU_WAVES * RW), nslots);
+        if (a.act == 0) launch_gu_slots<0>(a, RW, g1);
+        else if (a.act == 1) launch_gu_slots<1>(a, RW, g1);
+        else launch_gu_slots<2>(a, RW, g1);
+        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+    }
+    if (!(a.stages & 2)) return 0;
 
     const int lpr = pick_lpr(F >> 5);
     const int rpw = 64 / lpr;
     dim3 g2((d + rpw - 1) / rpw, a.T);
-    auto* hq = (const uint16_t*)a.h;
     auto* dq = (const uint32_t*)w->down.codes;
     auto* ds = (const uint16_t*)w->down.scales;
     auto* db = (const uint16_t*)w->down.biases;
-    auto* res = (const uint16_t*)a.residual;
-    auto* y = (uint16_t*)a.y;
-#define MOE_DN(L)                                                                                                 \
-    q4_down_slots<L><<<g2, 64 * DN_WAVES, 0, a.st>>>(hq, dq, ds, db, w->down.bias, a.idx, a.wts, a.k, d, F, E, \
-                                                      a.nored, res, y)
+#define MOE_DN(L)                                                                                              \
+    q4_down_slots<L><<<g2, 64 * DN_WAVES, 0, a.st>>>(a.hhi, a.hlo, dq, ds, db, w->down.bias, a.idx, a.wts, a.k, \
+                                                      d, F, E, a.nored, a.y32, a.residual, a.y)
     switch (lpr) {
         case 4: MOE_DN(4); break;
         case 8: MOE_DN(8); break;
@@ -446,7 +498,7 @@ static void launch_gu_grouped(const ExpertsArgs& a, dim3 grid) {
         (const uint16_t*)a.x, (const uint32_t*)w->gate.codes, (const uint16_t*)w->gate.scales,
         (const uint16_t*)w->gate.biases, (const uint32_t*)w->up.codes, (const uint16_t*)w->up.scales,
         (const uint16_t*)w->up.biases, w->gate.bias, w->up.bias, a.grp.counts, a.grp.offsets, a.grp.sorted,
-        a.grp.active, a.grp.meta, a.k, w->d, w->F, (uint16_t*)a.h);
+        a.grp.active, a.grp.meta, a.k, w->d, w->F, a.hhi, a.hlo);
 }
 
 int run_int4_grouped(const ExpertsArgs& a) {
@@ -454,25 +506,28 @@ int run_int4_grouped(const ExpertsArgs& a) {
     const int d = w->d, F = w->F, E = w->E;
     const int nslots = a.T * a.k;
     const int max_active = nslots < E ? nslots : E;
-    int rc = launch_group(a.idx, nslots, E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active, a.grp.meta, a.st);
-    if (rc) return rc;
-    constexpr int RW = 2;
-    dim3 g1((F + GU_WAVES * RW - 1) / (GU_WAVES * RW), max_active);
-    if (a.act == 0) launch_gu_grouped<0>(a, g1);
-    else if (a.act == 1) launch_gu_grouped<1>(a, g1);
-    else launch_gu_grouped<2>(a, g1);
-    if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+    if (a.stages & 1) {
+        int rc = launch_group(a.idx, nslots, E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active, a.grp.meta,
+                              a.st);
+        if (rc) return rc;
+        constexpr int RW = 2;
+        dim3 g1((F + GU_WAVES * RW - 1) / (GU_WAVES * RW), max_active);
+        if (a.act == 0) launch_gu_grouped<0>(a, g1);
+        else if (a.act == 1) launch_gu_grouped<1>(a, g1);
+        else launch_gu_grouped<2>(a, g1);
+        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+    }
+    if (!(a.stages & 2)) return 0;
 
     const int lpr = pick_lpr(F >> 5);
     const int rpw = 64 / lpr;
     dim3 g2((d + DN_WAVES * rpw - 1) / (DN_WAVES * rpw), max_active);
-    auto* hq = (const uint16_t*)a.h;
     auto* dq = (const uint32_t*)w->down.codes;
     auto* ds = (const uint16_t*)w->down.scales;
     auto* db = (const uint16_t*)w->down.biases;
-#define MOE_DNG(L)                                                                                            \
-    q4_down_grouped<L, 4><<<g2, 64 * DN_WAVES, 0, a.st>>>(hq, dq, ds, db, w->down.bias, a.wts, a.grp.counts, \
-                                                           a.grp.offsets, a.grp.sorted, a.grp.active,        \
+#define MOE_DNG(L)                                                                                                \
+    q4_down_grouped<L, 4><<<g2, 64 * DN_WAVES, 0, a.st>>>(a.hhi, a.hlo, dq, ds, db, w->down.bias, a.wts,         \
+                                                           a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active, \
                                                            a.grp.meta, d, F, a.yp)
     switch (lpr) {
         case 4: MOE_DNG(4); break;
@@ -483,15 +538,14 @@ int run_int4_grouped(const ExpertsArgs& a) {
     }
 #undef MOE_DNG
     if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
-    return launch_combine(a.yp, a.residual, a.y, a.T, a.k, d, a.x_dtype, a.st);
+    return launch_combine(a.yp, a.residual, a.y, a.T, a.k, d, a.y32, a.st);
 }
 
-int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int x_dtype, hipStream_t st) {
-    if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;
+int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st) {
     const size_t total4 = (size_t)T * d / 4;
-    dim3 grid((unsigned)((total4 + 255) / 256));
     if (total4 == 0) return 0;
-    q4_combine<<<grid, 256, 0, st>>>(yp, (const uint16_t*)residual, (uint16_t*)y, T, k, d);
+    dim3 grid((unsigned)((total4 + 255) / 256));
+    moe_combine<<<grid, 256, 0, st>>>(yp, residual, y, T, k, d, y32);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

@@ -32,11 +32,14 @@ struct ExpertsArgs {
     const int32_t* idx;
     const float* wts;
     int T, k, act, nored;
-    void* y;
-    const void* residual;
-    void* h;        // [T*k, F] activation-dtype scratch
+    void* y;              // [T, d] (or [T*k, d] when nored), fp32 when y32 else bf16
+    int y32;
+    const void* residual; // same dtype as y, or NULL
+    uint16_t* hhi;        // GLU output h = hi + lo, two bf16 planes [T*k, F]
+    uint16_t* hlo;
     float* yp;      // [T*k, d] fp32 scratch (grouped path)
     GroupBufs grp;  // grouped path
+    int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
     hipStream_t st;
 };
 
@@ -47,6 +50,6 @@ int run_int4_grouped(const ExpertsArgs& a);
 int run_mxfp4_slots(const ExpertsArgs& a);
 int run_mxfp4_grouped(const ExpertsArgs& a);
 // combine (moe_int4.hip): y[t] = residual[t] + sum_j yp[t*k + j]
-int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int x_dtype, hipStream_t st);
+int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);
 
 }  // namespace moe

@@ -46,8 +46,12 @@ def _desc(s):
     return desc
 
 
-def run_experts(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, nored=False, residual=None, out=None):
-    """y [T, d] (or [T*k, d] unweighted per slot when nored) on the GPU through moe_experts_run."""
+def run_experts(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, nored=False, residual=None, out=None, out_dtype=None,
+                stages=_lib.STAGE_ALL):
+    """y [T, d] (or [T*k, d] unweighted per slot when nored) on the GPU through moe_experts_run.
+    out_dtype: x.dtype (default, as the reference) or torch.float32 for the unrounded result;
+    residual, if given, is added inside the last kernel and has out_dtype.
+    stages: STAGE_ALL, or STAGE_GATE_UP then STAGE_DOWN as two calls sharing the per-device workspace."""
     _lib.require_device(x, "x")
     if x.dtype not in (torch.bfloat16,):
         raise NotImplementedError(f"activation dtype {x.dtype}: the gfx950 expert kernels take bf16")
@@ -60,11 +64,13 @@ def run_experts(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, nored=False, residua
     L = _lib.lib()
     nbytes = L.moe_experts_workspace_bytes(desc, T, k, path)
     ws = _lib.workspace(x.device, nbytes)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
     if out is None:
-        out = torch.empty((T * k if nored else T, d), dtype=x.dtype, device=x.device)
-    res = None if residual is None else residual.contiguous()
-    rc = L.moe_experts_run(desc, _lib.ptr(x), _lib.DTYPE[x.dtype], _lib.ptr(idx), _lib.ptr(wts), T, k, int(act),
-                           int(path), int(bool(nored)), _lib.ptr(out), _lib.ptr(res), _lib.ptr(ws), ws.numel(),
-                           _lib.stream_of(x.device))
-    _lib.check("moe_experts_run", rc)
+        out = torch.empty((T * k if nored else T, d), dtype=out_dtype, device=x.device)
+    assert out.dtype == out_dtype and out.dtype in (torch.bfloat16, torch.float32)
+    res = None if residual is None else residual.to(out_dtype).contiguous()
+    rc = L.moe_experts_run_stages(desc, _lib.ptr(x), _lib.DTYPE[x.dtype], _lib.ptr(idx), _lib.ptr(wts), T, k,
+                                  int(act), int(path), int(bool(nored)), _lib.ptr(out), _lib.DTYPE[out.dtype],
+                                  _lib.ptr(res), _lib.ptr(ws), ws.numel(), int(stages), _lib.stream_of(x.device))
+    _lib.check("moe_experts_run_stages", rc)
     return out

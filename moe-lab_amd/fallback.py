@@ -10,5 +10,5 @@ from . import _lib
 from .experts import run_experts
 
 
-def gather_moe(s, x, idx, wts, group_size=None, bits=None, mode="affine", act=0, residual=None):
-    return run_experts(s, x, idx, wts, act=act, path=_lib.PATH_SLOTS, residual=residual)
+def gather_moe(s, x, idx, wts, group_size=None, bits=None, mode="affine", act=0, residual=None, out_dtype=None):
+    return run_experts(s, x, idx, wts, act=act, path=_lib.PATH_SLOTS, residual=residual, out_dtype=out_dtype)

@@ -56,13 +56,15 @@ def run_slots(s, x, idx, act=0):
     return run_experts(s, x, idx, ones, act=act, path=_lib.PATH_SLOTS, nored=True)
 
 
-def run(s, x, idx, wts, act=0, residual=None):
+def run(s, x, idx, wts, act=0, residual=None, out_dtype=None):
     """act: 0 = SwiGLU, 1 = GeGLU (tanh-GELU), 2 = gpt-oss clamped SwiGLU. residual: optional [T, D]
-    added to the output inside the last kernel (y = residual + moe(x))."""
+    added to the output inside the last kernel (y = residual + moe(x)). out_dtype: x.dtype (default,
+    as the reference) or torch.float32 for the unrounded result."""
     T, k = idx.shape
+    kw = dict(act=act, residual=residual, out_dtype=out_dtype)
     if T == 1:
-        return run_experts(s, x, idx, wts, act=act, path=_lib.PATH_SLOTS, residual=residual)
+        return run_experts(s, x, idx, wts, path=_lib.PATH_SLOTS, **kw)
     E, D, F = dims(s)
     if not custom_wins(T, k, E, D, F):
-        return gather_moe(s, x, idx, wts, GS, BITS, act=act, residual=residual)
-    return run_experts(s, x, idx, wts, act=act, path=_lib.PATH_GROUPED, residual=residual)
+        return gather_moe(s, x, idx, wts, GS, BITS, **kw)
+    return run_experts(s, x, idx, wts, path=_lib.PATH_GROUPED, **kw)

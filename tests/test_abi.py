@@ -70,7 +70,8 @@ def test_argument_errors_before_launch(case, rc):
         path, nored = _lib.PATH_GROUPED, 1
     elif case == "misaligned":
         x = ctypes.c_void_p(4097)
-    got = L.moe_experts_run(w, x, dtype, x, x, 4, 2, act, path, nored, ctypes.c_void_p(4096), None, ws, wsb, None)
+    got = L.moe_experts_run(w, x, dtype, x, x, 4, 2, act, path, nored, ctypes.c_void_p(4096), 0, None, ws, wsb,
+                            None)
     assert got == rc
 
 

@@ -59,9 +59,12 @@ def check(shape, T, routing="uniform", seed=0, idx=None, wts=None, act=0, scale=
     wts = w0 if wts is None else torch.as_tensor(wts, dtype=torch.float32, device=DEV)
     print(f"case shape={shape} T={T} routing={routing} act={act}", flush=True)
     y = q4().run(s, x, idx, wts, act=act)
+    y32 = q4().run(s, x, idx, wts, act=act, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    assert y.shape == x.shape and y.dtype == x.dtype
-    assert_close(y, oracle_y(s, x, idx, wts, act), what=(shape, T))
+    assert y.shape == x.shape and y.dtype == x.dtype and y32.dtype == torch.float32
+    ref = oracle_y(s, x, idx, wts, act)
+    assert_close(y32, ref, what=(shape, T, "fp32 out"))
+    assert_close(y, ref, what=(shape, T, "bf16 out"))
     return y, s, x, idx, wts
 
 
@@ -165,8 +168,9 @@ def test_slots_path_equals_grouped(T):
     s = packed_state(sh, 7)
     x, idx, wts = inputs(sh, T, seed=7)
     ref = oracle_y(s, x, idx, wts)
-    assert_close(run_experts(s, x, idx, wts, path=_lib.PATH_SLOTS), ref, what="slots")
-    assert_close(run_experts(s, x, idx, wts, path=_lib.PATH_GROUPED), ref, what="grouped")
+    for path in (_lib.PATH_SLOTS, _lib.PATH_GROUPED):
+        for od in (torch.float32, torch.bfloat16):
+            assert_close(run_experts(s, x, idx, wts, path=path, out_dtype=od), ref, what=(path, od))
 
 
 @pytest.mark.parametrize("T", [1, 12])
@@ -179,6 +183,7 @@ def test_fused_residual(T):
     yr = q4().run(s, x, idx, wts, residual=res)
     ref = oracle_y(s, x, idx, wts) + res.float().cpu().numpy()
     assert_close(yr, ref)
+    assert_close(q4().run(s, x, idx, wts, residual=res.float(), out_dtype=torch.float32), ref)
     diff = (yr.float() - (y.float() + res.float())).abs().max().item()
     assert diff <= 2 * 2 ** -8 * max(1.0, (y.float() + res.float()).abs().max().item())
 
@@ -216,5 +221,6 @@ def test_qwen3_full_shape(T):
     lg_ref = orc.router_logits(np_u16(x), np_u16(layer["wr"]))
     idx_ref, wts_ref = orc.topk(lg_ref, sh.k)
     np.testing.assert_array_equal(idx.cpu().numpy(), idx_ref)
-    y = q4().run(s, x, idx, wts)
-    assert_close(y, oracle_y(s, x, idx, wts))
+    ref = oracle_y(s, x, idx, wts)
+    assert_close(q4().run(s, x, idx, wts, out_dtype=torch.float32), ref, what="fp32 out")
+    assert_close(q4().run(s, x, idx, wts), ref, what="bf16 out")
