@@ -10,9 +10,10 @@ contract (routing precomputed per layer, reference mlx_backend.py:91-117). The s
 fused router inside each layer is reported as `with_router`. BASELINE config 3 (T=32, uniform and
 Zipf(1.1) routing) reports the grouped expert path against the per-slot stock-style gather.
 
-roofline: the dominant kernel at T=1 is the gate/up GEMV (2/3 of the weight bytes). Its average launch
-duration is measured with HIP events on the stream it runs on, around graph replays of 48 gate/up-only
-launches; achieved = algorithmic bytes per launch (k unique experts x gate+up packed bytes) / duration.
+roofline: at T=1 each layer is one launch of the fused expert kernel (k_t1_fused), so the HIP events on
+the stream it runs on, around replays of the 48-launch chain, give its average launch duration directly;
+achieved = algorithmic bytes per launch (the k selected experts' packed gate+up+down rows) / duration.
+The two-launch per-slot path (gate/up GEMV, then down GEMV) is timed the same way for comparison.
 
 cpu_baseline: the reference's CPU torch path (torch_loop, reference variants/cuda/torch_loop.py:11-17)
 on dequantised fp32 weights of the selected experts, timed on this host for a bounded sample of layers.
@@ -95,7 +96,7 @@ def main():
     t0 = time.time()
     layers = [baseline_int4_layer(sh, seed=1000 + l, device=dev) for l in range(L)]
     torch.cuda.synchronize()
-    log(f"layers ready in {time.time() - t0:.1f}s ({L * 3 * per_expert / 1e9:.2f} GB packed experts)")
+    log(f"layers ready in {time.time() - t0:.1f}s ({L * sh.E * per_expert / 1e9:.2f} GB packed experts)")
 
     # one workspace for every graph below (graphs keep raw pointers into it)
     desc_probe = layers[0]
@@ -110,17 +111,19 @@ def main():
     U1 = [int(torch.unique(r[0]).numel()) for r in routes1]
     bytes1 = sum(U1) * per_expert
 
-    def chain_t1():
-        x = x1.clone()
-        for ly, (idx, wts) in zip(layers, routes1):
-            x = run_experts(ly, x, idx, wts, path=_lib.PATH_SLOTS, residual=x)
-        return x
+    def chain_t1(path=_lib.PATH_AUTO):
+        def f():
+            x = x1.clone()
+            for ly, (idx, wts) in zip(layers, routes1):
+                x = run_experts(ly, x, idx, wts, path=path, residual=x)
+            return x
+        return f
 
     def chain_t1_router():
         x = x1.clone()
         for ly in layers:
             idx, wts = router.route(x, ly["wr"], sh.k)
-            x = run_experts(ly, x, idx, wts, path=_lib.PATH_SLOTS, residual=x)
+            x = run_experts(ly, x, idx, wts, path=_lib.PATH_AUTO, residual=x)
         return x
 
     def gate_up_only():
@@ -131,9 +134,12 @@ def main():
         for ly, (idx, wts) in zip(layers, routes1):
             run_experts(ly, x1, idx, wts, path=_lib.PATH_SLOTS, stages=_lib.STAGE_DOWN)
 
-    g1, _ = graph_of(chain_t1)
+    g1, _ = graph_of(chain_t1())
     t_step = time_graph(g1, args.steps, args.warmup)
-    log(f"T=1 experts chain: {t_step * 1e6 / L:.2f} us/layer, {bytes1 / t_step / 1e9:.0f} GB/s")
+    log(f"T=1 experts chain (fused launch): {t_step * 1e6 / L:.2f} us/layer, {bytes1 / t_step / 1e9:.0f} GB/s")
+    g2, _ = graph_of(chain_t1(_lib.PATH_SLOTS))
+    t_step2 = time_graph(g2, args.steps, args.warmup)
+    log(f"T=1 experts chain (two launches): {t_step2 * 1e6 / L:.2f} us/layer")
     g1r, _ = graph_of(chain_t1_router)
     t_step_r = time_graph(g1r, args.steps, args.warmup)
     log(f"T=1 with router: {t_step_r * 1e6 / L:.2f} us/layer")
@@ -211,12 +217,14 @@ def main():
         "weight_bytes_per_step": bytes1,
         "with_router": {"us_per_layer": round(t_step_r * 1e6 / L, 3),
                         "weight_GBps": round(bytes1 / t_step_r / 1e9, 2)},
-        "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3)},
+        "two_launch_t1": {"us_per_layer": round(t_step2 * 1e6 / L, 3), "gate_up_us": round(t_gu * 1e6, 3),
+                          "down_us": round(t_dn * 1e6, 3)},
         "t32": t32,
-        "roofline": {"bound": "hbm", "kernel": "q4_gate_up_slots (T=1 gate/up GEMV + SwiGLU)",
-                     "achieved": round(gu_bytes / t_gu / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_bytes / t_gu / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": gu_bytes},
+        "roofline": {"bound": "hbm", "kernel": "k_t1_fused<FmtInt4, SwiGLU> (T=1 layer: gate/up/GLU + down)",
+                     "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "launch_us": round(t_step * 1e6 / L, 3),
+                     "algorithmic_bytes_per_launch": bytes1 / L},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -225,6 +233,7 @@ def main():
 def cpu_baseline(layers, routes, x, sh):
     """torch_loop (the reference's CPU torch path) on fp32 dense weights of the selected experts only."""
     from moelab_amd import formats
+    from moelab_amd.experts import unpack
     orc = __graft_entry__.load_oracle()
     cores = torch.get_num_threads()
     xs = x.float().cpu()
@@ -233,7 +242,7 @@ def cpu_baseline(layers, routes, x, sh):
         sel = sorted(set(idx.flatten().tolist()))
         w = {}
         for n in ("g", "u", "d"):
-            codes, sc, bi = ly[n]
+            codes, sc, bi = unpack(ly, n)
             w[n] = {e: formats.dequant_int4(codes[e], sc[e], bi[e]).cpu() for e in sel}
         dense.append((w, idx.cpu().long(), wts.cpu()))
 

@@ -41,9 +41,18 @@ extern "C" {
 #define MOE_DTYPE_F16 1
 #define MOE_DTYPE_F32 2
 
-/* weight formats (reference state layouts: metal_q4_decode_v4.py:161-169, metal_mxfp4_moe.py:448-455) */
-#define MOE_FMT_INT4_G64 0 /* codes u32 [E,N,K/8] (8 nibbles, low first), scales/biases bf16 [E,N,K/64] */
-#define MOE_FMT_MXFP4 1    /* codes u32 [E,N,K/8] (8 E2M1 nibbles, low first), scales u8 E8M0 [E,N,K/32] */
+/*
+ * Weight formats. The reference's state holds, per projection, codes u32 [E, N, K/8] (8 nibbles per word,
+ * low nibble first) plus scales/biases bf16 [E, N, K/64] (int4 g64, metal_q4_decode_v4.py:161-169) or E8M0
+ * bytes u8 [E, N, K/32] (MXFP4, metal_mxfp4_moe.py:448-455). This library takes the same numbers packed
+ * row by row: each of the E*N rows is one record of moe_row_bytes(fmt, K) bytes, the row's K/2 code bytes
+ * (the reference's words, unchanged) followed by its group metadata, zero-padded to a multiple of 16:
+ *   MOE_FMT_INT4_G64: K/64 words, word g = scale_g (bf16, low half) | bias_g (bf16, high half) << 16
+ *   MOE_FMT_MXFP4:    K/32 E8M0 bytes
+ * so a row streams as one contiguous run. moelab_amd.formats converts in both directions.
+ */
+#define MOE_FMT_INT4_G64 0
+#define MOE_FMT_MXFP4 1
 
 /* GLU activations (reference metal_q4_decode_v4.py:36-41, metal_mxfp4_gptoss.py:36-43) */
 #define MOE_ACT_SWIGLU 0      /* silu(g) * u */
@@ -51,17 +60,19 @@ extern "C" {
 #define MOE_ACT_GPTOSS 2      /* g = min(g,7), u = clip(u,-7,7), g * sigmoid(1.702 g) * (u + 1) */
 
 /* expert-path selection for moe_experts_run */
-#define MOE_PATH_AUTO 0       /* T == 1 -> per-slot GEMV; T > 1 -> grouped expert tiles */
-#define MOE_PATH_SLOTS 1      /* per-slot GEMV over all T*k slots, no grouping (the stock-style gather) */
+#define MOE_PATH_AUTO 0       /* T == 1 -> one fused launch when it fits (else per-slot GEMV); T > 1 -> grouped */
+#define MOE_PATH_SLOTS 1      /* per-slot GEMV over all T*k slots, no grouping, two launches (the stock-style
+                                 gather of the reference's pre-tile kernels) */
 #define MOE_PATH_GROUPED 2    /* grouped expert tiles: each selected expert's weights read once */
 
-/* One projection of all E experts: N output rows, K inputs. */
+/* One projection of all E experts: N output rows of K inputs. */
 typedef struct {
-    const void* codes;   /* u32 words [E, N, K/8] */
-    const void* scales;  /* int4: bf16 [E, N, K/64]; mxfp4: u8 [E, N, K/32] */
-    const void* biases;  /* int4: bf16 [E, N, K/64]; mxfp4: unused (NULL) */
+    const void* rows;    /* packed rows [E, N, moe_row_bytes(fmt, K)], 16-byte aligned */
     const float* bias;   /* optional additive row bias fp32 [E, N] (gpt-oss), NULL if none */
 } moe_proj_t;
+
+/* Bytes of one packed row of K inputs in format fmt (0 for an invalid fmt or K). */
+size_t moe_row_bytes(int fmt, int K);
 
 /* Expert weights: gate/up [E, F, d], down [E, d, F]. */
 typedef struct {
@@ -113,9 +124,14 @@ int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offset
  *   run_slots / NORED, metal_q4_moe.py:49-51; per-slot path only, residual must be NULL).
  *   Accumulation in fp32; the GLU output h is kept between the two launches as an unevaluated sum of two
  *   bf16 planes (about 16 significant bits, where the reference kernels store it in x.dtype).
- *   Requirements: d % 64 == 0 and F % 64 == 0; x, y, codes 16-byte aligned.
- *   workspace: moe_experts_workspace_bytes(...) bytes, any content.
+ *   Requirements: d % 64 == 0 and F % 64 == 0; x, y, rows 16-byte aligned.
+ *   workspace: moe_experts_workspace_bytes(...) bytes. Its first MOE_WORKSPACE_SYNC_BYTES bytes hold the
+ *   fused T == 1 kernel's completion counters: zero them once when the workspace is allocated; every call
+ *   leaves them zero. The rest may hold anything. Calls sharing a workspace must be stream-ordered.
+ *   The fused T == 1 kernel runs at most as many workgroups as the device holds at once and waits on the
+ *   others with a bounded spin; it needs the device to itself for the duration of the launch.
  */
+#define MOE_WORKSPACE_SYNC_BYTES 4096
 int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T,
                     int k, int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                     size_t workspace_bytes, void* stream);

@@ -20,7 +20,8 @@ PATH_AUTO, PATH_SLOTS, PATH_GROUPED = 0, 1, 2
 ACT_SWIGLU, ACT_GEGLU, ACT_GPTOSS = 0, 1, 2
 
 EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
-           "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_version")
+           "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_row_bytes", "moe_version")
+WORKSPACE_SYNC_BYTES = 4096
 STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 3
 
 _ERRORS = {
@@ -39,8 +40,7 @@ class MoeError(RuntimeError):
 
 
 class Proj(ctypes.Structure):
-    _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
-                ("bias", ctypes.c_void_p)]
+    _fields_ = [("rows", ctypes.c_void_p), ("bias", ctypes.c_void_p)]
 
 
 class Experts(ctypes.Structure):
@@ -68,6 +68,8 @@ def lib():
         L.moe_experts_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i, i, i]
         L.moe_experts_workspace_bytes.restype = sz
         L.moe_version.restype = ctypes.c_char_p
+        L.moe_row_bytes.argtypes = [i, i]
+        L.moe_row_bytes.restype = sz
         for n in ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
                   "moe_experts_run_stages"):
             getattr(L, n).restype = ctypes.c_int
@@ -98,10 +100,12 @@ _WS = {}
 
 
 def workspace(device, nbytes):
-    """Per-device scratch buffer, grown on demand (stream-ordered reuse through torch's allocator)."""
+    """Per-device scratch buffer, grown on demand (stream-ordered reuse through torch's allocator).
+    Allocated zeroed: its first WORKSPACE_SYNC_BYTES hold the fused kernel's counters, which every
+    call leaves at zero."""
     key = torch.device(device).index
     buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(int(nbytes), WORKSPACE_SYNC_BYTES), dtype=torch.uint8, device=device)
         _WS[key] = buf
     return buf

@@ -22,7 +22,7 @@ struct Layout {
 Layout layout(const moe_experts_t* w, int T, int k, int path) {
     Layout L{};
     const size_t nslots = (size_t)T * k;
-    size_t off = 0;
+    size_t off = MOE_WORKSPACE_SYNC_BYTES;   // fused-kernel counters live at offset 0
     L.h = off;
     off += align_up(nslots * (size_t)w->F * 2) * 2;   // hi and lo planes
     if (resolve_path(path, T) == MOE_PATH_GROUPED) {
@@ -43,10 +43,9 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
     return L;
 }
 
-int check_proj(const moe_proj_t& p, int fmt) {
-    if (!p.codes || !p.scales) return MOE_ERR_ARG;
-    if (fmt == MOE_FMT_INT4_G64 && !p.biases) return MOE_ERR_ARG;
-    if (!aligned16(p.codes)) return MOE_ERR_ALIGN;
+int check_proj(const moe_proj_t& p) {
+    if (!p.rows) return MOE_ERR_ARG;
+    if (!aligned16(p.rows)) return MOE_ERR_ALIGN;
     return MOE_OK;
 }
 
@@ -57,8 +56,7 @@ int check_experts(const moe_experts_t* w) {
     const int g = w->fmt == MOE_FMT_INT4_G64 ? 64 : 32;
     if (w->d % 64 || w->F % 64 || w->d % g || w->F % g) return MOE_ERR_ARG;
     int rc;
-    if ((rc = check_proj(w->gate, w->fmt)) || (rc = check_proj(w->up, w->fmt)) || (rc = check_proj(w->down, w->fmt)))
-        return rc;
+    if ((rc = check_proj(w->gate)) || (rc = check_proj(w->up)) || (rc = check_proj(w->down))) return rc;
     return MOE_OK;
 }
 
@@ -66,7 +64,14 @@ int check_experts(const moe_experts_t* w) {
 
 extern "C" {
 
-const char* moe_version(void) { return "moe_mi355x 0.1 (gfx950, wave64)"; }
+const char* moe_version(void) { return "moe_mi355x 0.2 (gfx950, wave64)"; }
+
+size_t moe_row_bytes(int fmt, int K) {
+    if (K < 64 || K % 64) return 0;
+    if (fmt == MOE_FMT_INT4_G64) return ((size_t)K / 2 + (size_t)K / 16 + 15) & ~(size_t)15;
+    if (fmt == MOE_FMT_MXFP4) return ((size_t)K / 2 + (size_t)K / 32 + 15) & ~(size_t)15;
+    return 0;
+}
 
 int moe_router_counter_count(int T) { return T < 1 ? 1 : moe::router_counter_slots(T); }
 
@@ -142,6 +147,8 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     a.hlo = a.hhi + align_up((size_t)T * k * w->F * 2) / 2;
     a.st = (hipStream_t)stream;
     a.stages = stages;
+    a.fused_t1 = path == MOE_PATH_AUTO;
+    a.sync = (int32_t*)ws;
     if (rpath == MOE_PATH_GROUPED) {
         a.yp = (float*)(ws + L.yp);
         a.grp.counts = (int32_t*)(ws + L.counts);
@@ -150,9 +157,7 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
         a.grp.active = (int32_t*)(ws + L.active);
         a.grp.meta = (int32_t*)(ws + L.meta);
     }
-    if (w->fmt == MOE_FMT_INT4_G64)
-        return rpath == MOE_PATH_GROUPED ? moe::run_int4_grouped(a) : moe::run_int4_slots(a);
-    return rpath == MOE_PATH_GROUPED ? moe::run_mxfp4_grouped(a) : moe::run_mxfp4_slots(a);
+    return rpath == MOE_PATH_GROUPED ? moe::run_experts_grouped(a) : moe::run_experts_slots(a);
 }
 
 }  // extern "C"

@@ -81,6 +81,30 @@ __device__ __forceinline__ void load_x32(const uint16_t* p, uint32_t xw[16]) {
     }
 }
 
+// ------------------------------------------------------------------------------------ DPP reductions
+// v + (v moved across lanes by a DPP pattern); lanes the pattern does not write add 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                     0xF, false));
+}
+// Sum over aligned groups of G lanes (G = 1..64, power of two) with DPP moves only (no LDS crossbar):
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror, row_bcast15, row_bcast31.
+// G <= 16: every lane of the group holds the sum. G == 32: lanes 16..31 of each 32-lane group do.
+// G == 64: lanes 48..63 do. sum_lane<G>() names one lane offset inside the group that holds it.
+template <int G>
+__device__ __forceinline__ float sum_lanes(float v) {
+    if (G >= 2) v = dpp_add<0xB1>(v);
+    if (G >= 4) v = dpp_add<0x4E>(v);
+    if (G >= 8) v = dpp_add<0x141>(v);
+    if (G >= 16) v = dpp_add<0x140>(v);
+    if (G >= 32) v = dpp_add<0x142, 0xA>(v);
+    if (G >= 64) v = dpp_add<0x143, 0xC>(v);
+    return v;
+}
+template <int G>
+__host__ __device__ constexpr int sum_lane() { return G <= 16 ? 0 : (G == 32 ? 16 : 48); }
+
 // ------------------------------------------------------------------------------------ wave reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

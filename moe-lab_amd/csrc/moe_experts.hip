@@ -1,0 +1,991 @@
+// Expert kernels for gfx950 (MI355X): int4 affine g64 and MXFP4, SwiGLU / GeGLU / gpt-oss clamped GLU.
+//
+// Packed rows. Every weight row of K inputs is one record in HBM (moe_row_bytes): K/2 bytes of 4-bit
+// codes (word j holds inputs 8j..8j+7, low nibble first, as the reference's state words,
+// metal_q4_decode_v4.py:57-64), then the row's group metadata, padded to 16 bytes:
+//   int4 g64: K/64 words (scale bf16 | bias bf16 << 16), w = scale*q + bias
+//   MXFP4:    K/32 E8M0 bytes, w = e2m1(q) * 2^(s-127)  (reference metal_mxfp4_moe.py:1-41)
+// A lane reads a 16-byte chunk (32 inputs) with one dwordx4 load and its metadata with one more load
+// from the same record, so a row streams from one DRAM page.
+//
+// Arithmetic. A chunk is decoded to 16 bf16 pairs and dotted with bf16 activation pairs on
+// v_dot2_f32_bf16 (exact products, fp32 accumulation):
+//   int4:  pairs hold 128 + q (exact: the ulp of 128 in bf16 is 1), and per 32-chunk
+//          sum_k (s q_k + b) x_k = s * sum_k (128 + q_k) x_k + (b - 128 s) * sum_k x_k
+//   MXFP4: pairs hold e2m1(q) from two v_perm_b32 byte lookups, and the chunk's dot is scaled by
+//          2^(s-127) in fp32 (one E8M0 group = one chunk).
+// Pairs are (input 8j+i, input 8j+i+4): the activation side is paired the same way (pair_x32).
+//
+// The GLU output h (gate/up -> down) is kept at ~16 significant bits as two bf16 planes h = hi + lo,
+// stored pre-paired (element n of a chunk at (n & ~7) | (n & 3) << 1 | (n >> 2) & 1), so the down
+// projection loads ready-made pairs.
+//
+// Kernels:
+//   k_gate_up_slots / k_down_slots   per-slot GEMV (any T; the stock-style per-slot gather at T > 1)
+//   k_gate_up_grouped / k_down_grouped + k_combine   grouped expert tiles for T > 1: each selected
+//                                    expert's rows are read once and applied to all of its slots
+//   k_t1_fused                       T == 1 in one launch: gate/up for all k slots, a device-wide
+//                                    completion count, then down + k-reduction (h staged in LDS)
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+// ============================================================================ packed row formats
+struct FmtInt4 {
+    static constexpr int FMT = MOE_FMT_INT4_G64;
+    static constexpr bool XSUM = true;   // the fold needs sum(x) over each chunk
+    __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) {
+        return *reinterpret_cast<const uint32_t*>(row + (K >> 1) + 4 * (c >> 1));
+    }
+    __device__ static __forceinline__ void decode(uint4 w, uint32_t qp[16]) {
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qp[4 * j + i] = ((ws[j] >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
+    }
+    __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float xsum) {
+        const float s = bf16lo(m), b = bf16hi(m);
+        return __builtin_fmaf(s, dot, __builtin_fmaf(__builtin_fmaf(-128.f, s, b), xsum, acc));
+    }
+};
+
+struct FmtMxfp4 {
+    static constexpr int FMT = MOE_FMT_MXFP4;
+    static constexpr bool XSUM = false;
+    __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) { return row[(K >> 1) + c]; }
+    // E2M1 magnitude index m (0..7) -> bf16 bytes of {0, .5, 1, 1.5, 2, 3, 4, 6}: low bytes {00,00,80,C0,00,40,
+    // 80,C0}, high bytes {00,3F,3F,3F,40,40,40,40}; v_perm_b32 looks up four indices (one per byte) at once.
+    __device__ static __forceinline__ void decode(uint4 w, uint32_t qp[16]) {
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t v = ws[j];
+            const uint32_t me = v & 0x07070707u, mo = (v >> 4) & 0x07070707u;   // nibbles 0,2,4,6 / 1,3,5,7
+            const uint32_t lo_e = __builtin_amdgcn_perm(0xC0804000u, 0xC0800000u, me);
+            const uint32_t hi_e = __builtin_amdgcn_perm(0x40404040u, 0x3F3F3F00u, me) | ((v & 0x08080808u) << 4);
+            const uint32_t lo_o = __builtin_amdgcn_perm(0xC0804000u, 0xC0800000u, mo);
+            const uint32_t hi_o = __builtin_amdgcn_perm(0x40404040u, 0x3F3F3F00u, mo) | (v & 0x80808080u);
+            qp[4 * j + 0] = __builtin_amdgcn_perm(hi_e, lo_e, 0x06020400u);   // (e0, e4)
+            qp[4 * j + 1] = __builtin_amdgcn_perm(hi_o, lo_o, 0x06020400u);   // (e1, e5)
+            qp[4 * j + 2] = __builtin_amdgcn_perm(hi_e, lo_e, 0x07030501u);   // (e2, e6)
+            qp[4 * j + 3] = __builtin_amdgcn_perm(hi_o, lo_o, 0x07030501u);   // (e3, e7)
+        }
+    }
+    __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float) {
+        return __builtin_fmaf(__uint_as_float(m << 23), dot, acc);
+    }
+};
+
+// ============================================================================ shared pieces
+__device__ __forceinline__ float dot16(const uint32_t qp[16], const uint32_t xp[16], float acc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2_bf16(qp[i], xp[i], acc);
+    return acc;
+}
+__device__ __forceinline__ void words16(const uint4 v[4], uint32_t w[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w[4 * i + 0] = v[i].x;
+        w[4 * i + 1] = v[i].y;
+        w[4 * i + 2] = v[i].z;
+        w[4 * i + 3] = v[i].w;
+    }
+}
+__device__ __forceinline__ float sum16(const uint32_t w[16], float acc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2_bf16(w[i], 0x3f803f80u, acc);
+    return acc;
+}
+
+// h element n -> position inside its chunk so that 16-byte loads yield (n, n+4) pairs
+__device__ __forceinline__ int paired_pos(int n) { return (n & ~7) | ((n & 3) << 1) | ((n >> 2) & 1); }
+__device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t base, int n, float v) {
+    const uint16_t hi = f32_to_bf16(v);
+    const size_t i = base + paired_pos(n);
+    hhi[i] = hi;
+    hlo[i] = f32_to_bf16(v - bf16_to_f32(hi));
+}
+
+__device__ __forceinline__ void store_y(void* y, size_t i, float v, int y32) {
+    if (y32) reinterpret_cast<float*>(y)[i] = v;
+    else reinterpret_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
+}
+__device__ __forceinline__ float load_y(const void* y, size_t i, int y32) {
+    return y32 ? reinterpret_cast<const float*>(y)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
+}
+
+__device__ __forceinline__ size_t rbytes(int fmt, int K) {
+    const size_t meta = fmt == MOE_FMT_INT4_G64 ? (size_t)K / 16 : (size_t)K / 32;
+    return ((size_t)K / 2 + meta + 15) & ~(size_t)15;
+}
+
+// ============================================================================ per-slot gate / up
+// grid (ceil(F / (4*NR)), T*k), block 256: wave w of block (bx, slot) computes gate and up rows
+// row0 .. row0+NR-1 of expert idx[slot]; the 64 lanes stride over the 16-byte chunks of the rows.
+template <class FMT, int ACT, int NR>
+__global__ void __launch_bounds__(256)
+k_gate_up_slots(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
+                const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
+                int d, int F, int E, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int slot = blockIdx.y;
+    const int row0 = (blockIdx.x * 4 + wave) * NR;
+    if (row0 >= F) return;
+    const int e = idx[slot];
+    const bool valid = (unsigned)e < (unsigned)E;
+    const size_t rb = rbytes(FMT::FMT, d);
+    const int nchunk = d >> 5;
+    float ag[NR], au[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) ag[r] = au[r] = 0.f;
+    if (valid) {
+        const uint16_t* xr = x + (size_t)(slot / k) * d;
+        const uint8_t* gb0 = G + ((size_t)e * F + row0) * rb;
+        const uint8_t* ub0 = U + ((size_t)e * F + row0) * rb;
+        for (int c0 = 0; c0 < nchunk; c0 += 64) {
+            const bool cv = c0 + lane < nchunk;
+            const int c = cv ? c0 + lane : nchunk - 1;
+            uint4 wg[NR], wu[NR];
+            uint32_t mg[NR], mu[NR], xw[16];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const size_t ro = (size_t)min(r, F - 1 - row0) * rb;
+                wg[r] = *reinterpret_cast<const uint4*>(gb0 + ro + 16 * c);
+                wu[r] = *reinterpret_cast<const uint4*>(ub0 + ro + 16 * c);
+                mg[r] = FMT::meta(gb0 + ro, d, c);
+                mu[r] = FMT::meta(ub0 + ro, d, c);
+            }
+            load_x32(xr + 32 * c, xw);
+            __builtin_amdgcn_sched_barrier(0);   // every load above is in flight before any use
+            uint32_t xp[16];
+            pair_x32(xw, xp);
+            const float xs = FMT::XSUM ? sum_x32(xw) : 0.f;
+            if (cv) {
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    uint32_t qp[16];
+                    FMT::decode(wg[r], qp);
+                    ag[r] = FMT::fold(ag[r], mg[r], dot16(qp, xp, 0.f), xs);
+                    FMT::decode(wu[r], qp);
+                    au[r] = FMT::fold(au[r], mu[r], dot16(qp, xp, 0.f), xs);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        ag[r] = sum_lanes<64>(ag[r]);
+        au[r] = sum_lanes<64>(au[r]);
+    }
+    const int r = lane - 48;   // lanes 48..63 hold the sums
+    if (r >= 0 && r < NR && row0 + r < F) {
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int q = 0; q < NR; ++q)
+            if (q == r) { g = ag[q]; u = au[q]; }
+        float hv = 0.f;
+        if (valid) {
+            if (bg) g += bg[(size_t)e * F + row0 + r];
+            if (bu) u += bu[(size_t)e * F + row0 + r];
+            hv = glu<ACT>(g, u);
+        }
+        store_h(hhi, hlo, (size_t)slot * F, row0 + r, hv);
+    }
+}
+
+// ============================================================================ per-slot down
+// grid (ceil(D / RPW), T), block 256, RPW = 64 / LPR rows per block (LPR lanes per row); the 4 waves
+// split the k slots of token t and reduce them in LDS into y[t] (or write unweighted per-slot rows, nored).
+template <class FMT, int LPR>
+__global__ void __launch_bounds__(256)
+k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
+             const float* __restrict__ bd, const int32_t* __restrict__ idx, const float* __restrict__ wts, int k, int D,
+             int F, int E, int nored, int y32, const void* __restrict__ resid, void* __restrict__ y) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int SL = sum_lane<LPR>();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.y;
+    const int rsub = lane / LPR, psub = lane % LPR;
+    const int n = blockIdx.x * RPW + rsub;
+    const bool row_ok = n < D;
+    const int nn = row_ok ? n : D - 1;
+    const size_t rb = rbytes(FMT::FMT, F);
+    const int cpr = F >> 5;
+    float yacc = 0.f;
+    for (int j = wave; j < k; j += 4) {
+        const int slot = t * k + j;
+        const int e = idx[slot];
+        if ((unsigned)e >= (unsigned)E) {
+            if (nored && psub == SL && row_ok) store_y(y, (size_t)slot * D + n, 0.f, y32);
+            continue;
+        }
+        const uint8_t* rowp = Dw + ((size_t)e * D + nn) * rb;
+        const uint4* hh = reinterpret_cast<const uint4*>(hhi + (size_t)slot * F);
+        const uint4* hl = reinterpret_cast<const uint4*>(hlo + (size_t)slot * F);
+        float acc = 0.f;
+        for (int p0 = psub; p0 < cpr; p0 += 2 * LPR) {
+            uint4 wv[2], vh[2][4], vl[2][4];
+            uint32_t m[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int p = min(p0 + i * LPR, cpr - 1);
+                wv[i] = *reinterpret_cast<const uint4*>(rowp + 16 * p);
+                m[i] = FMT::meta(rowp, F, p);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    vh[i][q] = hh[4 * p + q];
+                    vl[i][q] = hl[4 * p + q];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                if (p0 + i * LPR < cpr) {
+                    uint32_t qp[16], wh[16], wl[16];
+                    FMT::decode(wv[i], qp);
+                    words16(vh[i], wh);
+                    words16(vl[i], wl);
+                    const float dt = dot16(qp, wl, dot16(qp, wh, 0.f));
+                    const float hs = FMT::XSUM ? sum16(wl, sum16(wh, 0.f)) : 0.f;
+                    acc = FMT::fold(acc, m[i], dt, hs);
+                }
+            }
+        }
+        acc = sum_lanes<LPR>(acc);
+        if (bd) acc += bd[(size_t)e * D + nn];
+        if (nored) {
+            if (psub == SL && row_ok) store_y(y, (size_t)slot * D + n, acc, y32);
+        } else {
+            yacc = __builtin_fmaf(wts[slot], acc, yacc);
+        }
+    }
+    if (nored) return;
+    __shared__ float red[4][RPW];
+    if (psub == SL) red[wave][rsub] = yacc;
+    __syncthreads();
+    if (wave == 0 && lane < RPW) {
+        const int n2 = blockIdx.x * RPW + lane;
+        if (n2 < D) {
+            const float v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+            const size_t o = (size_t)t * D + n2;
+            store_y(y, o, resid ? v + load_y(resid, o, y32) : v, y32);
+        }
+    }
+}
+
+// ============================================================================ grouped gate / up
+// grid (ceil(F / (4*NR)), max_active), block 256. Block (bx, a) computes rows of expert active[a] for all
+// of its slots, NB per pass: each weight chunk is decoded once per pass and applied to NB activations.
+template <class FMT, int ACT, int NR, int NB>
+__global__ void __launch_bounds__(256)
+k_gate_up_grouped(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
+                  const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ counts,
+                  const int32_t* __restrict__ offsets, const int32_t* __restrict__ sorted,
+                  const int32_t* __restrict__ active, const int32_t* __restrict__ meta, int k, int d, int F,
+                  uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
+    static_assert(NR * NB <= 16, "results live in lanes 48..63");
+    const int a = blockIdx.y;
+    if (a >= meta[0]) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + wave) * NR;
+    if (row0 >= F) return;
+    const int e = active[a];
+    const int beg = offsets[e], cnt = counts[e];
+    const size_t rb = rbytes(FMT::FMT, d);
+    const int nchunk = d >> 5;
+    const uint8_t* gb0 = G + ((size_t)e * F + row0) * rb;
+    const uint8_t* ub0 = U + ((size_t)e * F + row0) * rb;
+    for (int tb = 0; tb < cnt; tb += NB) {
+        const int nb = min(NB, cnt - tb);
+        int sl[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) sl[i] = sorted[beg + tb + min(i, nb - 1)];
+        float ag[NR][NB], au[NR][NB];
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+            for (int i = 0; i < NB; ++i) ag[r][i] = au[r][i] = 0.f;
+        for (int c0 = 0; c0 < nchunk; c0 += 64) {
+            const bool cv = c0 + lane < nchunk;
+            const int c = cv ? c0 + lane : nchunk - 1;
+            uint4 wg[NR], wu[NR];
+            uint32_t mg[NR], mu[NR], xw[NB][16];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const size_t ro = (size_t)min(r, F - 1 - row0) * rb;
+                wg[r] = *reinterpret_cast<const uint4*>(gb0 + ro + 16 * c);
+                wu[r] = *reinterpret_cast<const uint4*>(ub0 + ro + 16 * c);
+                mg[r] = FMT::meta(gb0 + ro, d, c);
+                mu[r] = FMT::meta(ub0 + ro, d, c);
+            }
+#pragma unroll
+            for (int i = 0; i < NB; ++i) load_x32(x + (size_t)(sl[i] / k) * d + 32 * c, xw[i]);
+            __builtin_amdgcn_sched_barrier(0);
+            uint32_t xp[NB][16];
+            float xs[NB];
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                pair_x32(xw[i], xp[i]);
+                xs[i] = FMT::XSUM ? sum_x32(xw[i]) : 0.f;
+            }
+            if (cv) {
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    uint32_t qp[16];
+                    FMT::decode(wg[r], qp);
+#pragma unroll
+                    for (int i = 0; i < NB; ++i) ag[r][i] = FMT::fold(ag[r][i], mg[r], dot16(qp, xp[i], 0.f), xs[i]);
+                    FMT::decode(wu[r], qp);
+#pragma unroll
+                    for (int i = 0; i < NB; ++i) au[r][i] = FMT::fold(au[r][i], mu[r], dot16(qp, xp[i], 0.f), xs[i]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                ag[r][i] = sum_lanes<64>(ag[r][i]);
+                au[r][i] = sum_lanes<64>(au[r][i]);
+            }
+        const int q = lane - 48;   // lane 48 + r*NB + i writes row r of slot i
+        if (q >= 0 && q < NR * NB) {
+            const int r = q / NB, i = q % NB;
+            float g = 0.f, u = 0.f;
+            int s_i = 0;
+#pragma unroll
+            for (int rr = 0; rr < NR; ++rr)
+#pragma unroll
+                for (int ii = 0; ii < NB; ++ii)
+                    if (rr * NB + ii == q) { g = ag[rr][ii]; u = au[rr][ii]; s_i = sl[ii]; }
+            const int n = row0 + r;
+            if (n < F && i < nb) {
+                if (bg) g += bg[(size_t)e * F + n];
+                if (bu) u += bu[(size_t)e * F + n];
+                store_h(hhi, hlo, (size_t)s_i * F, n, glu<ACT>(g, u));
+            }
+        }
+    }
+}
+
+// ============================================================================ grouped down
+// grid (ceil(D / (4*RPW)), max_active), block 256; each wave owns RPW = 64/LPR rows of expert active[a].
+// The h chunks of NB slots are staged in LDS (with their sums) KT chunks at a time; each weight chunk is
+// decoded once and applied to the NB slots. Writes yp[slot] = wts[slot] * (W_d h[slot] + bd) in fp32.
+constexpr int DG_KT = 64;   // chunks of h per LDS tile (2048 inputs)
+
+template <class FMT, int LPR, int NB>
+__global__ void __launch_bounds__(256)
+k_down_grouped(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
+               const float* __restrict__ bd, const float* __restrict__ wts, const int32_t* __restrict__ counts,
+               const int32_t* __restrict__ offsets, const int32_t* __restrict__ sorted,
+               const int32_t* __restrict__ active, const int32_t* __restrict__ meta, int D, int F,
+               float* __restrict__ yp) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int SL = sum_lane<LPR>();
+    constexpr int MPL = DG_KT / LPR;                // chunks per lane per tile
+    __shared__ uint4 s_h[NB][DG_KT][8];             // pre-paired h: 4 x 16 B hi, then 4 x 16 B lo
+    __shared__ float s_sum[NB][DG_KT];
+    const int a = blockIdx.y;
+    if (a >= meta[0]) return;   // block-uniform
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rsub = lane / LPR, psub = lane % LPR;
+    const int n = (blockIdx.x * 4 + wave) * RPW + rsub;
+    const bool row_ok = n < D;
+    const int nn = row_ok ? n : D - 1;
+    const int e = active[a];
+    const int beg = offsets[e], cnt = counts[e];
+    const size_t rb = rbytes(FMT::FMT, F);
+    const int cpr = F >> 5;
+    const uint8_t* rowp = Dw + ((size_t)e * D + nn) * rb;
+    const float bias_n = bd ? bd[(size_t)e * D + nn] : 0.f;
+    for (int tb = 0; tb < cnt; tb += NB) {
+        const int nb = min(NB, cnt - tb);
+        int sl[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) sl[i] = sorted[beg + tb + min(i, nb - 1)];
+        float acc[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) acc[i] = 0.f;
+        for (int kt = 0; kt < cpr; kt += DG_KT) {
+            const int kn = min(DG_KT, cpr - kt);
+            // weights of this tile first: they do not depend on h
+            uint4 wv[MPL];
+            uint32_t m[MPL];
+#pragma unroll
+            for (int q = 0; q < MPL; ++q) {
+                const int p = psub + q * LPR;
+                if (p < kn) {
+                    wv[q] = *reinterpret_cast<const uint4*>(rowp + 16 * (kt + p));
+                    m[q] = FMT::meta(rowp, F, kt + p);
+                }
+            }
+            __syncthreads();   // the previous tile's readers are done with the LDS
+            for (int t = threadIdx.x; t < NB * kn; t += 256) {
+                const int i = t / kn, p = t % kn;
+                const size_t o = (size_t)sorted[beg + tb + min(i, nb - 1)] * F + 32 * (kt + p);
+                const uint4* hh = reinterpret_cast<const uint4*>(hhi + o);
+                const uint4* hl = reinterpret_cast<const uint4*>(hlo + o);
+                uint4 v[8];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[q] = hh[q];
+                    v[4 + q] = hl[q];
+                }
+                float s = 0.f;
+                if (FMT::XSUM) {
+                    uint32_t w[16];
+                    words16(v, w);
+                    s = sum16(w, 0.f);
+                    words16(v + 4, w);
+                    s = sum16(w, s);
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) s_h[i][p][q] = v[q];
+                s_sum[i][p] = s;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < MPL; ++q) {
+                const int p = psub + q * LPR;
+                if (p < kn) {
+                    uint32_t qp[16];
+                    FMT::decode(wv[q], qp);
+#pragma unroll
+                    for (int i = 0; i < NB; ++i) {
+                        if (i < nb) {
+                            uint32_t wh[16], wl[16];
+                            words16(&s_h[i][p][0], wh);
+                            words16(&s_h[i][p][4], wl);
+                            acc[i] = FMT::fold(acc[i], m[q], dot16(qp, wl, dot16(qp, wh, 0.f)), s_sum[i][p]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) acc[i] = sum_lanes<LPR>(acc[i]);
+        if (psub == SL && row_ok) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+                if (i < nb) yp[(size_t)sl[i] * D + n] = wts[sl[i]] * (acc[i] + bias_n);
+        }
+    }
+}
+
+// ============================================================================ combine
+// y[t, n] = residual[t, n] + sum_j yp[t*k + j, n]; 4 outputs per thread (D % 4 == 0).
+__global__ void __launch_bounds__(256)
+k_combine(const float* __restrict__ yp, const void* __restrict__ resid, void* __restrict__ y, int T, int k, int D,
+          int y32) {
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t total4 = (size_t)T * D / 4;
+    if (i4 >= total4) return;
+    const size_t i = i4 * 4;
+    const int t = (int)(i / D), n = (int)(i % D);
+    float4 acc = reinterpret_cast<const float4*>(yp + ((size_t)t * k) * D + n)[0];
+    for (int j = 1; j < k; ++j) {
+        const float4 v = reinterpret_cast<const float4*>(yp + ((size_t)t * k + j) * D + n)[0];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    if (y32) {
+        if (resid) {
+            const float4 r = reinterpret_cast<const float4*>(resid)[i4];
+            acc.x += r.x;
+            acc.y += r.y;
+            acc.z += r.z;
+            acc.w += r.w;
+        }
+        reinterpret_cast<float4*>(y)[i4] = acc;
+        return;
+    }
+    if (resid) {
+        const uint2 r = reinterpret_cast<const uint2*>(resid)[i4];
+        acc.x += bf16lo(r.x);
+        acc.y += bf16hi(r.x);
+        acc.z += bf16lo(r.y);
+        acc.w += bf16hi(r.y);
+    }
+    uint2 o;
+    o.x = (uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16);
+    o.y = (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16);
+    reinterpret_cast<uint2*>(y)[i4] = o;
+}
+
+// ============================================================================ fused T == 1
+// One launch for a decode token: phase A computes gate/up/GLU for all k slots (row pairs spread over
+// every wave of the grid, NRA per wave), stores h, and counts the block done in one of 16 counters;
+// phase B waits until all blocks are counted, stages h (both planes, with chunk sums) in LDS, and
+// computes RPB = 64/LPRB down rows per block for all k slots (4 waves split the slots), reduced into y.
+// The down weights of a block's first row block are loaded before the wait. The grid never exceeds the
+// number of co-resident blocks (host side), every wait is bounded by spin_limit (a timeout sets err and
+// skips the block's down rows), and the last block to finish resets the counters to zero.
+struct T1Args {
+    const uint16_t* x;
+    const uint8_t *G, *U, *Dn;
+    const float *bg, *bu, *bd;
+    const int32_t* idx;
+    const float* wts;
+    int k, d, F, E, D;
+    int rpw_a;     // row pairs per wave in phase A (<= NRA)
+    int nbtask;    // row blocks of RPB down rows
+    int y32;
+    void* y;
+    const void* resid;
+    uint16_t *hhi, *hlo;
+    int32_t* sync;   // [0..15]*32: phase-A counters, 16*32: blocks finished, 17*32: timeout flag
+    int spin_limit;
+};
+constexpr int T1_SYNC_STRIDE = 32;   // one counter per 128-byte line
+
+template <class FMT, int ACT, int NRA, int LPRB, int SPW, int NCB>
+__global__ void __launch_bounds__(256, 1)
+k_t1_fused(T1Args a) {
+    extern __shared__ uint4 s_dyn[];
+    constexpr int RPB = 64 / LPRB;
+    constexpr int SL = sum_lane<LPRB>();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int gw = blockIdx.x * 4 + wave;
+    const int k = a.k, d = a.d, F = a.F, D = a.D;
+    const size_t rbA = rbytes(FMT::FMT, d), rbB = rbytes(FMT::FMT, F);
+    const int nchA = d >> 5, cpr = F >> 5;
+    const int Q = k * F;
+
+    // ---------------- phase A loads (one 64-lane pass over d: d <= 2048)
+    const bool cvA = lane < nchA;
+    const int cA = cvA ? lane : nchA - 1;
+    const int q0 = gw * a.rpw_a;
+    uint4 wg[NRA], wu[NRA];
+    uint32_t mg[NRA], mu[NRA];
+    int eq[NRA];
+#pragma unroll
+    for (int i = 0; i < NRA; ++i) {
+        const int q = min(q0 + min(i, a.rpw_a - 1), Q - 1);
+        const int j = q / F, n = q - j * F;
+        int e = a.idx[j];
+        eq[i] = e;
+        e = (unsigned)e < (unsigned)a.E ? e : 0;
+        const uint8_t* gr = a.G + ((size_t)e * F + n) * rbA;
+        const uint8_t* ur = a.U + ((size_t)e * F + n) * rbA;
+        wg[i] = *reinterpret_cast<const uint4*>(gr + 16 * cA);
+        wu[i] = *reinterpret_cast<const uint4*>(ur + 16 * cA);
+        mg[i] = FMT::meta(gr, d, cA);
+        mu[i] = FMT::meta(ur, d, cA);
+    }
+    uint32_t xw[16];
+    load_x32(a.x + 32 * cA, xw);
+
+    // ---------------- phase B prefetch: first row block of this block
+    const int rsub = lane / LPRB, psub = lane % LPRB;
+    int bt = blockIdx.x;
+    uint4 wv[SPW][NCB];
+    uint32_t mv[SPW][NCB];
+    {
+        const int n = min(bt * RPB + rsub, D - 1);
+#pragma unroll
+        for (int s = 0; s < SPW; ++s) {
+            const int j = min(wave + 4 * s, k - 1);
+            int e = a.idx[j];
+            e = (unsigned)e < (unsigned)a.E ? e : 0;
+            const uint8_t* rowp = a.Dn + ((size_t)e * D + n) * rbB;
+#pragma unroll
+            for (int m = 0; m < NCB; ++m) {
+                const int p = min(psub + m * LPRB, cpr - 1);
+                wv[s][m] = *reinterpret_cast<const uint4*>(rowp + 16 * p);
+                mv[s][m] = FMT::meta(rowp, F, p);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---------------- phase A compute
+    {
+        uint32_t xp[16];
+        pair_x32(xw, xp);
+        const float xs = FMT::XSUM ? sum_x32(xw) : 0.f;
+        float ag[NRA], au[NRA];
+#pragma unroll
+        for (int i = 0; i < NRA; ++i) {
+            uint32_t qp[16];
+            FMT::decode(wg[i], qp);
+            ag[i] = cvA ? FMT::fold(0.f, mg[i], dot16(qp, xp, 0.f), xs) : 0.f;
+            FMT::decode(wu[i], qp);
+            au[i] = cvA ? FMT::fold(0.f, mu[i], dot16(qp, xp, 0.f), xs) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NRA; ++i) {
+            ag[i] = sum_lanes<64>(ag[i]);
+            au[i] = sum_lanes<64>(au[i]);
+        }
+        const int r = lane - 48;
+        if (r >= 0 && r < NRA && r < a.rpw_a && q0 + r < Q) {
+            float g = 0.f, u = 0.f;
+            int e = 0;
+#pragma unroll
+            for (int i = 0; i < NRA; ++i)
+                if (i == r) { g = ag[i]; u = au[i]; e = eq[i]; }
+            const int q = q0 + r, j = q / F, n = q - j * F;
+            float hv = 0.f;
+            if ((unsigned)e < (unsigned)a.E) {
+                if (a.bg) g += a.bg[(size_t)e * F + n];
+                if (a.bu) u += a.bu[(size_t)e * F + n];
+                hv = glu<ACT>(g, u);
+            }
+            store_h(a.hhi, a.hlo, (size_t)j * F, n, hv);
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(&a.sync[(blockIdx.x & 15) * T1_SYNC_STRIDE], 1);
+
+    // ---------------- wait for every block's phase A (bounded)
+    __shared__ int s_ok;
+    if (wave == 0) {
+        int spins = 0, total = 0;
+        while (true) {
+            const int v = lane < 16 ? __hip_atomic_load(&a.sync[lane * T1_SYNC_STRIDE], __ATOMIC_ACQUIRE,
+                                                        __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0;
+            total = __builtin_amdgcn_readfirstlane((int)sum_lanes<16>((float)v));
+            if (total >= (int)gridDim.x || ++spins > a.spin_limit) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (lane == 0) {
+            s_ok = total >= (int)gridDim.x;
+            if (!s_ok) __hip_atomic_store(&a.sync[17 * T1_SYNC_STRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (s_ok) {
+        // ---------------- stage h of all k slots in LDS: per chunk 8 x 16 B (hi, lo) + its sum
+        uint4* s_h = s_dyn;                                          // [k*cpr][8]
+        float* s_sum = reinterpret_cast<float*>(s_dyn + (size_t)8 * k * cpr);   // [k*cpr]
+        float* s_red = s_sum + k * cpr;                               // [4][RPB]
+        for (int t = threadIdx.x; t < k * cpr; t += 256) {
+            const int j = t / cpr, p = t - j * cpr;
+            const size_t o = (size_t)j * F + 32 * p;
+            const uint4* hh = reinterpret_cast<const uint4*>(a.hhi + o);
+            const uint4* hl = reinterpret_cast<const uint4*>(a.hlo + o);
+            uint4 v[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[q] = hh[q];
+                v[4 + q] = hl[q];
+            }
+            float s = 0.f;
+            if (FMT::XSUM) {
+                uint32_t w[16];
+                words16(v, w);
+                s = sum16(w, 0.f);
+                words16(v + 4, w);
+                s = sum16(w, s);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) s_h[(size_t)t * 8 + q] = v[q];
+            s_sum[t] = s;
+        }
+        __syncthreads();
+        // ---------------- phase B: down rows for all slots
+        for (; bt < a.nbtask; bt += gridDim.x) {
+            const bool first = bt == (int)blockIdx.x;
+            const int n = bt * RPB + rsub;
+            const int nn = min(n, D - 1);
+            float yacc = 0.f;
+#pragma unroll
+            for (int s = 0; s < SPW; ++s) {
+                const int j = wave + 4 * s;
+                if (j < k) {
+                    const int e = a.idx[j];
+                    if ((unsigned)e < (unsigned)a.E) {
+                        const uint8_t* rowp = a.Dn + ((size_t)e * D + nn) * rbB;
+                        float acc = 0.f;
+#pragma unroll
+                        for (int m = 0; m < NCB; ++m) {
+                            const int p = psub + m * LPRB;
+                            if (p < cpr) {
+                                uint4 w = wv[s][m];
+                                uint32_t mm = mv[s][m];
+                                if (!first) {
+                                    w = *reinterpret_cast<const uint4*>(rowp + 16 * p);
+                                    mm = FMT::meta(rowp, F, p);
+                                }
+                                uint32_t qp[16], wh[16], wl[16];
+                                FMT::decode(w, qp);
+                                const size_t c = (size_t)j * cpr + p;
+                                words16(&s_h[c * 8], wh);
+                                words16(&s_h[c * 8 + 4], wl);
+                                acc = FMT::fold(acc, mm, dot16(qp, wl, dot16(qp, wh, 0.f)), s_sum[c]);
+                            }
+                        }
+                        acc = sum_lanes<LPRB>(acc);
+                        if (a.bd) acc += a.bd[(size_t)e * D + nn];
+                        yacc = __builtin_fmaf(a.wts[j], acc, yacc);
+                    }
+                }
+            }
+            if (psub == SL) s_red[wave * RPB + rsub] = yacc;
+            __syncthreads();
+            if (wave == 0 && lane < RPB) {
+                const int n2 = bt * RPB + lane;
+                if (n2 < D) {
+                    const float v = ((s_red[lane] + s_red[RPB + lane]) + s_red[2 * RPB + lane]) + s_red[3 * RPB + lane];
+                    store_y(a.y, n2, a.resid ? v + load_y(a.resid, n2, a.y32) : v, a.y32);
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // ---------------- the last block out resets the counters for the next launch
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = atomicAdd(&a.sync[16 * T1_SYNC_STRIDE], 1);
+        if (old == (int)gridDim.x - 1) {
+            for (int i = 0; i < 16; ++i) a.sync[i * T1_SYNC_STRIDE] = 0;
+            a.sync[16 * T1_SYNC_STRIDE] = 0;
+        }
+    }
+}
+
+// ============================================================================ host side
+namespace {
+
+int pick_lpr(int cpr) {
+    // lanes per down row: smallest power of two >= cpr / 3 (about three 16-byte chunks per lane), in [4, 64]
+    int l = 4;
+    while (l < 64 && l * 3 < cpr) l *= 2;
+    return l;
+}
+
+struct ProjPtrs {
+    const uint8_t *G, *U, *Dn;
+};
+ProjPtrs ptrs(const moe_experts_t* w) {
+    return {(const uint8_t*)w->gate.rows, (const uint8_t*)w->up.rows, (const uint8_t*)w->down.rows};
+}
+
+template <class FMT, int ACT>
+void launch_gu_slots(const ExpertsArgs& a, int NR) {
+    const moe_experts_t* w = a.w;
+    const ProjPtrs P = ptrs(w);
+    const int nslots = a.T * a.k;
+    dim3 grid((w->F + 4 * NR - 1) / (4 * NR), nslots);
+#define MOE_GUS(R)                                                                                              \
+    k_gate_up_slots<FMT, ACT, R><<<grid, 256, 0, a.st>>>((const uint16_t*)a.x, P.G, P.U, w->gate.bias, w->up.bias, \
+                                                          a.idx, a.k, w->d, w->F, w->E, a.hhi, a.hlo)
+    if (NR == 4) MOE_GUS(4);
+    else if (NR == 2) MOE_GUS(2);
+    else MOE_GUS(1);
+#undef MOE_GUS
+}
+
+template <class FMT>
+void launch_dn_slots(const ExpertsArgs& a) {
+    const moe_experts_t* w = a.w;
+    const ProjPtrs P = ptrs(w);
+    const int lpr = pick_lpr(w->F >> 5);
+    const int rpw = 64 / lpr;
+    dim3 grid((w->d + rpw - 1) / rpw, a.T);
+#define MOE_DNS(L)                                                                                                \
+    k_down_slots<FMT, L><<<grid, 256, 0, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.idx, a.wts, a.k, w->d, w->F, \
+                                                  w->E, a.nored, a.y32, a.residual, a.y)
+    switch (lpr) {
+        case 4: MOE_DNS(4); break;
+        case 8: MOE_DNS(8); break;
+        case 16: MOE_DNS(16); break;
+        case 32: MOE_DNS(32); break;
+        default: MOE_DNS(64); break;
+    }
+#undef MOE_DNS
+}
+
+template <class FMT, int ACT>
+void launch_gu_grouped(const ExpertsArgs& a, int max_active) {
+    const moe_experts_t* w = a.w;
+    const ProjPtrs P = ptrs(w);
+    constexpr int NR = 2, NB = 4;
+    dim3 grid((w->F + 4 * NR - 1) / (4 * NR), max_active);
+    k_gate_up_grouped<FMT, ACT, NR, NB><<<grid, 256, 0, a.st>>>(
+        (const uint16_t*)a.x, P.G, P.U, w->gate.bias, w->up.bias, a.grp.counts, a.grp.offsets, a.grp.sorted,
+        a.grp.active, a.grp.meta, a.k, w->d, w->F, a.hhi, a.hlo);
+}
+
+template <class FMT>
+void launch_dn_grouped(const ExpertsArgs& a, int max_active) {
+    const moe_experts_t* w = a.w;
+    const ProjPtrs P = ptrs(w);
+    const int lpr = pick_lpr(min(w->F >> 5, DG_KT));
+    const int rpw = 64 / lpr;
+    dim3 grid((w->d + 4 * rpw - 1) / (4 * rpw), max_active);
+#define MOE_DNG(L)                                                                                                \
+    k_down_grouped<FMT, L, 4><<<grid, 256, 0, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.wts, a.grp.counts,      \
+                                                       a.grp.offsets, a.grp.sorted, a.grp.active, a.grp.meta, w->d, \
+                                                       w->F, a.yp)
+    switch (lpr) {
+        case 4: MOE_DNG(4); break;
+        case 8: MOE_DNG(8); break;
+        case 16: MOE_DNG(16); break;
+        case 32: MOE_DNG(32); break;
+        default: MOE_DNG(64); break;
+    }
+#undef MOE_DNG
+}
+
+template <class FMT>
+int run_slots_fmt(const ExpertsArgs& a) {
+    const int nslots = a.T * a.k;
+    if (a.stages & 1) {
+        // fewer rows per wave when the launch would be short of waves
+        const long waves4 = (long)nslots * a.w->F / 16;
+        const int NR = waves4 >= 1024 ? 4 : ((long)nslots * a.w->F / 8 >= 1024 ? 2 : 1);
+        if (a.act == 0) launch_gu_slots<FMT, 0>(a, NR);
+        else if (a.act == 1) launch_gu_slots<FMT, 1>(a, NR);
+        else launch_gu_slots<FMT, 2>(a, NR);
+        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+    }
+    if (a.stages & 2) {
+        launch_dn_slots<FMT>(a);
+        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+    }
+    return 0;
+}
+
+template <class FMT>
+int run_grouped_fmt(const ExpertsArgs& a) {
+    const int nslots = a.T * a.k;
+    const int max_active = nslots < a.w->E ? nslots : a.w->E;
+    if (a.stages & 1) {
+        int rc = launch_group(a.idx, nslots, a.w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
+                              a.grp.meta, a.st);
+        if (rc) return rc;
+        if (a.act == 0) launch_gu_grouped<FMT, 0>(a, max_active);
+        else if (a.act == 1) launch_gu_grouped<FMT, 1>(a, max_active);
+        else launch_gu_grouped<FMT, 2>(a, max_active);
+        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+    }
+    if (a.stages & 2) {
+        launch_dn_grouped<FMT>(a, max_active);
+        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+        return launch_combine(a.yp, a.residual, a.y, a.T, a.k, a.w->d, a.y32, a.st);
+    }
+    return 0;
+}
+
+// ---------------------------------------------------------------- fused T == 1
+constexpr int T1_NRA = 8;    // max row pairs per wave in phase A
+constexpr int T1_SPW = 4;    // max slots per wave in phase B (k <= 16)
+constexpr int T1_NCB = 4;    // max chunks per lane per down row
+constexpr int T1_LDS_MAX = 64 * 1024;
+
+int t1_lds_bytes(int k, int F, int rpb) { return k * (F >> 5) * (128 + 4) + 4 * rpb * 4; }
+
+template <class FMT, int ACT, int LPRB>
+int launch_t1(const ExpertsArgs& a, int32_t* sync) {
+    constexpr int RPB = 64 / LPRB;
+    auto kern = k_t1_fused<FMT, ACT, T1_NRA, LPRB, T1_SPW, T1_NCB>;
+    const moe_experts_t* w = a.w;
+    const int lds = t1_lds_bytes(a.k, w->F, RPB);
+    // co-resident capacity of this kernel on the current device (cached per device)
+    static int cap_cache[64] = {0};   // written once per device with the same value; a race is benign
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+    if (cap_cache[dev] == 0) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, T1_LDS_MAX) != hipSuccess) return 1;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 1;
+        cap_cache[dev] = per_cu * cus;
+    }
+    const int cap = cap_cache[dev];
+    const int nbtask = (w->d + RPB - 1) / RPB;
+    const int Q = a.k * w->F;
+    int grid = nbtask < cap ? nbtask : cap;
+    const int need = (Q + 4 * T1_NRA - 1) / (4 * T1_NRA);   // blocks so that phase A fits NRA per wave
+    if (need > grid) grid = need;
+    if (grid > cap || grid < 1) return 1;
+    T1Args t{};
+    t.x = (const uint16_t*)a.x;
+    const ProjPtrs P = ptrs(w);
+    t.G = P.G;
+    t.U = P.U;
+    t.Dn = P.Dn;
+    t.bg = w->gate.bias;
+    t.bu = w->up.bias;
+    t.bd = w->down.bias;
+    t.idx = a.idx;
+    t.wts = a.wts;
+    t.k = a.k;
+    t.d = w->d;
+    t.F = w->F;
+    t.E = w->E;
+    t.D = w->d;
+    t.rpw_a = (Q + 4 * grid - 1) / (4 * grid);
+    t.nbtask = nbtask;
+    t.y32 = a.y32;
+    t.y = a.y;
+    t.resid = a.residual;
+    t.hhi = a.hhi;
+    t.hlo = a.hlo;
+    t.sync = sync;
+    t.spin_limit = 1 << 22;
+    kern<<<grid, 256, lds, a.st>>>(t);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+// returns 1 when the fused kernel cannot take this call (the caller falls back to two launches)
+template <class FMT>
+int try_t1_fused(const ExpertsArgs& a, int32_t* sync) {
+    const moe_experts_t* w = a.w;
+    const int cpr = w->F >> 5;
+    const int lprb = pick_lpr(cpr);
+    if (a.T != 1 || a.nored || a.stages != 3 || !sync || a.k > 4 * T1_SPW || w->d > 2048 ||
+        (cpr + lprb - 1) / lprb > T1_NCB || lprb > 16 || t1_lds_bytes(a.k, w->F, 64 / lprb) > T1_LDS_MAX)
+        return 1;
+    int rc;
+#define MOE_T1(ACT)                                                         \
+    switch (lprb) {                                                         \
+        case 4: rc = launch_t1<FMT, ACT, 4>(a, sync); break;                \
+        case 8: rc = launch_t1<FMT, ACT, 8>(a, sync); break;                \
+        default: rc = launch_t1<FMT, ACT, 16>(a, sync); break;              \
+    }
+    if (a.act == 0) { MOE_T1(0) }
+    else if (a.act == 1) { MOE_T1(1) }
+    else { MOE_T1(2) }
+#undef MOE_T1
+    return rc;
+}
+
+}  // namespace
+
+int run_experts_slots(const ExpertsArgs& a) {
+    if (a.w->fmt == MOE_FMT_INT4_G64) {
+        if (a.fused_t1) {
+            const int rc = try_t1_fused<FmtInt4>(a, a.sync);
+            if (rc != 1) return rc;
+        }
+        return run_slots_fmt<FmtInt4>(a);
+    }
+    if (a.fused_t1) {
+        const int rc = try_t1_fused<FmtMxfp4>(a, a.sync);
+        if (rc != 1) return rc;
+    }
+    return run_slots_fmt<FmtMxfp4>(a);
+}
+
+int run_experts_grouped(const ExpertsArgs& a) {
+    return a.w->fmt == MOE_FMT_INT4_G64 ? run_grouped_fmt<FmtInt4>(a) : run_grouped_fmt<FmtMxfp4>(a);
+}
+
+int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st) {
+    const size_t total4 = (size_t)T * d / 4;
+    if (total4 == 0) return 0;
+    dim3 grid((unsigned)((total4 + 255) / 256));
+    k_combine<<<grid, 256, 0, st>>>(yp, residual, y, T, k, d, y32);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+}  // namespace moe

@@ -40,16 +40,15 @@ struct ExpertsArgs {
     float* yp;      // [T*k, d] fp32 scratch (grouped path)
     GroupBufs grp;  // grouped path
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
+    int fused_t1;   // T == 1: try the single-launch kernel first
+    int32_t* sync;  // zero-initialised counters of the fused kernel (left zero after every launch)
     hipStream_t st;
 };
 
-// int4 g64 expert kernels (moe_int4.hip)
-int run_int4_slots(const ExpertsArgs& a);
-int run_int4_grouped(const ExpertsArgs& a);
-// MXFP4 expert kernels (moe_mxfp4.hip)
-int run_mxfp4_slots(const ExpertsArgs& a);
-int run_mxfp4_grouped(const ExpertsArgs& a);
-// combine (moe_int4.hip): y[t] = residual[t] + sum_j yp[t*k + j]
+// expert kernels, both formats (moe_experts.hip)
+int run_experts_slots(const ExpertsArgs& a);
+int run_experts_grouped(const ExpertsArgs& a);
+// combine (moe_experts.hip): y[t] = residual[t] + sum_j yp[t*k + j]
 int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);
 
 }  // namespace moe

@@ -1,44 +1,58 @@
 """Host side of the expert path: packed-weight state, the C-ABI call, workspace handling.
 
 A state is a plain dict, as in the reference variants (reference metal_q4_moe.py:32-35,
-metal_mxfp4_gptoss.py:100-107):
-    "g", "u", "d": (codes, scales, biases) for int4 g64, (codes, scales) for MXFP4
-                   gate/up codes [E, F, d/8], down codes [E, d, F/8] (int32 words)
+metal_mxfp4_gptoss.py:100-107), holding the packed row records the library reads:
+    "fmt": "int4" | "mxfp4";  "shape": (E, d, F)
+    "g", "u": uint8 records [E, F, row_bytes(fmt, d)];  "d": uint8 records [E, d, row_bytes(fmt, F)]
     "bg", "bu", "bd": optional fp32 additive biases [E, F], [E, F], [E, d] (gpt-oss)
-    "fmt": "int4" | "mxfp4"
 """
 import torch
 
-from . import _lib
+from . import _lib, formats
 
 FMT = {"int4": _lib.FMT_INT4_G64, "mxfp4": _lib.FMT_MXFP4}
 
 
 def dims(s):
-    codes_g = s["g"][0]
-    E, F = codes_g.shape[0], codes_g.shape[1]
-    d = s["d"][0].shape[1]
+    E, d, F = s["shape"]
     return E, d, F
+
+
+def make_state(fmt, g, u, d, bg=None, bu=None, bd=None):
+    """State from (codes, scales[, biases]) triples in the reference's layout (packed into row records)."""
+    E, F, W = g[0].shape
+    s = {"fmt": fmt, "shape": (E, W * 8, F)}
+    for n, p in (("g", g), ("u", u), ("d", d)):
+        s[n] = formats.pack_rows(fmt, *p)
+    for n, b in (("bg", bg), ("bu", bu), ("bd", bd)):
+        if b is not None:
+            s[n] = b.to(torch.float32).contiguous()
+    return s
+
+
+def unpack(s, n):
+    """The reference-layout (codes, scales[, biases]) of projection n of a state."""
+    E, d, F = dims(s)
+    return formats.unpack_rows(s["fmt"], s[n], F if n == "d" else d)
 
 
 def _desc(s):
     """ctypes moe_experts_t for a state (cached; rebuilt if any tensor changed)."""
-    tensors = tuple(s["g"]) + tuple(s["u"]) + tuple(s["d"]) + tuple(s.get(b) for b in ("bg", "bu", "bd"))
+    tensors = (s["g"], s["u"], s["d"]) + tuple(s.get(b) for b in ("bg", "bu", "bd"))
     key = tuple(0 if t is None else t.data_ptr() for t in tensors)
     c = s.get("_c")
     if c is not None and c[0] == key:
         return c[1]
     E, d, F = dims(s)
+    for n, K, N in (("g", d, F), ("u", d, F), ("d", F, d)):
+        assert s[n].dtype == torch.uint8 and tuple(s[n].shape) == (E, N, formats.row_bytes(s["fmt"], K)), n
 
-    def proj(p, bias):
-        codes, scales = p[0], p[1]
-        biases = p[2] if len(p) > 2 else None
-        for t in (codes, scales, biases, bias):
+    def proj(rows, bias):
+        for t in (rows, bias):
             if t is not None:
                 _lib.require_device(t, "expert weights")
                 assert t.is_contiguous(), "expert weights must be contiguous"
-        return _lib.Proj(codes.data_ptr(), scales.data_ptr(), None if biases is None else biases.data_ptr(),
-                         None if bias is None else bias.data_ptr())
+        return _lib.Proj(rows.data_ptr(), None if bias is None else bias.data_ptr())
 
     desc = _lib.Experts(FMT[s.get("fmt", "int4")], E, d, F, proj(s["g"], s.get("bg")), proj(s["u"], s.get("bu")),
                         proj(s["d"], s.get("bd")))

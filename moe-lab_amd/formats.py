@@ -15,6 +15,11 @@ MXFP4 (``mx.quantize(mode="mxfp4")``):
     The scale byte is the float whose bit pattern is s << 23: exact 2^(s-127) for s = 1..254, 0 -> 0.
 
 Words are held in torch.int32 tensors (same bits as the reference's uint32).
+
+The GPU library takes each projection packed row by row (include/moe_mi355x.h): a row of K inputs is one
+record of row_bytes(fmt, K) bytes = the row's K/2 code bytes followed by its group metadata (int4: one
+32-bit word per group, scale bf16 in the low half, bias bf16 in the high half; MXFP4: the E8M0 bytes),
+zero-padded to a multiple of 16 bytes. pack_rows / unpack_rows convert between the two layouts.
 """
 import torch
 
@@ -40,6 +45,39 @@ def unpack_nibbles(words):
     shifts = torch.arange(0, 32, 4, device=w.device, dtype=torch.int64)
     q = (w.unsqueeze(-1) >> shifts) & 0xF
     return q.reshape(*words.shape[:-1], words.shape[-1] * 8)
+
+
+# ----------------------------------------------------------------------------------- row records
+FMT_INT4, FMT_MXFP4 = "int4", "mxfp4"
+
+
+def row_bytes(fmt, K):
+    meta = K // 16 if fmt == FMT_INT4 else K // 32
+    return (K // 2 + meta + 15) // 16 * 16
+
+
+def pack_rows(fmt, codes, scales, biases=None):
+    """(codes int32 [E, N, K/8], scales, biases) -> uint8 records [E, N, row_bytes(fmt, K)]."""
+    E, N, W = codes.shape
+    K = W * 8
+    rows = torch.zeros((E, N, row_bytes(fmt, K)), dtype=torch.uint8, device=codes.device)
+    rows[..., :K // 2] = codes.contiguous().view(torch.uint8).reshape(E, N, K // 2)
+    if fmt == FMT_INT4:
+        sb = torch.stack([scales.contiguous().view(torch.int16), biases.contiguous().view(torch.int16)], dim=-1)
+        rows[..., K // 2:K // 2 + K // 16] = sb.view(torch.uint8).reshape(E, N, K // 16)
+    else:
+        rows[..., K // 2:K // 2 + K // 32] = scales.to(torch.uint8)
+    return rows
+
+
+def unpack_rows(fmt, rows, K):
+    """Inverse of pack_rows: (codes int32 [E, N, K/8], scales, biases) or (codes, scales) for MXFP4."""
+    E, N, _ = rows.shape
+    codes = rows[..., :K // 2].contiguous().view(torch.int32).reshape(E, N, K // 8)
+    if fmt == FMT_INT4:
+        sb = rows[..., K // 2:K // 2 + K // 16].contiguous().view(torch.int16).reshape(E, N, K // 64, 2)
+        return codes, sb[..., 0].contiguous().view(torch.bfloat16), sb[..., 1].contiguous().view(torch.bfloat16)
+    return codes, rows[..., K // 2:K // 2 + K // 32].contiguous()
 
 
 # --------------------------------------------------------------------------------------------- int4

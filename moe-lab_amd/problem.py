@@ -90,15 +90,13 @@ def zipf_bias(E, s=1.1, seed=0):
 
 
 def baseline_int4_layer(shape, seed, device, router=True):
-    """One BASELINE int4 g64 SwiGLU layer, generated packed on the device."""
+    """One BASELINE int4 g64 SwiGLU layer (an expert state plus "wr"), generated packed on the device."""
+    from .experts import make_state
     g = torch.Generator(device=device).manual_seed(int(seed))
     E, d, F = shape.E, shape.d, shape.f
-    layer = {
-        "g": formats.random_int4(E, F, d, generator=g, device=device),
-        "u": formats.random_int4(E, F, d, generator=g, device=device),
-        "d": formats.random_int4(E, d, F, generator=g, device=device),
-        "fmt": "int4",
-    }
+    layer = make_state("int4", formats.random_int4(E, F, d, generator=g, device=device),
+                       formats.random_int4(E, F, d, generator=g, device=device),
+                       formats.random_int4(E, d, F, generator=g, device=device))
     if router:
         layer["wr"] = (torch.randn((E, d), generator=g, device=device) * 0.02).to(torch.bfloat16)
     return layer
@@ -107,14 +105,12 @@ def baseline_int4_layer(shape, seed, device, router=True):
 def baseline_mxfp4_layer(shape, seed, device, biases=True, router=True):
     """One BASELINE MXFP4 layer (gpt-oss: per-expert bf16 biases ~N(0, 0.01), kept as fp32 in the state
     like reference metal_mxfp4_gptoss.py:105)."""
+    from .experts import make_state
     g = torch.Generator(device=device).manual_seed(int(seed))
     E, d, F = shape.E, shape.d, shape.f
-    layer = {
-        "g": formats.random_mxfp4(E, F, d, generator=g, device=device),
-        "u": formats.random_mxfp4(E, F, d, generator=g, device=device),
-        "d": formats.random_mxfp4(E, d, F, generator=g, device=device),
-        "fmt": "mxfp4",
-    }
+    layer = make_state("mxfp4", formats.random_mxfp4(E, F, d, generator=g, device=device),
+                       formats.random_mxfp4(E, F, d, generator=g, device=device),
+                       formats.random_mxfp4(E, d, F, generator=g, device=device))
     if biases:
         for n, rows in (("bg", F), ("bu", F), ("bd", d)):
             b = (torch.randn((E, rows), generator=g, device=device) * 0.01).to(torch.bfloat16)

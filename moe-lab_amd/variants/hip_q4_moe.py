@@ -2,7 +2,8 @@
 
 Same variant contract and dispatch shape as the reference's production int4 dispatcher
 (reference moelab/variants/mlx/metal_q4_moe.py:1-64):
-    T == 1                  -> per-slot GEMV: gate+up+GLU fused, down + k-reduction fused (2 launches)
+    T == 1                  -> one launch: gate+up+GLU for the k slots, then down + k-reduction
+                               (two per-slot launches when the shape does not fit the fused kernel)
     T > 1, custom_wins(...) -> grouped expert tiles: each selected expert's rows are read once and
                                applied to all of its slots (group, gate/up, down, combine)
     otherwise               -> gather_moe (module attribute, monkeypatchable like the reference's)
@@ -12,7 +13,7 @@ gives the weights the fp32 reference uses.
 import torch
 
 from .. import _lib, formats
-from ..experts import dims, run_experts
+from ..experts import dims, make_state, run_experts, unpack
 from ..fallback import gather_moe  # noqa: F401  (module attribute the dispatcher calls; tests patch it)
 
 META = {"name": "hip_q4_moe", "description": "gfx950 HIP: per-slot GEMV at T=1, grouped expert tiles at T>1"}
@@ -25,22 +26,17 @@ def prepare(w_gate, w_up, w_down):
     """Dense weights gate/up [E, F, d], down [E, d, F] (any float dtype, on the GPU) -> packed state."""
     E, f, d = w_gate.shape
     assert d % 64 == 0 and f % 64 == 0, "d, f must be multiples of 64"
-    s = {n: formats.quantize_int4(w.contiguous()) for n, w in (("g", w_gate), ("u", w_up), ("d", w_down))}
-    s["fmt"] = "int4"
-    return s
+    q = {n: formats.quantize_int4(w.contiguous()) for n, w in (("g", w_gate), ("u", w_up), ("d", w_down))}
+    return make_state("int4", q["g"], q["u"], q["d"])
 
 
 def state_from_packed(g, u, d, bg=None, bu=None, bd=None):
-    """State from already-packed (codes, scales, biases) triples, e.g. a checkpoint or synthetic weights."""
-    s = {"g": tuple(g), "u": tuple(u), "d": tuple(d), "fmt": "int4"}
-    for n, b in (("bg", bg), ("bu", bu), ("bd", bd)):
-        if b is not None:
-            s[n] = b.to(torch.float32).contiguous()
-    return s
+    """State from (codes, scales, biases) triples in the reference's layout, e.g. a checkpoint."""
+    return make_state("int4", g, u, d, bg, bu, bd)
 
 
 def dequant(s):
-    return tuple(formats.dequant_int4(*s[n], group_size=GS) for n in ("g", "u", "d"))
+    return tuple(formats.dequant_int4(*unpack(s, n), group_size=GS) for n in ("g", "u", "d"))
 
 
 def custom_wins(T, k, E, D, F):
@@ -63,7 +59,7 @@ def run(s, x, idx, wts, act=0, residual=None, out_dtype=None):
     T, k = idx.shape
     kw = dict(act=act, residual=residual, out_dtype=out_dtype)
     if T == 1:
-        return run_experts(s, x, idx, wts, path=_lib.PATH_SLOTS, **kw)
+        return run_experts(s, x, idx, wts, path=_lib.PATH_AUTO, **kw)
     E, D, F = dims(s)
     if not custom_wins(T, k, E, D, F):
         return gather_moe(s, x, idx, wts, GS, BITS, **kw)

@@ -19,10 +19,12 @@ def np_words(t):
 
 
 def deq(state, name, experts=None):
-    """Oracle dequantisation (fp64) of projection `name` of a packed state, optionally only `experts`."""
-    p = state[name]
+    """Oracle dequantisation (fp64) of projection `name` of a packed state, optionally only `experts`.
+    The records are split back into the reference's (codes, scales[, biases]) layout first."""
+    from moelab_amd.experts import unpack
+    p = unpack(state, name)
     sel = (lambda t: t) if experts is None else (lambda t: t[experts])  # noqa: E731
-    if state.get("fmt", "int4") == "int4":
+    if state["fmt"] == "int4":
         return orc.dequant_int4(np_words(sel(p[0])), np_u16(sel(p[1])), np_u16(sel(p[2])))
     return orc.dequant_mxfp4(np_words(sel(p[0])), sel(p[1]).cpu().numpy())
 

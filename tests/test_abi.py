@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 def _desc(E=8, d=128, F=128, fmt=0):
     from moelab_amd import _lib
     fake = ctypes.c_void_p(4096)   # never dereferenced: argument checks return before any launch
-    p = _lib.Proj(fake, fake, fake, None)
+    p = _lib.Proj(fake, None)
     return _lib.Experts(fmt, E, d, F, p, p, p)
 
 

@@ -21,8 +21,7 @@ def q4():
 
 def packed_state(shape, seed, biases=False):
     from moelab_amd.problem import baseline_int4_layer
-    layer = baseline_int4_layer(shape, seed, DEV, router=False)
-    s = q4().state_from_packed(layer["g"], layer["u"], layer["d"])
+    s = baseline_int4_layer(shape, seed, DEV, router=False)
     if biases:
         g = torch.Generator(device=DEV).manual_seed(seed + 1)
         s["bg"] = torch.randn((shape.E, shape.f), generator=g, device=DEV) * 0.1
@@ -215,7 +214,7 @@ def test_qwen3_full_shape(T):
     from moelab_amd.shapes import SHAPES
     sh = SHAPES["qwen3-30b-a3b"]
     layer = baseline_int4_layer(sh, seed=11, device=DEV)
-    s = q4().state_from_packed(layer["g"], layer["u"], layer["d"])
+    s = layer
     x = baseline_x(T, sh.d, seed=11, device=DEV)
     idx, wts, logits = router.route(x, layer["wr"], sh.k, return_logits=True)
     lg_ref = orc.router_logits(np_u16(x), np_u16(layer["wr"]))
@@ -224,3 +223,41 @@ def test_qwen3_full_shape(T):
     ref = oracle_y(s, x, idx, wts)
     assert_close(q4().run(s, x, idx, wts, out_dtype=torch.float32), ref, what="fp32 out")
     assert_close(q4().run(s, x, idx, wts), ref, what="bf16 out")
+
+
+@pytest.mark.parametrize("T", [1])
+@pytest.mark.parametrize("shape_args", [(2048, 768, 128, 8), (512, 256, 8, 1), (2048, 1408, 64, 6),
+                                        (1024, 512, 16, 16), (256, 128, 4, 4)])
+def test_fused_t1_equals_two_launch_path(T, shape_args):
+    """The single-launch T=1 kernel (PATH_AUTO) and the two per-slot launches agree with the oracle, and the
+    fused kernel leaves its completion counters at zero with no timeout."""
+    from moelab_amd import _lib
+    from moelab_amd.experts import run_experts
+    sh = shape_("f", *shape_args)
+    s = packed_state(sh, 9)
+    x, idx, wts = inputs(sh, T, seed=9)
+    ref = oracle_y(s, x, idx, wts)
+    for _ in range(3):
+        for path in (_lib.PATH_AUTO, _lib.PATH_SLOTS):
+            assert_close(run_experts(s, x, idx, wts, path=path, out_dtype=torch.float32), ref, what=path)
+    torch.cuda.synchronize()
+    sync = _lib.workspace(x.device, 0)[:_lib.WORKSPACE_SYNC_BYTES].view(torch.int32).cpu()
+    assert int(sync.abs().sum()) == 0, sync.nonzero()
+
+
+def test_small_affine_scales():
+    """Tiny scales (x1e-6 weights, x1e6 activations) stay accurate: scale and bias are applied in fp32
+    (reference tests/test_int4_small_scales.py:23-32)."""
+    from moelab_amd import formats
+    from moelab_amd.experts import make_state, unpack
+    sh = shape_("tiny", 256, 256, 8, 2)
+    base = packed_state(sh, 10)
+    parts = {n: list(unpack(base, n)) for n in ("g", "u", "d")}
+    for n in ("g", "u"):
+        parts[n][1] = (parts[n][1].float() * 1e-6).to(torch.bfloat16)
+        parts[n][2] = (parts[n][1].float() * -8.0).to(torch.bfloat16)
+    s = make_state("int4", parts["g"], parts["u"], parts["d"])
+    for T in (1, 7):
+        x, idx, wts = inputs(sh, T, seed=10, scale=1e6)
+        assert_close(q4().run(s, x, idx, wts, out_dtype=torch.float32), oracle_y(s, x, idx, wts), what=T)
+    assert formats.GS_INT4 == 64
