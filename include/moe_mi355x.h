@@ -124,7 +124,7 @@ int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offset
  *   run_slots / NORED, metal_q4_moe.py:49-51; per-slot path only, residual must be NULL).
  *   Accumulation in fp32; the GLU output h is kept between the two launches as an unevaluated sum of two
  *   bf16 planes (about 16 significant bits, where the reference kernels store it in x.dtype).
- *   Requirements: d % 64 == 0 and F % 64 == 0; x, y, rows 16-byte aligned.
+ *   Requirements: d % 64 == 0, F % 64 == 0, F <= 16384; x, y, rows 16-byte aligned.
  *   workspace: moe_experts_workspace_bytes(...) bytes. Its first MOE_WORKSPACE_SYNC_BYTES bytes hold the
  *   fused T == 1 kernel's completion counters: zero them once when the workspace is allocated; every call
  *   leaves them zero. The rest may hold anything. Calls sharing a workspace must be stream-ordered.

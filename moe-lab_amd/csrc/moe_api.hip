@@ -54,7 +54,7 @@ int check_experts(const moe_experts_t* w) {
     if (w->fmt != MOE_FMT_INT4_G64 && w->fmt != MOE_FMT_MXFP4) return MOE_ERR_DTYPE;
     if (w->E < 1 || w->d < 1 || w->F < 1) return MOE_ERR_ARG;
     const int g = w->fmt == MOE_FMT_INT4_G64 ? 64 : 32;
-    if (w->d % 64 || w->F % 64 || w->d % g || w->F % g) return MOE_ERR_ARG;
+    if (w->d % 64 || w->F % 64 || w->d % g || w->F % g || w->F > 16384) return MOE_ERR_ARG;
     int rc;
     if ((rc = check_proj(w->gate)) || (rc = check_proj(w->up)) || (rc = check_proj(w->down))) return rc;
     return MOE_OK;

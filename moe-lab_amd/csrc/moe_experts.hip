@@ -196,16 +196,20 @@ k_gate_up_slots(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, c
 }
 
 // ============================================================================ per-slot down
-// grid (ceil(D / RPW), T), block 256, RPW = 64 / LPR rows per block (LPR lanes per row); the 4 waves
-// split the k slots of token t and reduce them in LDS into y[t] (or write unweighted per-slot rows, nored).
-template <class FMT, int LPR>
-__global__ void __launch_bounds__(256)
+// grid (ceil(D / RPW), T), block 64*NW (NW = min(k, 8) waves): wave j handles slot t*k + j (and j + NW, ...)
+// for RPW = 64/LPR rows (LPR lanes per row, NC chunks per lane: NC*LPR >= F/32). All of a slot's loads
+// (weight chunks, metadata, pre-paired h) are issued before any use; the waves reduce their slots in LDS
+// into y[t] (or write unweighted per-slot rows, nored).
+template <class FMT, int LPR, int NC>
+__global__ void __launch_bounds__(512)
 k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
              const float* __restrict__ bd, const int32_t* __restrict__ idx, const float* __restrict__ wts, int k, int D,
              int F, int E, int nored, int y32, const void* __restrict__ resid, void* __restrict__ y) {
     constexpr int RPW = 64 / LPR;
     constexpr int SL = sum_lane<LPR>();
+    __shared__ float red[8][RPW];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nw = blockDim.x >> 6;
     const int t = blockIdx.y;
     const int rsub = lane / LPR, psub = lane % LPR;
     const int n = blockIdx.x * RPW + rsub;
@@ -214,7 +218,7 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
     const size_t rb = rbytes(FMT::FMT, F);
     const int cpr = F >> 5;
     float yacc = 0.f;
-    for (int j = wave; j < k; j += 4) {
+    for (int j = wave; j < k; j += nw) {
         const int slot = t * k + j;
         const int e = idx[slot];
         if ((unsigned)e >= (unsigned)E) {
@@ -224,13 +228,15 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
         const uint8_t* rowp = Dw + ((size_t)e * D + nn) * rb;
         const uint4* hh = reinterpret_cast<const uint4*>(hhi + (size_t)slot * F);
         const uint4* hl = reinterpret_cast<const uint4*>(hlo + (size_t)slot * F);
+        constexpr int NG = NC < 4 ? NC : 4;   // chunks whose loads are in flight together
         float acc = 0.f;
-        for (int p0 = psub; p0 < cpr; p0 += 2 * LPR) {
-            uint4 wv[2], vh[2][4], vl[2][4];
-            uint32_t m[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int p = min(p0 + i * LPR, cpr - 1);
+        for (int g0 = 0; g0 < NC; g0 += NG) {
+            uint4 wv[NG], vh[NG][4], vl[NG][4];
+            uint32_t m[NG];
+#pragma unroll
+            for (int i = 0; i < NG; ++i) {
+                const int p = min(psub + (g0 + i) * LPR, cpr - 1);
                 wv[i] = *reinterpret_cast<const uint4*>(rowp + 16 * p);
                 m[i] = FMT::meta(rowp, F, p);
 #pragma unroll
@@ -241,8 +247,8 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                if (p0 + i * LPR < cpr) {
+            for (int i = 0; i < NG; ++i) {
+                if (psub + (g0 + i) * LPR < cpr) {
                     uint32_t qp[16], wh[16], wl[16];
                     FMT::decode(wv[i], qp);
                     words16(vh[i], wh);
@@ -262,13 +268,13 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
         }
     }
     if (nored) return;
-    __shared__ float red[4][RPW];
     if (psub == SL) red[wave][rsub] = yacc;
     __syncthreads();
     if (wave == 0 && lane < RPW) {
         const int n2 = blockIdx.x * RPW + lane;
         if (n2 < D) {
-            const float v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+            float v = red[0][lane];
+            for (int w = 1; w < nw; ++w) v += red[w][lane];
             const size_t o = (size_t)t * D + n2;
             store_y(y, o, resid ? v + load_y(resid, o, y32) : v, y32);
         }
@@ -639,16 +645,23 @@ k_t1_fused(T1Args a) {
             store_h(a.hhi, a.hlo, (size_t)j * F, n, hv);
         }
     }
-    __threadfence();
+    // release: every wave's h stores are complete before the barrier; one agent-scope release (an L2
+    // write-back, the XCDs' L2s are not coherent with each other) then publishes the block's h.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
-    if (threadIdx.x == 0) atomicAdd(&a.sync[(blockIdx.x & 15) * T1_SYNC_STRIDE], 1);
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __hip_atomic_fetch_add(&a.sync[(blockIdx.x & 15) * T1_SYNC_STRIDE], 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     // ---------------- wait for every block's phase A (bounded)
     __shared__ int s_ok;
     if (wave == 0) {
         int spins = 0, total = 0;
         while (true) {
-            const int v = lane < 16 ? __hip_atomic_load(&a.sync[lane * T1_SYNC_STRIDE], __ATOMIC_ACQUIRE,
+            // relaxed polls (no cache invalidation per poll); the acquire fence follows the loop
+            const int v = lane < 16 ? __hip_atomic_load(&a.sync[lane * T1_SYNC_STRIDE], __ATOMIC_RELAXED,
                                                         __HIP_MEMORY_SCOPE_AGENT)
                                     : 0;
             total = __builtin_amdgcn_readfirstlane((int)sum_lanes<16>((float)v));
@@ -660,8 +673,9 @@ k_t1_fused(T1Args a) {
             if (!s_ok) __hip_atomic_store(&a.sync[17 * T1_SYNC_STRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (s_ok) {
         // ---------------- stage h of all k slots in LDS: per chunk 8 x 16 B (hi, lo) + its sum
         uint4* s_h = s_dyn;                                          // [k*cpr][8]
@@ -784,23 +798,28 @@ void launch_gu_slots(const ExpertsArgs& a, int NR) {
 #undef MOE_GUS
 }
 
+// lanes per down row and chunks per lane for the per-slot down kernel: LPR a power of two in [4, 64] with
+// LPR * NC >= F/32, NC <= 4 (F up to 8192); longer rows use LPR = 64 and several passes (NC = 8).
 template <class FMT>
 void launch_dn_slots(const ExpertsArgs& a) {
     const moe_experts_t* w = a.w;
     const ProjPtrs P = ptrs(w);
-    const int lpr = pick_lpr(w->F >> 5);
+    const int cpr = w->F >> 5;
+    int lpr = 4;
+    while (lpr < 64 && lpr * 3 < cpr) lpr *= 2;
+    const int nc = (cpr + lpr - 1) / lpr;
     const int rpw = 64 / lpr;
+    const int nw = a.k < 8 ? a.k : 8;
     dim3 grid((w->d + rpw - 1) / rpw, a.T);
-#define MOE_DNS(L)                                                                                                \
-    k_down_slots<FMT, L><<<grid, 256, 0, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.idx, a.wts, a.k, w->d, w->F, \
-                                                  w->E, a.nored, a.y32, a.residual, a.y)
-    switch (lpr) {
-        case 4: MOE_DNS(4); break;
-        case 8: MOE_DNS(8); break;
-        case 16: MOE_DNS(16); break;
-        case 32: MOE_DNS(32); break;
-        default: MOE_DNS(64); break;
-    }
+#define MOE_DNS(L, C)                                                                                           \
+    k_down_slots<FMT, L, C><<<grid, 64 * nw, 0, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.idx, a.wts, a.k,      \
+                                                         w->d, w->F, w->E, a.nored, a.y32, a.residual, a.y)
+    if (lpr == 4) MOE_DNS(4, 3);
+    else if (lpr == 8) MOE_DNS(8, 3);
+    else if (lpr == 16) MOE_DNS(16, 3);
+    else if (lpr == 32) MOE_DNS(32, 3);
+    else if (nc <= 4) MOE_DNS(64, 4);
+    else MOE_DNS(64, 8);   // F <= 16384 (checked by the API)
 #undef MOE_DNS
 }
 

@@ -111,7 +111,7 @@ def test_all_tokens_one_expert_set(policy, T):
     check(shape_("o", 256, 256, 16, 4), T, idx=np.tile([[3, 7, 0, 15]], (T, 1)))
 
 
-@pytest.mark.parametrize("lo,hi", [(120, 140), (129, 160), (200, 254), (1, 20)])
+@pytest.mark.parametrize("lo,hi", [(120, 140), (129, 160), (150, 180), (1, 20)])
 @pytest.mark.parametrize("T", [1, 9])
 def test_e8m0_scale_regimes(lo, hi, T):
     """E8M0 bytes >= 129 overflowed a half-precision scale in the reference (test_mxfp4_large_scales.py:22-34);
@@ -120,8 +120,7 @@ def test_e8m0_scale_regimes(lo, hi, T):
     s = packed_state(sh, 3, scale_bytes=(lo, hi))
     x, idx, wts = inputs(sh, T, seed=3)
     ref = oracle_y(s, x, idx, wts)
-    if not np.isfinite(ref).all():
-        pytest.skip("reference overflows fp64 range at these scales")
+    assert np.isfinite(ref).all() and np.abs(ref).max() < 1e30, "case must stay inside the fp32 range"
     y32 = mx().run(s, x, idx, wts, out_dtype=torch.float32)
     assert_close(y32, ref, what=(lo, hi))
 
