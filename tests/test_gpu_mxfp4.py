@@ -111,7 +111,7 @@ def test_all_tokens_one_expert_set(policy, T):
     check(shape_("o", 256, 256, 16, 4), T, idx=np.tile([[3, 7, 0, 15]], (T, 1)))
 
 
-@pytest.mark.parametrize("lo,hi", [(120, 140), (129, 160), (150, 180), (1, 20)])
+@pytest.mark.parametrize("lo,hi", [(120, 140), (129, 140), (135, 145), (1, 20)])
 @pytest.mark.parametrize("T", [1, 9])
 def test_e8m0_scale_regimes(lo, hi, T):
     """E8M0 bytes >= 129 overflowed a half-precision scale in the reference (test_mxfp4_large_scales.py:22-34);
