@@ -105,6 +105,64 @@ __device__ __forceinline__ float sum_lanes(float v) {
 template <int G>
 __host__ __device__ constexpr int sum_lane() { return G <= 16 ? 0 : (G == 32 ? 16 : 48); }
 
+// Wave-wide max (fp32) / min (u32) with the same DPP pattern; every lane gets the result (read from lane 63).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_max(float v) {
+    const float o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY),
+                                                                         __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                         0xF, false));
+    return fmaxf(v, o);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_min(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)0xFFFFFFFFu, (int)v, CTRL, ROW_MASK, 0xF, false);
+    return o < v ? o : v;
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = dpp_max<0xB1>(v);
+    v = dpp_max<0x4E>(v);
+    v = dpp_max<0x141>(v);
+    v = dpp_max<0x140>(v);
+    v = dpp_max<0x142, 0xA>(v);
+    v = dpp_max<0x143, 0xC>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ uint32_t wave_min_dpp(uint32_t v) {
+    v = dpp_min<0xB1>(v);
+    v = dpp_min<0x4E>(v);
+    v = dpp_min<0x141>(v);
+    v = dpp_min<0x140>(v);
+    v = dpp_min<0x142, 0xA>(v);
+    v = dpp_min<0x143, 0xC>(v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = sum_lanes<64>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Cross-workgroup data on MI355X: the XCDs' L2 caches are not coherent with each other, and agent-scope
+// release/acquire fences write back / invalidate a whole L2. Data handed between workgroups of one launch
+// therefore goes through agent-scope atomic stores and loads (coherent at device level on their own), and a
+// producer waits for its stores (s_waitcnt vmcnt(0): gfx9 counts stores in vmcnt) before it counts itself
+// done with an agent-scope atomic add.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int load_agent(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_agent(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+
 // ------------------------------------------------------------------------------------ wave reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

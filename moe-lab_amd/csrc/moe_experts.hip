@@ -525,9 +525,12 @@ k_combine(const float* __restrict__ yp, const void* __restrict__ resid, void* __
 
 // ============================================================================ fused T == 1
 // One launch for a decode token: phase A computes gate/up/GLU for all k slots (row pairs spread over
-// every wave of the grid, NRA per wave), stores h, and counts the block done in one of 16 counters;
-// phase B waits until all blocks are counted, stages h (both planes, with chunk sums) in LDS, and
-// computes RPB = 64/LPRB down rows per block for all k slots (4 waves split the slots), reduced into y.
+// every wave of the grid, NRA per wave), stores h as one 32-bit word per element (bf16 hi | bf16 lo << 16)
+// with agent-scope atomic stores, and counts the block done in one of 16 counters; phase B waits until all
+// blocks are counted, stages h slot by slot (agent-scope loads, then the pre-paired planes and chunk sums)
+// in LDS, and computes RPB = 64/LPRB down rows per block for all k slots (4 waves split the slots).
+// The XCDs' L2s are not coherent with each other; the agent-scope atomics make the hand-off coherent
+// without writing back or invalidating any L2 (see store_agent in moe_common.h).
 // The down weights of a block's first row block are loaded before the wait. The grid never exceeds the
 // number of co-resident blocks (host side), every wait is bounded by spin_limit (a timeout sets err and
 // skips the block's down rows), and the last block to finish resets the counters to zero.
@@ -543,7 +546,7 @@ struct T1Args {
     int y32;
     void* y;
     const void* resid;
-    uint16_t *hhi, *hlo;
+    uint32_t* h32;   // [k, F] h words (bf16 hi | bf16 lo << 16), handed between blocks
     int32_t* sync;   // [0..15]*32: phase-A counters, 16*32: blocks finished, 17*32: timeout flag
     int spin_limit;
 };
@@ -642,28 +645,24 @@ k_t1_fused(T1Args a) {
                 if (a.bu) u += a.bu[(size_t)e * F + n];
                 hv = glu<ACT>(g, u);
             }
-            store_h(a.hhi, a.hlo, (size_t)j * F, n, hv);
+            const uint16_t hi = f32_to_bf16(hv);
+            const uint16_t lo = f32_to_bf16(hv - bf16_to_f32(hi));
+            store_agent(a.h32 + (size_t)j * F + n, (uint32_t)hi | ((uint32_t)lo << 16));
         }
     }
-    // release: every wave's h stores are complete before the barrier; one agent-scope release (an L2
-    // write-back, the XCDs' L2s are not coherent with each other) then publishes the block's h.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    // publish: this wave's h stores are complete (vmcnt(0)) before the block counts itself done
+    wait_stores();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (threadIdx.x == 0)
         __hip_atomic_fetch_add(&a.sync[(blockIdx.x & 15) * T1_SYNC_STRIDE], 1, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-    }
 
     // ---------------- wait for every block's phase A (bounded)
     __shared__ int s_ok;
     if (wave == 0) {
         int spins = 0, total = 0;
         while (true) {
-            // relaxed polls (no cache invalidation per poll); the acquire fence follows the loop
-            const int v = lane < 16 ? __hip_atomic_load(&a.sync[lane * T1_SYNC_STRIDE], __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT)
-                                    : 0;
+            const int v = lane < 16 ? load_agent(&a.sync[lane * T1_SYNC_STRIDE]) : 0;
             total = __builtin_amdgcn_readfirstlane((int)sum_lanes<16>((float)v));
             if (total >= (int)gridDim.x || ++spins > a.spin_limit) break;
             __builtin_amdgcn_s_sleep(2);
@@ -673,36 +672,37 @@ k_t1_fused(T1Args a) {
             if (!s_ok) __hip_atomic_store(&a.sync[17 * T1_SYNC_STRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (s_ok) {
-        // ---------------- stage h of all k slots in LDS: per chunk 8 x 16 B (hi, lo) + its sum
-        uint4* s_h = s_dyn;                                          // [k*cpr][8]
-        float* s_sum = reinterpret_cast<float*>(s_dyn + (size_t)8 * k * cpr);   // [k*cpr]
-        float* s_red = s_sum + k * cpr;                               // [4][RPB]
-        for (int t = threadIdx.x; t < k * cpr; t += 256) {
-            const int j = t / cpr, p = t - j * cpr;
-            const size_t o = (size_t)j * F + 32 * p;
-            const uint4* hh = reinterpret_cast<const uint4*>(a.hhi + o);
-            const uint4* hl = reinterpret_cast<const uint4*>(a.hlo + o);
-            uint4 v[8];
+        // ---------------- stage h in LDS, slot by slot: raw words (coalesced agent-scope loads), then per
+        // chunk 8 x 16 B of pre-paired (hi, lo) planes + the chunk's sum
+        uint4* s_h = s_dyn;                                                       // [k*cpr][8]
+        float* s_sum = reinterpret_cast<float*>(s_dyn + (size_t)8 * k * cpr);    // [k*cpr]
+        float* s_red = s_sum + k * cpr;                                           // [4][RPB]
+        uint32_t* s_raw = reinterpret_cast<uint32_t*>(s_red + 4 * RPB);           // [F]
+        for (int j = 0; j < k; ++j) {
+            for (int i = threadIdx.x; i < F; i += 256) s_raw[i] = load_agent(a.h32 + (size_t)j * F + i);
+            __syncthreads();
+            for (int p = threadIdx.x; p < cpr; p += 256) {
+                const uint32_t* rw = s_raw + 32 * p;
+                uint32_t wh[16], wl[16];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                v[q] = hh[q];
-                v[4 + q] = hl[q];
-            }
-            float s = 0.f;
-            if (FMT::XSUM) {
-                uint32_t w[16];
-                words16(v, w);
-                s = sum16(w, 0.f);
-                words16(v + 4, w);
-                s = sum16(w, s);
-            }
+                for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-            for (int q = 0; q < 8; ++q) s_h[(size_t)t * 8 + q] = v[q];
-            s_sum[t] = s;
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t w0 = rw[8 * jj + i], w4 = rw[8 * jj + i + 4];
+                        wh[4 * jj + i] = __builtin_amdgcn_perm(w4, w0, 0x05040100u);   // (hi_n, hi_n+4)
+                        wl[4 * jj + i] = __builtin_amdgcn_perm(w4, w0, 0x07060302u);   // (lo_n, lo_n+4)
+                    }
+                const size_t c = (size_t)j * cpr + p;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    s_h[c * 8 + q] = make_uint4(wh[4 * q], wh[4 * q + 1], wh[4 * q + 2], wh[4 * q + 3]);
+                    s_h[c * 8 + 4 + q] = make_uint4(wl[4 * q], wl[4 * q + 1], wl[4 * q + 2], wl[4 * q + 3]);
+                }
+                s_sum[c] = FMT::XSUM ? sum16(wl, sum16(wh, 0.f)) : 0.f;
+            }
+            __syncthreads();
         }
         __syncthreads();
         // ---------------- phase B: down rows for all slots
@@ -901,7 +901,7 @@ constexpr int T1_SPW = 4;    // max slots per wave in phase B (k <= 16)
 constexpr int T1_NCB = 4;    // max chunks per lane per down row
 constexpr int T1_LDS_MAX = 64 * 1024;
 
-int t1_lds_bytes(int k, int F, int rpb) { return k * (F >> 5) * (128 + 4) + 4 * rpb * 4; }
+int t1_lds_bytes(int k, int F, int rpb) { return k * (F >> 5) * (128 + 4) + 4 * rpb * 4 + F * 4; }
 
 template <class FMT, int ACT, int LPRB>
 int launch_t1(const ExpertsArgs& a, int32_t* sync) {
@@ -947,8 +947,7 @@ int launch_t1(const ExpertsArgs& a, int32_t* sync) {
     t.y32 = a.y32;
     t.y = a.y;
     t.resid = a.residual;
-    t.hhi = a.hhi;
-    t.hlo = a.hlo;
+    t.h32 = reinterpret_cast<uint32_t*>(a.hhi);   // the two h planes' space holds k*F words
     t.sync = sync;
     t.spin_limit = 1 << 22;
     kern<<<grid, 256, lds, a.st>>>(t);

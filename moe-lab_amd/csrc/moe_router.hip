@@ -21,11 +21,6 @@ constexpr int ROUTER_WAVES = 4;   // waves per block = experts per block
 constexpr int ROUTER_TPW = 4;     // tokens per wave (the Wr row chunk is reused across them)
 constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024
 
-template <bool ATOMIC_LOAD>
-__device__ __forceinline__ float load_logit(const float* p) {
-    if (ATOMIC_LOAD) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return *p;
-}
 
 template <typename LT>
 __device__ __forceinline__ float to_f32(LT v);
@@ -51,12 +46,12 @@ __device__ void wave_topk(F lg, int E, int k, int norm, float scale, int32_t* id
     float m0 = -INFINITY;
 #pragma unroll
     for (int j = 0; j < TOPK_MAX_J; ++j) m0 = fmaxf(m0, v[j]);
-    m0 = wave_max(m0);
+    m0 = wave_max_dpp(m0);
     float den = 0.f;
     if (!norm) {
 #pragma unroll
         for (int j = 0; j < TOPK_MAX_J; ++j) den += (v[j] == -INFINITY) ? 0.f : expf(v[j] - m0);
-        den = wave_sum(den);
+        den = wave_sum_dpp(den);
     }
     float myv = -INFINITY;   // lane r < k holds round r's value and id
     uint32_t myi = 0;
@@ -67,8 +62,8 @@ __device__ void wave_topk(F lg, int E, int k, int norm, float scale, int32_t* id
 #pragma unroll
         for (int j = 0; j < TOPK_MAX_J; ++j)
             if (v[j] > b) { b = v[j]; bi = (uint32_t)(j * 64 + lane); }
-        float m = wave_max(b);
-        uint32_t sel = wave_min_u32(b == m ? bi : 0xFFFFFFFFu);
+        float m = wave_max_dpp(b);
+        uint32_t sel = wave_min_dpp(b == m ? bi : 0xFFFFFFFFu);
         if (sel == 0xFFFFFFFFu) {   // no finite candidate left: lowest id not chosen yet, weight 0
             sel = 0;
             while (__ballot(lane < r && myi == sel) != 0ull) ++sel;
@@ -82,7 +77,7 @@ __device__ void wave_topk(F lg, int E, int k, int norm, float scale, int32_t* id
         if (lane == r) { myv = m; myi = sel; }
     }
     float s;
-    if (norm) s = wave_sum(lane < k ? expf(myv - top0) : 0.f);
+    if (norm) s = wave_sum_dpp(lane < k ? expf(myv - top0) : 0.f);
     else s = den;
     const float off = norm ? top0 : m0;
     if (lane < k) {
@@ -92,7 +87,10 @@ __device__ void wave_topk(F lg, int E, int k, int norm, float scale, int32_t* id
 }
 
 // grid (ceil(E / ROUTER_WAVES), ceil(T / ROUTER_TPW)), block 64 * ROUTER_WAVES.
-// counters[ty] must be 0 on entry; the last block of token group ty resets it to 0.
+// counters[ty] must be 0 on entry; the last block of token group ty resets it to 0. Logits pass between
+// blocks through agent-scope atomic stores / loads (no L2 write-back or invalidation).
+constexpr int ROUTER_MAXC = 4;   // 16-byte chunks per lane held in registers per pass (2048 inputs)
+
 __global__ void __launch_bounds__(64 * ROUTER_WAVES)
 router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, const float* __restrict__ bias,
                    int T, int d, int E, int k, int norm, float scale, float* __restrict__ logits,
@@ -107,21 +105,33 @@ router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ 
 #pragma unroll
         for (int i = 0; i < ROUTER_TPW; ++i) acc[i] = 0.f;
         const uint4* wrow = reinterpret_cast<const uint4*>(wr + (size_t)e * d);
-        for (int c = lane; c < nchunk; c += 64) {
-            const uint4 w = wrow[c];
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        for (int c0 = 0; c0 < nchunk; c0 += 64 * ROUTER_MAXC) {
+            // all loads of this pass first (chunks c0 + lane + 64m), then the fma chains in chunk order
+            uint4 w[ROUTER_MAXC], xv[ROUTER_TPW][ROUTER_MAXC];
 #pragma unroll
-            for (int i = 0; i < ROUTER_TPW; ++i) {
-                if (i < nt) {
-                    const uint4 xv = reinterpret_cast<const uint4*>(x + (size_t)(t0 + i) * d)[c];
-                    const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
-                    float a = acc[i];
+            for (int m = 0; m < ROUTER_MAXC; ++m) {
+                const int c = min(c0 + lane + 64 * m, nchunk - 1);
+                w[m] = wrow[c];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        a = __builtin_fmaf(bf16lo(xx[q]), bf16lo(ww[q]), a);
-                        a = __builtin_fmaf(bf16hi(xx[q]), bf16hi(ww[q]), a);
+                for (int i = 0; i < ROUTER_TPW; ++i)
+                    xv[i][m] = reinterpret_cast<const uint4*>(x + (size_t)(t0 + min(i, nt - 1)) * d)[c];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int m = 0; m < ROUTER_MAXC; ++m) {
+                if (c0 + lane + 64 * m < nchunk) {
+                    const uint32_t ww[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
+#pragma unroll
+                    for (int i = 0; i < ROUTER_TPW; ++i) {
+                        const uint32_t xx[4] = {xv[i][m].x, xv[i][m].y, xv[i][m].z, xv[i][m].w};
+                        float a = acc[i];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            a = __builtin_fmaf(bf16lo(xx[q]), bf16lo(ww[q]), a);
+                            a = __builtin_fmaf(bf16hi(xx[q]), bf16hi(ww[q]), a);
+                        }
+                        acc[i] = a;
                     }
-                    acc[i] = a;
                 }
             }
         }
@@ -131,24 +141,23 @@ router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ 
 #pragma unroll
             for (int s = 32; s >= 1; s >>= 1) a = a + __shfl_xor(a, s, 64);
             if (bias) a = a + bias[e];
-            if (lane == 0 && i < nt) logits[(size_t)(t0 + i) * E + e] = a;
+            if (lane == 0 && i < nt) store_agent(&logits[(size_t)(t0 + i) * E + e], a);
         }
     }
-    // last block of this token group runs the tail
+    // the last block of this token group runs the tail
     __shared__ int s_last;
-    __threadfence();
+    wait_stores();
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int old = atomicAdd(&counters[blockIdx.y], 1);
+        const int old = __hip_atomic_fetch_add(&counters[blockIdx.y], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (old == (int)gridDim.x - 1);
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     if (wave < nt) {
         const int t = t0 + wave;
         const float* lrow = logits + (size_t)t * E;
-        wave_topk([&](int ee) { return load_logit<true>(lrow + ee); }, E, k, norm, scale, idx + (size_t)t * k,
+        wave_topk([&](int ee) { return load_agent(lrow + ee); }, E, k, norm, scale, idx + (size_t)t * k,
                   wts + (size_t)t * k);
     }
     if (threadIdx.x == 0) counters[blockIdx.y] = 0;
