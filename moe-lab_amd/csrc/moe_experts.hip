@@ -674,35 +674,52 @@ k_t1_fused(T1Args a) {
     }
     __syncthreads();
     if (s_ok) {
-        // ---------------- stage h in LDS, slot by slot: raw words (coalesced agent-scope loads), then per
-        // chunk 8 x 16 B of pre-paired (hi, lo) planes + the chunk's sum
-        uint4* s_h = s_dyn;                                                       // [k*cpr][8]
+        // ---------------- stage h in LDS: all k*F words with coalesced agent-scope loads (32 in flight per
+        // thread), then each chunk is rewritten in place as 8 x 16 B of pre-paired (hi, lo) planes + its sum
+        uint4* s_h = s_dyn;                                                       // [k*cpr][8] (= raw words)
         float* s_sum = reinterpret_cast<float*>(s_dyn + (size_t)8 * k * cpr);    // [k*cpr]
         float* s_red = s_sum + k * cpr;                                           // [4][RPB]
-        uint32_t* s_raw = reinterpret_cast<uint32_t*>(s_red + 4 * RPB);           // [F]
-        for (int j = 0; j < k; ++j) {
-            for (int i = threadIdx.x; i < F; i += 256) s_raw[i] = load_agent(a.h32 + (size_t)j * F + i);
-            __syncthreads();
-            for (int p = threadIdx.x; p < cpr; p += 256) {
-                const uint32_t* rw = s_raw + 32 * p;
-                uint32_t wh[16], wl[16];
+        uint32_t* s_raw = reinterpret_cast<uint32_t*>(s_dyn);
+        const int kf = k * F;
+        for (int base = 0; base < kf; base += 256 * 32) {
+            uint32_t v[32];
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t w0 = rw[8 * jj + i], w4 = rw[8 * jj + i + 4];
-                        wh[4 * jj + i] = __builtin_amdgcn_perm(w4, w0, 0x05040100u);   // (hi_n, hi_n+4)
-                        wl[4 * jj + i] = __builtin_amdgcn_perm(w4, w0, 0x07060302u);   // (lo_n, lo_n+4)
-                    }
-                const size_t c = (size_t)j * cpr + p;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    s_h[c * 8 + q] = make_uint4(wh[4 * q], wh[4 * q + 1], wh[4 * q + 2], wh[4 * q + 3]);
-                    s_h[c * 8 + 4 + q] = make_uint4(wl[4 * q], wl[4 * q + 1], wl[4 * q + 2], wl[4 * q + 3]);
-                }
-                s_sum[c] = FMT::XSUM ? sum16(wl, sum16(wh, 0.f)) : 0.f;
+            for (int i = 0; i < 32; ++i) {
+                const int o = base + i * 256 + threadIdx.x;
+                if (o < kf) v[i] = load_agent(a.h32 + o);
             }
-            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int o = base + i * 256 + threadIdx.x;
+                if (o < kf) s_raw[o] = v[i];
+            }
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < k * cpr; c += 256) {
+            uint32_t rw[32];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint4 t4 = s_h[(size_t)c * 8 + q];
+                rw[4 * q] = t4.x;
+                rw[4 * q + 1] = t4.y;
+                rw[4 * q + 2] = t4.z;
+                rw[4 * q + 3] = t4.w;
+            }
+            uint32_t wh[16], wl[16];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t w0 = rw[8 * jj + i], w4 = rw[8 * jj + i + 4];
+                    wh[4 * jj + i] = __builtin_amdgcn_perm(w4, w0, 0x05040100u);   // (hi_n, hi_n+4)
+                    wl[4 * jj + i] = __builtin_amdgcn_perm(w4, w0, 0x07060302u);   // (lo_n, lo_n+4)
+                }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                s_h[(size_t)c * 8 + q] = make_uint4(wh[4 * q], wh[4 * q + 1], wh[4 * q + 2], wh[4 * q + 3]);
+                s_h[(size_t)c * 8 + 4 + q] = make_uint4(wl[4 * q], wl[4 * q + 1], wl[4 * q + 2], wl[4 * q + 3]);
+            }
+            s_sum[c] = FMT::XSUM ? sum16(wl, sum16(wh, 0.f)) : 0.f;
         }
         __syncthreads();
         // ---------------- phase B: down rows for all slots
@@ -901,7 +918,7 @@ constexpr int T1_SPW = 4;    // max slots per wave in phase B (k <= 16)
 constexpr int T1_NCB = 4;    // max chunks per lane per down row
 constexpr int T1_LDS_MAX = 64 * 1024;
 
-int t1_lds_bytes(int k, int F, int rpb) { return k * (F >> 5) * (128 + 4) + 4 * rpb * 4 + F * 4; }
+int t1_lds_bytes(int k, int F, int rpb) { return k * (F >> 5) * (128 + 4) + 4 * rpb * 4; }
 
 template <class FMT, int ACT, int LPRB>
 int launch_t1(const ExpertsArgs& a, int32_t* sync) {
