@@ -60,10 +60,13 @@ extern "C" {
 #define MOE_ACT_GPTOSS 2      /* g = min(g,7), u = clip(u,-7,7), g * sigmoid(1.702 g) * (u + 1) */
 
 /* expert-path selection for moe_experts_run */
-#define MOE_PATH_AUTO 0       /* T == 1 -> one fused launch when it fits (else per-slot GEMV); T > 1 -> grouped */
+#define MOE_PATH_AUTO 0       /* T == 1 -> per-slot GEMV (two launches); T > 1 -> grouped expert tiles */
 #define MOE_PATH_SLOTS 1      /* per-slot GEMV over all T*k slots, no grouping, two launches (the stock-style
                                  gather of the reference's pre-tile kernels) */
 #define MOE_PATH_GROUPED 2    /* grouped expert tiles: each selected expert's weights read once */
+#define MOE_PATH_FUSED_T1 3   /* T == 1 in one launch (gate/up, device-wide hand-off of h, down); falls back to
+                                 MOE_PATH_SLOTS for shapes it does not take. Measured slower than two launches
+                                 on MI355X at the Qwen3 shape: the cross-XCD hand-off costs more than a launch */
 
 /* One projection of all E experts: N output rows of K inputs. */
 typedef struct {

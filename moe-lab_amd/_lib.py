@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(HERE, "libmoe_mi355x.so")
 MOE_OK, MOE_ERR_ARG, MOE_ERR_DTYPE, MOE_ERR_WORKSPACE, MOE_ERR_LAUNCH, MOE_ERR_ALIGN = 0, -1, -2, -3, -4, -5
 DTYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 FMT_INT4_G64, FMT_MXFP4 = 0, 1
-PATH_AUTO, PATH_SLOTS, PATH_GROUPED = 0, 1, 2
+PATH_AUTO, PATH_SLOTS, PATH_GROUPED, PATH_FUSED_T1 = 0, 1, 2, 3
 ACT_SWIGLU, ACT_GEGLU, ACT_GPTOSS = 0, 1, 2
 
 EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",

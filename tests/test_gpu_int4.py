@@ -229,8 +229,8 @@ def test_qwen3_full_shape(T):
 @pytest.mark.parametrize("shape_args", [(2048, 768, 128, 8), (512, 256, 8, 1), (2048, 1408, 64, 6),
                                         (1024, 512, 16, 16), (256, 128, 4, 4)])
 def test_fused_t1_equals_two_launch_path(T, shape_args):
-    """The single-launch T=1 kernel (PATH_AUTO) and the two per-slot launches agree with the oracle, and the
-    fused kernel leaves its completion counters at zero with no timeout."""
+    """The single-launch T=1 kernel (PATH_FUSED_T1) and the two per-slot launches agree with the oracle, and
+    the fused kernel leaves its completion counters at zero with no timeout."""
     from moelab_amd import _lib
     from moelab_amd.experts import run_experts
     sh = shape_("f", *shape_args)
@@ -238,7 +238,7 @@ def test_fused_t1_equals_two_launch_path(T, shape_args):
     x, idx, wts = inputs(sh, T, seed=9)
     ref = oracle_y(s, x, idx, wts)
     for _ in range(3):
-        for path in (_lib.PATH_AUTO, _lib.PATH_SLOTS):
+        for path in (_lib.PATH_FUSED_T1, _lib.PATH_SLOTS, _lib.PATH_AUTO):
             assert_close(run_experts(s, x, idx, wts, path=path, out_dtype=torch.float32), ref, what=path)
     torch.cuda.synchronize()
     sync = _lib.workspace(x.device, 0)[:_lib.WORKSPACE_SYNC_BYTES].view(torch.int32).cpu()
