@@ -38,12 +38,18 @@ struct FmtInt4 {
     __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) {
         return *reinterpret_cast<const uint32_t*>(row + (K >> 1) + 4 * (c >> 1));
     }
+    // 7 VALU ops per word: t holds nibbles 0, 2, 4, 6 and u nibbles 1, 3, 5, 7 in the low halves of its
+    // bytes; each v_perm_b32 picks two of those bytes and puts the bf16 exponent byte 0x43 above each.
     __device__ static __forceinline__ void decode(uint4 w, uint32_t qp[16]) {
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) qp[4 * j + i] = ((ws[j] >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t t = ws[j] & 0x0F0F0F0Fu, u = (ws[j] >> 4) & 0x0F0F0F0Fu;
+            qp[4 * j + 0] = __builtin_amdgcn_perm(0x43434343u, t, 0x04020400u);   // (q0, q4)
+            qp[4 * j + 1] = __builtin_amdgcn_perm(0x43434343u, u, 0x04020400u);   // (q1, q5)
+            qp[4 * j + 2] = __builtin_amdgcn_perm(0x43434343u, t, 0x04030401u);   // (q2, q6)
+            qp[4 * j + 3] = __builtin_amdgcn_perm(0x43434343u, u, 0x04030401u);   // (q3, q7)
+        }
     }
     __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float xsum) {
         const float s = bf16lo(m), b = bf16hi(m);
@@ -119,6 +125,239 @@ __device__ __forceinline__ float load_y(const void* y, size_t i, int y32) {
 __device__ __forceinline__ size_t rbytes(int fmt, int K) {
     const size_t meta = fmt == MOE_FMT_INT4_G64 ? (size_t)K / 16 : (size_t)K / 32;
     return ((size_t)K / 2 + meta + 15) & ~(size_t)15;
+}
+
+__device__ __forceinline__ float glu_rt(int act, float g, float u) {
+    return act == 0 ? glu<0>(g, u) : (act == 1 ? glu<1>(g, u) : glu<2>(g, u));
+}
+
+// ============================================================================ per-slot gate / up, balanced
+// Work item q = slot * F + f: gate row f and up row f of expert idx[slot]. Wave gw = 4 * blockIdx.x + wave
+// takes items gw*R .. gw*R + R - 1; R divides F, so they are R consecutive row pairs of one slot, and every
+// wave (and every block) carries the same bytes. Lane l covers the 16-byte chunks l, l + 64, ... of a row,
+// NCH of them per pass. Order of memory operations: the expert id (scalar load), the x chunks of the first
+// pass (L2), then every weight chunk and metadata word of the pass, all before the first use; the math then
+// runs in load order, so it overlaps with the loads still arriving. h is written as the two pre-paired bf16
+// planes hi/lo (store_h).
+template <class FMT, int R, int NCH>
+__global__ void __launch_bounds__(256)
+k_gate_up_rows(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
+               const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
+               int d, int F, int E, int Q, int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
+    static_assert(R <= 16, "results live in lanes 48..63");
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int q0 = (blockIdx.x * 4 + wave) * R;
+    if (q0 >= Q) return;
+    const int s = q0 / F, f0 = q0 - s * F;
+    const int e = idx[s];   // wave-uniform: a scalar load
+    const size_t rb = rbytes(FMT::FMT, d);
+    const int nchunk = d >> 5;
+    const uint16_t* xr = x + (size_t)(s / k) * d;
+    float ag[R], au[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) ag[r] = au[r] = 0.f;
+    const bool valid = (unsigned)e < (unsigned)E;
+    const int ee = valid ? e : 0;
+    const uint8_t* gb0 = G + ((size_t)ee * F + f0) * rb;
+    const uint8_t* ub0 = U + ((size_t)ee * F + f0) * rb;
+    // the lane that writes row f0 + (lane - 48) fetches its additive biases now (gpt-oss), not after the sums
+    const int rl = lane - 48;
+    float bgl = 0.f, bul = 0.f;
+    if (valid && rl >= 0 && rl < R) {
+        if (bg) bgl = bg[(size_t)e * F + f0 + rl];
+        if (bu) bul = bu[(size_t)e * F + f0 + rl];
+    }
+    for (int c0 = 0; c0 < nchunk; c0 += 64 * NCH) {
+        int ch[NCH];
+        bool cv[NCH];
+        uint32_t xw[NCH][16];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            ch[c] = c0 + 64 * c + lane;
+            cv[c] = ch[c] < nchunk;
+            ch[c] = cv[c] ? ch[c] : nchunk - 1;
+            load_x32(xr + 32 * ch[c], xw[c]);
+        }
+        uint4 wg[R][NCH], wu[R][NCH];
+        uint32_t mg[R][NCH], mu[R][NCH];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                wg[r][c] = *reinterpret_cast<const uint4*>(gb0 + r * rb + 16 * ch[c]);
+                mg[r][c] = FMT::meta(gb0 + r * rb, d, ch[c]);
+                wu[r][c] = *reinterpret_cast<const uint4*>(ub0 + r * rb + 16 * ch[c]);
+                mu[r][c] = FMT::meta(ub0 + r * rb, d, ch[c]);
+            }
+        __builtin_amdgcn_sched_barrier(0);   // every load of the pass is in flight before any use
+        uint32_t xp[NCH][16];
+        float xs[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            pair_x32(xw[c], xp[c]);
+            xs[c] = FMT::XSUM ? sum_x32(xw[c]) : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                uint32_t qp[16];
+                FMT::decode(wg[r][c], qp);
+                const float dg = FMT::fold(0.f, mg[r][c], dot16(qp, xp[c], 0.f), xs[c]);
+                FMT::decode(wu[r][c], qp);
+                const float du = FMT::fold(0.f, mu[r][c], dot16(qp, xp[c], 0.f), xs[c]);
+                ag[r] += cv[c] ? dg : 0.f;
+                au[r] += cv[c] ? du : 0.f;
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        ag[r] = sum_lanes<64>(ag[r]);
+        au[r] = sum_lanes<64>(au[r]);
+    }
+    if (rl >= 0 && rl < R) {   // lanes 48..63 hold the sums
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int q = 0; q < R; ++q)
+            if (q == rl) { g = ag[q]; u = au[q]; }
+        const float hv = valid ? glu_rt(act, g + bgl, u + bul) : 0.f;
+        store_h(hhi, hlo, (size_t)s * F, f0 + rl, hv);
+    }
+}
+
+// ============================================================================ per-slot down, h staged in LDS
+// grid (ceil(D / RB), T), block 64 * NW (NW waves); every block computes RB = NW * RR rows of y[t] over all
+// k slots of token t. Lane l of a wave: chunk phase p = l % L, slot j = l / L (64 / L >= k slot lanes, L a
+// power of two), so one wave covers every (slot, chunk) pair of its RR rows, and the k-reduction is an
+// in-wave DPP sum. A lane handles chunks p, p + L, ..., p + (NC-1) L of rows n .. n + RR - 1 and reuses
+// each h chunk for the RR rows. The pre-paired h planes of the k slots are copied once per block into LDS,
+// with each chunk's sum (the int4 fold needs it). Order of memory operations: the lane's expert id and
+// routing weight, the first h chunks (L2), every weight chunk and metadata word of the lane (branch-free:
+// chunk indices past the row are clamped into it and masked out of the math), the LDS staging, then the
+// math in load order.
+template <class FMT, int NC, int RR, int NW>
+__global__ void __launch_bounds__(64 * NW)
+k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
+            const float* __restrict__ bd, const int32_t* __restrict__ idx, const float* __restrict__ wts, int k,
+            int D, int F, int E, int lgL, int nored, int y32, const void* __restrict__ resid,
+            void* __restrict__ y) {
+    constexpr int SL = sum_lane<64>();
+    constexpr int RB = NW * RR;
+    extern __shared__ uint4 s_dyn[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int t = blockIdx.y;
+    const int L = 1 << lgL;
+    const int p = lane & (L - 1), j = lane >> lgL;
+    const int cpr = F >> 5;
+    const int nch = k * cpr;   // chunks of h to stage
+    uint4* s_h = s_dyn;                                                 // [nch][8]: hi pairs x4, lo pairs x4
+    float* s_sum = reinterpret_cast<float*>(s_dyn + (size_t)8 * nch);   // [nch]
+    // ---- expert id and routing weight of this lane's slot
+    const bool jv = j < k;
+    const int slot = t * k + (jv ? j : k - 1);
+    const int e = idx[slot];
+    const float wraw = wts[slot];
+    // ---- first staging chunk of this thread (L2)
+    const size_t hbase = (size_t)t * k * F;
+    const int c_st = threadIdx.x;
+    uint4 hv[8];
+    {
+        const int c = min(c_st, nch - 1);
+        const uint4* sh = reinterpret_cast<const uint4*>(hhi + hbase + 32 * (size_t)c);
+        const uint4* sl = reinterpret_cast<const uint4*>(hlo + hbase + 32 * (size_t)c);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            hv[q] = sh[q];
+            hv[4 + q] = sl[q];
+        }
+    }
+    // ---- weights of this lane
+    const bool ev = jv && (unsigned)e < (unsigned)E;
+    const int ee = ev ? e : 0;
+    const size_t rb = rbytes(FMT::FMT, F);
+    const int n0 = blockIdx.x * RB + wave * RR;
+    const uint8_t* rows[RR];
+#pragma unroll
+    for (int i = 0; i < RR; ++i) rows[i] = Dw + ((size_t)ee * D + min(n0 + i, D - 1)) * rb;
+    float bdv[RR];
+#pragma unroll
+    for (int i = 0; i < RR; ++i) bdv[i] = (bd && ev && p == 0) ? bd[(size_t)e * D + min(n0 + i, D - 1)] : 0.f;
+    uint4 wv[NC][RR];
+    uint32_t mv[NC][RR];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int chk = min(p + c * L, cpr - 1);
+#pragma unroll
+        for (int i = 0; i < RR; ++i) {
+            wv[c][i] = *reinterpret_cast<const uint4*>(rows[i] + 16 * chk);
+            mv[c][i] = FMT::meta(rows[i], F, chk);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- stage h: this thread's first chunk, then any further chunks (only when k * cpr > 64 * NW)
+    for (int c = c_st; c < nch; c += 64 * NW) {
+        if (c != c_st) {
+            const uint4* sh = reinterpret_cast<const uint4*>(hhi + hbase + 32 * (size_t)c);
+            const uint4* sl = reinterpret_cast<const uint4*>(hlo + hbase + 32 * (size_t)c);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                hv[q] = sh[q];
+                hv[4 + q] = sl[q];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s_h[(size_t)c * 8 + q] = hv[q];
+        if (FMT::XSUM) {
+            uint32_t w[16];
+            words16(hv, w);
+            const float sm = sum16(w, 0.f);
+            words16(hv + 4, w);
+            s_sum[c] = sum16(w, sm);
+        }
+    }
+    __syncthreads();
+    // ---- math
+    float acc[RR];
+#pragma unroll
+    for (int i = 0; i < RR; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int chk = p + c * L;
+        const bool cv = ev && chk < cpr;
+        const size_t hc = (size_t)(jv ? j : 0) * cpr + min(chk, cpr - 1);
+        uint32_t wh[16], wl[16];
+        words16(&s_h[hc * 8], wh);
+        words16(&s_h[hc * 8 + 4], wl);
+        const float hs = FMT::XSUM ? s_sum[hc] : 0.f;
+#pragma unroll
+        for (int i = 0; i < RR; ++i) {
+            uint32_t qp[16];
+            FMT::decode(wv[c][i], qp);
+            const float v = FMT::fold(0.f, mv[c][i], dot16(qp, wl, dot16(qp, wh, 0.f)), hs);
+            acc[i] += cv ? v : 0.f;
+        }
+    }
+    if (nored) {
+#pragma unroll
+        for (int i = 0; i < RR; ++i) {
+            const int n = n0 + i;
+            float v = acc[i] + bdv[i];
+            // sum over the L lanes of the slot: xor butterfly within the group
+            for (int s2 = 1; s2 < L; s2 <<= 1) v += __shfl_xor(v, s2, 64);
+            if (p == 0 && jv && n < D) store_y(y, (size_t)slot * D + n, v, y32);
+        }
+        return;
+    }
+    const float wj = ev ? wraw : 0.f;
+#pragma unroll
+    for (int i = 0; i < RR; ++i) {
+        const int n = n0 + i;
+        const float v = sum_lanes<64>((acc[i] + bdv[i]) * wj);
+        if (lane == SL && n < D) {
+            const size_t o = (size_t)t * D + n;
+            store_y(y, o, resid ? v + load_y(resid, o, y32) : v, y32);
+        }
+    }
 }
 
 // ============================================================================ per-slot gate / up
@@ -872,9 +1111,132 @@ void launch_dn_grouped(const ExpertsArgs& a, int max_active) {
 #undef MOE_DNG
 }
 
+// ---------------------------------------------------------------- balanced per-slot kernels
+// gate/up: R row pairs per wave (R divides F), as many as keeps >= 2048 waves in flight (2 blocks per CU on
+// 256 CUs); NCH chunks per lane per pass (2 when a row has more than 64 chunks).
+template <class FMT, int NCH>
+int launch_gu_rows_n(const ExpertsArgs& a, int R) {
+    const moe_experts_t* w = a.w;
+    const ProjPtrs P = ptrs(w);
+    const int Q = a.T * a.k * w->F;
+    const int grid = (Q / R + 3) / 4;
+#define MOE_GUR(RR)                                                                                              \
+    k_gate_up_rows<FMT, RR, NCH><<<grid, 256, 0, a.st>>>((const uint16_t*)a.x, P.G, P.U, w->gate.bias, w->up.bias, \
+                                                        a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, a.hlo)
+    switch (R) {
+        case 8: MOE_GUR(8); break;
+        case 6: MOE_GUR(6); break;
+        case 4: MOE_GUR(4); break;
+        case 3: MOE_GUR(3); break;
+        case 2: MOE_GUR(2); break;
+        default: MOE_GUR(1); break;
+    }
+#undef MOE_GUR
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+#ifndef MOE_GU_MIN_WAVES
+#define MOE_GU_MIN_WAVES 2048   // gate/up: fewest waves a launch should have before rows per wave grow
+#endif
+#ifndef MOE_GU_RMAX
+#define MOE_GU_RMAX 8
+#endif
+int pick_rows_per_wave(int Q, int F, int rmax) {
+    const int cand[6] = {8, 6, 4, 3, 2, 1};
+    for (int r : cand)
+        if (r <= rmax && r <= MOE_GU_RMAX && F % r == 0 && Q / r >= MOE_GU_MIN_WAVES) return r;
+    return 1;
+}
+
+template <class FMT>
+int launch_gu_rows(const ExpertsArgs& a) {
+    const int Q = a.T * a.k * a.w->F;
+    if ((a.w->d >> 5) <= 64) return launch_gu_rows_n<FMT, 1>(a, pick_rows_per_wave(Q, a.w->F, 8));
+    return launch_gu_rows_n<FMT, 2>(a, pick_rows_per_wave(Q, a.w->F, 4));
+}
+
+// down: L = 64 / KP lanes per row (KP = the power of two >= k), NCM >= cpr / L chunks per lane, RR rows per
+// lane. Returns 1 when the shape does not fit (k > 64, or k * F too large for LDS): the caller falls back.
+constexpr int DR_LDS_MAX = 150 * 1024;
+
+int down_rows_lds(int k, int F) { return k * (F >> 5) * (128 + 4); }
+
+#ifndef MOE_DN_NW
+#define MOE_DN_NW 4   // waves per down block
+#endif
+#ifndef MOE_DN_RR2_NC
+#define MOE_DN_RR2_NC 4   // two rows per lane while NC <= this
+#endif
+template <class FMT, int NC, int RR>
+int launch_dn_rows_k(const ExpertsArgs& a, int lgL) {
+    constexpr int NW = MOE_DN_NW;
+    const moe_experts_t* w = a.w;
+    const ProjPtrs P = ptrs(w);
+    auto kern = k_down_rows<FMT, NC, RR, NW>;
+    const int lds = down_rows_lds(a.k, w->F);
+    if (lds > 64 * 1024) {
+        static bool attr_set = false;   // per instantiation; setting it twice is harmless
+        if (!attr_set) {
+            if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, DR_LDS_MAX) !=
+                hipSuccess)
+                return MOE_ERR_LAUNCH;
+            attr_set = true;
+        }
+    }
+    dim3 grid((w->d + NW * RR - 1) / (NW * RR), a.T);
+    kern<<<grid, 64 * NW, lds, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.idx, a.wts, a.k, w->d, w->F, w->E, lgL,
+                                   a.nored, a.y32, a.residual, a.y);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+// lanes per down row L = 64 / KP (KP = the power of two >= k); chunks per lane NC >= cpr / L, from a fixed
+// menu; two rows per lane while NC <= 4
+int down_rows_plan(int k, int F, int* lgL) {
+    if (k > 32 || k < 1) return 0;
+    int kp = 1;
+    while (kp < k) kp *= 2;
+    const int L = 64 / kp;
+    *lgL = 0;
+    while ((1 << *lgL) < L) ++*lgL;
+    const int need = ((F >> 5) + L - 1) / L;
+    const int menu[8] = {1, 2, 3, 4, 6, 8, 12, 16};
+    for (int nc : menu)
+        if (nc >= need) return down_rows_lds(k, F) <= DR_LDS_MAX ? nc : 0;
+    return 0;
+}
+
+bool down_rows_fits(int k, int F) {
+    int lgL;
+    return down_rows_plan(k, F, &lgL) != 0;
+}
+
+template <class FMT>
+int launch_dn_rows(const ExpertsArgs& a) {
+    int lgL = 0;
+    switch (down_rows_plan(a.k, a.w->F, &lgL)) {
+        case 1: return launch_dn_rows_k<FMT, 1, (1 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
+        case 2: return launch_dn_rows_k<FMT, 2, (2 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
+        case 3: return launch_dn_rows_k<FMT, 3, (3 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
+        case 4: return launch_dn_rows_k<FMT, 4, (4 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
+        case 6: return launch_dn_rows_k<FMT, 6, 1>(a, lgL);
+        case 8: return launch_dn_rows_k<FMT, 8, 1>(a, lgL);
+        case 12: return launch_dn_rows_k<FMT, 12, 1>(a, lgL);
+        case 16: return launch_dn_rows_k<FMT, 16, 1>(a, lgL);
+        default: return MOE_ERR_ARG;
+    }
+}
+
 template <class FMT>
 int run_slots_fmt(const ExpertsArgs& a) {
     const int nslots = a.T * a.k;
+    if (down_rows_fits(a.k, a.w->F)) {
+        if (a.stages & 1) {
+            const int rc = launch_gu_rows<FMT>(a);
+            if (rc) return rc;
+        }
+        if (a.stages & 2) return launch_dn_rows<FMT>(a);
+        return 0;
+    }
     if (a.stages & 1) {
         // fewer rows per wave when the launch would be short of waves
         const long waves4 = (long)nslots * a.w->F / 16;
