@@ -11,7 +11,8 @@ import os
 import torch  # noqa: F401  (loads the HIP runtime before the library)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmoe_mi355x.so")
+# MOELAB_AMD_LIB names another build of the same library (e.g. one compiled with different tuning macros)
+LIB_PATH = os.environ.get("MOELAB_AMD_LIB") or os.path.join(HERE, "libmoe_mi355x.so")
 
 MOE_OK, MOE_ERR_ARG, MOE_ERR_DTYPE, MOE_ERR_WORKSPACE, MOE_ERR_LAUNCH, MOE_ERR_ALIGN = 0, -1, -2, -3, -4, -5
 DTYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

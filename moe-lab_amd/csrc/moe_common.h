@@ -202,4 +202,8 @@ __device__ __forceinline__ float glu(float g, float u) {
     return g / (1.f + expf(-1.702f * g)) * (u + 1.f);
 }
 
+__device__ __forceinline__ float glu_act(int act, float g, float u) {
+    return act == 0 ? glu<0>(g, u) : (act == 1 ? glu<1>(g, u) : glu<2>(g, u));
+}
+
 }  // namespace moe

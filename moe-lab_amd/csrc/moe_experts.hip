@@ -27,62 +27,10 @@
 //   k_t1_fused                       T == 1 in one launch: gate/up for all k slots, a device-wide
 //                                    completion count, then down + k-reduction (h staged in LDS)
 #include "moe_common.h"
+#include "moe_formats.h"
 #include "moe_internal.h"
 
 namespace moe {
-
-// ============================================================================ packed row formats
-struct FmtInt4 {
-    static constexpr int FMT = MOE_FMT_INT4_G64;
-    static constexpr bool XSUM = true;   // the fold needs sum(x) over each chunk
-    __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) {
-        return *reinterpret_cast<const uint32_t*>(row + (K >> 1) + 4 * (c >> 1));
-    }
-    // 7 VALU ops per word: t holds nibbles 0, 2, 4, 6 and u nibbles 1, 3, 5, 7 in the low halves of its
-    // bytes; each v_perm_b32 picks two of those bytes and puts the bf16 exponent byte 0x43 above each.
-    __device__ static __forceinline__ void decode(uint4 w, uint32_t qp[16]) {
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t t = ws[j] & 0x0F0F0F0Fu, u = (ws[j] >> 4) & 0x0F0F0F0Fu;
-            qp[4 * j + 0] = __builtin_amdgcn_perm(0x43434343u, t, 0x04020400u);   // (q0, q4)
-            qp[4 * j + 1] = __builtin_amdgcn_perm(0x43434343u, u, 0x04020400u);   // (q1, q5)
-            qp[4 * j + 2] = __builtin_amdgcn_perm(0x43434343u, t, 0x04030401u);   // (q2, q6)
-            qp[4 * j + 3] = __builtin_amdgcn_perm(0x43434343u, u, 0x04030401u);   // (q3, q7)
-        }
-    }
-    __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float xsum) {
-        const float s = bf16lo(m), b = bf16hi(m);
-        return __builtin_fmaf(s, dot, __builtin_fmaf(__builtin_fmaf(-128.f, s, b), xsum, acc));
-    }
-};
-
-struct FmtMxfp4 {
-    static constexpr int FMT = MOE_FMT_MXFP4;
-    static constexpr bool XSUM = false;
-    __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) { return row[(K >> 1) + c]; }
-    // E2M1 magnitude index m (0..7) -> bf16 bytes of {0, .5, 1, 1.5, 2, 3, 4, 6}: low bytes {00,00,80,C0,00,40,
-    // 80,C0}, high bytes {00,3F,3F,3F,40,40,40,40}; v_perm_b32 looks up four indices (one per byte) at once.
-    __device__ static __forceinline__ void decode(uint4 w, uint32_t qp[16]) {
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t v = ws[j];
-            const uint32_t me = v & 0x07070707u, mo = (v >> 4) & 0x07070707u;   // nibbles 0,2,4,6 / 1,3,5,7
-            const uint32_t lo_e = __builtin_amdgcn_perm(0xC0804000u, 0xC0800000u, me);
-            const uint32_t hi_e = __builtin_amdgcn_perm(0x40404040u, 0x3F3F3F00u, me) | ((v & 0x08080808u) << 4);
-            const uint32_t lo_o = __builtin_amdgcn_perm(0xC0804000u, 0xC0800000u, mo);
-            const uint32_t hi_o = __builtin_amdgcn_perm(0x40404040u, 0x3F3F3F00u, mo) | (v & 0x80808080u);
-            qp[4 * j + 0] = __builtin_amdgcn_perm(hi_e, lo_e, 0x06020400u);   // (e0, e4)
-            qp[4 * j + 1] = __builtin_amdgcn_perm(hi_o, lo_o, 0x06020400u);   // (e1, e5)
-            qp[4 * j + 2] = __builtin_amdgcn_perm(hi_e, lo_e, 0x07030501u);   // (e2, e6)
-            qp[4 * j + 3] = __builtin_amdgcn_perm(hi_o, lo_o, 0x07030501u);   // (e3, e7)
-        }
-    }
-    __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float) {
-        return __builtin_fmaf(__uint_as_float(m << 23), dot, acc);
-    }
-};
 
 // ============================================================================ shared pieces
 __device__ __forceinline__ float dot16(const uint32_t qp[16], const uint32_t xp[16], float acc) {
@@ -122,14 +70,7 @@ __device__ __forceinline__ float load_y(const void* y, size_t i, int y32) {
     return y32 ? reinterpret_cast<const float*>(y)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
 }
 
-__device__ __forceinline__ size_t rbytes(int fmt, int K) {
-    const size_t meta = fmt == MOE_FMT_INT4_G64 ? (size_t)K / 16 : (size_t)K / 32;
-    return ((size_t)K / 2 + meta + 15) & ~(size_t)15;
-}
 
-__device__ __forceinline__ float glu_rt(int act, float g, float u) {
-    return act == 0 ? glu<0>(g, u) : (act == 1 ? glu<1>(g, u) : glu<2>(g, u));
-}
 
 // ============================================================================ per-slot gate / up, balanced
 // Work item q = slot * F + f: gate row f and up row f of expert idx[slot]. Wave gw = 4 * blockIdx.x + wave
@@ -220,7 +161,7 @@ k_gate_up_rows(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, co
 #pragma unroll
         for (int q = 0; q < R; ++q)
             if (q == rl) { g = ag[q]; u = au[q]; }
-        const float hv = valid ? glu_rt(act, g + bgl, u + bul) : 0.f;
+        const float hv = valid ? glu_act(act, g + bgl, u + bul) : 0.f;
         store_h(hhi, hlo, (size_t)s * F, f0 + rl, hv);
     }
 }

@@ -1,0 +1,78 @@
+// Packed weight formats of the gfx950 MoE kernels: how a 16-byte chunk (32 inputs) of a row record is
+// decoded to bf16 pairs and how its group metadata folds into the fp32 accumulator.
+//
+// A row record of K inputs: K/2 code bytes (8 nibbles per 32-bit word, low nibble first, as the reference's
+// state words, metal_q4_decode_v4.py:57-64), then the group metadata, zero-padded to 16 bytes:
+//   int4 g64: K/64 words (scale bf16 | bias bf16 << 16), w = scale*q + bias
+//   MXFP4:    K/32 E8M0 bytes, w = e2m1(q) * 2^(s-127)  (reference metal_mxfp4_moe.py:1-41)
+// Decoded pairs hold the elements (8j+i, 8j+i+4) of word j (i = 0..3), so the activation side is paired the
+// same way (pair_x32), and an 8-element group handed to MFMA is in the order (0,4,1,5,2,6,3,7).
+#pragma once
+#include "moe_common.h"
+#include "moe_mi355x.h"
+
+namespace moe {
+
+// bytes of one packed row record of K inputs (include/moe_mi355x.h: moe_row_bytes)
+__host__ __device__ __forceinline__ size_t rbytes(int fmt, int K) {
+    const size_t meta = fmt == MOE_FMT_INT4_G64 ? (size_t)K / 16 : (size_t)K / 32;
+    return ((size_t)K / 2 + meta + 15) & ~(size_t)15;
+}
+
+// ============================================================================ packed row formats
+struct FmtInt4 {
+    static constexpr int FMT = MOE_FMT_INT4_G64;
+    static constexpr bool XSUM = true;   // the fold needs sum(x) over each chunk
+    __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) {
+        return *reinterpret_cast<const uint32_t*>(row + (K >> 1) + 4 * (c >> 1));
+    }
+    // 7 VALU ops per word: t holds nibbles 0, 2, 4, 6 and u nibbles 1, 3, 5, 7 in the low halves of its
+    // bytes; each v_perm_b32 picks two of those bytes and puts the bf16 exponent byte 0x43 above each.
+    __device__ static __forceinline__ void decode_word(uint32_t w, uint32_t q[4]) {
+        const uint32_t t = w & 0x0F0F0F0Fu, u = (w >> 4) & 0x0F0F0F0Fu;
+        q[0] = __builtin_amdgcn_perm(0x43434343u, t, 0x04020400u);   // (q0, q4)
+        q[1] = __builtin_amdgcn_perm(0x43434343u, u, 0x04020400u);   // (q1, q5)
+        q[2] = __builtin_amdgcn_perm(0x43434343u, t, 0x04030401u);   // (q2, q6)
+        q[3] = __builtin_amdgcn_perm(0x43434343u, u, 0x04030401u);   // (q3, q7)
+    }
+    __device__ static __forceinline__ void decode(uint4 w, uint32_t qp[16]) {
+        decode_word(w.x, qp);
+        decode_word(w.y, qp + 4);
+        decode_word(w.z, qp + 8);
+        decode_word(w.w, qp + 12);
+    }
+    __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float xsum) {
+        const float s = bf16lo(m), b = bf16hi(m);
+        return __builtin_fmaf(s, dot, __builtin_fmaf(__builtin_fmaf(-128.f, s, b), xsum, acc));
+    }
+};
+
+struct FmtMxfp4 {
+    static constexpr int FMT = MOE_FMT_MXFP4;
+    static constexpr bool XSUM = false;
+    __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) { return row[(K >> 1) + c]; }
+    // E2M1 magnitude index m (0..7) -> bf16 bytes of {0, .5, 1, 1.5, 2, 3, 4, 6}: low bytes {00,00,80,C0,00,40,
+    // 80,C0}, high bytes {00,3F,3F,3F,40,40,40,40}; v_perm_b32 looks up four indices (one per byte) at once.
+    __device__ static __forceinline__ void decode_word(uint32_t v, uint32_t q[4]) {
+        const uint32_t me = v & 0x07070707u, mo = (v >> 4) & 0x07070707u;   // nibbles 0,2,4,6 / 1,3,5,7
+        const uint32_t lo_e = __builtin_amdgcn_perm(0xC0804000u, 0xC0800000u, me);
+        const uint32_t hi_e = __builtin_amdgcn_perm(0x40404040u, 0x3F3F3F00u, me) | ((v & 0x08080808u) << 4);
+        const uint32_t lo_o = __builtin_amdgcn_perm(0xC0804000u, 0xC0800000u, mo);
+        const uint32_t hi_o = __builtin_amdgcn_perm(0x40404040u, 0x3F3F3F00u, mo) | (v & 0x80808080u);
+        q[0] = __builtin_amdgcn_perm(hi_e, lo_e, 0x06020400u);   // (e0, e4)
+        q[1] = __builtin_amdgcn_perm(hi_o, lo_o, 0x06020400u);   // (e1, e5)
+        q[2] = __builtin_amdgcn_perm(hi_e, lo_e, 0x07030501u);   // (e2, e6)
+        q[3] = __builtin_amdgcn_perm(hi_o, lo_o, 0x07030501u);   // (e3, e7)
+    }
+    __device__ static __forceinline__ void decode(uint4 w, uint32_t qp[16]) {
+        decode_word(w.x, qp);
+        decode_word(w.y, qp + 4);
+        decode_word(w.z, qp + 8);
+        decode_word(w.w, qp + 12);
+    }
+    __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float) {
+        return __builtin_fmaf(__uint_as_float(m << 23), dot, acc);
+    }
+};
+
+}  // namespace moe

@@ -48,6 +48,8 @@ struct ExpertsArgs {
 // expert kernels, both formats (moe_experts.hip)
 int run_experts_slots(const ExpertsArgs& a);
 int run_experts_grouped(const ExpertsArgs& a);
+// grouped expert tiles on MFMA (moe_tiles.hip): grouping, gate/up + GLU, down, combine
+int run_experts_tiles(const ExpertsArgs& a);
 // combine (moe_experts.hip): y[t] = residual[t] + sum_j yp[t*k + j]
 int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);
 

@@ -1,10 +1,12 @@
 // Router and slot grouping kernels for gfx950.
 //
-// router_logits_topk: logits[t, e] = x[t] . Wr[e] (+ b[e]) in fp32, one wave per (expert, token group),
+// router_logits_topk: logits[t, e] = x[t] . Wr[e] (+ b[e]) in fp32, one wave per EPW experts x TPW tokens,
 // then the last block to finish a token group runs the router tail (top-k, softmax) for its tokens.
-// The logit reduction order is fixed (lane l takes 8-element chunks l, l+64, ... with fused
-// multiply-adds in element order; the 64 lane partials are combined by an xor butterfly 32..1; the bias
-// is added last), so a CPU restatement reproduces every logit bit for bit and top-k ids match exactly.
+// The logit reduction order is fixed, so a CPU restatement reproduces every logit bit for bit and top-k ids
+// match exactly: lane l takes the 8-element chunks l, l+64, ... in order with fused multiply-adds in
+// element order, starting from +0; the 64 lane partials a[0..63] are combined by the DPP tree of
+// sum_lanes<64>: quads Q[q] = (a[4q] + a[4q+1]) + (a[4q+2] + a[4q+3]), half-rows H[h] = Q[2h] + Q[2h+1],
+// rows R[r] = H[2r] + H[2r+1], total = (R[3] + R[2]) + (R[1] + R[0]); the bias is added last.
 //
 // Router tail semantics follow reference moelab/router.py:1-66: NaN counts as -inf, k rounds of arg-max
 // with the lowest expert id winning ties, fewer than k finite logits -> lowest unused ids with weight 0,
@@ -17,8 +19,8 @@
 
 namespace moe {
 
-constexpr int ROUTER_WAVES = 4;   // waves per block = experts per block
-constexpr int ROUTER_TPW = 4;     // tokens per wave (the Wr row chunk is reused across them)
+constexpr int ROUTER_WAVES = 4;   // waves per block
+constexpr int ROUTER_TPW = 4;     // tokens per wave for T > 1 (the Wr row chunk is reused across them)
 constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024
 
 
@@ -86,63 +88,74 @@ __device__ void wave_topk(F lg, int E, int k, int norm, float scale, int32_t* id
     }
 }
 
-// grid (ceil(E / ROUTER_WAVES), ceil(T / ROUTER_TPW)), block 64 * ROUTER_WAVES.
+// grid (ceil(E / (ROUTER_WAVES * EPW)), ceil(T / TPW)), block 64 * ROUTER_WAVES.
 // counters[ty] must be 0 on entry; the last block of token group ty resets it to 0. Logits pass between
 // blocks through agent-scope atomic stores / loads (no L2 write-back or invalidation).
 constexpr int ROUTER_MAXC = 4;   // 16-byte chunks per lane held in registers per pass (2048 inputs)
 
+template <int TPW, int EPW>
 __global__ void __launch_bounds__(64 * ROUTER_WAVES)
 router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, const float* __restrict__ bias,
                    int T, int d, int E, int k, int norm, float scale, float* __restrict__ logits,
                    int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* __restrict__ counters) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = blockIdx.x * ROUTER_WAVES + wave;
-    const int t0 = blockIdx.y * ROUTER_TPW;
-    const int nt = min(ROUTER_TPW, T - t0);
+    const int bx = blockIdx.x, nbx = gridDim.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int e0 = (bx * ROUTER_WAVES + wave) * EPW;
+    const int t0 = blockIdx.y * TPW;
+    const int nt = min(TPW, T - t0);
     const int nchunk = d >> 3;
-    if (e < E) {
-        float acc[ROUTER_TPW];
+    if (e0 < E) {
+        float acc[EPW][TPW];
 #pragma unroll
-        for (int i = 0; i < ROUTER_TPW; ++i) acc[i] = 0.f;
-        const uint4* wrow = reinterpret_cast<const uint4*>(wr + (size_t)e * d);
+        for (int q = 0; q < EPW; ++q)
+#pragma unroll
+            for (int i = 0; i < TPW; ++i) acc[q][i] = 0.f;
         for (int c0 = 0; c0 < nchunk; c0 += 64 * ROUTER_MAXC) {
             // all loads of this pass first (chunks c0 + lane + 64m), then the fma chains in chunk order
-            uint4 w[ROUTER_MAXC], xv[ROUTER_TPW][ROUTER_MAXC];
+            uint4 w[EPW][ROUTER_MAXC], xv[TPW][ROUTER_MAXC];
 #pragma unroll
             for (int m = 0; m < ROUTER_MAXC; ++m) {
                 const int c = min(c0 + lane + 64 * m, nchunk - 1);
-                w[m] = wrow[c];
 #pragma unroll
-                for (int i = 0; i < ROUTER_TPW; ++i)
+                for (int q = 0; q < EPW; ++q)
+                    w[q][m] = reinterpret_cast<const uint4*>(wr + (size_t)min(e0 + q, E - 1) * d)[c];
+#pragma unroll
+                for (int i = 0; i < TPW; ++i)
                     xv[i][m] = reinterpret_cast<const uint4*>(x + (size_t)(t0 + min(i, nt - 1)) * d)[c];
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int m = 0; m < ROUTER_MAXC; ++m) {
                 if (c0 + lane + 64 * m < nchunk) {
-                    const uint32_t ww[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
 #pragma unroll
-                    for (int i = 0; i < ROUTER_TPW; ++i) {
-                        const uint32_t xx[4] = {xv[i][m].x, xv[i][m].y, xv[i][m].z, xv[i][m].w};
-                        float a = acc[i];
+                    for (int q = 0; q < EPW; ++q) {
+                        const uint32_t ww[4] = {w[q][m].x, w[q][m].y, w[q][m].z, w[q][m].w};
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            a = __builtin_fmaf(bf16lo(xx[q]), bf16lo(ww[q]), a);
-                            a = __builtin_fmaf(bf16hi(xx[q]), bf16hi(ww[q]), a);
+                        for (int i = 0; i < TPW; ++i) {
+                            const uint32_t xx[4] = {xv[i][m].x, xv[i][m].y, xv[i][m].z, xv[i][m].w};
+                            float a = acc[q][i];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                a = __builtin_fmaf(bf16lo(xx[r]), bf16lo(ww[r]), a);
+                                a = __builtin_fmaf(bf16hi(xx[r]), bf16hi(ww[r]), a);
+                            }
+                            acc[q][i] = a;
                         }
-                        acc[i] = a;
                     }
                 }
             }
         }
 #pragma unroll
-        for (int i = 0; i < ROUTER_TPW; ++i) {
-            float a = acc[i];
+        for (int q = 0; q < EPW; ++q)
 #pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) a = a + __shfl_xor(a, s, 64);
-            if (bias) a = a + bias[e];
-            if (lane == 0 && i < nt) store_agent(&logits[(size_t)(t0 + i) * E + e], a);
-        }
+            for (int i = 0; i < TPW; ++i) {
+                float a = sum_lanes<64>(acc[q][i]);   // lanes 48..63 hold the total
+                const int e = e0 + q;
+                if (lane == 63 && i < nt && e < E) {
+                    if (bias) a = a + bias[e];
+                    store_agent(&logits[(size_t)(t0 + i) * E + e], a);
+                }
+            }
     }
     // the last block of this token group runs the tail
     __shared__ int s_last;
@@ -150,12 +163,12 @@ router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ 
     __syncthreads();
     if (threadIdx.x == 0) {
         const int old = __hip_atomic_fetch_add(&counters[blockIdx.y], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == (int)gridDim.x - 1);
+        s_last = (old == nbx - 1);
     }
     __syncthreads();
     if (!s_last) return;
-    if (wave < nt) {
-        const int t = t0 + wave;
+    for (int i = wave; i < nt; i += ROUTER_WAVES) {
+        const int t = t0 + i;
         const float* lrow = logits + (size_t)t * E;
         wave_topk([&](int ee) { return load_agent(lrow + ee); }, E, k, norm, scale, idx + (size_t)t * k,
                   wts + (size_t)t * k);
@@ -259,9 +272,16 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
 // ------------------------------------------------------------------------------------ host launchers
 int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
                   float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st) {
-    dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, (T + ROUTER_TPW - 1) / ROUTER_TPW);
-    router_logits_topk<<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, k, norm, scale, logits, idx, wts,
-                                                            counters);
+    if (T == 1) {   // one expert per wave (fewer, larger waves measured slower)
+        constexpr int EPW = 1;
+        dim3 grid((E + ROUTER_WAVES * EPW - 1) / (ROUTER_WAVES * EPW), 1);
+        router_logits_topk<1, EPW><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, k, norm, scale, logits,
+                                                                        idx, wts, counters);
+    } else {
+        dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, (T + ROUTER_TPW - 1) / ROUTER_TPW);
+        router_logits_topk<ROUTER_TPW, 1><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, k, norm, scale,
+                                                                               logits, idx, wts, counters);
+    }
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

@@ -12,8 +12,9 @@
  *   - the d inputs are cut into chunks of 8 consecutive elements; lane l (0..63) takes chunks
  *     l, l+64, l+128, ... in increasing order and within a chunk accumulates the 8 products in
  *     element order with a fused multiply-add, starting from +0.0f;
- *   - the 64 lane partials are combined by a butterfly: for s = 32,16,8,4,2,1 every lane adds the
- *     partial of lane (l xor s); lane 0's value is the sum;
+ *   - the 64 lane partials a[0..63] are combined by a fixed tree (the DPP reduction the kernel uses):
+ *     quads Q[q] = (a[4q] + a[4q+1]) + (a[4q+2] + a[4q+3]), half-rows H[h] = Q[2h] + Q[2h+1],
+ *     rows R[r] = H[2r] + H[2r+1], total = (R[3] + R[2]) + (R[1] + R[0]);
  *   - the bias is added last (one fp32 addition).
  *
  * Router tail (reference moelab/router.py:15-66, semantics router.py:1-12):
@@ -59,12 +60,11 @@ int oracle_router_logits(const uint16_t *x, const uint16_t *wr, const float *bia
                         acc = fmaf(bf16_to_f32(xr[8 * c + i]), bf16_to_f32(wrow[8 * c + i]), acc);
                 part[l] = acc;
             }
-            for (int s = 32; s >= 1; s >>= 1) {
-                float nxt[64];
-                for (int l = 0; l < 64; ++l) nxt[l] = part[l] + part[l ^ s];
-                memcpy(part, nxt, sizeof(part));
-            }
-            float v = part[0];
+            float q[16], h[8], r[4];
+            for (int i = 0; i < 16; ++i) q[i] = (part[4 * i] + part[4 * i + 1]) + (part[4 * i + 2] + part[4 * i + 3]);
+            for (int i = 0; i < 8; ++i) h[i] = q[2 * i] + q[2 * i + 1];
+            for (int i = 0; i < 4; ++i) r[i] = h[2 * i] + h[2 * i + 1];
+            float v = (r[3] + r[2]) + (r[1] + r[0]);
             if (bias) v = v + bias[e];
             logits[(size_t)t * E + e] = v;
         }

@@ -100,23 +100,48 @@ def test_router_logits_close_to_fp64(orc):
     assert (np.abs(lg - exact) <= bound).all()
 
 
+def _tree64(part):
+    """The documented combination of 64 fp32 lane partials: quads, half-rows, rows, then
+    (R3 + R2) + (R1 + R0), each addition rounded to fp32."""
+    f = np.float32
+    q = [f(f(part[4 * i] + part[4 * i + 1]) + f(part[4 * i + 2] + part[4 * i + 3])) for i in range(16)]
+    h = [f(q[2 * i] + q[2 * i + 1]) for i in range(8)]
+    r = [f(h[2 * i] + h[2 * i + 1]) for i in range(4)]
+    return f(f(r[3] + r[2]) + f(r[1] + r[0]))
+
+
 def test_router_logits_order_is_the_documented_one(orc):
     """Values whose fp32 sum depends on the order: the oracle must equal the documented order
-    (lane chunks, butterfly), not a plain sequential sum."""
+    (lane chunks, then the quad/half-row/row tree), not a sequential sum and not an xor butterfly."""
     d = 1024
     x = np.zeros((1, d), np.float32)
     w = np.ones((1, d), np.float32)
-    x[0, 0] = 2.0 ** 24        # lane 0, chunk 0
+    x[0, 0] = 2.0 ** 24        # lane 0 (chunk 0)
     x[0, 8] = 1.0              # lane 1 (chunk 1)
-    x[0, 16] = 1.0             # lane 2 (chunk 2)
-    # sequential: (2^24 + 1) + 1 = 2^24 (both ones absorbed); documented: lane partials 2^24, 1, 1, ...
-    # butterfly s=1 adds lanes 0+1 -> 2^24 (tie to even), lanes 2+3 -> 1, s=2: 2^24 + 1 -> 2^24.
+    x[0, 16] = -(2.0 ** 24)    # lane 2 (chunk 2)
     lg = orc.router_logits(orc_bits(x), orc_bits(w))
     part = np.zeros(64, np.float32)
-    part[0], part[1], part[2] = 2.0 ** 24, 1.0, 1.0
+    part[0], part[1], part[2] = 2.0 ** 24, 1.0, -(2.0 ** 24)
+    tree = _tree64(part)
+    # the tree adds 2^24 + 1 first (rounds to 2^24), then -2^24: 0; a butterfly adds 2^24 - 2^24 first: 1
+    bfly = part.copy()
     for s in (32, 16, 8, 4, 2, 1):
-        part = (part + part[np.arange(64) ^ s]).astype(np.float32)
-    assert lg[0, 0] == part[0]
+        bfly = (bfly + bfly[np.arange(64) ^ s]).astype(np.float32)
+    assert tree == 0.0 and bfly[0] == 1.0
+    assert lg[0, 0] == tree
+    # lanes 0, 16, 32, 48 (one per row) hold 1, 1, 2^24, 1: the tree gives (1 + 2^24) + (1 + 1) = 2^24 + 2,
+    # a sequential sum ((1 + 1) + 2^24) + 1 = 2^24 + 4 (2^24 + 3 rounds to even)
+    x2 = np.zeros((1, d), np.float32)
+    x2[0, 8 * 0], x2[0, 8 * 16], x2[0, 8 * 32], x2[0, 8 * 48] = 1.0, 1.0, 2.0 ** 24, 1.0
+    part2 = np.zeros(64, np.float32)
+    part2[0], part2[16], part2[32], part2[48] = 1.0, 1.0, 2.0 ** 24, 1.0
+    seq = np.float32(0.0)
+    for v in part2:
+        seq = np.float32(seq + v)
+    tree2 = _tree64(part2)
+    assert tree2 == 2.0 ** 24 + 2 and seq == 2.0 ** 24 + 4
+    lg2 = orc.router_logits(orc_bits(x2), orc_bits(w))
+    assert lg2[0, 0] == tree2
 
 
 def test_topk_matches_stable_argsort(orc):
