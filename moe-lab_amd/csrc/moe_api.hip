@@ -17,7 +17,7 @@ int resolve_path(int path, int T) {
 }
 
 struct Layout {
-    size_t h, yp, counts, offsets, sorted, active, meta, total;
+    size_t h, yp, xperm, counts, offsets, sorted, active, meta, total;
 };
 
 Layout layout(const moe_experts_t* w, int T, int k, int path) {
@@ -29,6 +29,8 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
     if (resolve_path(path, T) == MOE_PATH_GROUPED) {
         L.yp = off;
         off += align_up(nslots * (size_t)w->d * 4);
+        L.xperm = off;
+        off += align_up((size_t)T * w->d * 2);
         L.counts = off;
         off += align_up((size_t)w->E * 4);
         L.offsets = off;
@@ -152,6 +154,7 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     a.sync = (int32_t*)ws;
     if (rpath == MOE_PATH_GROUPED) {
         a.yp = (float*)(ws + L.yp);
+        a.xperm = (uint16_t*)(ws + L.xperm);
         a.grp.counts = (int32_t*)(ws + L.counts);
         a.grp.offsets = (int32_t*)(ws + L.offsets);
         a.grp.sorted = (int32_t*)(ws + L.sorted);

@@ -38,6 +38,7 @@ struct ExpertsArgs {
     uint16_t* hhi;        // GLU output h = hi + lo, two bf16 planes [T*k, F]
     uint16_t* hlo;
     float* yp;      // [T*k, d] fp32 scratch (grouped path)
+    uint16_t* xperm;   // [T, d] bf16 scratch: x with each 8-input group in the decoded-code order (grouped path)
     GroupBufs grp;  // grouped path
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
     int fused_t1;   // T == 1: try the single-launch kernel first

@@ -4,11 +4,12 @@
 //
 // A block owns one active expert and TL_ROWS = 64 weight rows (16 per wave). For gate/up the same wave owns
 // gate row r and up row r, so the GLU is applied in registers; for down it owns 16 rows of W_down. The
-// expert's slots (stable, ascending slot id: the grouping of moe_group) are taken 16 * NT at a time; each
-// pass streams the block's rows in K slices of TL_KC chunks (128 inputs) through LDS:
-//   A (codes): each thread loads one 16-byte chunk of one row and scatters its 4 words so that lane (r, g)
-//              later reads word g of the slice's 4 chunks with one ds_read_b128 (g = lane / 16 is the MFMA
-//              K group of 8 inputs, r = lane % 16 the row);
+// expert's slots (stable, ascending slot id: the grouping of moe_group) are taken 16 * NT at a time, pass z
+// of an expert by the block with blockIdx.z = z mod gridDim.z (so a popular expert spreads over blocks); each
+// pass streams the block's rows in K slices of TL_KC chunks (256 inputs) through LDS:
+//   A (codes): each thread loads 16-byte chunks of the rows and scatters their 4 words so that lane (r, g)
+//              later reads word g of the slice's chunks with ds_read_b128 (g = lane / 16 is the MFMA K group
+//              of 8 inputs, r = lane % 16 the row);
 //   metadata:  int4 (scale, bias - 128 scale) per 64-group, MXFP4 2^(s-127) per 32-group, as fp32;
 //   B (activations of the pass's tokens): 16-byte pieces of 8 inputs, reordered (0,4,1,5,2,6,3,7) like the
 //              decoded codes; tokens past the expert's count and inputs past K are zero.
@@ -31,9 +32,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int TL_ROWS = 64;   // weight rows per block
-constexpr int TL_KC = 4;      // chunks (32 inputs) per K slice
-constexpr int TL_APAD = 20;   // words per staged row: [g 0..3][chunk 0..3] + 4 words of padding
-constexpr int TL_BPAD = 17;   // 16-byte pieces per staged token: 16 + 1 of padding
+constexpr int TL_KC = 8;      // chunks (32 inputs) per K slice
+constexpr int TL_APAD = 4 * TL_KC + 4;   // words per staged row: [g 0..3][chunk 0..KC-1] + 4 words of padding
+constexpr int TL_BPAD = 4 * TL_KC + 1;   // 16-byte pieces per staged token (8 inputs each) + 1 of padding
+constexpr int TL_GMAX = TL_KC;           // scale groups per slice at most (MXFP4: one per chunk)
 
 struct TileArgs {
     const uint16_t* actv;  // gate/up: x [T, K]; down: h [T*k, K] (bf16; the hi plane of h = hi + lo)
@@ -75,7 +77,7 @@ k_tile(TileArgs a) {
     constexpr bool INT4 = FMT::XSUM;
     constexpr int HL = NPROJ == 2 ? 1 : 2;   // activation planes
     __shared__ uint32_t sA[NPROJ][TL_ROWS][TL_APAD];
-    __shared__ float4 sM[NPROJ][TL_ROWS];   // int4: (s0, c0, s1, c1) of the slice's 2 groups; MXFP4: 4 scales
+    __shared__ float sM[NPROJ][TL_ROWS][TL_GMAX];   // int4: (s, b - 128 s) of the slice's 4 groups; MXFP4: 8 scales
     __shared__ uint4 sB[HL][NTOK][TL_BPAD];
 
     if ((int)blockIdx.y >= a.meta[0]) return;   // block-uniform: fewer active experts than the grid allows
@@ -91,19 +93,21 @@ k_tile(TileArgs a) {
     const size_t rb = rbytes(FMT::FMT, K);
     const uint8_t* Wp[2] = {a.W0 + ((size_t)e * N + row0) * rb, NPROJ == 2 ? a.W1 + ((size_t)e * N + row0) * rb : nullptr};
 
-    // staging assignment of this thread
-    const int arow = tid >> 2, achunk = tid & 3;   // A: one chunk of one row per projection
-    const int mrow = (tid & 127) >> 1, mgi = tid & 1, mproj = tid >> 7;   // int4 metadata word
+    // staging assignment of this thread: A chunks (arow, achunk + 4 j), j = 0, 1, of every projection;
+    // int4 metadata: word mgi of row mrow of projection mproj (4 groups per slice); MXFP4: 8 bytes of row
+    const int arow = tid >> 2, achunk = tid & 3;
+    const int mrow = (tid & 127) >> 1, mgi = tid & 1, mproj = tid >> 7;
     const uint32_t ones = 0x3F803F80u;
     const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
 
-    for (int tok0 = 0; tok0 < n; tok0 += NTOK) {
+    for (int tok0 = NTOK * blockIdx.z; tok0 < n; tok0 += NTOK * gridDim.z) {
         // activation rows of this pass's tokens (staging: piece i of this thread is token (tid + 256 i) / 16)
-        size_t brow[NT];
-        bool bval[NT];
+        constexpr int BPT0 = NT * TL_KC / 4;   // activation pieces (8 inputs) per thread per plane per slice
+        size_t brow[BPT0];
+        bool bval[BPT0];
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            const int tk = (tid + 256 * i) >> 4;
+        for (int i = 0; i < BPT0; ++i) {
+            const int tk = (tid + 256 * i) / (4 * TL_KC);
             bval[i] = tok0 + tk < n;
             const int slot = a.sorted[beg + min(tok0 + tk, n - 1)];
             brow[i] = (size_t)(slot / a.act_div) * K;
@@ -114,27 +118,33 @@ k_tile(TileArgs a) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) acc[p][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-        uint4 ra[NPROJ], rbv[HL][NT];
-        uint32_t rm = 0;
+        constexpr int BPT = BPT0;
+        uint4 ra[NPROJ][2], rbv[HL][BPT];
+        uint2 rm = make_uint2(0u, 0u);
         auto load_slice = [&](int s) {
-            const int c = s * TL_KC + achunk;
 #pragma unroll
-            for (int p = 0; p < NPROJ; ++p)
-                if (c < cpr) ra[p] = *reinterpret_cast<const uint4*>(Wp[p] + (size_t)arow * rb + 16 * c);
-            if (INT4) {
-                const int grp = 2 * s + mgi;
+            for (int j = 0; j < 2; ++j) {
+                const int c = s * TL_KC + achunk + 4 * j;
+#pragma unroll
+                for (int p = 0; p < NPROJ; ++p)
+                    if (c < cpr) ra[p][j] = *reinterpret_cast<const uint4*>(Wp[p] + (size_t)arow * rb + 16 * c);
+            }
+            if (INT4) {   // groups 4s + 2 mgi, 4s + 2 mgi + 1: one 8-byte load
+                const int grp = 4 * s + 2 * mgi;
                 if (mproj < NPROJ && grp < (K >> 6))
-                    rm = *reinterpret_cast<const uint32_t*>(Wp[mproj] + (size_t)mrow * rb + (K >> 1) + 4 * grp);
-            } else {
+                    rm = *reinterpret_cast<const uint2*>(Wp[mproj] + (size_t)mrow * rb + (K >> 1) + 4 * grp);
+            } else {   // E8M0 bytes 8s .. 8s + 7 (past the last group: record padding or the next record)
                 if (tid < NPROJ * TL_ROWS) {
                     const int pr = tid / TL_ROWS, rw = tid % TL_ROWS;
-                    rm = *reinterpret_cast<const uint32_t*>(Wp[pr] + (size_t)rw * rb + (K >> 1) + 4 * s);
+                    const uint8_t* mp = Wp[pr] + (size_t)rw * rb + (K >> 1) + 8 * s;
+                    rm.x = *reinterpret_cast<const uint32_t*>(mp);
+                    if (8 * s + 4 < cpr) rm.y = *reinterpret_cast<const uint32_t*>(mp + 4);
                 }
             }
 #pragma unroll
-            for (int i = 0; i < NT; ++i) {
-                const int q = (tid + 256 * i) & 15;
-                const int k0 = s * 128 + 8 * q;
+            for (int i = 0; i < BPT; ++i) {
+                const int q = (tid + 256 * i) % (4 * TL_KC);
+                const int k0 = s * (32 * TL_KC) + 8 * q;
 #pragma unroll
                 for (int hl = 0; hl < HL; ++hl) {
                     rbv[hl][i] = make_uint4(0u, 0u, 0u, 0u);
@@ -147,39 +157,44 @@ k_tile(TileArgs a) {
         for (int s = 0; s < nslice; ++s) {
             __syncthreads();   // the previous slice's readers are done with the LDS
             {
-                const int c = s * TL_KC + achunk;
 #pragma unroll
-                for (int p = 0; p < NPROJ; ++p) {
-                    const uint4 v = c < cpr ? ra[p] : make_uint4(0u, 0u, 0u, 0u);
-                    sA[p][arow][0 * 4 + achunk] = v.x;
-                    sA[p][arow][1 * 4 + achunk] = v.y;
-                    sA[p][arow][2 * 4 + achunk] = v.z;
-                    sA[p][arow][3 * 4 + achunk] = v.w;
+                for (int j = 0; j < 2; ++j) {
+                    const int cl = achunk + 4 * j, c = s * TL_KC + cl;
+#pragma unroll
+                    for (int p = 0; p < NPROJ; ++p) {
+                        const uint4 v = c < cpr ? ra[p][j] : make_uint4(0u, 0u, 0u, 0u);
+                        sA[p][arow][0 * TL_KC + cl] = v.x;
+                        sA[p][arow][1 * TL_KC + cl] = v.y;
+                        sA[p][arow][2 * TL_KC + cl] = v.z;
+                        sA[p][arow][3 * TL_KC + cl] = v.w;
+                    }
                 }
                 if (INT4) {
                     if (mproj < NPROJ) {
-                        const bool ok = 2 * s + mgi < (K >> 6);
-                        const float sc = ok ? bf16lo(rm) : 0.f, bi = ok ? bf16hi(rm) : 0.f;
-                        float* m = reinterpret_cast<float*>(&sM[mproj][mrow]);
-                        m[2 * mgi] = sc;
-                        m[2 * mgi + 1] = __builtin_fmaf(-128.f, sc, bi);
+                        const int grp = 4 * s + 2 * mgi;
+                        const uint32_t w2[2] = {rm.x, rm.y};
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const bool ok = grp + u < (K >> 6);
+                            const float sc = ok ? bf16lo(w2[u]) : 0.f, bi = ok ? bf16hi(w2[u]) : 0.f;
+                            sM[mproj][mrow][2 * (2 * mgi + u)] = sc;
+                            sM[mproj][mrow][2 * (2 * mgi + u) + 1] = __builtin_fmaf(-128.f, sc, bi);
+                        }
                     }
                 } else if (tid < NPROJ * TL_ROWS) {
                     const int pr = tid / TL_ROWS, rw = tid % TL_ROWS;
-                    float4 m;
-                    // E8M0 byte s -> the fp32 with bits s << 23: 2^(s-127) for s = 1..254, 0 for s = 0;
-                    // groups past K read the zero padding of the record or the next row's codes, so they
-                    // are zeroed here (their activations are zero as well)
-                    const int g0 = 4 * s;
-                    m.x = g0 + 0 < cpr ? __uint_as_float((rm & 0xFFu) << 23) : 0.f;
-                    m.y = g0 + 1 < cpr ? __uint_as_float(((rm >> 8) & 0xFFu) << 23) : 0.f;
-                    m.z = g0 + 2 < cpr ? __uint_as_float(((rm >> 16) & 0xFFu) << 23) : 0.f;
-                    m.w = g0 + 3 < cpr ? __uint_as_float((rm >> 24) << 23) : 0.f;
-                    sM[pr][rw] = m;
+                    // E8M0 byte s -> the fp32 with bits s << 23: 2^(s-127) for s = 1..254, 0 for s = 0; groups
+                    // past K (record padding or the next record's bytes) are zeroed, as are their activations
+                    const uint32_t w2[2] = {rm.x, rm.y};
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const uint32_t b = (w2[u >> 2] >> (8 * (u & 3))) & 0xFFu;
+                        sM[pr][rw][u] = 8 * s + u < cpr ? __uint_as_float(b << 23) : 0.f;
+                    }
                 }
 #pragma unroll
-                for (int i = 0; i < NT; ++i) {
-                    const int tk = (tid + 256 * i) >> 4, q = (tid + 256 * i) & 15;
+                for (int i = 0; i < BPT; ++i) {
+                    const int tk = (tid + 256 * i) / (4 * TL_KC), q = (tid + 256 * i) % (4 * TL_KC);
 #pragma unroll
                     for (int hl = 0; hl < HL; ++hl) sB[hl][tk][q] = pair8(rbv[hl][i]);
                 }
@@ -188,25 +203,36 @@ k_tile(TileArgs a) {
             if (s + 1 < nslice) load_slice(s + 1);   // in flight during this slice's math
 
             // ---- math: this wave's 16 rows, every token tile of the pass
-            uint4 aw[NPROJ];
-            float4 mr[NPROJ][4];
+            uint32_t awv[NPROJ][TL_KC];
 #pragma unroll
-            for (int p = 0; p < NPROJ; ++p) {
-                aw[p] = *reinterpret_cast<const uint4*>(&sA[p][16 * wave + lr][4 * lg]);
+            for (int p = 0; p < NPROJ; ++p)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) mr[p][v] = sM[p][16 * wave + 4 * lg + v];
-            }
-            uint32_t awv[NPROJ][4];
-#pragma unroll
-            for (int p = 0; p < NPROJ; ++p) {
-                awv[p][0] = aw[p].x;
-                awv[p][1] = aw[p].y;
-                awv[p][2] = aw[p].z;
-                awv[p][3] = aw[p].w;
-            }
+                for (int q = 0; q < TL_KC / 4; ++q) {
+                    const uint4 aw = *reinterpret_cast<const uint4*>(&sA[p][16 * wave + lr][TL_KC * lg + 4 * q]);
+                    awv[p][4 * q] = aw.x;
+                    awv[p][4 * q + 1] = aw.y;
+                    awv[p][4 * q + 2] = aw.z;
+                    awv[p][4 * q + 3] = aw.w;
+                }
             constexpr int CPG = INT4 ? 2 : 1;   // chunks per scale group
 #pragma unroll
             for (int gi = 0; gi < TL_KC / CPG; ++gi) {
+                // this group's metadata for the lane's 4 output rows: (s, b - 128 s) or the MXFP4 scale
+                float ms[NPROJ][4], mc[NPROJ][4];
+#pragma unroll
+                for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float* m = &sM[p][16 * wave + 4 * lg + v][0];
+                        if (INT4) {
+                            const float2 m2 = *reinterpret_cast<const float2*>(m + 2 * gi);
+                            ms[p][v] = m2.x;
+                            mc[p][v] = m2.y;
+                        } else {
+                            ms[p][v] = m[gi];
+                            mc[p][v] = 0.f;
+                        }
+                    }
                 bf16x8 A[NPROJ][CPG];
 #pragma unroll
                 for (int p = 0; p < NPROJ; ++p)
@@ -223,7 +249,7 @@ k_tile(TileArgs a) {
                     for (int hl = 0; hl < HL; ++hl)
 #pragma unroll
                         for (int cc = 0; cc < CPG; ++cc) {
-                            const uint4 bv = sB[hl][16 * t + lr][4 * (gi * CPG + cc) + lg];
+                            const uint4 bv = sB[hl][16 * t + lr][4 * (gi * CPG + cc) + lg];   // piece = 4 chunk + g
                             B[hl][cc] = as_bf16x8(bv.x, bv.y, bv.z, bv.w);
                         }
                     f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -244,14 +270,10 @@ k_tile(TileArgs a) {
                                 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[p][cc], B[hl][cc], P, 0, 0, 0);
 #pragma unroll
                         for (int v = 0; v < 4; ++v) {
-                            const float4 m = mr[p][v];
-                            if (INT4) {
-                                const float sc = gi == 0 ? m.x : m.z, cb = gi == 0 ? m.y : m.w;
-                                acc[p][t][v] = __builtin_fmaf(sc, P[v], __builtin_fmaf(cb, xs[v], acc[p][t][v]));
-                            } else {
-                                const float sc = gi == 0 ? m.x : (gi == 1 ? m.y : (gi == 2 ? m.z : m.w));
-                                acc[p][t][v] = __builtin_fmaf(sc, P[v], acc[p][t][v]);
-                            }
+                            if (INT4)
+                                acc[p][t][v] = __builtin_fmaf(ms[p][v], P[v], __builtin_fmaf(mc[p][v], xs[v], acc[p][t][v]));
+                            else
+                                acc[p][t][v] = __builtin_fmaf(ms[p][v], P[v], acc[p][t][v]);
                         }
                     }
                 }
@@ -300,6 +322,286 @@ k_tile(TileArgs a) {
     }
 }
 
+// ============================================================================ DMA-ring tiles (NT <= 2)
+// The same tile arithmetic with every operand brought into LDS by direct global->LDS DMA
+// (global_load_lds_dwordx4: 16 bytes per lane, written at M0 + 16 * lane) into a ring of DR_NS stages, so
+// DR_NS - 1 slices per block are in flight without holding registers. The stage buffers are distinct
+// __shared__ objects indexed at compile time (the ring is unrolled), and blocks sync with a bare s_barrier,
+// so the waits on the DMA are the explicit per-stage vmcnt waits below, not a full drain.
+// Stage layouts (a K slice = DR_KC chunks = 256 inputs):
+//   A [proj][row 0..63][pos 0..7] 16-byte chunks, pos = chunk ^ (row & 7) (bank spread for the reads of
+//     lane (r, g): word g of chunk c of row r);
+//   M int4: [proj][row] 16 bytes = the slice's 4 (scale | bias) words; MXFP4: [proj][word 0..1][row] 4 bytes;
+//   B [plane][token 0..NTOK-1][pos 0..31] 16-byte pieces of 8 inputs, pos = piece ^ (token & 7); the
+//     activations are already in the decoded-code order (x copied by k_pair8_rows, h written so).
+// Chunks past K are clamped onto the row's last chunk and masked to zero on the A side; tokens past the
+// expert's count are clamped onto its last token and their output columns dropped.
+constexpr int DR_KC = 8;
+constexpr int DR_NS = 3;
+
+#define MOE_LDSP(p) ((__attribute__((address_space(3))) void*)(p))
+// workgroup barrier without a memory fence (a fence would drain every outstanding DMA); the "memory" clobber
+// keeps the compiler from moving LDS accesses across it
+#define MOE_BARRIER() asm volatile("s_barrier" ::: "memory")
+#define MOE_VMWAIT(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (((N) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+
+template <class FMT, int NPROJ, int NT>
+struct DrStage {
+    static constexpr int NTOK = 16 * NT;
+    static constexpr int HL = NPROJ == 2 ? 1 : 2;
+    static constexpr int MBYTES = FMT::XSUM ? 16 : 8;
+    uint4 A[NPROJ][TL_ROWS][DR_KC];
+    uint32_t M[NPROJ][TL_ROWS * MBYTES / 4];
+    uint4 B[HL][NTOK][4 * DR_KC];
+};
+
+template <class FMT, int NPROJ, int NT>
+__device__ __forceinline__ void dr_issue(DrStage<FMT, NPROJ, NT>& S, int s, const uint8_t* const Wp[2], size_t rb,
+                                         int K, int cpr, const size_t* brow, const uint16_t* act0,
+                                         const uint16_t* act1, int wave, int lane) {
+    using St = DrStage<FMT, NPROJ, NT>;
+    // A: 8 instructions per projection, 8 rows x 8 chunks each; wave w takes instructions w, w + 4
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = wave + 4 * j;
+            const int row = 8 * i + (lane >> 3), pos = lane & 7;
+            const int gc = min(s * DR_KC + (pos ^ (row & 7)), cpr - 1);
+            __builtin_amdgcn_global_load_lds((const void*)(Wp[p] + (size_t)row * rb + 16 * gc),
+                                             MOE_LDSP(&S.A[p][8 * i][0]), 16, 0, 0);
+        }
+    // M
+    if (FMT::XSUM) {
+        if (wave < NPROJ) {   // the slice's 4 group words of row `lane` (record padding covers a short last slice)
+            __builtin_amdgcn_global_load_lds((const void*)(Wp[wave] + (size_t)lane * rb + (K >> 1) + 16 * s),
+                                             MOE_LDSP(&S.M[wave][0]), 16, 0, 0);
+        }
+    } else {
+        if (wave < 2 * NPROJ) {   // E8M0 bytes 8s .. 8s+3 (word 0) and 8s+4 .. 8s+7 (word 1)
+            const int p = wave >> 1, wj = wave & 1;
+            const int byte0 = 8 * s + 4 * ((8 * s + 4 < cpr) ? wj : 0);
+            __builtin_amdgcn_global_load_lds((const void*)(Wp[p] + (size_t)lane * rb + (K >> 1) + byte0),
+                                             MOE_LDSP(&S.M[p][wj * TL_ROWS]), 4, 0, 0);
+        }
+    }
+    // B: 2 tokens x 32 pieces per instruction; wave w takes instructions w, w + 4, ...
+    constexpr int NBI = St::NTOK / 2;
+#pragma unroll
+    for (int hl = 0; hl < St::HL; ++hl)
+#pragma unroll
+        for (int j = 0; j < NBI / 4; ++j) {
+            const int i = wave + 4 * j;
+            const int tk = 2 * i + (lane >> 5), pos = lane & 31;
+            const int piece = pos ^ (tk & 7);
+            const int k0 = min(s * (32 * DR_KC) + 8 * piece, K - 8);
+            __builtin_amdgcn_global_load_lds((const void*)((hl ? act1 : act0) + brow[j] + k0),
+                                             MOE_LDSP(&S.B[hl][2 * i][0]), 16, 0, 0);
+        }
+}
+
+// DMA instructions every wave issues per stage (A and B); waves that also fetch metadata issue one more
+template <class FMT, int NPROJ, int NT>
+__host__ __device__ constexpr int dr_wave_issues() {
+    return 2 * NPROJ + (NPROJ == 2 ? 1 : 2) * (16 * NT / 2) / 4;
+}
+template <class FMT, int NPROJ>
+__device__ __forceinline__ bool dr_wave_fetches_meta(int wave) {
+    return FMT::XSUM ? wave < NPROJ : wave < 2 * NPROJ;
+}
+
+template <class FMT, int NPROJ, int NT>
+__device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s, int cpr, int K, int wave, int lr,
+                                        int lg, f32x4 (&acc)[NPROJ][NT]) {
+    constexpr bool INT4 = FMT::XSUM;
+    constexpr int HL = NPROJ == 2 ? 1 : 2;
+    constexpr int CPG = INT4 ? 2 : 1;
+    const uint32_t ones = 0x3F803F80u;
+    const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
+    const int R = 16 * wave + lr;
+    uint32_t awv[NPROJ][DR_KC];
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p) {
+        const uint32_t* rowp = reinterpret_cast<const uint32_t*>(&S.A[p][R][0]);
+#pragma unroll
+        for (int c = 0; c < DR_KC; ++c) awv[p][c] = rowp[4 * (c ^ (R & 7)) + lg];
+    }
+    const int nvalid = cpr - s * DR_KC;   // chunks of this slice inside the row (>= DR_KC: all)
+#pragma unroll
+    for (int gi = 0; gi < DR_KC / CPG; ++gi) {
+        float ms[NPROJ][4], mc[NPROJ][4];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r2 = 16 * wave + 4 * lg + v;
+                if (INT4) {
+                    const uint32_t m = S.M[p][4 * r2 + gi];
+                    const bool ok = 4 * s + gi < (K >> 6);
+                    const float sc = ok ? bf16lo(m) : 0.f;
+                    ms[p][v] = sc;
+                    mc[p][v] = ok ? __builtin_fmaf(-128.f, sc, bf16hi(m)) : 0.f;
+                } else {
+                    const uint32_t b = (S.M[p][(gi >> 2) * TL_ROWS + r2] >> (8 * (gi & 3))) & 0xFFu;
+                    ms[p][v] = gi < nvalid ? __uint_as_float(b << 23) : 0.f;
+                    mc[p][v] = 0.f;
+                }
+            }
+        bf16x8 A[NPROJ][CPG];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int cc = 0; cc < CPG; ++cc) {
+                uint32_t q[4];
+                FMT::decode_word(awv[p][gi * CPG + cc], q);
+                if (gi * CPG + cc >= nvalid) q[0] = q[1] = q[2] = q[3] = 0u;   // chunk past K
+                A[p][cc] = as_bf16x8(q[0], q[1], q[2], q[3]);
+            }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int tk = 16 * t + lr;
+            bf16x8 B[HL][CPG];
+#pragma unroll
+            for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                for (int cc = 0; cc < CPG; ++cc) {
+                    const int piece = 4 * (gi * CPG + cc) + lg;
+                    const uint4 bv = S.B[hl][tk][piece ^ (tk & 7)];
+                    B[hl][cc] = as_bf16x8(bv.x, bv.y, bv.z, bv.w);
+                }
+            f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (INT4) {
+#pragma unroll
+                for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                    for (int cc = 0; cc < CPG; ++cc)
+                        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ONES, B[hl][cc], xs, 0, 0, 0);
+            }
+#pragma unroll
+            for (int p = 0; p < NPROJ; ++p) {
+                f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                    for (int cc = 0; cc < CPG; ++cc)
+                        P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[p][cc], B[hl][cc], P, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if (INT4)
+                        acc[p][t][v] = __builtin_fmaf(ms[p][v], P[v], __builtin_fmaf(mc[p][v], xs[v], acc[p][t][v]));
+                    else
+                        acc[p][t][v] = __builtin_fmaf(ms[p][v], P[v], acc[p][t][v]);
+                }
+            }
+        }
+    }
+}
+
+// position of element i (0..7) of an 8-input group in the decoded-code order (0,4,1,5,2,6,3,7)
+__device__ __forceinline__ int code_pos8(int i) { return i < 4 ? 2 * i : 2 * (i - 4) + 1; }
+
+template <class FMT, int NPROJ, int NT>
+__global__ void __launch_bounds__(256)
+k_tile_dma(TileArgs a) {
+    using St = DrStage<FMT, NPROJ, NT>;
+    constexpr int NTOK = St::NTOK;
+    constexpr int NBI = NTOK / 2;
+    __shared__ St S0, S1, S2;
+
+    if ((int)blockIdx.y >= a.meta[0]) return;
+    const int e = a.active[blockIdx.y];
+    const int n = a.counts[e], beg = a.offsets[e];
+    const int row0 = blockIdx.x * TL_ROWS;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int K = a.K, N = a.N;
+    const int cpr = K >> 5;
+    const int nslice = (cpr + DR_KC - 1) / DR_KC;
+    const size_t rb = rbytes(FMT::FMT, K);
+    const uint8_t* const Wp[2] = {a.W0 + ((size_t)e * N + row0) * rb,
+                                  NPROJ == 2 ? a.W1 + ((size_t)e * N + row0) * rb : a.W0};
+    constexpr int WI = dr_wave_issues<FMT, NPROJ, NT>();
+    const bool meta_wave = dr_wave_fetches_meta<FMT, NPROJ>(wave);   // wave-uniform
+
+    for (int tok0 = NTOK * blockIdx.z; tok0 < n; tok0 += NTOK * gridDim.z) {
+        // activation row offsets of the B instructions this lane issues (token 2i + lane/32, i = wave + 4j)
+        size_t brow[NBI / 4 > 0 ? NBI / 4 : 1];
+#pragma unroll
+        for (int j = 0; j < NBI / 4; ++j) {
+            const int tk = 2 * (wave + 4 * j) + (lane >> 5);
+            const int slot = a.sorted[beg + min(tok0 + tk, n - 1)];
+            brow[j] = (size_t)(slot / a.act_div) * K;
+        }
+        f32x4 acc[NPROJ][NT];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[p][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        MOE_BARRIER();   // every wave is done reading the ring from the previous pass
+        dr_issue(S0, 0, Wp, rb, K, cpr, brow, a.actv, a.actv2, wave, lane);
+        if (nslice > 1) dr_issue(S1, 1, Wp, rb, K, cpr, brow, a.actv, a.actv2, wave, lane);
+        for (int s = 0; s < nslice; s += DR_NS) {
+#define MOE_DR_STEP(CUR, NXT, OFF)                                                                          \
+    if (s + OFF < nslice) {                                                                                 \
+        if (s + OFF + 1 >= nslice) MOE_VMWAIT(0);                                                           \
+        else if (meta_wave) MOE_VMWAIT(WI + 1);                                                             \
+        else MOE_VMWAIT(WI);                                                                                \
+        MOE_BARRIER();                                                                                      \
+        if (s + OFF + 2 < nslice) dr_issue(NXT, s + OFF + 2, Wp, rb, K, cpr, brow, a.actv, a.actv2, wave, lane); \
+        dr_math(CUR, s + OFF, cpr, K, wave, lr, lg, acc);                                                   \
+    }
+            MOE_DR_STEP(S0, S2, 0)
+            MOE_DR_STEP(S1, S0, 1)
+            MOE_DR_STEP(S2, S1, 2)
+#undef MOE_DR_STEP
+        }
+        // ---- epilogue (rows 16 wave + 4 lg + v of token column lr of each tile)
+        const int rbase = row0 + 16 * wave + 4 * lg;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int j = tok0 + 16 * t + lr;
+            if (j >= n) continue;
+            const int slot = a.sorted[beg + j];
+            if (NPROJ == 2) {
+                // h written in the decoded-code order inside each 8-input group: row r -> 8 (r / 8) + pos8(r % 8)
+                uint16_t* hh = a.hout + (size_t)slot * N + (rbase & ~7);
+                uint16_t* hl2 = a.hout2 + (size_t)slot * N + (rbase & ~7);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float g = acc[0][t][v], up = acc[NPROJ - 1][t][v];
+                    if (a.b0) g += a.b0[(size_t)e * N + rbase + v];
+                    if (a.b1) up += a.b1[(size_t)e * N + rbase + v];
+                    const float hv = glu_act(a.act, g, up);
+                    const uint16_t hi = f32_to_bf16(hv);
+                    const int pos = code_pos8((rbase & 7) + v);
+                    hh[pos] = hi;
+                    hl2[pos] = f32_to_bf16(hv - bf16_to_f32(hi));
+                }
+            } else {
+                const float w = a.wts[slot];
+                float4 o;
+                float* ov = reinterpret_cast<float*>(&o);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float y = acc[0][t][v];
+                    if (a.b0) y += a.b0[(size_t)e * N + rbase + v];
+                    ov[v] = w * y;
+                }
+                *reinterpret_cast<float4*>(a.yp + (size_t)slot * N + rbase) = o;
+            }
+        }
+    }
+}
+
+// x [T, d] -> the same rows with each 8-input group in the decoded-code order (for the DMA tiles' B side)
+__global__ void __launch_bounds__(256)
+k_pair8_rows(const uint4* __restrict__ x, uint4* __restrict__ xp, size_t npieces) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < npieces) xp[i] = pair8(x[i]);
+}
+
 // ------------------------------------------------------------------------------------ host side
 namespace {
 
@@ -309,8 +611,10 @@ int tokens_per_pass_tiles(int T, int k, int E) {
 }
 
 template <class FMT, int NPROJ>
-int launch_tile(const TileArgs& t, int nt, int max_active, hipStream_t st) {
-    dim3 grid(t.N / TL_ROWS, max_active);
+int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st) {
+    // token passes spread over blockIdx.z: an expert has at most T slots when a token's k ids are distinct
+    const int zp = (T + 16 * nt - 1) / (16 * nt);
+    dim3 grid(t.N / TL_ROWS, max_active, zp < 1 ? 1 : (zp > 16 ? 16 : zp));
     switch (nt) {
         case 1: k_tile<FMT, NPROJ, 1><<<grid, 256, 0, st>>>(t); break;
         case 2: k_tile<FMT, NPROJ, 2><<<grid, 256, 0, st>>>(t); break;
@@ -319,6 +623,19 @@ int launch_tile(const TileArgs& t, int nt, int max_active, hipStream_t st) {
     }
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
+
+template <class FMT, int NPROJ>
+int launch_tile_dma(const TileArgs& t, int nt, int max_active, int T, hipStream_t st) {
+    const int zp = (T + 16 * nt - 1) / (16 * nt);
+    dim3 grid(t.N / TL_ROWS, max_active, zp < 1 ? 1 : (zp > 16 ? 16 : zp));
+    if (nt == 1) k_tile_dma<FMT, NPROJ, 1><<<grid, 256, 0, st>>>(t);
+    else k_tile_dma<FMT, NPROJ, 2><<<grid, 256, 0, st>>>(t);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+#ifndef MOE_TILE_DMA_NT
+#define MOE_TILE_DMA_NT 2   // token tiles per pass up to which the DMA-ring kernels run
+#endif
 
 template <class FMT>
 int run_tiles_fmt(const ExpertsArgs& a) {
@@ -340,6 +657,11 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         if (rc) return rc;
         TileArgs g = t;
         g.actv = (const uint16_t*)a.x;
+        if (nt <= MOE_TILE_DMA_NT) {   // the DMA tiles read x in the decoded-code order
+            const size_t np = (size_t)a.T * w->d / 8;
+            k_pair8_rows<<<(unsigned)((np + 255) / 256), 256, 0, a.st>>>((const uint4*)a.x, (uint4*)a.xperm, np);
+            g.actv = a.xperm;
+        }
         g.act_div = a.k;
         g.K = w->d;
         g.N = w->F;
@@ -349,7 +671,8 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         g.b1 = w->up.bias;
         g.hout = a.hhi;
         g.hout2 = a.hlo;
-        rc = launch_tile<FMT, 2>(g, nt, max_active, a.st);
+        rc = nt <= MOE_TILE_DMA_NT ? launch_tile_dma<FMT, 2>(g, nt, max_active, a.T, a.st)
+                                   : launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
         if (rc) return rc;
     }
     if (a.stages & 2) {
@@ -363,7 +686,8 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.b0 = w->down.bias;
         d.wts = a.wts;
         d.yp = a.yp;
-        int rc = launch_tile<FMT, 1>(d, nt, max_active, a.st);
+        int rc = nt <= MOE_TILE_DMA_NT ? launch_tile_dma<FMT, 1>(d, nt, max_active, a.T, a.st)
+                                       : launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
         return launch_combine(a.yp, a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
     }
