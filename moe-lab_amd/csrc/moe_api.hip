@@ -161,11 +161,7 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
         a.grp.active = (int32_t*)(ws + L.active);
         a.grp.meta = (int32_t*)(ws + L.meta);
     }
-#ifdef MOE_GROUPED_DOT2
-    return rpath == MOE_PATH_GROUPED ? moe::run_experts_grouped(a) : moe::run_experts_slots(a);
-#else
     return rpath == MOE_PATH_GROUPED ? moe::run_experts_tiles(a) : moe::run_experts_slots(a);
-#endif
 }
 
 }  // extern "C"

@@ -22,8 +22,8 @@
 //
 // Kernels:
 //   k_gate_up_slots / k_down_slots   per-slot GEMV (any T; the stock-style per-slot gather at T > 1)
-//   k_gate_up_grouped / k_down_grouped + k_combine   grouped expert tiles for T > 1: each selected
-//                                    expert's rows are read once and applied to all of its slots
+//   k_combine                        y = residual + sum over a token's slots of wts * (yp + b_down); the
+//                                    combine step of the grouped expert tiles (moe_tiles.hip)
 //   k_t1_fused                       T == 1 in one launch: gate/up for all k slots, a device-wide
 //                                    completion count, then down + k-reduction (h staged in LDS)
 #include "moe_common.h"
@@ -461,223 +461,36 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
     }
 }
 
-// ============================================================================ grouped gate / up
-// grid (ceil(F / (4*NR)), max_active), block 256. Block (bx, a) computes rows of expert active[a] for all
-// of its slots, NB per pass: each weight chunk is decoded once per pass and applied to NB activations.
-template <class FMT, int ACT, int NR, int NB>
-__global__ void __launch_bounds__(256)
-k_gate_up_grouped(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
-                  const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ counts,
-                  const int32_t* __restrict__ offsets, const int32_t* __restrict__ sorted,
-                  const int32_t* __restrict__ active, const int32_t* __restrict__ meta, int k, int d, int F,
-                  uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
-    static_assert(NR * NB <= 16, "results live in lanes 48..63");
-    const int a = blockIdx.y;
-    if (a >= meta[0]) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + wave) * NR;
-    if (row0 >= F) return;
-    const int e = active[a];
-    const int beg = offsets[e], cnt = counts[e];
-    const size_t rb = rbytes(FMT::FMT, d);
-    const int nchunk = d >> 5;
-    const uint8_t* gb0 = G + ((size_t)e * F + row0) * rb;
-    const uint8_t* ub0 = U + ((size_t)e * F + row0) * rb;
-    for (int tb = 0; tb < cnt; tb += NB) {
-        const int nb = min(NB, cnt - tb);
-        int sl[NB];
-#pragma unroll
-        for (int i = 0; i < NB; ++i) sl[i] = sorted[beg + tb + min(i, nb - 1)];
-        float ag[NR][NB], au[NR][NB];
-#pragma unroll
-        for (int r = 0; r < NR; ++r)
-#pragma unroll
-            for (int i = 0; i < NB; ++i) ag[r][i] = au[r][i] = 0.f;
-        for (int c0 = 0; c0 < nchunk; c0 += 64) {
-            const bool cv = c0 + lane < nchunk;
-            const int c = cv ? c0 + lane : nchunk - 1;
-            uint4 wg[NR], wu[NR];
-            uint32_t mg[NR], mu[NR], xw[NB][16];
-#pragma unroll
-            for (int r = 0; r < NR; ++r) {
-                const size_t ro = (size_t)min(r, F - 1 - row0) * rb;
-                wg[r] = *reinterpret_cast<const uint4*>(gb0 + ro + 16 * c);
-                wu[r] = *reinterpret_cast<const uint4*>(ub0 + ro + 16 * c);
-                mg[r] = FMT::meta(gb0 + ro, d, c);
-                mu[r] = FMT::meta(ub0 + ro, d, c);
-            }
-#pragma unroll
-            for (int i = 0; i < NB; ++i) load_x32(x + (size_t)(sl[i] / k) * d + 32 * c, xw[i]);
-            __builtin_amdgcn_sched_barrier(0);
-            uint32_t xp[NB][16];
-            float xs[NB];
-#pragma unroll
-            for (int i = 0; i < NB; ++i) {
-                pair_x32(xw[i], xp[i]);
-                xs[i] = FMT::XSUM ? sum_x32(xw[i]) : 0.f;
-            }
-            if (cv) {
-#pragma unroll
-                for (int r = 0; r < NR; ++r) {
-                    uint32_t qp[16];
-                    FMT::decode(wg[r], qp);
-#pragma unroll
-                    for (int i = 0; i < NB; ++i) ag[r][i] = FMT::fold(ag[r][i], mg[r], dot16(qp, xp[i], 0.f), xs[i]);
-                    FMT::decode(wu[r], qp);
-#pragma unroll
-                    for (int i = 0; i < NB; ++i) au[r][i] = FMT::fold(au[r][i], mu[r], dot16(qp, xp[i], 0.f), xs[i]);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < NR; ++r)
-#pragma unroll
-            for (int i = 0; i < NB; ++i) {
-                ag[r][i] = sum_lanes<64>(ag[r][i]);
-                au[r][i] = sum_lanes<64>(au[r][i]);
-            }
-        const int q = lane - 48;   // lane 48 + r*NB + i writes row r of slot i
-        if (q >= 0 && q < NR * NB) {
-            const int r = q / NB, i = q % NB;
-            float g = 0.f, u = 0.f;
-            int s_i = 0;
-#pragma unroll
-            for (int rr = 0; rr < NR; ++rr)
-#pragma unroll
-                for (int ii = 0; ii < NB; ++ii)
-                    if (rr * NB + ii == q) { g = ag[rr][ii]; u = au[rr][ii]; s_i = sl[ii]; }
-            const int n = row0 + r;
-            if (n < F && i < nb) {
-                if (bg) g += bg[(size_t)e * F + n];
-                if (bu) u += bu[(size_t)e * F + n];
-                store_h(hhi, hlo, (size_t)s_i * F, n, glu<ACT>(g, u));
-            }
-        }
-    }
-}
-
-// ============================================================================ grouped down
-// grid (ceil(D / (4*RPW)), max_active), block 256; each wave owns RPW = 64/LPR rows of expert active[a].
-// The h chunks of NB slots are staged in LDS (with their sums) KT chunks at a time; each weight chunk is
-// decoded once and applied to the NB slots. Writes yp[slot] = wts[slot] * (W_d h[slot] + bd) in fp32.
-constexpr int DG_KT = 64;   // chunks of h per LDS tile (2048 inputs)
-
-template <class FMT, int LPR, int NB>
-__global__ void __launch_bounds__(256)
-k_down_grouped(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
-               const float* __restrict__ bd, const float* __restrict__ wts, const int32_t* __restrict__ counts,
-               const int32_t* __restrict__ offsets, const int32_t* __restrict__ sorted,
-               const int32_t* __restrict__ active, const int32_t* __restrict__ meta, int D, int F,
-               float* __restrict__ yp) {
-    constexpr int RPW = 64 / LPR;
-    constexpr int SL = sum_lane<LPR>();
-    constexpr int MPL = DG_KT / LPR;                // chunks per lane per tile
-    __shared__ uint4 s_h[NB][DG_KT][8];             // pre-paired h: 4 x 16 B hi, then 4 x 16 B lo
-    __shared__ float s_sum[NB][DG_KT];
-    const int a = blockIdx.y;
-    if (a >= meta[0]) return;   // block-uniform
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rsub = lane / LPR, psub = lane % LPR;
-    const int n = (blockIdx.x * 4 + wave) * RPW + rsub;
-    const bool row_ok = n < D;
-    const int nn = row_ok ? n : D - 1;
-    const int e = active[a];
-    const int beg = offsets[e], cnt = counts[e];
-    const size_t rb = rbytes(FMT::FMT, F);
-    const int cpr = F >> 5;
-    const uint8_t* rowp = Dw + ((size_t)e * D + nn) * rb;
-    const float bias_n = bd ? bd[(size_t)e * D + nn] : 0.f;
-    for (int tb = 0; tb < cnt; tb += NB) {
-        const int nb = min(NB, cnt - tb);
-        int sl[NB];
-#pragma unroll
-        for (int i = 0; i < NB; ++i) sl[i] = sorted[beg + tb + min(i, nb - 1)];
-        float acc[NB];
-#pragma unroll
-        for (int i = 0; i < NB; ++i) acc[i] = 0.f;
-        for (int kt = 0; kt < cpr; kt += DG_KT) {
-            const int kn = min(DG_KT, cpr - kt);
-            // weights of this tile first: they do not depend on h
-            uint4 wv[MPL];
-            uint32_t m[MPL];
-#pragma unroll
-            for (int q = 0; q < MPL; ++q) {
-                const int p = psub + q * LPR;
-                if (p < kn) {
-                    wv[q] = *reinterpret_cast<const uint4*>(rowp + 16 * (kt + p));
-                    m[q] = FMT::meta(rowp, F, kt + p);
-                }
-            }
-            __syncthreads();   // the previous tile's readers are done with the LDS
-            for (int t = threadIdx.x; t < NB * kn; t += 256) {
-                const int i = t / kn, p = t % kn;
-                const size_t o = (size_t)sorted[beg + tb + min(i, nb - 1)] * F + 32 * (kt + p);
-                const uint4* hh = reinterpret_cast<const uint4*>(hhi + o);
-                const uint4* hl = reinterpret_cast<const uint4*>(hlo + o);
-                uint4 v[8];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    v[q] = hh[q];
-                    v[4 + q] = hl[q];
-                }
-                float s = 0.f;
-                if (FMT::XSUM) {
-                    uint32_t w[16];
-                    words16(v, w);
-                    s = sum16(w, 0.f);
-                    words16(v + 4, w);
-                    s = sum16(w, s);
-                }
-#pragma unroll
-                for (int q = 0; q < 8; ++q) s_h[i][p][q] = v[q];
-                s_sum[i][p] = s;
-            }
-            __syncthreads();
-#pragma unroll
-            for (int q = 0; q < MPL; ++q) {
-                const int p = psub + q * LPR;
-                if (p < kn) {
-                    uint32_t qp[16];
-                    FMT::decode(wv[q], qp);
-#pragma unroll
-                    for (int i = 0; i < NB; ++i) {
-                        if (i < nb) {
-                            uint32_t wh[16], wl[16];
-                            words16(&s_h[i][p][0], wh);
-                            words16(&s_h[i][p][4], wl);
-                            acc[i] = FMT::fold(acc[i], m[q], dot16(qp, wl, dot16(qp, wh, 0.f)), s_sum[i][p]);
-                        }
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < NB; ++i) acc[i] = sum_lanes<LPR>(acc[i]);
-        if (psub == SL && row_ok) {
-#pragma unroll
-            for (int i = 0; i < NB; ++i)
-                if (i < nb) yp[(size_t)sl[i] * D + n] = wts[sl[i]] * (acc[i] + bias_n);
-        }
-    }
-}
-
 // ============================================================================ combine
-// y[t, n] = residual[t, n] + sum_j yp[t*k + j, n]; 4 outputs per thread (D % 4 == 0).
+// y[t, n] = residual[t, n] + sum_j wts[t, j] * (yp[t*k + j, n] + bd[idx[t, j], n]); slots whose id is outside
+// [0, E) add nothing. 4 outputs per thread (D % 4 == 0).
 __global__ void __launch_bounds__(256)
-k_combine(const float* __restrict__ yp, const void* __restrict__ resid, void* __restrict__ y, int T, int k, int D,
-          int y32) {
+k_combine(const float* __restrict__ yp, const int32_t* __restrict__ idx, const float* __restrict__ wts,
+          const float* __restrict__ bd, int E, const void* __restrict__ resid, void* __restrict__ y, int T, int k,
+          int D, int y32) {
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total4 = (size_t)T * D / 4;
     if (i4 >= total4) return;
     const size_t i = i4 * 4;
     const int t = (int)(i / D), n = (int)(i % D);
-    float4 acc = reinterpret_cast<const float4*>(yp + ((size_t)t * k) * D + n)[0];
-    for (int j = 1; j < k; ++j) {
-        const float4 v = reinterpret_cast<const float4*>(yp + ((size_t)t * k + j) * D + n)[0];
-        acc.x += v.x;
-        acc.y += v.y;
-        acc.z += v.z;
-        acc.w += v.w;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < k; ++j) {
+        const int slot = t * k + j;
+        const int e = idx[slot];
+        if ((unsigned)e >= (unsigned)E) continue;
+        const float w = wts[slot];
+        float4 v = reinterpret_cast<const float4*>(yp + (size_t)slot * D + n)[0];
+        if (bd) {
+            const float4 b = reinterpret_cast<const float4*>(bd + (size_t)e * D + n)[0];
+            v.x += b.x;
+            v.y += b.y;
+            v.z += b.z;
+            v.w += b.w;
+        }
+        acc.x = __builtin_fmaf(w, v.x, acc.x);
+        acc.y = __builtin_fmaf(w, v.y, acc.y);
+        acc.z = __builtin_fmaf(w, v.z, acc.z);
+        acc.w = __builtin_fmaf(w, v.w, acc.w);
     }
     if (y32) {
         if (resid) {
@@ -1020,38 +833,6 @@ void launch_dn_slots(const ExpertsArgs& a) {
 #undef MOE_DNS
 }
 
-template <class FMT, int ACT>
-void launch_gu_grouped(const ExpertsArgs& a, int max_active) {
-    const moe_experts_t* w = a.w;
-    const ProjPtrs P = ptrs(w);
-    constexpr int NR = 2, NB = 4;
-    dim3 grid((w->F + 4 * NR - 1) / (4 * NR), max_active);
-    k_gate_up_grouped<FMT, ACT, NR, NB><<<grid, 256, 0, a.st>>>(
-        (const uint16_t*)a.x, P.G, P.U, w->gate.bias, w->up.bias, a.grp.counts, a.grp.offsets, a.grp.sorted,
-        a.grp.active, a.grp.meta, a.k, w->d, w->F, a.hhi, a.hlo);
-}
-
-template <class FMT>
-void launch_dn_grouped(const ExpertsArgs& a, int max_active) {
-    const moe_experts_t* w = a.w;
-    const ProjPtrs P = ptrs(w);
-    const int lpr = pick_lpr(min(w->F >> 5, DG_KT));
-    const int rpw = 64 / lpr;
-    dim3 grid((w->d + 4 * rpw - 1) / (4 * rpw), max_active);
-#define MOE_DNG(L)                                                                                                \
-    k_down_grouped<FMT, L, 4><<<grid, 256, 0, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.wts, a.grp.counts,      \
-                                                       a.grp.offsets, a.grp.sorted, a.grp.active, a.grp.meta, w->d, \
-                                                       w->F, a.yp)
-    switch (lpr) {
-        case 4: MOE_DNG(4); break;
-        case 8: MOE_DNG(8); break;
-        case 16: MOE_DNG(16); break;
-        case 32: MOE_DNG(32); break;
-        default: MOE_DNG(64); break;
-    }
-#undef MOE_DNG
-}
-
 // ---------------------------------------------------------------- balanced per-slot kernels
 // gate/up: R row pairs per wave (R divides F), as many as keeps >= 2048 waves in flight (2 blocks per CU on
 // 256 CUs); NCH chunks per lane per pass (2 when a row has more than 64 chunks).
@@ -1194,27 +975,6 @@ int run_slots_fmt(const ExpertsArgs& a) {
     return 0;
 }
 
-template <class FMT>
-int run_grouped_fmt(const ExpertsArgs& a) {
-    const int nslots = a.T * a.k;
-    const int max_active = nslots < a.w->E ? nslots : a.w->E;
-    if (a.stages & 1) {
-        int rc = launch_group(a.idx, nslots, a.w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
-                              a.grp.meta, a.st);
-        if (rc) return rc;
-        if (a.act == 0) launch_gu_grouped<FMT, 0>(a, max_active);
-        else if (a.act == 1) launch_gu_grouped<FMT, 1>(a, max_active);
-        else launch_gu_grouped<FMT, 2>(a, max_active);
-        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
-    }
-    if (a.stages & 2) {
-        launch_dn_grouped<FMT>(a, max_active);
-        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
-        return launch_combine(a.yp, a.residual, a.y, a.T, a.k, a.w->d, a.y32, a.st);
-    }
-    return 0;
-}
-
 // ---------------------------------------------------------------- fused T == 1
 constexpr int T1_NRA = 8;    // max row pairs per wave in phase A
 constexpr int T1_SPW = 4;    // max slots per wave in phase B (k <= 16)
@@ -1314,15 +1074,12 @@ int run_experts_slots(const ExpertsArgs& a) {
     return run_slots_fmt<FmtMxfp4>(a);
 }
 
-int run_experts_grouped(const ExpertsArgs& a) {
-    return a.w->fmt == MOE_FMT_INT4_G64 ? run_grouped_fmt<FmtInt4>(a) : run_grouped_fmt<FmtMxfp4>(a);
-}
-
-int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st) {
+int launch_combine(const float* yp, const int32_t* idx, const float* wts, const float* bd, int E,
+                   const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st) {
     const size_t total4 = (size_t)T * d / 4;
     if (total4 == 0) return 0;
     dim3 grid((unsigned)((total4 + 255) / 256));
-    k_combine<<<grid, 256, 0, st>>>(yp, residual, y, T, k, d, y32);
+    k_combine<<<grid, 256, 0, st>>>(yp, idx, wts, bd, E, residual, y, T, k, d, y32);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

@@ -48,10 +48,10 @@ struct ExpertsArgs {
 
 // expert kernels, both formats (moe_experts.hip)
 int run_experts_slots(const ExpertsArgs& a);
-int run_experts_grouped(const ExpertsArgs& a);
 // grouped expert tiles on MFMA (moe_tiles.hip): grouping, gate/up + GLU, down, combine
 int run_experts_tiles(const ExpertsArgs& a);
-// combine (moe_experts.hip): y[t] = residual[t] + sum_j yp[t*k + j]
-int launch_combine(const float* yp, const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);
+// combine (moe_experts.hip): y[t] = residual[t] + sum_j wts[t*k + j] * (yp[t*k + j] + bd[idx[t*k + j]])
+int launch_combine(const float* yp, const int32_t* idx, const float* wts, const float* bd, int E,
+                   const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);
 
 }  // namespace moe

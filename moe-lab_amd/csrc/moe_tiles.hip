@@ -21,10 +21,12 @@
 // all-ones A operand; then acc += s * P + (b - 128 s) * XS (int4) or acc += 2^(s-127) * P (MXFP4).
 // The GLU output h is stored as two bf16 planes h = hi + lo (about 16 significant bits; the reference keeps
 // it in x.dtype); the down projection runs one MFMA per plane into the same accumulator. The down output is
-// yp[slot] = wts[slot] * (W_down h + b_down) in fp32, summed over the k slots of a token by k_combine.
+// yp[slot] = W_down h in fp32; k_combine adds b_down, applies the routing weights and sums a token's slots.
 #include "moe_common.h"
 #include "moe_formats.h"
 #include "moe_internal.h"
+
+#include <math.h>
 
 namespace moe {
 
@@ -46,8 +48,9 @@ struct TileArgs {
     const float* b0;       // additive row biases [E, N] (gpt-oss) or null
     const float* b1;
     const int32_t *counts, *offsets, *sorted, *active, *meta;
-    const float* wts;      // routing weight per slot (down)
     int K, N, E, act;      // act: GLU kind (gate/up)
+    int rpb;               // row tiles per block (k_tile_run)
+    int kslots;            // k (slots per token)
     uint16_t* hout;        // gate/up: h = hi + lo as two bf16 planes [T*k, N]
     uint16_t* hout2;
     float* yp;             // down: [T*k, N] fp32
@@ -69,9 +72,16 @@ __device__ __forceinline__ uint4 pair8(uint4 v) {
     return o;
 }
 
+// workgroup barrier after this wave's LDS writes have completed, without a memory fence (a fence would also
+// wait for every global load in flight); the "memory" clobber keeps the compiler from moving LDS accesses across
+#define MOE_BARRIER_LDS() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
 // NPROJ = 2: gate/up (+ GLU, h out as hi/lo planes); NPROJ = 1: down (activation h = hi + lo: HL = 2 planes)
+#ifndef MOE_TILE_MINB
+#define MOE_TILE_MINB 1   // blocks per CU the register allocation must allow
+#endif
 template <class FMT, int NPROJ, int NT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, MOE_TILE_MINB)
 k_tile(TileArgs a) {
     constexpr int NTOK = 16 * NT;
     constexpr bool INT4 = FMT::XSUM;
@@ -307,16 +317,8 @@ k_tile(TileArgs a) {
                 *reinterpret_cast<uint2*>(a.hout + (size_t)slot * N + rbase) = make_uint2(phi[0], phi[1]);
                 *reinterpret_cast<uint2*>(a.hout2 + (size_t)slot * N + rbase) = make_uint2(plo[0], plo[1]);
             } else {
-                const float w = a.wts[slot];
-                float4 o;
-                float* ov = reinterpret_cast<float*>(&o);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    float y = acc[0][t][v];
-                    if (a.b0) y += a.b0[(size_t)e * N + rbase + v];
-                    ov[v] = w * y;
-                }
-                *reinterpret_cast<float4*>(a.yp + (size_t)slot * N + rbase) = o;
+                *reinterpret_cast<float4*>(a.yp + (size_t)slot * N + rbase) =
+                    make_float4(acc[0][t][0], acc[0][t][1], acc[0][t][2], acc[0][t][3]);
             }
         }
     }
@@ -358,7 +360,7 @@ struct DrStage {
 template <class FMT, int NPROJ, int NT>
 __device__ __forceinline__ void dr_issue(DrStage<FMT, NPROJ, NT>& S, int s, const uint8_t* const Wp[2], size_t rb,
                                          int K, int cpr, const size_t* brow, const uint16_t* act0,
-                                         const uint16_t* act1, int wave, int lane) {
+                                         const uint16_t* act1, int wave, int lane, int npair) {
     using St = DrStage<FMT, NPROJ, NT>;
     // A: 8 instructions per projection, 8 rows x 8 chunks each; wave w takes instructions w, w + 4
 #pragma unroll
@@ -385,13 +387,15 @@ __device__ __forceinline__ void dr_issue(DrStage<FMT, NPROJ, NT>& S, int s, cons
                                              MOE_LDSP(&S.M[p][wj * TL_ROWS]), 4, 0, 0);
         }
     }
-    // B: 2 tokens x 32 pieces per instruction; wave w takes instructions w, w + 4, ...
+    // B: 2 tokens x 32 pieces per instruction; wave w takes instructions w, w + 4, ... below npair (the token
+    // pairs the pass has: columns past the expert's count are never read into the math's kept outputs)
     constexpr int NBI = St::NTOK / 2;
 #pragma unroll
     for (int hl = 0; hl < St::HL; ++hl)
 #pragma unroll
         for (int j = 0; j < NBI / 4; ++j) {
             const int i = wave + 4 * j;
+            if (i >= npair) continue;   // wave-uniform
             const int tk = 2 * i + (lane >> 5), pos = lane & 31;
             const int piece = pos ^ (tk & 7);
             const int k0 = min(s * (32 * DR_KC) + 8 * piece, K - 8);
@@ -400,16 +404,44 @@ __device__ __forceinline__ void dr_issue(DrStage<FMT, NPROJ, NT>& S, int s, cons
         }
 }
 
-// DMA instructions every wave issues per stage (A and B); waves that also fetch metadata issue one more
+// DMA instructions a wave issues per stage: 2 per projection for A, one for the metadata on the waves that
+// fetch it, and one per activation plane for each of its token-pair instructions below npair
 template <class FMT, int NPROJ, int NT>
-__host__ __device__ constexpr int dr_wave_issues() {
-    return 2 * NPROJ + (NPROJ == 2 ? 1 : 2) * (16 * NT / 2) / 4;
+__device__ __forceinline__ int dr_wave_issues(int wave, int npair) {
+    constexpr int NBI = 16 * NT / 2;
+    int b = 0;
+#pragma unroll
+    for (int j = 0; j < NBI / 4; ++j) b += (wave + 4 * j < npair) ? 1 : 0;
+    const bool meta = FMT::XSUM ? wave < NPROJ : wave < 2 * NPROJ;
+    return 2 * NPROJ + (meta ? 1 : 0) + (NPROJ == 2 ? 1 : 2) * b;
 }
-template <class FMT, int NPROJ>
-__device__ __forceinline__ bool dr_wave_fetches_meta(int wave) {
-    return FMT::XSUM ? wave < NPROJ : wave < 2 * NPROJ;
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 15]
+__device__ __forceinline__ void vm_wait_n(int n) {
+    switch (n) {
+        case 0: MOE_VMWAIT(0); break;
+        case 1: MOE_VMWAIT(1); break;
+        case 2: MOE_VMWAIT(2); break;
+        case 3: MOE_VMWAIT(3); break;
+        case 4: MOE_VMWAIT(4); break;
+        case 5: MOE_VMWAIT(5); break;
+        case 6: MOE_VMWAIT(6); break;
+        case 7: MOE_VMWAIT(7); break;
+        case 8: MOE_VMWAIT(8); break;
+        case 9: MOE_VMWAIT(9); break;
+        case 10: MOE_VMWAIT(10); break;
+        case 11: MOE_VMWAIT(11); break;
+        case 12: MOE_VMWAIT(12); break;
+        case 13: MOE_VMWAIT(13); break;
+        case 14: MOE_VMWAIT(14); break;
+        default: MOE_VMWAIT(15); break;
+    }
 }
 
+
+// Transposed MFMA for the DMA tiles: the activations are the 16 x 32 operand (16 tokens), the decoded codes the
+// 32 x 16 one (16 weight rows), so lane (lr, lg) ends with tokens 4 lg + v (v = 0..3) of weight row lr: one
+// metadata word per group and projection per lane, and xs (sum of a token's inputs over the group) comes
+// from the same MFMA with an all-ones weight operand.
 template <class FMT, int NPROJ, int NT>
 __device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s, int cpr, int K, int wave, int lr,
                                         int lg, f32x4 (&acc)[NPROJ][NT]) {
@@ -418,7 +450,7 @@ __device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s,
     constexpr int CPG = INT4 ? 2 : 1;
     const uint32_t ones = 0x3F803F80u;
     const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
-    const int R = 16 * wave + lr;
+    const int R = 16 * wave + lr;   // this lane's weight row inside the tile
     uint32_t awv[NPROJ][DR_KC];
 #pragma unroll
     for (int p = 0; p < NPROJ; ++p) {
@@ -426,28 +458,40 @@ __device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s,
 #pragma unroll
         for (int c = 0; c < DR_KC; ++c) awv[p][c] = rowp[4 * (c ^ (R & 7)) + lg];
     }
+    // metadata of row R: int4 4 group words, MXFP4 8 E8M0 bytes
+    uint32_t mw[NPROJ][INT4 ? 4 : 2];
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p) {
+        if (INT4) {
+            const uint4 m4 = *reinterpret_cast<const uint4*>(&S.M[p][4 * R]);
+            mw[p][0] = m4.x;
+            mw[p][1] = m4.y;
+            mw[p][2] = m4.z;
+            mw[p][3] = m4.w;
+        } else {
+            mw[p][0] = S.M[p][R];
+            mw[p][INT4 ? 0 : 1] = S.M[p][TL_ROWS + R];
+        }
+    }
     const int nvalid = cpr - s * DR_KC;   // chunks of this slice inside the row (>= DR_KC: all)
 #pragma unroll
     for (int gi = 0; gi < DR_KC / CPG; ++gi) {
-        float ms[NPROJ][4], mc[NPROJ][4];
+        float ms[NPROJ], mc[NPROJ];
 #pragma unroll
-        for (int p = 0; p < NPROJ; ++p)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r2 = 16 * wave + 4 * lg + v;
-                if (INT4) {
-                    const uint32_t m = S.M[p][4 * r2 + gi];
-                    const bool ok = 4 * s + gi < (K >> 6);
-                    const float sc = ok ? bf16lo(m) : 0.f;
-                    ms[p][v] = sc;
-                    mc[p][v] = ok ? __builtin_fmaf(-128.f, sc, bf16hi(m)) : 0.f;
-                } else {
-                    const uint32_t b = (S.M[p][(gi >> 2) * TL_ROWS + r2] >> (8 * (gi & 3))) & 0xFFu;
-                    ms[p][v] = gi < nvalid ? __uint_as_float(b << 23) : 0.f;
-                    mc[p][v] = 0.f;
-                }
+        for (int p = 0; p < NPROJ; ++p) {
+            if (INT4) {
+                const uint32_t m = mw[p][gi];
+                const bool ok = 4 * s + gi < (K >> 6);
+                const float sc = ok ? bf16lo(m) : 0.f;
+                ms[p] = sc;
+                mc[p] = ok ? __builtin_fmaf(-128.f, sc, bf16hi(m)) : 0.f;
+            } else {
+                const uint32_t b = (mw[p][gi >> 2] >> (8 * (gi & 3))) & 0xFFu;
+                ms[p] = gi < nvalid ? __uint_as_float(b << 23) : 0.f;
+                mc[p] = 0.f;
             }
-        bf16x8 A[NPROJ][CPG];
+        }
+        bf16x8 W[NPROJ][CPG];
 #pragma unroll
         for (int p = 0; p < NPROJ; ++p)
 #pragma unroll
@@ -455,19 +499,19 @@ __device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s,
                 uint32_t q[4];
                 FMT::decode_word(awv[p][gi * CPG + cc], q);
                 if (gi * CPG + cc >= nvalid) q[0] = q[1] = q[2] = q[3] = 0u;   // chunk past K
-                A[p][cc] = as_bf16x8(q[0], q[1], q[2], q[3]);
+                W[p][cc] = as_bf16x8(q[0], q[1], q[2], q[3]);
             }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int tk = 16 * t + lr;
-            bf16x8 B[HL][CPG];
+            bf16x8 X[HL][CPG];
 #pragma unroll
             for (int hl = 0; hl < HL; ++hl)
 #pragma unroll
                 for (int cc = 0; cc < CPG; ++cc) {
                     const int piece = 4 * (gi * CPG + cc) + lg;
                     const uint4 bv = S.B[hl][tk][piece ^ (tk & 7)];
-                    B[hl][cc] = as_bf16x8(bv.x, bv.y, bv.z, bv.w);
+                    X[hl][cc] = as_bf16x8(bv.x, bv.y, bv.z, bv.w);
                 }
             f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
             if (INT4) {
@@ -475,7 +519,7 @@ __device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s,
                 for (int hl = 0; hl < HL; ++hl)
 #pragma unroll
                     for (int cc = 0; cc < CPG; ++cc)
-                        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ONES, B[hl][cc], xs, 0, 0, 0);
+                        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[hl][cc], ONES, xs, 0, 0, 0);
             }
 #pragma unroll
             for (int p = 0; p < NPROJ; ++p) {
@@ -484,13 +528,13 @@ __device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s,
                 for (int hl = 0; hl < HL; ++hl)
 #pragma unroll
                     for (int cc = 0; cc < CPG; ++cc)
-                        P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[p][cc], B[hl][cc], P, 0, 0, 0);
+                        P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[hl][cc], W[p][cc], P, 0, 0, 0);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     if (INT4)
-                        acc[p][t][v] = __builtin_fmaf(ms[p][v], P[v], __builtin_fmaf(mc[p][v], xs[v], acc[p][t][v]));
+                        acc[p][t][v] = __builtin_fmaf(ms[p], P[v], __builtin_fmaf(mc[p], xs[v], acc[p][t][v]));
                     else
-                        acc[p][t][v] = __builtin_fmaf(ms[p][v], P[v], acc[p][t][v]);
+                        acc[p][t][v] = __builtin_fmaf(ms[p], P[v], acc[p][t][v]);
                 }
             }
         }
@@ -500,9 +544,14 @@ __device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s,
 // position of element i (0..7) of an 8-input group in the decoded-code order (0,4,1,5,2,6,3,7)
 __device__ __forceinline__ int code_pos8(int i) { return i < 4 ? 2 * i : 2 * (i - 4) + 1; }
 
+// One block: one active expert (blockIdx.y), token pass blockIdx.z, and the row tiles
+// blockIdx.x * RPB .. + RPB - 1 of that expert (RPB = a.rpb). The ring runs across the block's tiles, so
+// the next tile's first slices are in flight while the current tile finishes. A tile's output is computed
+// in registers at its last slice and stored at the next step, after that step's wait and barrier (stores
+// issued after a stage's DMA would be counted ahead of it by the next vmcnt wait).
 template <class FMT, int NPROJ, int NT>
 __global__ void __launch_bounds__(256)
-k_tile_dma(TileArgs a) {
+k_tile_run(TileArgs a) {
     using St = DrStage<FMT, NPROJ, NT>;
     constexpr int NTOK = St::NTOK;
     constexpr int NBI = NTOK / 2;
@@ -511,7 +560,6 @@ k_tile_dma(TileArgs a) {
     if ((int)blockIdx.y >= a.meta[0]) return;
     const int e = a.active[blockIdx.y];
     const int n = a.counts[e], beg = a.offsets[e];
-    const int row0 = blockIdx.x * TL_ROWS;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lr = lane & 15, lg = lane >> 4;
@@ -519,79 +567,113 @@ k_tile_dma(TileArgs a) {
     const int cpr = K >> 5;
     const int nslice = (cpr + DR_KC - 1) / DR_KC;
     const size_t rb = rbytes(FMT::FMT, K);
-    const uint8_t* const Wp[2] = {a.W0 + ((size_t)e * N + row0) * rb,
-                                  NPROJ == 2 ? a.W1 + ((size_t)e * N + row0) * rb : a.W0};
-    constexpr int WI = dr_wave_issues<FMT, NPROJ, NT>();
-    const bool meta_wave = dr_wave_fetches_meta<FMT, NPROJ>(wave);   // wave-uniform
+    const int RT = N / TL_ROWS;
+    const int rt0 = blockIdx.x * a.rpb;
+    const int ntile = min(a.rpb, RT - rt0);
+    if (ntile <= 0) return;
+    const int U = ntile * nslice;
+    const uint8_t* const W0e = a.W0 + (size_t)e * N * rb;
+    const uint8_t* const W1e = (NPROJ == 2 ? a.W1 : a.W0) + (size_t)e * N * rb;
 
     for (int tok0 = NTOK * blockIdx.z; tok0 < n; tok0 += NTOK * gridDim.z) {
-        // activation row offsets of the B instructions this lane issues (token 2i + lane/32, i = wave + 4j)
+        const int npair = (min(NTOK, n - tok0) + 1) >> 1;   // token pairs of this pass
+        const int WI = dr_wave_issues<FMT, NPROJ, NT>(wave, npair);   // this wave's DMA count per stage (<= 15)
+        // activation rows of the B instructions this lane issues, and the output slot of each token column
         size_t brow[NBI / 4 > 0 ? NBI / 4 : 1];
 #pragma unroll
         for (int j = 0; j < NBI / 4; ++j) {
             const int tk = 2 * (wave + 4 * j) + (lane >> 5);
-            const int slot = a.sorted[beg + min(tok0 + tk, n - 1)];
-            brow[j] = (size_t)(slot / a.act_div) * K;
+            brow[j] = (size_t)(a.sorted[beg + min(tok0 + tk, n - 1)] / a.act_div) * K;
         }
+        int oslot[NT][4];   // output slot of token 16 t + 4 lg + v (-1: past the expert's count)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int j = tok0 + 16 * t + 4 * lg + v;
+                oslot[t][v] = j < n ? a.sorted[beg + j] : -1;
+            }
         f32x4 acc[NPROJ][NT];
+        float pbias[NPROJ];   // gate/up additive biases of this lane's row of the current tile
+        // pending output of the last finished tile, per token: gate/up (hi | lo << 16); down fp32
+        uint32_t pend[NT][4];
+        int pend_row = -1;   // output row of the pending tile for this lane (-1: nothing pending)
+
+        auto flush = [&]() {
+            if (pend_row < 0) return;
+            // h is written in the decoded-code order inside each 8-input group: row r -> 8 (r / 8) + pos8(r % 8)
+            const int hpos = (pend_row & ~7) + code_pos8(pend_row & 7);
 #pragma unroll
-        for (int p = 0; p < NPROJ; ++p)
+            for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[p][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int v = 0; v < 4; ++v) {
+                    if (oslot[t][v] < 0) continue;
+                    if (NPROJ == 2) {
+                        a.hout[(size_t)oslot[t][v] * N + hpos] = (uint16_t)(pend[t][v] & 0xFFFFu);
+                        a.hout2[(size_t)oslot[t][v] * N + hpos] = (uint16_t)(pend[t][v] >> 16);
+                    } else {
+                        a.yp[(size_t)oslot[t][v] * N + pend_row] = __uint_as_float(pend[t][v]);
+                    }
+                }
+            pend_row = -1;
+        };
+        auto issue = [&](auto& S, int u) {
+            const int q = u / nslice, si = u - q * nslice;
+            const size_t roff = (size_t)(rt0 + q) * TL_ROWS * rb;
+            const uint8_t* const Wp[2] = {W0e + roff, W1e + roff};
+            dr_issue(S, si, Wp, rb, K, cpr, brow, a.actv, a.actv2, wave, lane, npair);
+        };
+        auto compute = [&](const auto& S, int u) {
+            const int q = u / nslice, si = u - q * nslice;
+            if (si == 0) {
+#pragma unroll
+                for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) acc[p][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                // loaded here, ahead of the tile's later stages, so waiting for them at the tile's end
+                // never waits for a stage that is not needed yet
+                const int row = (rt0 + q) * TL_ROWS + 16 * wave + lr;
+                pbias[0] = (NPROJ == 2 && a.b0) ? a.b0[(size_t)e * N + row] : 0.f;
+                pbias[NPROJ - 1] = (NPROJ == 2 && a.b1) ? a.b1[(size_t)e * N + row] : 0.f;
+            }
+            dr_math(S, si, cpr, K, wave, lr, lg, acc);
+            if (si == nslice - 1) {   // tile done: its output into registers, stored at the next step
+                const int rbase = (rt0 + q) * TL_ROWS + 16 * wave + lr;   // this lane's output row
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        if (NPROJ == 2) {
+                            const float g = acc[0][t][v] + pbias[0], up = acc[NPROJ - 1][t][v] + pbias[NPROJ - 1];
+                            const float hv = glu_act(a.act, g, up);
+                            const uint16_t hi = f32_to_bf16(hv);
+                            pend[t][v] = (uint32_t)hi | ((uint32_t)f32_to_bf16(hv - bf16_to_f32(hi)) << 16);
+                        } else {
+                            pend[t][v] = __float_as_uint(acc[0][t][v]);
+                        }
+                    }
+                pend_row = rbase;
+            }
+        };
 
         MOE_BARRIER();   // every wave is done reading the ring from the previous pass
-        dr_issue(S0, 0, Wp, rb, K, cpr, brow, a.actv, a.actv2, wave, lane);
-        if (nslice > 1) dr_issue(S1, 1, Wp, rb, K, cpr, brow, a.actv, a.actv2, wave, lane);
-        for (int s = 0; s < nslice; s += DR_NS) {
-#define MOE_DR_STEP(CUR, NXT, OFF)                                                                          \
-    if (s + OFF < nslice) {                                                                                 \
-        if (s + OFF + 1 >= nslice) MOE_VMWAIT(0);                                                           \
-        else if (meta_wave) MOE_VMWAIT(WI + 1);                                                             \
-        else MOE_VMWAIT(WI);                                                                                \
-        MOE_BARRIER();                                                                                      \
-        if (s + OFF + 2 < nslice) dr_issue(NXT, s + OFF + 2, Wp, rb, K, cpr, brow, a.actv, a.actv2, wave, lane); \
-        dr_math(CUR, s + OFF, cpr, K, wave, lr, lg, acc);                                                   \
+        issue(S0, 0);
+        if (U > 1) issue(S1, 1);
+        for (int u = 0; u < U; u += DR_NS) {
+#define MOE_DR_STEP(CUR, NXT, OFF)                                         \
+    if (u + OFF < U) {                                                     \
+        vm_wait_n(u + OFF + 1 >= U ? 0 : WI);                              \
+        MOE_BARRIER();                                                     \
+        flush();                                                           \
+        if (u + OFF + 2 < U) issue(NXT, u + OFF + 2);                      \
+        compute(CUR, u + OFF);                                             \
     }
             MOE_DR_STEP(S0, S2, 0)
             MOE_DR_STEP(S1, S0, 1)
             MOE_DR_STEP(S2, S1, 2)
 #undef MOE_DR_STEP
         }
-        // ---- epilogue (rows 16 wave + 4 lg + v of token column lr of each tile)
-        const int rbase = row0 + 16 * wave + 4 * lg;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int j = tok0 + 16 * t + lr;
-            if (j >= n) continue;
-            const int slot = a.sorted[beg + j];
-            if (NPROJ == 2) {
-                // h written in the decoded-code order inside each 8-input group: row r -> 8 (r / 8) + pos8(r % 8)
-                uint16_t* hh = a.hout + (size_t)slot * N + (rbase & ~7);
-                uint16_t* hl2 = a.hout2 + (size_t)slot * N + (rbase & ~7);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    float g = acc[0][t][v], up = acc[NPROJ - 1][t][v];
-                    if (a.b0) g += a.b0[(size_t)e * N + rbase + v];
-                    if (a.b1) up += a.b1[(size_t)e * N + rbase + v];
-                    const float hv = glu_act(a.act, g, up);
-                    const uint16_t hi = f32_to_bf16(hv);
-                    const int pos = code_pos8((rbase & 7) + v);
-                    hh[pos] = hi;
-                    hl2[pos] = f32_to_bf16(hv - bf16_to_f32(hi));
-                }
-            } else {
-                const float w = a.wts[slot];
-                float4 o;
-                float* ov = reinterpret_cast<float*>(&o);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    float y = acc[0][t][v];
-                    if (a.b0) y += a.b0[(size_t)e * N + rbase + v];
-                    ov[v] = w * y;
-                }
-                *reinterpret_cast<float4*>(a.yp + (size_t)slot * N + rbase) = o;
-            }
-        }
+        flush();
     }
 }
 
@@ -624,17 +706,32 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
+#ifndef MOE_TILE_BLOCKS
+#define MOE_TILE_BLOCKS 512   // blocks the DMA tile launch aims at (2 per CU); tiles per block follow from it
+#endif
 template <class FMT, int NPROJ>
-int launch_tile_dma(const TileArgs& t, int nt, int max_active, int T, hipStream_t st) {
-    const int zp = (T + 16 * nt - 1) / (16 * nt);
-    dim3 grid(t.N / TL_ROWS, max_active, zp < 1 ? 1 : (zp > 16 ? 16 : zp));
-    if (nt == 1) k_tile_dma<FMT, NPROJ, 1><<<grid, 256, 0, st>>>(t);
-    else k_tile_dma<FMT, NPROJ, 2><<<grid, 256, 0, st>>>(t);
+int launch_tile_dma(TileArgs t, int nt, int max_active, int T, hipStream_t st) {
+    const int zp0 = (T + 16 * nt - 1) / (16 * nt);
+    const int zp = zp0 < 1 ? 1 : (zp0 > 16 ? 16 : zp0);
+    const int RT = t.N / TL_ROWS;
+    // row tiles per block so that the busy blocks come near MOE_TILE_BLOCKS when routing is uniform (E(1 -
+    // (1 - k/E)^T) experts active); capped at 2 so skewed routing, with few experts, still fills the device
+    const double kE = (double)t.kslots / (double)t.E;
+    double act = t.E * (1.0 - pow(1.0 - (kE < 1.0 ? kE : 1.0), (double)T));
+    if (act > max_active) act = max_active;
+    int rpb = (int)((act * RT + MOE_TILE_BLOCKS - 1) / MOE_TILE_BLOCKS);
+    rpb = rpb < 1 ? 1 : (rpb > 2 ? 2 : rpb);
+    if (rpb > RT) rpb = RT;
+    t.rpb = rpb;
+    dim3 grid((RT + rpb - 1) / rpb, max_active, zp);
+    if (nt == 1) k_tile_run<FMT, NPROJ, 1><<<grid, 256, 0, st>>>(t);
+    else k_tile_run<FMT, NPROJ, 2><<<grid, 256, 0, st>>>(t);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
 #ifndef MOE_TILE_DMA_NT
-#define MOE_TILE_DMA_NT 2   // token tiles per pass up to which the DMA-ring kernels run
+#define MOE_TILE_DMA_NT 0   // token tiles per pass up to which the DMA-ring kernels run (0: never; measured
+                            // slower than the register-staged tiles at the Qwen3 T = 16..64 shapes)
 #endif
 
 template <class FMT>
@@ -651,6 +748,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     t.meta = a.grp.meta;
     t.E = w->E;
     t.act = a.act;
+    t.kslots = a.k;
     if (a.stages & 1) {
         int rc = launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
                               a.grp.meta, a.st);
@@ -683,13 +781,11 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.K = w->F;
         d.N = w->d;
         d.W0 = (const uint8_t*)w->down.rows;
-        d.b0 = w->down.bias;
-        d.wts = a.wts;
         d.yp = a.yp;
         int rc = nt <= MOE_TILE_DMA_NT ? launch_tile_dma<FMT, 1>(d, nt, max_active, a.T, a.st)
                                        : launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
-        return launch_combine(a.yp, a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
+        return launch_combine(a.yp, a.idx, a.wts, w->down.bias, w->E, a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
     }
     return 0;
 }
