@@ -72,10 +72,32 @@ extern "C" {
 typedef struct {
     const void* rows;    /* packed rows [E, N, moe_row_bytes(fmt, K)], 16-byte aligned */
     const float* bias;   /* optional additive row bias fp32 [E, N] (gpt-oss), NULL if none */
+    const void* tiles;   /* optional: the same weights in the tile-major layout below (moe_tiles_pack of rows),
+                            E * moe_tile_bytes(fmt, N, K) bytes, 16-byte aligned. The grouped path (T > 1)
+                            streams these; NULL in any of gate/up/down: it reads rows (slower) */
 } moe_proj_t;
 
 /* Bytes of one packed row of K inputs in format fmt (0 for an invalid fmt or K). */
 size_t moe_row_bytes(int fmt, int K);
+
+/*
+ * Tile-major layout (no counterpart in the reference, whose Metal kernels read its words row by row): the
+ * grouped T > 1 path loads 16 rows x 128 inputs per MFMA step group, and HBM delivers such loads near its peak
+ * only as contiguous bursts, so the same numbers are re-laid out once, at load time, on the device:
+ *   tiles [E][N/16][S = ceil(K/128)][slice record], a slice record = 16 rows x 128 inputs:
+ *     1024 bytes of code words: 16 bytes at offset 16 * (r + 16 g) (row r, lane group g = 0..3) hold the
+ *     row's words (index within the row, s = slice)
+ *         MOE_FMT_INT4_G64: 16s + 2g, 16s + 2g + 1, 16s + 8 + 2g, 16s + 9 + 2g
+ *         MOE_FMT_MXFP4:    16s + g, 16s + 4 + g, 16s + 8 + g, 16s + 12 + g
+ *     then the metadata of the slice's groups, per row r:
+ *         MOE_FMT_INT4_G64: 8 bytes at 1024 + 8r = group words 2s, 2s + 1   (record: 1152 bytes)
+ *         MOE_FMT_MXFP4:    4 bytes at 1024 + 4r = E8M0 bytes of groups 4s .. 4s + 3   (record: 1088 bytes)
+ *     words and groups past K (K % 128 == 64) are zero.
+ * moe_tile_bytes: bytes of one expert's N x K projection in this layout (0 if N % 16, K % 64 or fmt invalid).
+ * moe_tiles_pack: rows [E, N, moe_row_bytes(fmt, K)] -> tiles [E * moe_tile_bytes(fmt, N, K)], on `stream`.
+ */
+size_t moe_tile_bytes(int fmt, int N, int K);
+int moe_tiles_pack(int fmt, int E, int N, int K, const void* rows, void* tiles, void* stream);
 
 /* Expert weights: gate/up [E, F, d], down [E, d, F]. */
 typedef struct {

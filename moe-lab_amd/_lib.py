@@ -21,7 +21,8 @@ PATH_AUTO, PATH_SLOTS, PATH_GROUPED, PATH_FUSED_T1 = 0, 1, 2, 3
 ACT_SWIGLU, ACT_GEGLU, ACT_GPTOSS = 0, 1, 2
 
 EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
-           "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_row_bytes", "moe_version")
+           "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_row_bytes", "moe_tile_bytes",
+           "moe_tiles_pack", "moe_version")
 WORKSPACE_SYNC_BYTES = 4096
 STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 3
 
@@ -41,7 +42,7 @@ class MoeError(RuntimeError):
 
 
 class Proj(ctypes.Structure):
-    _fields_ = [("rows", ctypes.c_void_p), ("bias", ctypes.c_void_p)]
+    _fields_ = [("rows", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("tiles", ctypes.c_void_p)]
 
 
 class Experts(ctypes.Structure):
@@ -71,8 +72,11 @@ def lib():
         L.moe_version.restype = ctypes.c_char_p
         L.moe_row_bytes.argtypes = [i, i]
         L.moe_row_bytes.restype = sz
+        L.moe_tile_bytes.argtypes = [i, i, i]
+        L.moe_tile_bytes.restype = sz
+        L.moe_tiles_pack.argtypes = [i, i, i, i, vp, vp, vp]
         for n in ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
-                  "moe_experts_run_stages"):
+                  "moe_experts_run_stages", "moe_tiles_pack"):
             getattr(L, n).restype = ctypes.c_int
         _lib = L
     return _lib

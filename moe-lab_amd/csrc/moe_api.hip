@@ -2,6 +2,7 @@
 // Validates arguments before any launch, carves the caller's workspace and dispatches to the kernels.
 #include <stdint.h>
 
+#include "moe_formats.h"
 #include "moe_internal.h"
 
 namespace {
@@ -17,7 +18,7 @@ int resolve_path(int path, int T) {
 }
 
 struct Layout {
-    size_t h, yp, xperm, counts, offsets, sorted, active, meta, total;
+    size_t h, yp, counts, offsets, sorted, active, meta, total;
 };
 
 Layout layout(const moe_experts_t* w, int T, int k, int path) {
@@ -29,8 +30,6 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
     if (resolve_path(path, T) == MOE_PATH_GROUPED) {
         L.yp = off;
         off += align_up(nslots * (size_t)w->d * 4);
-        L.xperm = off;
-        off += align_up((size_t)T * w->d * 2);
         L.counts = off;
         off += align_up((size_t)w->E * 4);
         L.offsets = off;
@@ -48,7 +47,7 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
 
 int check_proj(const moe_proj_t& p) {
     if (!p.rows) return MOE_ERR_ARG;
-    if (!aligned16(p.rows)) return MOE_ERR_ALIGN;
+    if (!aligned16(p.rows) || (p.tiles && !aligned16(p.tiles))) return MOE_ERR_ALIGN;
     return MOE_OK;
 }
 
@@ -74,6 +73,19 @@ size_t moe_row_bytes(int fmt, int K) {
     if (fmt == MOE_FMT_INT4_G64) return ((size_t)K / 2 + (size_t)K / 16 + 15) & ~(size_t)15;
     if (fmt == MOE_FMT_MXFP4) return ((size_t)K / 2 + (size_t)K / 32 + 15) & ~(size_t)15;
     return 0;
+}
+
+size_t moe_tile_bytes(int fmt, int N, int K) {
+    if ((fmt != MOE_FMT_INT4_G64 && fmt != MOE_FMT_MXFP4) || N < 16 || N % 16 || K < 64 || K % 64) return 0;
+    return moe::tile_bytes(fmt, N, K);
+}
+
+int moe_tiles_pack(int fmt, int E, int N, int K, const void* rows, void* tiles, void* stream) {
+    if (fmt != MOE_FMT_INT4_G64 && fmt != MOE_FMT_MXFP4) return MOE_ERR_DTYPE;
+    if (E < 1 || N < 16 || N % 16 || K < 64 || K % 64 || N > 65535 * 16 || E > 65535) return MOE_ERR_ARG;
+    if (!rows || !tiles) return MOE_ERR_ARG;
+    if (!aligned16(rows) || !aligned16(tiles)) return MOE_ERR_ALIGN;
+    return moe::launch_pack_tiles(fmt, E, N, K, rows, tiles, (hipStream_t)stream);
 }
 
 int moe_router_counter_count(int T) { return T < 1 ? 1 : moe::router_counter_slots(T); }
@@ -154,7 +166,6 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     a.sync = (int32_t*)ws;
     if (rpath == MOE_PATH_GROUPED) {
         a.yp = (float*)(ws + L.yp);
-        a.xperm = (uint16_t*)(ws + L.xperm);
         a.grp.counts = (int32_t*)(ws + L.counts);
         a.grp.offsets = (int32_t*)(ws + L.offsets);
         a.grp.sorted = (int32_t*)(ws + L.sorted);

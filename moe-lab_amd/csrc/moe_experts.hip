@@ -463,34 +463,53 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
 
 // ============================================================================ combine
 // y[t, n] = residual[t, n] + sum_j wts[t, j] * (yp[t*k + j, n] + bd[idx[t, j], n]); slots whose id is outside
-// [0, E) add nothing. 4 outputs per thread (D % 4 == 0).
+// [0, E) add nothing. 4 outputs per thread (D % 4 == 0). The slots are taken 8 at a time: their ids and
+// weights first, then every yp row (and bias row) load of the 8 at once (rows of skipped slots are read
+// too, then discarded by a select, so no load waits on an id), then the sums in slot order.
 __global__ void __launch_bounds__(256)
 k_combine(const float* __restrict__ yp, const int32_t* __restrict__ idx, const float* __restrict__ wts,
           const float* __restrict__ bd, int E, const void* __restrict__ resid, void* __restrict__ y, int T, int k,
           int D, int y32) {
+    constexpr int KC = 8;
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total4 = (size_t)T * D / 4;
     if (i4 >= total4) return;
     const size_t i = i4 * 4;
     const int t = (int)(i / D), n = (int)(i % D);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j < k; ++j) {
-        const int slot = t * k + j;
-        const int e = idx[slot];
-        if ((unsigned)e >= (unsigned)E) continue;
-        const float w = wts[slot];
-        float4 v = reinterpret_cast<const float4*>(yp + (size_t)slot * D + n)[0];
-        if (bd) {
-            const float4 b = reinterpret_cast<const float4*>(bd + (size_t)e * D + n)[0];
-            v.x += b.x;
-            v.y += b.y;
-            v.z += b.z;
-            v.w += b.w;
+    for (int j0 = 0; j0 < k; j0 += KC) {
+        int e[KC];
+        float w[KC];
+        float4 v[KC], b[KC];
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const int slot = t * k + (j0 + j < k ? j0 + j : k - 1);
+            e[j] = idx[slot];
+            w[j] = wts[slot];
+            v[j] = reinterpret_cast<const float4*>(yp + (size_t)slot * D + n)[0];
         }
-        acc.x = __builtin_fmaf(w, v.x, acc.x);
-        acc.y = __builtin_fmaf(w, v.y, acc.y);
-        acc.z = __builtin_fmaf(w, v.z, acc.z);
-        acc.w = __builtin_fmaf(w, v.w, acc.w);
+        if (bd) {
+#pragma unroll
+            for (int j = 0; j < KC; ++j) {
+                const int ee = (unsigned)e[j] < (unsigned)E ? e[j] : 0;
+                b[j] = reinterpret_cast<const float4*>(bd + (size_t)ee * D + n)[0];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const bool ok = j0 + j < k && (unsigned)e[j] < (unsigned)E;
+            float4 u = v[j];
+            if (bd) {
+                u.x += b[j].x;
+                u.y += b[j].y;
+                u.z += b[j].z;
+                u.w += b[j].w;
+            }
+            acc.x = ok ? __builtin_fmaf(w[j], u.x, acc.x) : acc.x;
+            acc.y = ok ? __builtin_fmaf(w[j], u.y, acc.y) : acc.y;
+            acc.z = ok ? __builtin_fmaf(w[j], u.z, acc.z) : acc.z;
+            acc.w = ok ? __builtin_fmaf(w[j], u.w, acc.w) : acc.w;
+        }
     }
     if (y32) {
         if (resid) {

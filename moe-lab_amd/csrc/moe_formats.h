@@ -19,6 +19,14 @@ __host__ __device__ __forceinline__ size_t rbytes(int fmt, int K) {
     return ((size_t)K / 2 + meta + 15) & ~(size_t)15;
 }
 
+// tile-major slice records (include/moe_mi355x.h: moe_tile_bytes): 16 rows x 128 inputs of codes + metadata
+constexpr int TILE_SLICE_INT4 = 1024 + 16 * 8;
+constexpr int TILE_SLICE_MXFP4 = 1024 + 16 * 4;
+__host__ __device__ __forceinline__ size_t tile_bytes(int fmt, int N, int K) {
+    const size_t sb = fmt == MOE_FMT_INT4_G64 ? TILE_SLICE_INT4 : TILE_SLICE_MXFP4;
+    return (size_t)(N / 16) * (size_t)((K + 127) / 128) * sb;
+}
+
 // ============================================================================ packed row formats
 struct FmtInt4 {
     static constexpr int FMT = MOE_FMT_INT4_G64;

@@ -38,7 +38,6 @@ struct ExpertsArgs {
     uint16_t* hhi;        // GLU output h = hi + lo, two bf16 planes [T*k, F]
     uint16_t* hlo;
     float* yp;      // [T*k, d] fp32 scratch (grouped path)
-    uint16_t* xperm;   // [T, d] bf16 scratch: x with each 8-input group in the decoded-code order (grouped path)
     GroupBufs grp;  // grouped path
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
     int fused_t1;   // T == 1: try the single-launch kernel first
@@ -50,6 +49,8 @@ struct ExpertsArgs {
 int run_experts_slots(const ExpertsArgs& a);
 // grouped expert tiles on MFMA (moe_tiles.hip): grouping, gate/up + GLU, down, combine
 int run_experts_tiles(const ExpertsArgs& a);
+// rows -> tile-major records (moe_tiles.hip; layout in include/moe_mi355x.h)
+int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tiles, hipStream_t st);
 // combine (moe_experts.hip): y[t] = residual[t] + sum_j wts[t*k + j] * (yp[t*k + j] + bd[idx[t*k + j]])
 int launch_combine(const float* yp, const int32_t* idx, const float* wts, const float* bd, int E,
                    const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);

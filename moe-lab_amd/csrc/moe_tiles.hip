@@ -1,32 +1,36 @@
 // Grouped expert tiles for T > 1 on bf16 MFMA (gfx950 v_mfma_f32_16x16x32_bf16): the expert-tile grouped
 // GEMM of the reference's T > 1 path (metal_q4_tiles_v2.py:160-360 gate/up and down tiles, one MMA tile per
-// 8 rows x 8 slots there), re-cut for 64-wide waves and MFMA.
+// 8 rows x 8 slots there), re-cut for 64-wide waves and MFMA. Two kernels, by weight layout:
+//   k_wave_tile  tile-major weights (moe_tiles_pack): one wave per 16 * RT rows and 16 tokens, no LDS, every
+//                weight load a contiguous 1 KB burst (the fast path; layout and method described below);
+//   k_tile       row records only: a block per 64 rows, K slices staged through LDS (described here).
+// Arithmetic, both (exact operands, fp32 accumulation; the reference's raw-code MMA with per-group fp32 fix-up,
+// metal_q4_tiles_v2.py:242-263): codes decode to bf16 128 + q (int4) or e2m1(q) (MXFP4), exactly; per scale
+// group the MFMA sums P = sum (128 + q) x over the group and, for int4, XS = sum x from one more MFMA with an
+// all-ones operand; then acc += s * P + (b - 128 s) * XS (int4) or acc += 2^(s-127) * P (MXFP4).
+// The GLU output h is stored as two bf16 planes h = hi + lo (about 16 significant bits; the reference keeps
+// it in x.dtype); the down projection runs one MFMA per plane into the same accumulator. The down output is
+// yp[slot] = W_down h in fp32; k_combine adds b_down, applies the routing weights and sums a token's slots.
 //
-// A block owns one active expert and TL_ROWS = 64 weight rows (16 per wave). For gate/up the same wave owns
-// gate row r and up row r, so the GLU is applied in registers; for down it owns 16 rows of W_down. The
+// k_tile: a block owns one active expert and TL_ROWS = 64 weight rows (16 per wave). For gate/up the same wave
+// owns gate row r and up row r, so the GLU is applied in registers; for down it owns 16 rows of W_down. The
 // expert's slots (stable, ascending slot id: the grouping of moe_group) are taken 16 * NT at a time, pass z
 // of an expert by the block with blockIdx.z = z mod gridDim.z (so a popular expert spreads over blocks); each
 // pass streams the block's rows in K slices of TL_KC chunks (256 inputs) through LDS:
 //   A (codes): each thread loads 16-byte chunks of the rows and scatters their 4 words so that lane (r, g)
-//              later reads word g of the slice's chunks with ds_read_b128 (g = lane / 16 is the MFMA K group
-//              of 8 inputs, r = lane % 16 the row);
+//              later reads word g of the slice's chunks (g = lane / 16 is the MFMA K group of 8 inputs,
+//              r = lane % 16 the row);
 //   metadata:  int4 (scale, bias - 128 scale) per 64-group, MXFP4 2^(s-127) per 32-group, as fp32;
 //   B (activations of the pass's tokens): 16-byte pieces of 8 inputs, reordered (0,4,1,5,2,6,3,7) like the
 //              decoded codes; tokens past the expert's count and inputs past K are zero.
 // The next slice's global loads are issued before the current slice's MFMAs (register double buffer).
-//
-// Arithmetic (exact operands, fp32 accumulation; the reference's raw-code MMA with per-group fp32 fix-up,
-// metal_q4_tiles_v2.py:242-263): codes decode to bf16 128 + q (int4) or e2m1(q) (MXFP4), exactly; per scale
-// group the MFMA sums P = sum (128 + q) x over the group and, for int4, XS = sum x from one more MFMA with an
-// all-ones A operand; then acc += s * P + (b - 128 s) * XS (int4) or acc += 2^(s-127) * P (MXFP4).
-// The GLU output h is stored as two bf16 planes h = hi + lo (about 16 significant bits; the reference keeps
-// it in x.dtype); the down projection runs one MFMA per plane into the same accumulator. The down output is
-// yp[slot] = W_down h in fp32; k_combine adds b_down, applies the routing weights and sums a token's slots.
 #include "moe_common.h"
 #include "moe_formats.h"
 #include "moe_internal.h"
 
 #include <math.h>
+
+#include <type_traits>
 
 namespace moe {
 
@@ -213,20 +217,10 @@ k_tile(TileArgs a) {
             if (s + 1 < nslice) load_slice(s + 1);   // in flight during this slice's math
 
             // ---- math: this wave's 16 rows, every token tile of the pass
-            uint32_t awv[NPROJ][TL_KC];
-#pragma unroll
-            for (int p = 0; p < NPROJ; ++p)
-#pragma unroll
-                for (int q = 0; q < TL_KC / 4; ++q) {
-                    const uint4 aw = *reinterpret_cast<const uint4*>(&sA[p][16 * wave + lr][TL_KC * lg + 4 * q]);
-                    awv[p][4 * q] = aw.x;
-                    awv[p][4 * q + 1] = aw.y;
-                    awv[p][4 * q + 2] = aw.z;
-                    awv[p][4 * q + 3] = aw.w;
-                }
             constexpr int CPG = INT4 ? 2 : 1;   // chunks per scale group
 #pragma unroll
             for (int gi = 0; gi < TL_KC / CPG; ++gi) {
+                __builtin_amdgcn_sched_barrier(0);
                 // this group's metadata for the lane's 4 output rows: (s, b - 128 s) or the MXFP4 scale
                 float ms[NPROJ][4], mc[NPROJ][4];
 #pragma unroll
@@ -249,7 +243,7 @@ k_tile(TileArgs a) {
 #pragma unroll
                     for (int cc = 0; cc < CPG; ++cc) {
                         uint32_t q[4];
-                        FMT::decode_word(awv[p][gi * CPG + cc], q);
+                        FMT::decode_word(sA[p][16 * wave + lr][TL_KC * lg + gi * CPG + cc], q);
                         A[p][cc] = as_bf16x8(q[0], q[1], q[2], q[3]);
                     }
 #pragma unroll
@@ -324,364 +318,266 @@ k_tile(TileArgs a) {
     }
 }
 
-// ============================================================================ DMA-ring tiles (NT <= 2)
-// The same tile arithmetic with every operand brought into LDS by direct global->LDS DMA
-// (global_load_lds_dwordx4: 16 bytes per lane, written at M0 + 16 * lane) into a ring of DR_NS stages, so
-// DR_NS - 1 slices per block are in flight without holding registers. The stage buffers are distinct
-// __shared__ objects indexed at compile time (the ring is unrolled), and blocks sync with a bare s_barrier,
-// so the waits on the DMA are the explicit per-stage vmcnt waits below, not a full drain.
-// Stage layouts (a K slice = DR_KC chunks = 256 inputs):
-//   A [proj][row 0..63][pos 0..7] 16-byte chunks, pos = chunk ^ (row & 7) (bank spread for the reads of
-//     lane (r, g): word g of chunk c of row r);
-//   M int4: [proj][row] 16 bytes = the slice's 4 (scale | bias) words; MXFP4: [proj][word 0..1][row] 4 bytes;
-//   B [plane][token 0..NTOK-1][pos 0..31] 16-byte pieces of 8 inputs, pos = piece ^ (token & 7); the
-//     activations are already in the decoded-code order (x copied by k_pair8_rows, h written so).
-// Chunks past K are clamped onto the row's last chunk and masked to zero on the A side; tokens past the
-// expert's count are clamped onto its last token and their output columns dropped.
-constexpr int DR_KC = 8;
-constexpr int DR_NS = 3;
-
-#define MOE_LDSP(p) ((__attribute__((address_space(3))) void*)(p))
-// workgroup barrier without a memory fence (a fence would drain every outstanding DMA); the "memory" clobber
-// keeps the compiler from moving LDS accesses across it
-#define MOE_BARRIER() asm volatile("s_barrier" ::: "memory")
-#define MOE_VMWAIT(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (((N) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
-
-template <class FMT, int NPROJ, int NT>
-struct DrStage {
-    static constexpr int NTOK = 16 * NT;
-    static constexpr int HL = NPROJ == 2 ? 1 : 2;
-    static constexpr int MBYTES = FMT::XSUM ? 16 : 8;
-    uint4 A[NPROJ][TL_ROWS][DR_KC];
-    uint32_t M[NPROJ][TL_ROWS * MBYTES / 4];
-    uint4 B[HL][NTOK][4 * DR_KC];
-};
-
-template <class FMT, int NPROJ, int NT>
-__device__ __forceinline__ void dr_issue(DrStage<FMT, NPROJ, NT>& S, int s, const uint8_t* const Wp[2], size_t rb,
-                                         int K, int cpr, const size_t* brow, const uint16_t* act0,
-                                         const uint16_t* act1, int wave, int lane, int npair) {
-    using St = DrStage<FMT, NPROJ, NT>;
-    // A: 8 instructions per projection, 8 rows x 8 chunks each; wave w takes instructions w, w + 4
-#pragma unroll
-    for (int p = 0; p < NPROJ; ++p)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int i = wave + 4 * j;
-            const int row = 8 * i + (lane >> 3), pos = lane & 7;
-            const int gc = min(s * DR_KC + (pos ^ (row & 7)), cpr - 1);
-            __builtin_amdgcn_global_load_lds((const void*)(Wp[p] + (size_t)row * rb + 16 * gc),
-                                             MOE_LDSP(&S.A[p][8 * i][0]), 16, 0, 0);
-        }
-    // M
-    if (FMT::XSUM) {
-        if (wave < NPROJ) {   // the slice's 4 group words of row `lane` (record padding covers a short last slice)
-            __builtin_amdgcn_global_load_lds((const void*)(Wp[wave] + (size_t)lane * rb + (K >> 1) + 16 * s),
-                                             MOE_LDSP(&S.M[wave][0]), 16, 0, 0);
-        }
-    } else {
-        if (wave < 2 * NPROJ) {   // E8M0 bytes 8s .. 8s+3 (word 0) and 8s+4 .. 8s+7 (word 1)
-            const int p = wave >> 1, wj = wave & 1;
-            const int byte0 = 8 * s + 4 * ((8 * s + 4 < cpr) ? wj : 0);
-            __builtin_amdgcn_global_load_lds((const void*)(Wp[p] + (size_t)lane * rb + (K >> 1) + byte0),
-                                             MOE_LDSP(&S.M[p][wj * TL_ROWS]), 4, 0, 0);
-        }
-    }
-    // B: 2 tokens x 32 pieces per instruction; wave w takes instructions w, w + 4, ... below npair (the token
-    // pairs the pass has: columns past the expert's count are never read into the math's kept outputs)
-    constexpr int NBI = St::NTOK / 2;
-#pragma unroll
-    for (int hl = 0; hl < St::HL; ++hl)
-#pragma unroll
-        for (int j = 0; j < NBI / 4; ++j) {
-            const int i = wave + 4 * j;
-            if (i >= npair) continue;   // wave-uniform
-            const int tk = 2 * i + (lane >> 5), pos = lane & 31;
-            const int piece = pos ^ (tk & 7);
-            const int k0 = min(s * (32 * DR_KC) + 8 * piece, K - 8);
-            __builtin_amdgcn_global_load_lds((const void*)((hl ? act1 : act0) + brow[j] + k0),
-                                             MOE_LDSP(&S.B[hl][2 * i][0]), 16, 0, 0);
-        }
+// ============================================================================ wave tiles (tile-major weights)
+// The grouped path's weights in the tile-major layout of moe_tiles_pack (include/moe_mi355x.h): for every
+// expert, 16-row tile and slice of 128 inputs, one contiguous record holding the 16 rows' codes already in
+// the MFMA operand order, then their group metadata. A wave's load of one slice of one tile is one 1 KB
+// contiguous burst (16 B per lane, lane order); HBM streams such bursts near its peak, where loads that
+// stride across row records (16 rows x 64 B per instruction) do not.
+//
+// Each 64-lane wave is a workgroup of its own and owns 16 * RT rows (of gate and up, or of down) for 16 * NT
+// tokens of one expert; there is no LDS and no barrier. The product is computed token-major,
+// D[token, row] = X[token, :] . W[row, :], on v_mfma_f32_16x16x32_bf16 with the activations as the A operand
+// (lane (m, g) = token m, 8 inputs) and the decoded codes as the B operand (lane (r, g) = row r, 8 codes), so
+// an output lane holds 4 tokens of ONE row and needs that row's group metadata only.
+// A slice is 4 MFMA steps j; lane (r, g) holds the 4 code words it supplies, word j for step j, which are the
+// row's words (w = 16 s + ...)
+//     int4 g64:  j = 0, 1: 2 g + j        j = 2, 3: 8 + 2 g + (j - 2)     (steps 0,1 group 2s; 2,3 group 2s+1)
+//     MXFP4 g32: 4 j + g                                                  (step j = group 4 s + j)
+// and the A lane of token m loads the 8 activations of the same word (the piece with its index). x arrives in
+// natural order and is paired in registers (pair8); h is written by the gate/up wave tile already paired, as
+// the decoded codes are: element order (0,4,1,5,2,6,3,7) within each 8.
+// Every global load of slice s is issued D slices ahead into a register ring, in one fixed order, so the
+// in-order vmcnt wait for slice s leaves the D - 1 slices behind it in flight.
+// Tokens past the expert's count load the count's last token again (same addresses: no extra traffic); their
+// D rows are dropped (a row of D depends on the same row of X only). Inputs past K (the last slice when
+// K % 128 == 64) have zero codes and zero metadata in the record, and their activation loads are clamped into
+// the row, so they add 0.
+__device__ __forceinline__ int paired_pos(int r) {   // position of element r of its 8 in the paired order
+    const int j = r & 7;
+    return (r & ~7) | (j < 4 ? 2 * j : 2 * j - 7);
 }
 
-// DMA instructions a wave issues per stage: 2 per projection for A, one for the metadata on the waves that
-// fetch it, and one per activation plane for each of its token-pair instructions below npair
-template <class FMT, int NPROJ, int NT>
-__device__ __forceinline__ int dr_wave_issues(int wave, int npair) {
-    constexpr int NBI = 16 * NT / 2;
-    int b = 0;
-#pragma unroll
-    for (int j = 0; j < NBI / 4; ++j) b += (wave + 4 * j < npair) ? 1 : 0;
-    const bool meta = FMT::XSUM ? wave < NPROJ : wave < 2 * NPROJ;
-    return 2 * NPROJ + (meta ? 1 : 0) + (NPROJ == 2 ? 1 : 2) * b;
-}
-// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 15]
-__device__ __forceinline__ void vm_wait_n(int n) {
-    switch (n) {
-        case 0: MOE_VMWAIT(0); break;
-        case 1: MOE_VMWAIT(1); break;
-        case 2: MOE_VMWAIT(2); break;
-        case 3: MOE_VMWAIT(3); break;
-        case 4: MOE_VMWAIT(4); break;
-        case 5: MOE_VMWAIT(5); break;
-        case 6: MOE_VMWAIT(6); break;
-        case 7: MOE_VMWAIT(7); break;
-        case 8: MOE_VMWAIT(8); break;
-        case 9: MOE_VMWAIT(9); break;
-        case 10: MOE_VMWAIT(10); break;
-        case 11: MOE_VMWAIT(11); break;
-        case 12: MOE_VMWAIT(12); break;
-        case 13: MOE_VMWAIT(13); break;
-        case 14: MOE_VMWAIT(14); break;
-        default: MOE_VMWAIT(15); break;
-    }
+template <class FMT>
+__host__ __device__ constexpr int tile_slice_bytes() {
+    return FMT::XSUM ? TILE_SLICE_INT4 : TILE_SLICE_MXFP4;
 }
 
-
-// Transposed MFMA for the DMA tiles: the activations are the 16 x 32 operand (16 tokens), the decoded codes the
-// 32 x 16 one (16 weight rows), so lane (lr, lg) ends with tokens 4 lg + v (v = 0..3) of weight row lr: one
-// metadata word per group and projection per lane, and xs (sum of a token's inputs over the group) comes
-// from the same MFMA with an all-ones weight operand.
-template <class FMT, int NPROJ, int NT>
-__device__ __forceinline__ void dr_math(const DrStage<FMT, NPROJ, NT>& S, int s, int cpr, int K, int wave, int lr,
-                                        int lg, f32x4 (&acc)[NPROJ][NT]) {
+template <class FMT, int NPROJ, int NT, int RT, int D>
+__global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     constexpr bool INT4 = FMT::XSUM;
-    constexpr int HL = NPROJ == 2 ? 1 : 2;
-    constexpr int CPG = INT4 ? 2 : 1;
-    const uint32_t ones = 0x3F803F80u;
-    const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
-    const int R = 16 * wave + lr;   // this lane's weight row inside the tile
-    uint32_t awv[NPROJ][DR_KC];
-#pragma unroll
-    for (int p = 0; p < NPROJ; ++p) {
-        const uint32_t* rowp = reinterpret_cast<const uint32_t*>(&S.A[p][R][0]);
-#pragma unroll
-        for (int c = 0; c < DR_KC; ++c) awv[p][c] = rowp[4 * (c ^ (R & 7)) + lg];
-    }
-    // metadata of row R: int4 4 group words, MXFP4 8 E8M0 bytes
-    uint32_t mw[NPROJ][INT4 ? 4 : 2];
-#pragma unroll
-    for (int p = 0; p < NPROJ; ++p) {
-        if (INT4) {
-            const uint4 m4 = *reinterpret_cast<const uint4*>(&S.M[p][4 * R]);
-            mw[p][0] = m4.x;
-            mw[p][1] = m4.y;
-            mw[p][2] = m4.z;
-            mw[p][3] = m4.w;
-        } else {
-            mw[p][0] = S.M[p][R];
-            mw[p][INT4 ? 0 : 1] = S.M[p][TL_ROWS + R];
-        }
-    }
-    const int nvalid = cpr - s * DR_KC;   // chunks of this slice inside the row (>= DR_KC: all)
-#pragma unroll
-    for (int gi = 0; gi < DR_KC / CPG; ++gi) {
-        float ms[NPROJ], mc[NPROJ];
-#pragma unroll
-        for (int p = 0; p < NPROJ; ++p) {
-            if (INT4) {
-                const uint32_t m = mw[p][gi];
-                const bool ok = 4 * s + gi < (K >> 6);
-                const float sc = ok ? bf16lo(m) : 0.f;
-                ms[p] = sc;
-                mc[p] = ok ? __builtin_fmaf(-128.f, sc, bf16hi(m)) : 0.f;
-            } else {
-                const uint32_t b = (mw[p][gi >> 2] >> (8 * (gi & 3))) & 0xFFu;
-                ms[p] = gi < nvalid ? __uint_as_float(b << 23) : 0.f;
-                mc[p] = 0.f;
-            }
-        }
-        bf16x8 W[NPROJ][CPG];
-#pragma unroll
-        for (int p = 0; p < NPROJ; ++p)
-#pragma unroll
-            for (int cc = 0; cc < CPG; ++cc) {
-                uint32_t q[4];
-                FMT::decode_word(awv[p][gi * CPG + cc], q);
-                if (gi * CPG + cc >= nvalid) q[0] = q[1] = q[2] = q[3] = 0u;   // chunk past K
-                W[p][cc] = as_bf16x8(q[0], q[1], q[2], q[3]);
-            }
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int tk = 16 * t + lr;
-            bf16x8 X[HL][CPG];
-#pragma unroll
-            for (int hl = 0; hl < HL; ++hl)
-#pragma unroll
-                for (int cc = 0; cc < CPG; ++cc) {
-                    const int piece = 4 * (gi * CPG + cc) + lg;
-                    const uint4 bv = S.B[hl][tk][piece ^ (tk & 7)];
-                    X[hl][cc] = as_bf16x8(bv.x, bv.y, bv.z, bv.w);
-                }
-            f32x4 xs = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (INT4) {
-#pragma unroll
-                for (int hl = 0; hl < HL; ++hl)
-#pragma unroll
-                    for (int cc = 0; cc < CPG; ++cc)
-                        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[hl][cc], ONES, xs, 0, 0, 0);
-            }
-#pragma unroll
-            for (int p = 0; p < NPROJ; ++p) {
-                f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int hl = 0; hl < HL; ++hl)
-#pragma unroll
-                    for (int cc = 0; cc < CPG; ++cc)
-                        P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[hl][cc], W[p][cc], P, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    if (INT4)
-                        acc[p][t][v] = __builtin_fmaf(ms[p], P[v], __builtin_fmaf(mc[p], xs[v], acc[p][t][v]));
-                    else
-                        acc[p][t][v] = __builtin_fmaf(ms[p], P[v], acc[p][t][v]);
-                }
-            }
-        }
-    }
-}
-
-// position of element i (0..7) of an 8-input group in the decoded-code order (0,4,1,5,2,6,3,7)
-__device__ __forceinline__ int code_pos8(int i) { return i < 4 ? 2 * i : 2 * (i - 4) + 1; }
-
-// One block: one active expert (blockIdx.y), token pass blockIdx.z, and the row tiles
-// blockIdx.x * RPB .. + RPB - 1 of that expert (RPB = a.rpb). The ring runs across the block's tiles, so
-// the next tile's first slices are in flight while the current tile finishes. A tile's output is computed
-// in registers at its last slice and stored at the next step, after that step's wait and barrier (stores
-// issued after a stage's DMA would be counted ahead of it by the next vmcnt wait).
-template <class FMT, int NPROJ, int NT>
-__global__ void __launch_bounds__(256)
-k_tile_run(TileArgs a) {
-    using St = DrStage<FMT, NPROJ, NT>;
-    constexpr int NTOK = St::NTOK;
-    constexpr int NBI = NTOK / 2;
-    __shared__ St S0, S1, S2;
-
+    constexpr int HL = NPROJ == 2 ? 1 : 2;   // activation planes: x, or h = hi + lo
+    constexpr int SB = tile_slice_bytes<FMT>();
     if ((int)blockIdx.y >= a.meta[0]) return;
     const int e = a.active[blockIdx.y];
     const int n = a.counts[e], beg = a.offsets[e];
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int lr = lane & 15, lg = lane >> 4;
+    const int lane = threadIdx.x, lr = lane & 15, lg = lane >> 4;
     const int K = a.K, N = a.N;
-    const int cpr = K >> 5;
-    const int nslice = (cpr + DR_KC - 1) / DR_KC;
-    const size_t rb = rbytes(FMT::FMT, K);
-    const int RT = N / TL_ROWS;
-    const int rt0 = blockIdx.x * a.rpb;
-    const int ntile = min(a.rpb, RT - rt0);
-    if (ntile <= 0) return;
-    const int U = ntile * nslice;
-    const uint8_t* const W0e = a.W0 + (size_t)e * N * rb;
-    const uint8_t* const W1e = (NPROJ == 2 ? a.W1 : a.W0) + (size_t)e * N * rb;
-
-    for (int tok0 = NTOK * blockIdx.z; tok0 < n; tok0 += NTOK * gridDim.z) {
-        const int npair = (min(NTOK, n - tok0) + 1) >> 1;   // token pairs of this pass
-        const int WI = dr_wave_issues<FMT, NPROJ, NT>(wave, npair);   // this wave's DMA count per stage (<= 15)
-        // activation rows of the B instructions this lane issues, and the output slot of each token column
-        size_t brow[NBI / 4 > 0 ? NBI / 4 : 1];
+    const int nsl = (K + 127) >> 7;
+    const int lastp = (K >> 3) - 1;   // last activation piece of a row
+    const int r0 = blockIdx.x * 16 * RT;
+    // wave-uniform tile bases (tile r0 / 16 + rt of expert e); lane offsets stay 32-bit
+    const uint8_t* tb[NPROJ][RT];
 #pragma unroll
-        for (int j = 0; j < NBI / 4; ++j) {
-            const int tk = 2 * (wave + 4 * j) + (lane >> 5);
-            brow[j] = (size_t)(a.sorted[beg + min(tok0 + tk, n - 1)] / a.act_div) * K;
+    for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            tb[p][rt] = (p ? a.W1 : a.W0) + ((size_t)e * (N >> 4) + (r0 >> 4) + rt) * (size_t)nsl * SB;
+    const uint32_t ones = 0x3F803F80u;
+    const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
+
+    for (int tok0 = 16 * NT * blockIdx.z; tok0 < n; tok0 += 16 * NT * gridDim.z) {
+        // byte offset of the lane's activation row (A side: token tok0 + 16 t + lr)
+        uint32_t xo[NT];
+        int slotA[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int m = tok0 + 16 * t + lr;
+            slotA[t] = a.sorted[beg + (m < n ? m : n - 1)];
+            xo[t] = (uint32_t)(slotA[t] / a.act_div) * (uint32_t)K * 2u;
         }
-        int oslot[NT][4];   // output slot of token 16 t + 4 lg + v (-1: past the expert's count)
+        const uint8_t* xbase[HL];
+        xbase[0] = reinterpret_cast<const uint8_t*>(a.actv);
+        if (HL == 2) xbase[HL - 1] = reinterpret_cast<const uint8_t*>(a.actv2);
+        // register ring: code words, metadata, activation pieces of D slices
+        uint4 rq[D][NPROJ][RT];
+        uint2 rm[D][NPROJ][RT];
+        uint4 rx[D][HL][NT][4];
+        auto issue = [&](int s, uint4 (&q)[NPROJ][RT], uint2 (&m)[NPROJ][RT], uint4 (&x)[HL][NT][4]) {
+#pragma unroll
+            for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const uint8_t* sl = tb[p][rt] + (uint32_t)s * (uint32_t)SB;
+                    q[p][rt] = *reinterpret_cast<const uint4*>(sl + 16 * lane);
+                    if (INT4) m[p][rt] = *reinterpret_cast<const uint2*>(sl + 1024 + 8 * lr);
+                    else m[p][rt].x = *reinterpret_cast<const uint32_t*>(sl + 1024 + 4 * lr);
+                }
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        int piece = INT4 ? 16 * s + 8 * (j >> 1) + 2 * lg + (j & 1) : 16 * s + 4 * j + lg;
+                        piece = piece < lastp ? piece : lastp;
+                        x[hl][t][j] = *reinterpret_cast<const uint4*>(xbase[hl] + (xo[t] + 16u * piece));
+                    }
+        };
+        f32x4 acc[NPROJ][RT][NT];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[p][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto compute = [&](bool live, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT],
+                           const uint4 (&x)[HL][NT][4]) {
+            bf16x8 X[HL][NT][4];
+#pragma unroll
+            for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint4 v = NPROJ == 2 ? pair8(x[hl][t][j]) : x[hl][t][j];
+                        X[hl][t][j] = as_bf16x8(v.x, v.y, v.z, v.w);
+                    }
+            f32x4 xs[NT][2];   // int4: sum of the activations over each of the slice's two groups
+            if (INT4) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int G = 0; G < 2; ++G) {
+                        xs[t][G] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                            for (int u = 0; u < 2; ++u)
+                                xs[t][G] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[hl][t][2 * G + u], ONES, xs[t][G], 0, 0, 0);
+                    }
+            }
+#pragma unroll
+            for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const uint32_t w4[4] = {q[p][rt].x, q[p][rt].y, q[p][rt].z, q[p][rt].w};
+                    bf16x8 B[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t c4[4];
+                        FMT::decode_word(w4[j], c4);
+                        B[j] = as_bf16x8(c4[0], c4[1], c4[2], c4[3]);
+                    }
+                    if (INT4) {
+#pragma unroll
+                        for (int G = 0; G < 2; ++G) {
+                            const uint32_t mw = live ? (G ? m[p][rt].y : m[p][rt].x) : 0u;
+                            const float sc = bf16lo(mw), cb = __builtin_fmaf(-128.f, sc, bf16hi(mw));
+#pragma unroll
+                            for (int t = 0; t < NT; ++t) {
+                                f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                                for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                                    for (int u = 0; u < 2; ++u)
+                                        P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[hl][t][2 * G + u], B[2 * G + u], P, 0, 0, 0);
+#pragma unroll
+                                for (int v = 0; v < 4; ++v)
+                                    acc[p][rt][t][v] = __builtin_fmaf(sc, P[v], __builtin_fmaf(cb, xs[t][G][v], acc[p][rt][t][v]));
+                            }
+                        }
+                    } else {
+                        const uint32_t mw = live ? m[p][rt].x : 0u;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const float sc = __uint_as_float(((mw >> (8 * j)) & 0xFFu) << 23);
+#pragma unroll
+                            for (int t = 0; t < NT; ++t) {
+                                f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                                for (int hl = 0; hl < HL; ++hl)
+                                    P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[hl][t][j], B[j], P, 0, 0, 0);
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) acc[p][rt][t][v] = __builtin_fmaf(sc, P[v], acc[p][rt][t][v]);
+                            }
+                        }
+                    }
+                }
+        };
+        // ring: slices s0 .. s0 + D - 1 in flight at the top of each step. The walk is rounded up to a multiple
+        // of D: slices past the last re-load the last one (cache hits) and fold with scale 0, so the loop body
+        // has no branch. Issued slice by slice in the steady state's order, so the vmcnt waits at the loop top
+        // are the same on entry and on the back edge.
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            issue(i < nsl ? i : nsl - 1, rq[i], rm[i], rx[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int s0 = 0; s0 < nsl; s0 += D) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                compute(s0 + i < nsl, rq[i], rm[i], rx[i]);
+                // keep the slot's re-load below its last reads, so each slot stays in one register set
+                __builtin_amdgcn_sched_barrier(0);
+                const int sn = s0 + i + D;
+                issue(sn < nsl ? sn : nsl - 1, rq[i], rm[i], rx[i]);
+            }
+        }
+        // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int j = tok0 + 16 * t + 4 * lg + v;
-                oslot[t][v] = j < n ? a.sorted[beg + j] : -1;
-            }
-        f32x4 acc[NPROJ][NT];
-        float pbias[NPROJ];   // gate/up additive biases of this lane's row of the current tile
-        // pending output of the last finished tile, per token: gate/up (hi | lo << 16); down fp32
-        uint32_t pend[NT][4];
-        int pend_row = -1;   // output row of the pending tile for this lane (-1: nothing pending)
-
-        auto flush = [&]() {
-            if (pend_row < 0) return;
-            // h is written in the decoded-code order inside each 8-input group: row r -> 8 (r / 8) + pos8(r % 8)
-            const int hpos = (pend_row & ~7) + code_pos8(pend_row & 7);
+                const int j = 4 * lg + v;
+                const int slot = __shfl(slotA[t], j, 64);   // lane j (any lane group) holds token j's slot
+                if (tok0 + 16 * t + j >= n) continue;
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    if (oslot[t][v] < 0) continue;
+                for (int rt = 0; rt < RT; ++rt) {
+                    const int r = r0 + 16 * rt + lr;
                     if (NPROJ == 2) {
-                        a.hout[(size_t)oslot[t][v] * N + hpos] = (uint16_t)(pend[t][v] & 0xFFFFu);
-                        a.hout2[(size_t)oslot[t][v] * N + hpos] = (uint16_t)(pend[t][v] >> 16);
+                        float g = acc[0][rt][t][v], up = acc[NPROJ - 1][rt][t][v];
+                        if (a.b0) g += a.b0[(size_t)e * N + r];
+                        if (a.b1) up += a.b1[(size_t)e * N + r];
+                        const float hv = glu_act(a.act, g, up);
+                        const uint16_t hi = f32_to_bf16(hv);
+                        const size_t o = (size_t)slot * N + paired_pos(r);
+                        a.hout[o] = hi;
+                        a.hout2[o] = f32_to_bf16(hv - bf16_to_f32(hi));
                     } else {
-                        a.yp[(size_t)oslot[t][v] * N + pend_row] = __uint_as_float(pend[t][v]);
+                        a.yp[(size_t)slot * N + r] = acc[0][rt][t][v];
                     }
                 }
-            pend_row = -1;
-        };
-        auto issue = [&](auto& S, int u) {
-            const int q = u / nslice, si = u - q * nslice;
-            const size_t roff = (size_t)(rt0 + q) * TL_ROWS * rb;
-            const uint8_t* const Wp[2] = {W0e + roff, W1e + roff};
-            dr_issue(S, si, Wp, rb, K, cpr, brow, a.actv, a.actv2, wave, lane, npair);
-        };
-        auto compute = [&](const auto& S, int u) {
-            const int q = u / nslice, si = u - q * nslice;
-            if (si == 0) {
-#pragma unroll
-                for (int p = 0; p < NPROJ; ++p)
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) acc[p][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-                // loaded here, ahead of the tile's later stages, so waiting for them at the tile's end
-                // never waits for a stage that is not needed yet
-                const int row = (rt0 + q) * TL_ROWS + 16 * wave + lr;
-                pbias[0] = (NPROJ == 2 && a.b0) ? a.b0[(size_t)e * N + row] : 0.f;
-                pbias[NPROJ - 1] = (NPROJ == 2 && a.b1) ? a.b1[(size_t)e * N + row] : 0.f;
             }
-            dr_math(S, si, cpr, K, wave, lr, lg, acc);
-            if (si == nslice - 1) {   // tile done: its output into registers, stored at the next step
-                const int rbase = (rt0 + q) * TL_ROWS + 16 * wave + lr;   // this lane's output row
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        if (NPROJ == 2) {
-                            const float g = acc[0][t][v] + pbias[0], up = acc[NPROJ - 1][t][v] + pbias[NPROJ - 1];
-                            const float hv = glu_act(a.act, g, up);
-                            const uint16_t hi = f32_to_bf16(hv);
-                            pend[t][v] = (uint32_t)hi | ((uint32_t)f32_to_bf16(hv - bf16_to_f32(hi)) << 16);
-                        } else {
-                            pend[t][v] = __float_as_uint(acc[0][t][v]);
-                        }
-                    }
-                pend_row = rbase;
-            }
-        };
-
-        MOE_BARRIER();   // every wave is done reading the ring from the previous pass
-        issue(S0, 0);
-        if (U > 1) issue(S1, 1);
-        for (int u = 0; u < U; u += DR_NS) {
-#define MOE_DR_STEP(CUR, NXT, OFF)                                         \
-    if (u + OFF < U) {                                                     \
-        vm_wait_n(u + OFF + 1 >= U ? 0 : WI);                              \
-        MOE_BARRIER();                                                     \
-        flush();                                                           \
-        if (u + OFF + 2 < U) issue(NXT, u + OFF + 2);                      \
-        compute(CUR, u + OFF);                                             \
-    }
-            MOE_DR_STEP(S0, S2, 0)
-            MOE_DR_STEP(S1, S0, 1)
-            MOE_DR_STEP(S2, S1, 2)
-#undef MOE_DR_STEP
-        }
-        flush();
     }
 }
 
-// x [T, d] -> the same rows with each 8-input group in the decoded-code order (for the DMA tiles' B side)
-__global__ void __launch_bounds__(256)
-k_pair8_rows(const uint4* __restrict__ x, uint4* __restrict__ xp, size_t npieces) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < npieces) xp[i] = pair8(x[i]);
+// rows [E, N, rbytes] -> tiles [E, N/16, ceil(K/128), slice record]; grid (slices, N/16, E), 64 lanes
+template <class FMT>
+__global__ void __launch_bounds__(64) k_pack_tiles(const uint8_t* __restrict__ rows, uint8_t* __restrict__ tiles,
+                                                   int N, int K) {
+    constexpr int SB = tile_slice_bytes<FMT>();
+    const int s = blockIdx.x, tile = blockIdx.y, e = blockIdx.z;
+    const int lane = threadIdx.x, r = lane & 15, g = lane >> 4;
+    const int nsl = gridDim.x;
+    const size_t rb = rbytes(FMT::FMT, K);
+    const uint8_t* row = rows + ((size_t)e * N + 16 * tile + r) * rb;
+    const uint32_t* words = reinterpret_cast<const uint32_t*>(row);
+    uint8_t* rec = tiles + (((size_t)e * (N >> 4) + tile) * nsl + s) * SB;
+    const int nw = K >> 3;   // code words of a row
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int wi = FMT::XSUM ? 16 * s + 8 * (j >> 1) + 2 * g + (j & 1) : 16 * s + 4 * j + g;
+        w[j] = wi < nw ? words[wi] : 0u;
+    }
+    *reinterpret_cast<uint4*>(rec + 16 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
+    if (g == 0) {
+        if (FMT::XSUM) {   // group words 2s, 2s + 1
+            const int ng = K >> 6;
+            const uint32_t* mw = reinterpret_cast<const uint32_t*>(row + (K >> 1));
+            const uint32_t m0 = 2 * s < ng ? mw[2 * s] : 0u, m1 = 2 * s + 1 < ng ? mw[2 * s + 1] : 0u;
+            *reinterpret_cast<uint2*>(rec + 1024 + 8 * r) = make_uint2(m0, m1);
+        } else {           // E8M0 bytes of groups 4s .. 4s + 3
+            const int ng = K >> 5;
+            const uint8_t* mb = row + (K >> 1);
+            uint32_t m = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * s + j < ng) m |= (uint32_t)mb[4 * s + j] << (8 * j);
+            *reinterpret_cast<uint32_t*>(rec + 1024 + 4 * r) = m;
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------ host side
@@ -706,33 +602,32 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-#ifndef MOE_TILE_BLOCKS
-#define MOE_TILE_BLOCKS 512   // blocks the DMA tile launch aims at (2 per CU); tiles per block follow from it
+#ifndef MOE_WAVE_NT
+#define MOE_WAVE_NT 2   // token tiles per pass up to which the wave tiles run (above: LDS-staged k_tile)
 #endif
-template <class FMT, int NPROJ>
-int launch_tile_dma(TileArgs t, int nt, int max_active, int T, hipStream_t st) {
-    const int zp0 = (T + 16 * nt - 1) / (16 * nt);
-    const int zp = zp0 < 1 ? 1 : (zp0 > 16 ? 16 : zp0);
-    const int RT = t.N / TL_ROWS;
-    // row tiles per block so that the busy blocks come near MOE_TILE_BLOCKS when routing is uniform (E(1 -
-    // (1 - k/E)^T) experts active); capped at 2 so skewed routing, with few experts, still fills the device
-    const double kE = (double)t.kslots / (double)t.E;
-    double act = t.E * (1.0 - pow(1.0 - (kE < 1.0 ? kE : 1.0), (double)T));
-    if (act > max_active) act = max_active;
-    int rpb = (int)((act * RT + MOE_TILE_BLOCKS - 1) / MOE_TILE_BLOCKS);
-    rpb = rpb < 1 ? 1 : (rpb > 2 ? 2 : rpb);
-    if (rpb > RT) rpb = RT;
-    t.rpb = rpb;
-    dim3 grid((RT + rpb - 1) / rpb, max_active, zp);
-    if (nt == 1) k_tile_run<FMT, NPROJ, 1><<<grid, 256, 0, st>>>(t);
-    else k_tile_run<FMT, NPROJ, 2><<<grid, 256, 0, st>>>(t);
+// Wave-tile shape (measured on MI355X at the Qwen3 T = 16..64 shapes): more rows per wave share each activation
+// load across more weight bursts, more slices in flight hide more latency; both cost registers (occupancy).
+#ifndef MOE_WAVE_D_GU
+#define MOE_WAVE_D_GU 2    // slices (128 inputs) in flight per wave, gate/up
+#endif
+#ifndef MOE_WAVE_D_DN
+#define MOE_WAVE_D_DN 2    // slices in flight per wave, down (its activations are two planes)
+#endif
+#ifndef MOE_WAVE_RT_GU
+#define MOE_WAVE_RT_GU 2   // 16-row tiles per wave, gate/up (F % 32 == 0: F % 64 == 0 is required)
+#endif
+#ifndef MOE_WAVE_RT_DN
+#define MOE_WAVE_RT_DN 4   // 16-row tiles per wave, down (d % 64 == 0)
+#endif
+template <class FMT, int NPROJ, int RT, int D>
+int launch_wave_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st) {
+    if (t.N % (16 * RT)) return MOE_ERR_ARG;
+    const int zp = (T + 16 * nt - 1) / (16 * nt);
+    dim3 grid(t.N / (16 * RT), max_active, zp < 1 ? 1 : (zp > 16 ? 16 : zp));
+    if (nt == 1) k_wave_tile<FMT, NPROJ, 1, RT, D><<<grid, 64, 0, st>>>(t);
+    else k_wave_tile<FMT, NPROJ, 2, RT, D><<<grid, 64, 0, st>>>(t);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
-
-#ifndef MOE_TILE_DMA_NT
-#define MOE_TILE_DMA_NT 0   // token tiles per pass up to which the DMA-ring kernels run (0: never; measured
-                            // slower than the register-staged tiles at the Qwen3 T = 16..64 shapes)
-#endif
 
 template <class FMT>
 int run_tiles_fmt(const ExpertsArgs& a) {
@@ -749,17 +644,14 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     t.E = w->E;
     t.act = a.act;
     t.kslots = a.k;
+    // tile-major weights present: wave tiles (their h is written paired; both stages take the same branch)
+    const bool wave = w->gate.tiles && w->up.tiles && w->down.tiles && nt <= MOE_WAVE_NT;
     if (a.stages & 1) {
         int rc = launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
                               a.grp.meta, a.st);
         if (rc) return rc;
         TileArgs g = t;
         g.actv = (const uint16_t*)a.x;
-        if (nt <= MOE_TILE_DMA_NT) {   // the DMA tiles read x in the decoded-code order
-            const size_t np = (size_t)a.T * w->d / 8;
-            k_pair8_rows<<<(unsigned)((np + 255) / 256), 256, 0, a.st>>>((const uint4*)a.x, (uint4*)a.xperm, np);
-            g.actv = a.xperm;
-        }
         g.act_div = a.k;
         g.K = w->d;
         g.N = w->F;
@@ -769,8 +661,12 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         g.b1 = w->up.bias;
         g.hout = a.hhi;
         g.hout2 = a.hlo;
-        rc = nt <= MOE_TILE_DMA_NT ? launch_tile_dma<FMT, 2>(g, nt, max_active, a.T, a.st)
-                                   : launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
+        if (wave) {
+            g.W0 = (const uint8_t*)w->gate.tiles;
+            g.W1 = (const uint8_t*)w->up.tiles;
+        }
+        rc = wave ? launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, max_active, a.T, a.st)
+                  : launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
         if (rc) return rc;
     }
     if (a.stages & 2) {
@@ -782,8 +678,9 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.N = w->d;
         d.W0 = (const uint8_t*)w->down.rows;
         d.yp = a.yp;
-        int rc = nt <= MOE_TILE_DMA_NT ? launch_tile_dma<FMT, 1>(d, nt, max_active, a.T, a.st)
-                                       : launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
+        if (wave) d.W0 = (const uint8_t*)w->down.tiles;
+        int rc = wave ? launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, max_active, a.T, a.st)
+                      : launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
         return launch_combine(a.yp, a.idx, a.wts, w->down.bias, w->E, a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
     }
@@ -794,6 +691,15 @@ int run_tiles_fmt(const ExpertsArgs& a) {
 
 int run_experts_tiles(const ExpertsArgs& a) {
     return a.w->fmt == MOE_FMT_INT4_G64 ? run_tiles_fmt<FmtInt4>(a) : run_tiles_fmt<FmtMxfp4>(a);
+}
+
+int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tiles, hipStream_t st) {
+    dim3 grid((K + 127) / 128, N / 16, E);
+    if (fmt == MOE_FMT_INT4_G64)
+        k_pack_tiles<FmtInt4><<<grid, 64, 0, st>>>((const uint8_t*)rows, (uint8_t*)tiles, N, K);
+    else
+        k_pack_tiles<FmtMxfp4><<<grid, 64, 0, st>>>((const uint8_t*)rows, (uint8_t*)tiles, N, K);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
 }  // namespace moe

@@ -5,6 +5,8 @@ metal_mxfp4_gptoss.py:100-107), holding the packed row records the library reads
     "fmt": "int4" | "mxfp4";  "shape": (E, d, F)
     "g", "u": uint8 records [E, F, row_bytes(fmt, d)];  "d": uint8 records [E, d, row_bytes(fmt, F)]
     "bg", "bu", "bd": optional fp32 additive biases [E, F], [E, F], [E, d] (gpt-oss)
+    "gt", "ut", "dt": optional uint8 tile-major copies of g, u, d (moe_tiles_pack, built on the device by
+                      add_tiles); the grouped T > 1 path streams them when all three are present
 """
 import torch
 
@@ -18,8 +20,10 @@ def dims(s):
     return E, d, F
 
 
-def make_state(fmt, g, u, d, bg=None, bu=None, bd=None):
-    """State from (codes, scales[, biases]) triples in the reference's layout (packed into row records)."""
+def make_state(fmt, g, u, d, bg=None, bu=None, bd=None, tiles=True):
+    """State from (codes, scales[, biases]) triples in the reference's layout (packed into row records).
+    tiles: also build the tile-major copies the grouped path streams (GPU states only; twice the weight
+    memory, in exchange for full-bandwidth weight loads at T > 1)."""
     E, F, W = g[0].shape
     s = {"fmt": fmt, "shape": (E, W * 8, F)}
     for n, p in (("g", g), ("u", u), ("d", d)):
@@ -27,7 +31,37 @@ def make_state(fmt, g, u, d, bg=None, bu=None, bd=None):
     for n, b in (("bg", bg), ("bu", bu), ("bd", bd)):
         if b is not None:
             s[n] = b.to(torch.float32).contiguous()
+    if tiles and s["g"].is_cuda:
+        add_tiles(s)
     return s
+
+
+def tile_bytes(fmt, N, K):
+    """Bytes of one expert's N x K projection in the tile-major layout (include/moe_mi355x.h)."""
+    return int(_lib.lib().moe_tile_bytes(FMT[fmt], N, K))
+
+
+def add_tiles(s):
+    """Build s["gt"], s["ut"], s["dt"] from the row records on the device (moe_tiles_pack)."""
+    E, d, F = dims(s)
+    L = _lib.lib()
+    for n, K, N in (("g", d, F), ("u", d, F), ("d", F, d)):
+        rows = s[n]
+        _lib.require_device(rows, "expert weights")
+        nb = tile_bytes(s["fmt"], N, K)
+        if nb == 0:
+            raise ValueError(f"no tile layout for N={N}, K={K}")
+        t = torch.empty(E * nb, dtype=torch.uint8, device=rows.device)
+        _lib.check("moe_tiles_pack", L.moe_tiles_pack(FMT[s["fmt"]], E, N, K, _lib.ptr(rows.contiguous()),
+                                                      _lib.ptr(t), _lib.stream_of(rows.device)))
+        s[n + "t"] = t
+    s["_tiles_of"] = tuple(s[n].data_ptr() for n in ("g", "u", "d"))
+    return s
+
+
+def drop_tiles(s):
+    """The same state without tile-major copies (the grouped path then reads the row records)."""
+    return {k: v for k, v in s.items() if k not in ("gt", "ut", "dt", "_c", "_tiles_of")}
 
 
 def unpack(s, n):
@@ -38,7 +72,7 @@ def unpack(s, n):
 
 def _desc(s):
     """ctypes moe_experts_t for a state (cached; rebuilt if any tensor changed)."""
-    tensors = (s["g"], s["u"], s["d"]) + tuple(s.get(b) for b in ("bg", "bu", "bd"))
+    tensors = (s["g"], s["u"], s["d"]) + tuple(s.get(b) for b in ("bg", "bu", "bd", "gt", "ut", "dt"))
     key = tuple(0 if t is None else t.data_ptr() for t in tensors)
     c = s.get("_c")
     if c is not None and c[0] == key:
@@ -46,16 +80,24 @@ def _desc(s):
     E, d, F = dims(s)
     for n, K, N in (("g", d, F), ("u", d, F), ("d", F, d)):
         assert s[n].dtype == torch.uint8 and tuple(s[n].shape) == (E, N, formats.row_bytes(s["fmt"], K)), n
+    if any(n in s for n in ("gt", "ut", "dt")):
+        assert s.get("_tiles_of") == tuple(s[n].data_ptr() for n in ("g", "u", "d")), \
+            "tile-major copies were built from other row records: call add_tiles(s) again"
 
-    def proj(rows, bias):
-        for t in (rows, bias):
+    def proj(n, bias):
+        rows, tiles = s[n], s.get(n + "t")
+        for t in (rows, bias, tiles):
             if t is not None:
                 _lib.require_device(t, "expert weights")
                 assert t.is_contiguous(), "expert weights must be contiguous"
-        return _lib.Proj(rows.data_ptr(), None if bias is None else bias.data_ptr())
+        if tiles is not None:
+            K, N = (F, d) if n == "d" else (d, F)
+            assert tiles.dtype == torch.uint8 and tiles.numel() == E * tile_bytes(s["fmt"], N, K), n + "t"
+        return _lib.Proj(rows.data_ptr(), None if bias is None else bias.data_ptr(),
+                         None if tiles is None else tiles.data_ptr())
 
-    desc = _lib.Experts(FMT[s.get("fmt", "int4")], E, d, F, proj(s["g"], s.get("bg")), proj(s["u"], s.get("bu")),
-                        proj(s["d"], s.get("bd")))
+    desc = _lib.Experts(FMT[s.get("fmt", "int4")], E, d, F, proj("g", s.get("bg")), proj("u", s.get("bu")),
+                        proj("d", s.get("bd")))
     s["_c"] = (key, desc)
     return desc
 

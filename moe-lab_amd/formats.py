@@ -80,6 +80,46 @@ def unpack_rows(fmt, rows, K):
     return codes, rows[..., K // 2:K // 2 + K // 32].contiguous()
 
 
+# ------------------------------------------------------------------------------------ tile-major copy
+TILE_SLICE_BYTES = {FMT_INT4: 1024 + 16 * 8, FMT_MXFP4: 1024 + 16 * 4}
+
+
+def tile_word_index(fmt, s, g, j):
+    """Row word (8 codes) that lane group g supplies for MFMA step j of slice s (include/moe_mi355x.h)."""
+    if fmt == FMT_INT4:
+        return 16 * s + 8 * (j >> 1) + 2 * g + (j & 1)
+    return 16 * s + 4 * j + g
+
+
+def pack_tiles_ref(fmt, rows, K):
+    """Host restatement of moe_tiles_pack: uint8 row records [E, N, row_bytes] -> uint8 [E * tile bytes].
+    Test-side only (the library packs on the device); a plain loop over the documented layout."""
+    rows = rows.cpu()
+    E, N, _ = rows.shape
+    S = (K + 127) // 128
+    sb = TILE_SLICE_BYTES[fmt]
+    words = rows[..., :K // 2].contiguous().view(torch.int32).reshape(E, N, K // 8)
+    out = torch.zeros((E, N // 16, S, sb), dtype=torch.uint8)
+    wi = torch.tensor([[[tile_word_index(fmt, s, g, j) for j in range(4)] for g in range(4)] for s in range(S)])
+    valid = wi < K // 8
+    for e in range(E):
+        for t in range(N // 16):
+            w = words[e, 16 * t:16 * t + 16]                                  # [16 rows, K/8]
+            cw = torch.where(valid[None], w[:, wi.clamp(max=K // 8 - 1)], 0)  # [16, S, 4 g, 4 j]
+            out[e, t, :, :1024] = cw.permute(1, 2, 0, 3).contiguous().view(torch.uint8).reshape(S, 1024)
+            meta = rows[e, 16 * t:16 * t + 16, K // 2:]
+            if fmt == FMT_INT4:
+                mw = meta[:, :K // 16].contiguous().view(torch.int32)        # [16, K/64]
+                mw = torch.cat([mw, torch.zeros((16, 2 * S - K // 64), dtype=torch.int32)], 1)
+                out[e, t, :, 1024:] = mw.reshape(16, S, 2).permute(1, 0, 2).contiguous().view(torch.uint8) \
+                    .reshape(S, 128)
+            else:
+                mb = meta[:, :K // 32]
+                mb = torch.cat([mb, torch.zeros((16, 4 * S - K // 32), dtype=torch.uint8)], 1)
+                out[e, t, :, 1024:] = mb.reshape(16, S, 4).permute(1, 0, 2).reshape(S, 64)
+    return out.reshape(-1)
+
+
 # --------------------------------------------------------------------------------------------- int4
 def quantize_int4(w, group_size=GS_INT4):
     """Affine 4-bit quantisation per group along the last axis, after MLX's affine quantiser:

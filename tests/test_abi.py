@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 def _desc(E=8, d=128, F=128, fmt=0):
     from moelab_amd import _lib
     fake = ctypes.c_void_p(4096)   # never dereferenced: argument checks return before any launch
-    p = _lib.Proj(fake, None)
+    p = _lib.Proj(fake, None, None)
     return _lib.Experts(fmt, E, d, F, p, p, p)
 
 
@@ -83,3 +83,29 @@ def test_router_argument_errors():
     assert L.moe_router(p, p, None, 1, 2048, 128, 33, 1, 1.0, p, p, p, p, None) == -1   # k > 32
     assert L.moe_topk(p, 0, 1, 16, 17, 1, 1.0, p, p, None) == -1                        # k > E
     assert L.moe_group(p, 4, 0, p, p, p, p, p, None) == -1                              # E < 1
+
+
+def test_tile_bytes_and_pack_argument_errors():
+    from moelab_amd import _lib
+    L = _lib.lib()
+    assert L.moe_tile_bytes(0, 768, 2048) == 48 * 16 * 1152
+    assert L.moe_tile_bytes(1, 2880, 2880) == 180 * 23 * 1088
+    assert L.moe_tile_bytes(0, 24, 2048) == 0 and L.moe_tile_bytes(0, 32, 96) == 0 and L.moe_tile_bytes(5, 32, 64) == 0
+    p, q = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    assert L.moe_tiles_pack(0, 2, 24, 128, p, q, None) == _lib.MOE_ERR_ARG
+    assert L.moe_tiles_pack(0, 2, 32, 96, p, q, None) == _lib.MOE_ERR_ARG
+    assert L.moe_tiles_pack(7, 2, 32, 128, p, q, None) == _lib.MOE_ERR_DTYPE
+    assert L.moe_tiles_pack(0, 2, 32, 128, ctypes.c_void_p(4100), q, None) == _lib.MOE_ERR_ALIGN
+    assert L.moe_tiles_pack(0, 2, 32, 128, p, None, None) == _lib.MOE_ERR_ARG
+
+
+def test_misaligned_tiles_rejected_before_launch():
+    from moelab_amd import _lib
+    L = _lib.lib()
+    fake = ctypes.c_void_p(4096)
+    p = _lib.Proj(fake, None, ctypes.c_void_p(4104))
+    w = _lib.Experts(0, 8, 128, 128, p, p, p)
+    x = ctypes.c_void_p(4096)
+    got = L.moe_experts_run(w, x, 0, x, x, 4, 2, 0, _lib.PATH_GROUPED, 0, x, 0, None, ctypes.c_void_p(8192), 1 << 30,
+                            None)
+    assert got == _lib.MOE_ERR_ALIGN

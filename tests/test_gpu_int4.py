@@ -261,3 +261,57 @@ def test_small_affine_scales():
         x, idx, wts = inputs(sh, T, seed=10, scale=1e6)
         assert_close(q4().run(s, x, idx, wts, out_dtype=torch.float32), oracle_y(s, x, idx, wts), what=T)
     assert formats.GS_INT4 == 64
+
+
+@pytest.mark.parametrize("fmt", ["int4", "mxfp4"])
+@pytest.mark.parametrize("N,K", [(16, 128), (48, 192), (32, 2048), (48, 2880)])
+def test_tiles_pack_matches_host_restatement(fmt, N, K):
+    """moe_tiles_pack on the device == formats.pack_tiles_ref, byte for byte (incl. K % 128 == 64 padding)."""
+    from moelab_amd import _lib, formats
+    from moelab_amd.experts import FMT, tile_bytes
+    g = torch.Generator(device=DEV).manual_seed(N + K)
+    E = 3
+    parts = (formats.random_int4 if fmt == "int4" else formats.random_mxfp4)(E, N, K, generator=g, device=DEV)
+    rows = formats.pack_rows(fmt, *parts)
+    tiles = torch.full((E * tile_bytes(fmt, N, K),), 0xA5, dtype=torch.uint8, device=DEV)
+    print(f"case pack fmt={fmt} N={N} K={K}", flush=True)
+    _lib.check("moe_tiles_pack", _lib.lib().moe_tiles_pack(FMT[fmt], E, N, K, _lib.ptr(rows), _lib.ptr(tiles),
+                                                           _lib.stream_of(DEV)))
+    torch.cuda.synchronize()
+    assert torch.equal(tiles.cpu(), formats.pack_tiles_ref(fmt, rows, K))
+
+
+def grouped(s, x, idx, wts, out_dtype=None):
+    from moelab_amd import _lib
+    from moelab_amd.experts import run_experts
+    return run_experts(s, x, idx, wts, path=_lib.PATH_GROUPED, out_dtype=out_dtype)
+
+
+@pytest.mark.parametrize("T", [2, 9, 33, 65, 130])
+def test_grouped_without_tile_copies(T):
+    """The grouped path forced on row records only (no tile-major copies): the row-major MFMA tiles."""
+    from moelab_amd.experts import drop_tiles
+    sh = shape_("r", 256, 320, 16, 4)
+    s = drop_tiles(packed_state(sh, 7))
+    x, idx, wts = inputs(sh, T, "zipf", seed=T)
+    print(f"case grouped-rows T={T}", flush=True)
+    y = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    assert_close(y, oracle_y(s, x, idx, wts), what=("rows", T))
+
+
+@pytest.mark.parametrize("T", [2, 16, 40, 130])
+def test_tile_copies_and_row_records_agree(T):
+    """The grouped path forced with and without the tile-major copies (wave tiles vs row-major tiles): each
+    within the gate of the oracle, and of each other up to fp32 reassociation."""
+    from moelab_amd.experts import drop_tiles
+    sh = shape_("t", 512, 384, 16, 4)
+    s = packed_state(sh, 9)
+    x, idx, wts = inputs(sh, T, "uniform", seed=T)
+    print(f"case tiles-vs-rows T={T}", flush=True)
+    y1 = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    y2 = grouped(drop_tiles(s), x, idx, wts, out_dtype=torch.float32)
+    ref = oracle_y(s, x, idx, wts)
+    assert_close(y1, ref, what=("tiles", T))
+    assert_close(y2, ref, what=("rows", T))
+    rms = float(y1.pow(2).mean().sqrt())
+    assert float((y1 - y2).abs().max()) <= 1e-3 * rms

@@ -42,6 +42,9 @@ def packed_state(shape, seed, biases=False, scale_bytes=None):
             sc = torch.randint(lo, hi + 1, sc.shape, generator=g, device=DEV).to(torch.uint8)
             s[n] = formats.pack_rows("mxfp4", codes, sc)
         s.pop("_c", None)
+        if "gt" in s:   # the tile-major copies follow the new records
+            from moelab_amd.experts import add_tiles
+            add_tiles(s)
     return s
 
 
@@ -181,3 +184,21 @@ def test_gptoss_full_shape(T):
     idx, wts = router.route(x, s["wr"], sh.k)
     y = gpt().run(s, x, idx, wts, out_dtype=torch.float32)
     assert_close(y, oracle_y(s, x, idx, wts, act=2))
+
+
+@pytest.mark.parametrize("T", [2, 17, 40])
+def test_mxfp4_tile_copies_and_row_records_agree(T):
+    """MXFP4 grouped path forced with and without the tile-major copies, against the oracle and each other."""
+    from moelab_amd import _lib
+    from moelab_amd.experts import drop_tiles, run_experts
+    sh = shape_("t", 512, 384, 16, 4)
+    s = packed_state(sh, 5)
+    x, idx, wts = inputs(sh, T, "uniform", seed=T)
+    print(f"case mxfp4 tiles-vs-rows T={T}", flush=True)
+    y1 = run_experts(s, x, idx, wts, path=_lib.PATH_GROUPED, out_dtype=torch.float32)
+    y2 = run_experts(drop_tiles(s), x, idx, wts, path=_lib.PATH_GROUPED, out_dtype=torch.float32)
+    ref = oracle_y(s, x, idx, wts)
+    assert_close(y1, ref, what=("tiles", T))
+    assert_close(y2, ref, what=("rows", T))
+    rms = float(y1.pow(2).mean().sqrt())
+    assert float((y1 - y2).abs().max()) <= 1e-3 * rms
