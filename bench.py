@@ -34,6 +34,11 @@ import __graft_entry__  # noqa: E402
 
 METRIC = "MoE layer µs/call + weight-byte GB/s vs HBM peak at T=1 and T=32"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the T=1 gate/up kernel, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
+# `bench.py --layers 8 --steps 5 --warmup 2 --no-t32 --cpu-layers 0 --copy-calibrate 256`, each scaled by what
+# the counter reads for the 256 MiB device copy of the same run (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0):
+# 2 x 6974.9 KiB + 48.0 KiB (profiles/k_gate_up_rows_qwen3_t1_traffic.md)
+GU_T1_TRAFFIC_BYTES = int(round((2.0 * 6974.9 + 48.0) * 1024))
 
 
 def log(*a):
@@ -76,6 +81,8 @@ def main():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU-baseline sample (0: skip)")
     ap.add_argument("--no-t32", action="store_true")
+    ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MIB",
+                    help="finish with 3 device copies of MIB MiB (the plain-copy reference for --pmc traffic runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one MI355X: the expert path is single-GPU (expert "
@@ -176,6 +183,16 @@ def main():
                 t = time_graph(g, max(5, args.steps // 5), max(2, args.warmup // 5))
                 res[name] = t
                 del g
+
+            def stage(st):   # one stage of the grouped path over the 48 layers (x fixed: timing only)
+                def f():
+                    for ly, (idx, wts) in zip(layers, routes):
+                        run_experts(ly, x32, idx, wts, path=_lib.PATH_GROUPED, stages=st)
+                return f
+            for name, st in (("gate_up", _lib.STAGE_GATE_UP), ("down", _lib.STAGE_DOWN)):
+                g, _ = graph_of(stage(st))
+                res[name] = time_graph(g, max(5, args.steps // 5), max(2, args.warmup // 5))
+                del g
             ub = sum(U) * per_expert
             t32[dist] = {
                 "us_per_layer_grouped": res["grouped"] * 1e6 / L,
@@ -184,6 +201,12 @@ def main():
                 "unique_experts_mean": float(np.mean(U)),
                 "weight_GBps_grouped": ub / res["grouped"] / 1e9,
                 "slot_weight_GBps_per_slot": L * T * sh.k * per_expert / res["per_slot"] / 1e9,
+                # stage split of the grouped path: grouping + gate/up wave tiles (2/3 of the bytes), then
+                # down wave tiles + combine (1/3)
+                "gate_up_stage_us": res["gate_up"] * 1e6 / L,
+                "down_stage_us": res["down"] * 1e6 / L,
+                "gate_up_stage_GBps": ub * 2 / 3 / res["gate_up"] / 1e9,
+                "down_stage_GBps": ub / 3 / res["down"] / 1e9,
             }
             log(f"T=32 {dist}: grouped {t32[dist]['us_per_layer_grouped']:.1f} us/layer, per-slot "
                 f"{t32[dist]['us_per_layer_per_slot']:.1f} us/layer, speedup {t32[dist]['speedup_per_token']:.2f}x, "
@@ -221,13 +244,21 @@ def main():
         "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3),
                        "fused_single_launch_us_per_layer": round(t_step_f * 1e6 / L, 3)},
         "t32": t32,
-        "roofline": {"bound": "hbm", "kernel": "k_gate_up_slots<FmtInt4, SwiGLU> (T=1 gate/up GEMV + GLU)",
+        "roofline": {"bound": "hbm", "kernel": "k_gate_up_rows<FmtInt4, 3, 1> (T=1 gate/up GEMV + GLU)",
                      "achieved": round(gu_bytes / t_gu / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_bytes / t_gu / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_bytes / t_gu / 1e9 / HBM_PEAK_GBS, 4), "traffic": GU_T1_TRAFFIC_BYTES,
                      "launch_us": round(t_gu * 1e6, 3), "algorithmic_bytes_per_launch": gu_bytes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+    if args.copy_calibrate > 0:
+        n = args.copy_calibrate << 20
+        a = torch.empty(n, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 device copies of {n} bytes")
 
 
 def cpu_baseline(layers, routes, x, sh):
