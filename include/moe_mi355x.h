@@ -177,6 +177,25 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
                            int T, int k, int act, int path, int nored, void* y, int y_dtype, const void* residual,
                            void* workspace, size_t workspace_bytes, int stages, void* stream);
 
+/*
+ * Shared experts: S always-on experts added to every token, the caller semantics of the reference's model
+ * patches (reference e2e.py:66-68 Qwen-style gated shared expert, sigmoid(x . w_gate) * shared_expert(x);
+ * e2e.py:146-147 DeepSeek, + shared_experts(x)). The reference runs them as stock mlx-lm modules; here they go
+ * through the same expert kernels as the routed experts:
+ *   y[t] = residual[t] + g_t * sum_s ( down_s( act(gate_s x_t + bg_s, up_s x_t + bu_s) ) + bd_s ),
+ *   g_t = sigmoid(x_t . gate) (gate: bf16 [d], fp32 dot in a fixed order) or 1 when gate is NULL.
+ *   ws: the S shared experts as an expert set (E = S <= 32; same formats, packing and optional tile copies).
+ *   x, y, residual, dtypes, act: as moe_experts_run (path auto: per-slot GEMV at T == 1, grouped tiles above).
+ *   workspace: moe_shared_experts_workspace_bytes(ws, T); its first MOE_WORKSPACE_SYNC_BYTES bytes are zero on
+ *   entry and on exit, as for moe_experts_run.
+ * A layer with routed and shared experts is moe_experts_run (routed, into y) followed by this call with
+ * residual = y.
+ */
+int moe_shared_experts_run(const moe_experts_t* ws, const void* x, int x_dtype, int T, int act, const void* gate,
+                           void* y, int y_dtype, const void* residual, void* workspace, size_t workspace_bytes,
+                           void* stream);
+size_t moe_shared_experts_workspace_bytes(const moe_experts_t* ws, int T);
+
 /* Library version and build target, for logs. */
 const char* moe_version(void);
 

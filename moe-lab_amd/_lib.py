@@ -22,7 +22,7 @@ ACT_SWIGLU, ACT_GEGLU, ACT_GPTOSS = 0, 1, 2
 
 EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
            "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_row_bytes", "moe_tile_bytes",
-           "moe_tiles_pack", "moe_version")
+           "moe_tiles_pack", "moe_shared_experts_run", "moe_shared_experts_workspace_bytes", "moe_version")
 WORKSPACE_SYNC_BYTES = 4096
 STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 3
 
@@ -75,8 +75,11 @@ def lib():
         L.moe_tile_bytes.argtypes = [i, i, i]
         L.moe_tile_bytes.restype = sz
         L.moe_tiles_pack.argtypes = [i, i, i, i, vp, vp, vp]
+        L.moe_shared_experts_run.argtypes = [ctypes.POINTER(Experts), vp, i, i, i, vp, vp, i, vp, vp, sz, vp]
+        L.moe_shared_experts_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i]
+        L.moe_shared_experts_workspace_bytes.restype = sz
         for n in ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
-                  "moe_experts_run_stages", "moe_tiles_pack"):
+                  "moe_experts_run_stages", "moe_tiles_pack", "moe_shared_experts_run"):
             getattr(L, n).restype = ctypes.c_int
         _lib = L
     return _lib

@@ -120,6 +120,34 @@ size_t moe_experts_workspace_bytes(const moe_experts_t* w, int T, int k, int pat
     return layout(w, T, k, path).total;
 }
 
+size_t moe_shared_experts_workspace_bytes(const moe_experts_t* ws, int T) {
+    if (!ws || T < 0 || ws->E < 1) return 0;
+    const size_t n = (size_t)T * ws->E;
+    return layout(ws, T, ws->E, MOE_PATH_AUTO).total + 2 * align_up(n * 4);
+}
+
+int moe_shared_experts_run(const moe_experts_t* ws, const void* x, int x_dtype, int T, int act, const void* gate,
+                           void* y, int y_dtype, const void* residual, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+    int rc = check_experts(ws);
+    if (rc) return rc;
+    if (ws->E > 32 || T < 0) return MOE_ERR_ARG;
+    if (T == 0) return MOE_OK;
+    if (!x || !y || !workspace) return x && y ? MOE_ERR_WORKSPACE : MOE_ERR_ARG;
+    if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;
+    if (!aligned16(x) || (gate && !aligned16(gate)) || !aligned16(workspace)) return MOE_ERR_ALIGN;
+    const size_t base = layout(ws, T, ws->E, MOE_PATH_AUTO).total;
+    if (workspace_bytes < moe_shared_experts_workspace_bytes(ws, T)) return MOE_ERR_WORKSPACE;
+    const size_t n = (size_t)T * ws->E;
+    int32_t* idx = (int32_t*)((char*)workspace + base);
+    float* wts = (float*)((char*)workspace + base + align_up(n * 4));
+    rc = moe::launch_shared_route((const uint16_t*)x, (const uint16_t*)gate, T, ws->d, ws->E, idx, wts,
+                                  (hipStream_t)stream);
+    if (rc) return rc;
+    return moe_experts_run_stages(ws, x, x_dtype, idx, wts, T, ws->E, act, MOE_PATH_AUTO, 0, y, y_dtype, residual,
+                                  workspace, base, MOE_STAGE_ALL, stream);
+}
+
 int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T,
                     int k, int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                     size_t workspace_bytes, void* stream) {

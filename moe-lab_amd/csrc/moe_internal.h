@@ -15,6 +15,8 @@ int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, fl
                 hipStream_t st);
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
                  int32_t* active, int32_t* meta, hipStream_t st);
+int launch_shared_route(const uint16_t* x, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
+                        hipStream_t st);
 
 // grouping scratch inside an experts workspace
 struct GroupBufs {

@@ -269,6 +269,39 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
     }
 }
 
+// shared experts: the slots of token t are (t, s) for s < S, weight g_t = sigmoid(x_t . gate) or 1. One wave per
+// token: lane l dots the 8-element chunks l, l + 64, ... in element order, the lane sums are added as the DPP
+// tree of sum_lanes<64>, lanes 48..63 hold the total.
+__global__ void __launch_bounds__(256)
+shared_route(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate, int T, int d, int S,
+             int32_t* __restrict__ idx, float* __restrict__ wts) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= T) return;
+    float g = 1.f;
+    if (gate) {
+        const uint16_t* xr = x + (size_t)t * d;
+        float acc = 0.f;
+        for (int c = lane; c < (d >> 3); c += 64) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(xr + 8 * c);
+            const uint4 gv = *reinterpret_cast<const uint4*>(gate + 8 * c);
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc = __builtin_fmaf(bf16lo(xw[i]), bf16lo(gw[i]), acc);
+                acc = __builtin_fmaf(bf16hi(xw[i]), bf16hi(gw[i]), acc);
+            }
+        }
+        acc = sum_lanes<64>(acc);
+        acc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 63));
+        g = 1.f / (1.f + expf(-acc));
+    }
+    if (lane < S) {
+        idx[(size_t)t * S + lane] = lane;
+        wts[(size_t)t * S + lane] = g;
+    }
+}
+
 // ------------------------------------------------------------------------------------ host launchers
 int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
                   float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st) {
@@ -298,6 +331,13 @@ int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, fl
         topk_kernel<_Float16><<<grid, 256, 0, st>>>((const _Float16*)logits, T, E, k, norm, scale, idx, wts);
     else
         return MOE_ERR_DTYPE;
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+int launch_shared_route(const uint16_t* x, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
+                        hipStream_t st) {
+    if (T <= 0) return 0;
+    shared_route<<<(T + 3) / 4, 256, 0, st>>>(x, gate, T, d, S, idx, wts);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

@@ -130,3 +130,39 @@ def run_experts(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, nored=False, residua
                                   _lib.ptr(res), _lib.ptr(ws), ws.numel(), int(stages), _lib.stream_of(x.device))
     _lib.check("moe_experts_run_stages", rc)
     return out
+
+
+def run_shared(s, x, gate=None, act=0, residual=None, out=None, out_dtype=None):
+    """Shared experts (always on) through moe_shared_experts_run: y = residual + g_t * sum_s expert_s(x_t),
+    g_t = sigmoid(x_t . gate) for a bf16 gate vector [d] (Qwen-style gated shared expert, reference
+    e2e.py:66-68) or 1 (DeepSeek, e2e.py:146-147). s: an expert state whose E experts are the shared ones."""
+    _lib.require_device(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError(f"activation dtype {x.dtype}: the gfx950 expert kernels take bf16")
+    T, d = x.shape
+    x = x.contiguous()
+    desc = _desc(s)
+    L = _lib.lib()
+    ws = _lib.workspace(x.device, L.moe_shared_experts_workspace_bytes(desc, T))
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((T, d), dtype=out_dtype, device=x.device)
+    assert out.dtype == out_dtype and out.dtype in (torch.bfloat16, torch.float32)
+    res = None if residual is None else residual.to(out_dtype).contiguous()
+    g = None if gate is None else gate.to(torch.bfloat16).contiguous()
+    rc = L.moe_shared_experts_run(desc, _lib.ptr(x), _lib.DTYPE[x.dtype], T, int(act), _lib.ptr(g), _lib.ptr(out),
+                                  _lib.DTYPE[out.dtype], _lib.ptr(res), _lib.ptr(ws), ws.numel(),
+                                  _lib.stream_of(x.device))
+    _lib.check("moe_shared_experts_run", rc)
+    return out
+
+
+def run_layer(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, residual=None, out_dtype=None):
+    """Routed experts, then the state's shared experts if it has them (s["shared"], optional
+    s["shared_gate"]): the routed sum stays fp32 until the shared call adds to it."""
+    if "shared" not in s:
+        return run_experts(s, x, idx, wts, act=act, path=path, residual=residual, out_dtype=out_dtype)
+    y = run_experts(s, x, idx, wts, act=act, path=path, residual=residual, out_dtype=torch.float32)
+    return run_shared(s["shared"], x, gate=s.get("shared_gate"), act=act, residual=y,
+                      out_dtype=x.dtype if out_dtype is None else out_dtype)
+

@@ -7,8 +7,8 @@ expert's packed rows, with no grouping, and y = sum_j wts[t, j] * expert_j(x_t).
 "per-slot stock-style gather" arm the grouped path is measured against.
 """
 from . import _lib
-from .experts import run_experts
+from .experts import run_layer
 
 
 def gather_moe(s, x, idx, wts, group_size=None, bits=None, mode="affine", act=0, residual=None, out_dtype=None):
-    return run_experts(s, x, idx, wts, act=act, path=_lib.PATH_SLOTS, residual=residual, out_dtype=out_dtype)
+    return run_layer(s, x, idx, wts, act=act, path=_lib.PATH_SLOTS, residual=residual, out_dtype=out_dtype)

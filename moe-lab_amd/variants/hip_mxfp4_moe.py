@@ -10,7 +10,7 @@ the scale applied in fp32 per group (exact for every byte 1..254; reference meta
 import torch
 
 from .. import _lib, formats
-from ..experts import dims, make_state, run_experts, unpack
+from ..experts import dims, make_state, run_experts, run_layer, unpack
 from ..fallback import gather_moe  # noqa: F401  (module attribute the dispatcher calls; tests patch it)
 
 META = {"name": "hip_mxfp4_moe", "description": "gfx950 HIP MXFP4: fused T=1 launch, grouped expert tiles at T>1"}
@@ -45,11 +45,11 @@ def run(s, x, idx, wts, act=0, residual=None, out_dtype=None):
     T, k = idx.shape
     kw = dict(act=act, residual=residual, out_dtype=out_dtype)
     if T == 1:
-        return run_experts(s, x, idx, wts, path=_lib.PATH_AUTO, **kw)
+        return run_layer(s, x, idx, wts, path=_lib.PATH_AUTO, **kw)
     E, D, F = dims(s)
     if T * k / E > load_max(D, F):
         return gather_moe(s, x, idx, wts, GS, BITS, MODE, **kw)
-    return run_experts(s, x, idx, wts, path=_lib.PATH_GROUPED, **kw)
+    return run_layer(s, x, idx, wts, path=_lib.PATH_GROUPED, **kw)
 
 
 def run_slots(s, x, idx, act=0):

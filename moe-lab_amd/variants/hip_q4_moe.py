@@ -13,7 +13,7 @@ gives the weights the fp32 reference uses.
 import torch
 
 from .. import _lib, formats
-from ..experts import dims, make_state, run_experts, unpack
+from ..experts import dims, make_state, run_experts, run_layer, unpack
 from ..fallback import gather_moe  # noqa: F401  (module attribute the dispatcher calls; tests patch it)
 
 META = {"name": "hip_q4_moe", "description": "gfx950 HIP: per-slot GEMV at T=1, grouped expert tiles at T>1"}
@@ -59,8 +59,8 @@ def run(s, x, idx, wts, act=0, residual=None, out_dtype=None):
     T, k = idx.shape
     kw = dict(act=act, residual=residual, out_dtype=out_dtype)
     if T == 1:
-        return run_experts(s, x, idx, wts, path=_lib.PATH_AUTO, **kw)
+        return run_layer(s, x, idx, wts, path=_lib.PATH_AUTO, **kw)
     E, D, F = dims(s)
     if not custom_wins(T, k, E, D, F):
         return gather_moe(s, x, idx, wts, GS, BITS, **kw)
-    return run_experts(s, x, idx, wts, path=_lib.PATH_GROUPED, **kw)
+    return run_layer(s, x, idx, wts, path=_lib.PATH_GROUPED, **kw)

@@ -180,10 +180,12 @@ def act_fn(g, u, act):
     raise ValueError(act)
 
 
-def moe_reference(x, wg, wu, wd, idx, wts, act=0, bg=None, bu=None, bd=None, shared=None):
+def moe_reference(x, wg, wu, wd, idx, wts, act=0, bg=None, bu=None, bd=None, shared=None, shared_gate=None):
     """fp64 per-expert loop. x [T, d]; wg/wu: callables e -> [F, d] (or arrays [E, F, d]); wd: e -> [d, F].
     bg/bu [E, F], bd [E, d]: optional additive biases (gpt-oss), bd inside the routing weight.
-    shared: optional list of (wg_s [Fs, d], wu_s, wd_s) always-on SwiGLU experts, added with weight 1.
+    shared: optional list of (wg_s [Fs, d], wu_s, wd_s) always-on SwiGLU experts, added with weight 1, or with
+    weight sigmoid(x_t . shared_gate) per token when shared_gate [d] is given (Qwen-style gated shared expert,
+    reference e2e.py:66-68; DeepSeek adds them ungated, e2e.py:146-147).
     Returns y [T, d] float64."""
     get = lambda w, e: w(e) if callable(w) else w[e]  # noqa: E731
     x = np.asarray(x, dtype=np.float64)
@@ -203,10 +205,12 @@ def moe_reference(x, wg, wu, wd, idx, wts, act=0, bg=None, bu=None, bd=None, sha
         if bd is not None:
             o = o + np.asarray(bd[e], dtype=np.float64)
         np.add.at(y, t, o * np.asarray(wts, dtype=np.float64)[t, j][:, None])
+    gs = np.ones((T, 1)) if shared_gate is None else \
+        1.0 / (1.0 + np.exp(-(x @ np.asarray(shared_gate, dtype=np.float64))))[:, None]
     for (sg, su, sd) in (shared or []):
         g = x @ np.asarray(sg, dtype=np.float64).T
         u = x @ np.asarray(su, dtype=np.float64).T
-        y += (g / (1.0 + np.exp(-g)) * u) @ np.asarray(sd, dtype=np.float64).T
+        y += gs * ((g / (1.0 + np.exp(-g)) * u) @ np.asarray(sd, dtype=np.float64).T)
     return y
 
 

@@ -40,10 +40,20 @@ class LazyExperts:
 
 
 def oracle_y(state, x, idx, wts, act=0):
+    """The oracle's layer for a packed state; the state's shared experts (state["shared"], optional
+    state["shared_gate"]) are added as the oracle's shared list."""
     xs = orc.bf16_bits_to_f32(np_u16(x)) if x.dtype == torch.bfloat16 else x.float().cpu().numpy()
     b = {n: state[n].cpu().numpy().astype(np.float64) for n in ("bg", "bu", "bd") if n in state}
+    shared, sgate = None, None
+    if "shared" in state:
+        sh = state["shared"]
+        wg, wu, wd = (deq(sh, n) for n in ("g", "u", "d"))
+        shared = [(wg[s], wu[s], wd[s]) for s in range(wg.shape[0])]
+        if state.get("shared_gate") is not None:
+            sgate = orc.bf16_bits_to_f32(np_u16(state["shared_gate"]))
     return orc.moe_reference(xs, LazyExperts(state, "g"), LazyExperts(state, "u"), LazyExperts(state, "d"),
-                             idx.cpu().numpy(), wts.cpu().numpy(), act, b.get("bg"), b.get("bu"), b.get("bd"))
+                             idx.cpu().numpy(), wts.cpu().numpy(), act, b.get("bg"), b.get("bu"), b.get("bd"),
+                             shared=shared, shared_gate=sgate)
 
 
 def assert_close(y, y_ref, tol=TOL_MAXABS_RMS, what=""):

@@ -315,3 +315,46 @@ def test_tile_copies_and_row_records_agree(T):
     assert_close(y2, ref, what=("rows", T))
     rms = float(y1.pow(2).mean().sqrt())
     assert float((y1 - y2).abs().max()) <= 1e-3 * rms
+
+
+def shared_state(d, Fs, S, seed, fmt="int4"):
+    from moelab_amd import formats
+    from moelab_amd.experts import make_state
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    rnd = formats.random_int4 if fmt == "int4" else formats.random_mxfp4
+    return make_state(fmt, rnd(S, Fs, d, generator=g, device=DEV), rnd(S, Fs, d, generator=g, device=DEV),
+                      rnd(S, d, Fs, generator=g, device=DEV))
+
+
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_shared_experts(T, gated):
+    """Routed + always-on shared experts (DeepSeek ungated, reference e2e.py:146-147; Qwen-style sigmoid gate,
+    e2e.py:66-68) through moe_shared_experts_run, against the oracle's shared list."""
+    sh = shape_("s", 256, 384, 16, 4)
+    s = packed_state(sh, 21)
+    s["shared"] = shared_state(sh.d, 320, 2, seed=22)
+    if gated:
+        g = torch.Generator(device=DEV).manual_seed(23)
+        s["shared_gate"] = (torch.randn(sh.d, generator=g, device=DEV) * 0.05).to(torch.bfloat16)
+    x, idx, wts = inputs(sh, T, "uniform", seed=T)
+    print(f"case shared T={T} gated={gated}", flush=True)
+    y32 = q4().run(s, x, idx, wts, out_dtype=torch.float32)
+    y = q4().run(s, x, idx, wts)
+    ref = oracle_y(s, x, idx, wts)
+    assert_close(y32, ref, what=("shared fp32", T, gated))
+    assert_close(y, ref, what=("shared bf16", T, gated))
+
+
+def test_shared_experts_argument_errors():
+    from moelab_amd import _lib
+    from moelab_amd.experts import _desc
+    s = shared_state(256, 320, 2, seed=24)
+    L = _lib.lib()
+    x = torch.zeros((4, 256), dtype=torch.bfloat16, device=DEV)
+    y = torch.empty_like(x)
+    desc = _desc(s)
+    assert L.moe_shared_experts_run(desc, _lib.ptr(x), 0, 4, 0, None, _lib.ptr(y), 0, None, None, 0, None) == \
+        _lib.MOE_ERR_WORKSPACE
+    assert L.moe_shared_experts_run(desc, _lib.ptr(x), 2, 4, 0, None, _lib.ptr(y), 0, None, _lib.ptr(y), 1 << 20,
+                                    None) == _lib.MOE_ERR_DTYPE

@@ -286,6 +286,25 @@ def test_moe_reference_biases_and_shared(orc):
     np.testing.assert_allclose(ys - y0, (orc.act_fn(x @ sg.T, x @ su.T, 0)) @ sd.T, rtol=1e-10, atol=1e-12)
 
 
+def test_moe_reference_gated_shared_expert(orc):
+    """Gated shared expert, token by token: sigmoid(x . w) * down(silu(g) * u); a gate of 0 halves it,
+    a large positive gate passes it whole, a large negative one removes it."""
+    rng = np.random.default_rng(14)
+    x, wg, wu, wd, idx, wts = _problem(rng, 3, 64, 32, 4, 2)
+    sg, su, sd = rng.standard_normal((16, 64)), rng.standard_normal((16, 64)), rng.standard_normal((64, 16))
+    w = rng.standard_normal(64)
+    y0 = orc.moe_reference(x, wg, wu, wd, idx, wts)
+    ys = orc.moe_reference(x, wg, wu, wd, idx, wts, shared=[(sg, su, sd)], shared_gate=w)
+    for t in range(3):
+        sh = sd @ (sg @ x[t] / (1.0 + np.exp(-(sg @ x[t]))) * (su @ x[t]))
+        np.testing.assert_allclose(ys[t] - y0[t], sh / (1.0 + np.exp(-(x[t] @ w))), rtol=1e-10, atol=1e-12)
+    full = orc.moe_reference(x, wg, wu, wd, idx, wts, shared=[(sg, su, sd)])
+    half = orc.moe_reference(x, wg, wu, wd, idx, wts, shared=[(sg, su, sd)], shared_gate=np.zeros(64))
+    np.testing.assert_allclose(half - y0, 0.5 * (full - y0), rtol=1e-12, atol=1e-12)
+    on = orc.moe_reference(x, wg, wu, wd, idx, wts, shared=[(sg, su, sd)], shared_gate=np.full(64, 1e3) * np.sign(x[0]))
+    np.testing.assert_allclose(on[0], full[0], rtol=1e-12)
+
+
 def test_torch_loop_matches_reference(orc):
     rng = np.random.default_rng(13)
     x, wg, wu, wd, idx, wts = _problem(rng, 5, 64, 32, 6, 2)
