@@ -81,6 +81,7 @@ def main():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU-baseline sample (0: skip)")
     ap.add_argument("--no-t32", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 4, 5a, 5b (reported beside)")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MIB",
                     help="finish with 3 device copies of MIB MiB (the plain-copy reference for --pmc traffic runs)")
     args = ap.parse_args()
@@ -212,10 +213,18 @@ def main():
                 f"{t32[dist]['us_per_layer_per_slot']:.1f} us/layer, speedup {t32[dist]['speedup_per_token']:.2f}x, "
                 f"U={t32[dist]['unique_experts_mean']:.1f}")
 
+    # ------------------------------------------------------------------ BASELINE configs 4, 5a, 5b
+    configs = {}
+    if not args.no_configs:
+        del layers
+        torch.cuda.empty_cache()
+        configs = other_configs(dev, args)
+
     # ------------------------------------------------------------------ CPU baseline (bounded sample)
     cpu = None
     if args.cpu_layers > 0:
-        cpu = cpu_baseline(layers[:args.cpu_layers], routes1[:args.cpu_layers], x1, sh)
+        cpu_layers = [baseline_int4_layer(sh, seed=1000 + l, device=dev) for l in range(args.cpu_layers)]
+        cpu = cpu_baseline(cpu_layers, routes1[:args.cpu_layers], x1, sh)
         log(f"CPU baseline: {cpu['value']:.1f} us/layer on {cpu['cores']} threads")
 
     value = bytes1 / t_step / 1e9
@@ -244,6 +253,7 @@ def main():
         "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3),
                        "fused_single_launch_us_per_layer": round(t_step_f * 1e6 / L, 3)},
         "t32": t32,
+        "configs": configs,
         "roofline": {"bound": "hbm", "kernel": "k_gate_up_rows<FmtInt4, 3, 1> (T=1 gate/up GEMV + GLU)",
                      "achieved": round(gu_bytes / t_gu / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_bytes / t_gu / 1e9 / HBM_PEAK_GBS, 4), "traffic": GU_T1_TRAFFIC_BYTES,
@@ -259,6 +269,76 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log(f"copy calibration: 3 device copies of {n} bytes")
+
+
+def other_configs(dev, args):
+    """BASELINE configs 4 (gpt-oss-20b MXFP4 + biases, clamped SwiGLU, T=1 and T=32), 5a (Mixtral-8x7B int4,
+    T=512, MFMA-bound) and 5b (DeepSeek-V2-Lite int4, T=256, 2 shared experts): dependent residual chains of
+    seeded layers (enough of them to exceed the 256 MB Infinity Cache), uniform router logits, timed like the
+    headline. Reported beside `value`."""
+    from moelab_amd import _lib, roofline, router
+    from moelab_amd.experts import make_state, run_layer
+    from moelab_amd import formats
+    from moelab_amd.problem import baseline_int4_layer, baseline_mxfp4_layer, baseline_x
+    from moelab_amd.shapes import SHAPES
+    out = {}
+
+    def chain_time(layers, x, routes, act):
+        def f():
+            y = x.clone()
+            for ly, (idx, wts) in zip(layers, routes):
+                y = run_layer(ly, y, idx, wts, act=act, residual=y)
+            return y
+        g, _ = graph_of(f)
+        t = time_graph(g, max(5, args.steps // 5), max(2, args.warmup // 5))
+        del g
+        return t
+
+    def report(name, sh, fmt, layers, T, act, shared_f=0, bias_bytes=0.0):
+        x = baseline_x(T, sh.d, seed=T, device=dev)
+        routes = [router.route(x, ly["wr"], sh.k) for ly in layers]
+        U = [int(torch.unique(r[0]).numel()) for r in routes]
+        t = chain_time(layers, x, routes, act) / len(layers)
+        per_e = roofline.expert_bytes(sh.d, sh.f, fmt) + bias_bytes
+        wb = np.mean(U) * per_e + (roofline.expert_bytes(sh.d, shared_f, fmt) if shared_f else 0.0)
+        fl = 6.0 * sh.d * sh.f * T * sh.k + 6.0 * sh.d * shared_f * T
+        hbm_floor = wb / (HBM_PEAK_GBS * 1e9)
+        mfma_floor = fl / 2.5e15
+        r = {"T": T, "us_per_layer": round(t * 1e6, 2), "tokens_per_s": round(T / t, 1),
+             "unique_experts_mean": round(float(np.mean(U)), 2), "weight_MB_per_layer": round(wb / 1e6, 2),
+             "weight_GBps": round(wb / t / 1e9, 1), "TFLOPs": round(fl / t / 1e12, 2),
+             "bound": "mfma" if mfma_floor > hbm_floor else "hbm",
+             "frac_of_roofline": round(max(hbm_floor, mfma_floor) / t, 4), "layers": len(layers)}
+        out[name] = r
+        log(f"{name}: {r}")
+
+    # config 4: gpt-oss-20b MXFP4, biases, clamped SwiGLU (act 2), softmax over the top-4
+    sh = SHAPES["gpt-oss-20b"]
+    layers = [baseline_mxfp4_layer(sh, seed=2000 + l, device=dev) for l in range(8)]
+    bias_b = 2 * (2 * sh.f + sh.d)   # bf16 gate/up/down biases per expert
+    for T in (1, 32):
+        report(f"gptoss20b_mxfp4_T{T}", sh, "mxfp4", layers, T, 2, bias_bytes=bias_b)
+    del layers
+    torch.cuda.empty_cache()
+    # config 5a: Mixtral-8x7B int4 T=512
+    sh = SHAPES["mixtral-8x7b"]
+    layers = [baseline_int4_layer(sh, seed=3000 + l, device=dev) for l in range(2)]
+    report("mixtral8x7b_int4_T512", sh, "int4", layers, 512, 0)
+    del layers
+    torch.cuda.empty_cache()
+    # config 5b: DeepSeek-V2-Lite int4 T=256, routed top-6 of 64 plus 2 shared experts (F=1408 each)
+    sh = SHAPES["deepseek-v2-lite"]
+    layers = []
+    for l in range(8):
+        ly = baseline_int4_layer(sh, seed=4000 + l, device=dev)
+        g = torch.Generator(device=dev).manual_seed(4100 + l)
+        ly["shared"] = make_state("int4", *(formats.random_int4(sh.shared, n, k, generator=g, device=dev)
+                                            for n, k in ((sh.f, sh.d), (sh.f, sh.d), (sh.d, sh.f))))
+        layers.append(ly)
+    report("dsv2lite_int4_T256_shared2", sh, "int4", layers, 256, 0, shared_f=sh.shared * sh.f)
+    del layers
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(layers, routes, x, sh):
