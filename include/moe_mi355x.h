@@ -89,6 +89,7 @@ size_t moe_row_bytes(int fmt, int K);
  *     row's words (index within the row, s = slice)
  *         MOE_FMT_INT4_G64: 16s + 2g, 16s + 2g + 1, 16s + 8 + 2g, 16s + 9 + 2g
  *         MOE_FMT_MXFP4:    16s + g, 16s + 4 + g, 16s + 8 + g, 16s + 12 + g
+ *     each with its nibbles (codes e0 .. e7, low nibble first) stored as e0 e2 e4 e6 e1 e3 e5 e7
  *     then the metadata of the slice's groups, per row r:
  *         MOE_FMT_INT4_G64: 8 bytes at 1024 + 8r = group words 2s, 2s + 1   (record: 1152 bytes)
  *         MOE_FMT_MXFP4:    4 bytes at 1024 + 4r = E8M0 bytes of groups 4s .. 4s + 3   (record: 1088 bytes)

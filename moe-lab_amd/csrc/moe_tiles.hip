@@ -29,6 +29,7 @@
 #include "moe_internal.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 #include <type_traits>
 
@@ -334,20 +335,15 @@ k_tile(TileArgs a) {
 // row's words (w = 16 s + ...)
 //     int4 g64:  j = 0, 1: 2 g + j        j = 2, 3: 8 + 2 g + (j - 2)     (steps 0,1 group 2s; 2,3 group 2s+1)
 //     MXFP4 g32: 4 j + g                                                  (step j = group 4 s + j)
-// and the A lane of token m loads the 8 activations of the same word (the piece with its index). x arrives in
-// natural order and is paired in registers (pair8); h is written by the gate/up wave tile already paired, as
-// the decoded codes are: element order (0,4,1,5,2,6,3,7) within each 8.
+// and the A lane of token m loads the 8 activations of the same word (the piece with its index). The records
+// store each word's nibbles interleaved (elements 0,2,4,6,1,3,5,7), so the 7-op decode yields its codes in
+// natural order and x and h are read as they lie in memory.
 // Every global load of slice s is issued D slices ahead into a register ring, in one fixed order, so the
 // in-order vmcnt wait for slice s leaves the D - 1 slices behind it in flight.
 // Tokens past the expert's count load the count's last token again (same addresses: no extra traffic); their
 // D rows are dropped (a row of D depends on the same row of X only). Inputs past K (the last slice when
 // K % 128 == 64) have zero codes and zero metadata in the record, and their activation loads are clamped into
 // the row, so they add 0.
-__device__ __forceinline__ int paired_pos(int r) {   // position of element r of its 8 in the paired order
-    const int j = r & 7;
-    return (r & ~7) | (j < 4 ? 2 * j : 2 * j - 7);
-}
-
 template <class FMT>
 __host__ __device__ constexpr int tile_slice_bytes() {
     return FMT::XSUM ? TILE_SLICE_INT4 : TILE_SLICE_MXFP4;
@@ -430,7 +426,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint4 v = NPROJ == 2 ? pair8(x[hl][t][j]) : x[hl][t][j];
+                        const uint4 v = x[hl][t][j];
                         X[hl][t][j] = as_bf16x8(v.x, v.y, v.z, v.w);
                     }
             f32x4 xs[NT][2];   // int4: sum of the activations over each of the slice's two groups
@@ -531,7 +527,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
                         if (a.b1) up += a.b1[(size_t)e * N + r];
                         const float hv = glu_act(a.act, g, up);
                         const uint16_t hi = f32_to_bf16(hv);
-                        const size_t o = (size_t)slot * N + paired_pos(r);
+                        const size_t o = (size_t)slot * N + r;
                         a.hout[o] = hi;
                         a.hout2[o] = f32_to_bf16(hv - bf16_to_f32(hi));
                     } else {
@@ -540,6 +536,255 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
                 }
             }
     }
+}
+
+// ============================================================================ dense tiles (many tokens per expert)
+// Where an expert's token count makes the contraction dense (tens to hundreds of tokens per expert: prefill, the
+// shared experts), each block keeps its weight tiles for a whole pass of 64 tokens and multiplies them on
+// MFMA against activations staged once per block in LDS. k_dense: a block of 4 waves owns BN rows of one expert
+// (gate and up: 128 rows of each, the GLU applied in registers; down: 256 rows) and 16 * NT tokens of it (one
+// pass; further passes loop); each wave covers all the pass's tokens for its 64 rows. Per K slice of 128 inputs:
+//   activations: the pass's token rows, brought into LDS by global_load_lds_dwordx4 (16 bytes per lane, 4 token
+//     rows of 256 bytes per instruction); piece p (8 inputs) of token m lies at position p ^ (m & 15) of the
+//     token's row, so the MFMA operand reads (16 tokens x one piece) hit distinct banks. Two buffers (distinct
+//     objects, so the compiler's LDS-DMA tracking sees that a read of one does not wait for the DMA into the
+//     other): slice s + 1 is in flight while slice s is multiplied; one vmcnt(0) + barrier per slice.
+//   weights: each wave streams its own 16-row tiles from the tile-major records (1 KB code burst + metadata per
+//     tile and slice) into registers one slice ahead and decodes them exactly (int4: bf16 128 + q; MXFP4:
+//     e2m1(q)), in natural order (the records interleave each word's nibbles for that).
+//   product: token-major like the wave tiles, D[token, row] on v_mfma_f32_16x16x32_bf16 (activations A, codes
+//     B) with the same per-group fp32 fold: per scale group P = sum code * x, int4 XS = sum x (one MFMA with an
+//     all-ones operand per token tile), acc += s P + (b - 128 s) XS, or acc += 2^(e-127) P.
+// Rounding the dequantised weights to bf16 instead would put up to ~2% of RMS of error on the outputs, and h
+// kept in one bf16 plane (the reference keeps h in x.dtype) ~1%; the exact operands and h as two bf16 planes
+// h = hi + lo (natural order, the wave tiles' layout) keep the error to fp32 accumulation. Down runs one MFMA
+// per plane into the same accumulator and writes yp[slot] in fp32 for k_combine.
+#define MOE_LDSP(p) ((__attribute__((address_space(3))) void*)(p))
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding)
+#define MOE_VMWAIT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
+// workgroup barrier without a memory fence; the "memory" clobber keeps LDS accesses on their side of it
+#define MOE_BARRIER() asm volatile("s_barrier" ::: "memory")
+
+template <class FMT, int NPROJ, int NT>
+__global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
+    constexpr bool INT4 = FMT::XSUM;
+    constexpr int SPG = INT4 ? 2 : 1;     // MFMA steps (32 inputs) per scale group
+    constexpr int RT = 4 / NPROJ;         // 16-row tiles per projection per wave
+    constexpr int BM = 16 * NT;           // tokens per pass
+    constexpr int BN = 4 * 16 * RT;       // rows per block (per projection)
+    constexpr int SB = tile_slice_bytes<FMT>();
+    constexpr int HL = NPROJ == 2 ? 1 : 2;   // activation planes: x, or h = hi + lo
+    constexpr int NDMA = BM / 16;         // DMA instructions per wave per slice and plane (4 token rows each)
+    __shared__ __attribute__((aligned(1024))) uint8_t sX0[HL * BM * 256];
+    __shared__ __attribute__((aligned(1024))) uint8_t sX1[HL * BM * 256];
+    __shared__ int sSlot[BM];
+
+    if ((int)blockIdx.y >= a.meta[0]) return;   // block-uniform
+    const int e = a.active[blockIdx.y];
+    const int n = a.counts[e], beg = a.offsets[e];
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int K = a.K, N = a.N;
+    const int nsl = (K + 127) >> 7;
+    const int lastp = (K >> 3) - 1;       // last 8-input piece of an activation row
+    const int r0 = blockIdx.x * BN + wave * 16 * RT;
+    const bool wvalid = r0 < N;           // N % (16 RT) == 0: a wave's rows are all in range or all out
+    const uint8_t* tb[NPROJ][RT];
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            tb[p][rt] = (p ? a.W1 : a.W0) +
+                        ((size_t)e * (N >> 4) + (wvalid ? (r0 >> 4) + rt : 0)) * (size_t)nsl * SB;
+    const uint8_t* xb[HL];
+    xb[0] = reinterpret_cast<const uint8_t*>(a.actv);
+    if (HL == 2) xb[HL - 1] = reinterpret_cast<const uint8_t*>(a.actv2);
+    // the DMA lanes: instruction i of this wave writes token rows 4 (wave + 4 i) + (lane >> 4), position lane & 15
+    const int psw = (lane & 15) ^ ((4 * wave + (lane >> 4)) & 15);   // piece loaded by this lane
+    const uint32_t ones = 0x3F803F80u;
+    const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
+
+    for (int tok0 = BM * blockIdx.z; tok0 < n; tok0 += BM * gridDim.z) {
+        const int nlive = n - tok0 < BM ? n - tok0 : BM;
+        const int ntiles = (nlive + 15) >> 4;
+        __syncthreads();   // the previous pass is done with sSlot and the buffers
+        if (tid < BM) sSlot[tid] = a.sorted[beg + (tok0 + tid < n ? tok0 + tid : n - 1)];
+        __syncthreads();
+        uint32_t xrow[NDMA];
+#pragma unroll
+        for (int i = 0; i < NDMA; ++i)
+            xrow[i] = (uint32_t)(sSlot[4 * (wave + 4 * i) + (lane >> 4)] / a.act_div) * (uint32_t)K * 2u;
+        auto dma = [&](int s, uint8_t* buf) __attribute__((always_inline)) {
+            int piece = 16 * s + psw;
+            piece = piece < lastp ? piece : lastp;   // inputs past K meet zero codes and zero metadata
+#pragma unroll
+            for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                for (int i = 0; i < NDMA; ++i) {
+                    // 32-bit offset from the uniform base (kept opaque so no 64-bit address is held per row)
+                    uint32_t o = xrow[i];
+                    asm volatile("" : "+v"(o));
+                    __builtin_amdgcn_global_load_lds((const void*)(xb[hl] + (o + 16u * (uint32_t)piece)),
+                                                     MOE_LDSP(buf + (hl * BM + 4 * (wave + 4 * i)) * 256), 16, 0, 0);
+                }
+        };
+        uint4 rq[2][NPROJ][RT];
+        uint2 rm[2][NPROJ][RT];
+        auto wissue = [&](int s, uint4 (&q)[NPROJ][RT], uint2 (&m)[NPROJ][RT]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const uint8_t* sl = tb[p][rt] + (uint32_t)s * (uint32_t)SB;
+                    q[p][rt] = *reinterpret_cast<const uint4*>(sl + 16 * lane);
+                    if (INT4) m[p][rt] = *reinterpret_cast<const uint2*>(sl + 1024 + 8 * lr);
+                    else m[p][rt].x = *reinterpret_cast<const uint32_t*>(sl + 1024 + 4 * lr);
+                }
+        };
+        f32x4 acc[NPROJ][RT][NT];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[p][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // one slice, scale group by scale group; lane (m, g) of MFMA step j supplies word wi(j, g) of its row
+        // (the record order). FULL: every token tile of the pass is live (no branch inside the slice)
+        auto compute = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT],
+                           const uint2 (&m)[NPROJ][RT]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int G = 0; G < 4 / SPG; ++G) {
+                __builtin_amdgcn_sched_barrier(0);   // one group at a time: bounds the live operands
+                bf16x8 B[NPROJ][RT][SPG];
+                float ms[NPROJ][RT], mc[NPROJ][RT];
+#pragma unroll
+                for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+                        for (int u = 0; u < SPG; ++u) {
+                            const int j = SPG * G + u;
+                            const uint32_t w = j == 0 ? q[p][rt].x : (j == 1 ? q[p][rt].y : (j == 2 ? q[p][rt].z : q[p][rt].w));
+                            uint32_t c4[4];
+                            FMT::decode_word(w, c4);
+                            B[p][rt][u] = as_bf16x8(c4[0], c4[1], c4[2], c4[3]);
+                        }
+                        if (INT4) {
+                            const uint32_t mw = G ? m[p][rt].y : m[p][rt].x;
+                            ms[p][rt] = bf16lo(mw);
+                            mc[p][rt] = __builtin_fmaf(-128.f, ms[p][rt], bf16hi(mw));
+                        } else {
+                            ms[p][rt] = __uint_as_float(((m[p][rt].x >> (8 * G)) & 0xFFu) << 23);
+                            mc[p][rt] = 0.f;
+                        }
+                    }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    if (decltype(full)::value || t < ntiles) {   // wave-uniform
+                        bf16x8 A[HL][SPG];
+#pragma unroll
+                        for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                            for (int u = 0; u < SPG; ++u) {
+                                const int j = SPG * G + u;
+                                const int wi = INT4 ? (j < 2 ? 2 * lg + j : 8 + 2 * lg + (j - 2)) : 4 * j + lg;
+                                const uint4 av = *reinterpret_cast<const uint4*>(
+                                    xs + (hl * BM + 16 * t + lr) * 256 + 16 * (wi ^ lr));
+                                A[hl][u] = as_bf16x8(av.x, av.y, av.z, av.w);
+                            }
+                        f32x4 xsum = f32x4{0.f, 0.f, 0.f, 0.f};
+                        if (INT4) {
+#pragma unroll
+                            for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                                for (int u = 0; u < SPG; ++u)
+                                    xsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[hl][u], ONES, xsum, 0, 0, 0);
+                        }
+#pragma unroll
+                        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                            for (int rt = 0; rt < RT; ++rt) {
+                                f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                                for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                                    for (int u = 0; u < SPG; ++u)
+                                        P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[hl][u], B[p][rt][u], P, 0, 0, 0);
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) {
+                                    if (INT4)
+                                        acc[p][rt][t][v] = __builtin_fmaf(ms[p][rt], P[v],
+                                                                          __builtin_fmaf(mc[p][rt], xsum[v], acc[p][rt][t][v]));
+                                    else
+                                        acc[p][rt][t][v] = __builtin_fmaf(ms[p][rt], P[v], acc[p][rt][t][v]);
+                                }
+                            }
+                    }
+                }
+            }
+        };
+        // slice s sits in buffer / ring slot s & 1; slice s + 1 is fetched during slice s (the last slice fetches
+        // itself again into the idle slot: no branch around the loads)
+        auto run = [&](auto full) __attribute__((always_inline)) {
+            dma(0, sX0);
+            wissue(0, rq[0], rm[0]);
+            MOE_VMWAIT0();
+            MOE_BARRIER();
+            int s = 0;
+            for (; s + 2 <= nsl; s += 2) {
+                wissue(s + 1, rq[1], rm[1]);
+                dma(s + 1, sX1);
+                compute(full, sX0, rq[0], rm[0]);
+                MOE_VMWAIT0();
+                MOE_BARRIER();
+                const int sn = s + 2 < nsl ? s + 2 : s + 1;
+                wissue(sn, rq[0], rm[0]);
+                dma(sn, sX0);
+                compute(full, sX1, rq[1], rm[1]);
+                MOE_VMWAIT0();
+                MOE_BARRIER();
+            }
+            if (s < nsl) compute(full, sX0, rq[0], rm[0]);   // odd count: the last slice is in slot 0
+        };
+        if (ntiles == NT) run(std::true_type{});
+        else run(std::false_type{});
+
+        // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
+        if (wvalid) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int jt = 16 * t + 4 * lg + v;
+                    if (jt >= nlive) continue;
+                    const int slot = sSlot[jt];
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const int r = r0 + 16 * rt + lr;
+                        if (NPROJ == 2) {
+                            float g = acc[0][rt][t][v], up = acc[NPROJ - 1][rt][t][v];
+                            if (a.b0) g += a.b0[(size_t)e * N + r];
+                            if (a.b1) up += a.b1[(size_t)e * N + r];
+                            const float hv = glu_act(a.act, g, up);
+                            const uint16_t hi = f32_to_bf16(hv);
+                            a.hout[(size_t)slot * N + r] = hi;
+                            a.hout2[(size_t)slot * N + r] = f32_to_bf16(hv - bf16_to_f32(hi));
+                        } else {
+                            a.yp[(size_t)slot * N + r] = acc[0][rt][t][v];
+                        }
+                    }
+                }
+        }
+    }
+}
+
+// nibbles (e0 .. e7) of a word -> (e0, e2, e4, e6, e1, e3, e5, e7): the decode pairs nibbles i and i + 4, which
+// then hold the adjacent elements (2i, 2i + 1)
+__device__ __forceinline__ uint32_t interleave_nibbles(uint32_t w) {
+    auto squeeze = [](uint32_t b) {   // low nibbles of the 4 bytes -> 16 bits
+        return (b & 0xFu) | ((b >> 4) & 0xF0u) | ((b >> 8) & 0xF00u) | ((b >> 12) & 0xF000u);
+    };
+    return squeeze(w & 0x0F0F0F0Fu) | (squeeze((w >> 4) & 0x0F0F0F0Fu) << 16);
 }
 
 // rows [E, N, rbytes] -> tiles [E, N/16, ceil(K/128), slice record]; grid (slices, N/16, E), 64 lanes
@@ -559,7 +804,7 @@ __global__ void __launch_bounds__(64) k_pack_tiles(const uint8_t* __restrict__ r
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int wi = FMT::XSUM ? 16 * s + 8 * (j >> 1) + 2 * g + (j & 1) : 16 * s + 4 * j + g;
-        w[j] = wi < nw ? words[wi] : 0u;
+        w[j] = interleave_nibbles(wi < nw ? words[wi] : 0u);
     }
     *reinterpret_cast<uint4*>(rec + 16 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
     if (g == 0) {
@@ -629,6 +874,28 @@ int launch_wave_tile(const TileArgs& t, int nt, int max_active, int T, hipStream
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
+// dense tiles: DENSE_NT token tiles (64 tokens) per pass, passes over blockIdx.z. 64 tokens x 64 rows per wave
+// keep the fold's accumulators (64 VGPRs) and everything else within 256 VGPRs at 2 waves per SIMD; 128 tokens
+// would push the accumulators into AGPRs, which the fold's VALU cannot use in place.
+constexpr int DENSE_NT = 4;
+
+template <class FMT, int NPROJ>
+int launch_dense(const TileArgs& t, int T, int max_active, hipStream_t st) {
+    constexpr int BN = 64 * (4 / NPROJ);
+    if (t.N % (64 / NPROJ)) return MOE_ERR_ARG;
+    const int zp = (T + 16 * DENSE_NT - 1) / (16 * DENSE_NT);   // an expert has at most T slots
+    dim3 grid((t.N + BN - 1) / BN, max_active, zp < 1 ? 1 : (zp > 32 ? 32 : zp));
+    k_dense<FMT, NPROJ, DENSE_NT><<<grid, 256, 0, st>>>(t);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+// MOE_DENSE (environment, read per call; a tuning and test knob): 0 turns the dense tiles off (the LDS-staged
+// row tiles run instead for many tokens per expert)
+bool dense_enabled() {
+    const char* v = getenv("MOE_DENSE");
+    return !(v && atoi(v) == 0);
+}
+
 template <class FMT>
 int run_tiles_fmt(const ExpertsArgs& a) {
     const moe_experts_t* w = a.w;
@@ -644,8 +911,11 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     t.E = w->E;
     t.act = a.act;
     t.kslots = a.k;
-    // tile-major weights present: wave tiles (their h is written paired; both stages take the same branch)
-    const bool wave = w->gate.tiles && w->up.tiles && w->down.tiles && nt <= MOE_WAVE_NT;
+    // tile-major weights present: wave tiles for few tokens per expert, dense tiles for many; the choice
+    // depends on (T, k, E) only, so separately launched stages agree on the layout of h between them
+    const bool tiled = w->gate.tiles && w->up.tiles && w->down.tiles;
+    const bool wave = tiled && nt <= MOE_WAVE_NT;
+    const bool dense = tiled && !wave && dense_enabled();
     if (a.stages & 1) {
         int rc = launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
                               a.grp.meta, a.st);
@@ -661,12 +931,13 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         g.b1 = w->up.bias;
         g.hout = a.hhi;
         g.hout2 = a.hlo;
-        if (wave) {
+        if (wave || dense) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
         }
-        rc = wave ? launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, max_active, a.T, a.st)
-                  : launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
+        if (dense) rc = launch_dense<FMT, 2>(g, a.T, max_active, a.st);
+        else if (wave) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, max_active, a.T, a.st);
+        else rc = launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
         if (rc) return rc;
     }
     if (a.stages & 2) {
@@ -678,9 +949,11 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.N = w->d;
         d.W0 = (const uint8_t*)w->down.rows;
         d.yp = a.yp;
-        if (wave) d.W0 = (const uint8_t*)w->down.tiles;
-        int rc = wave ? launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, max_active, a.T, a.st)
-                      : launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
+        if (wave || dense) d.W0 = (const uint8_t*)w->down.tiles;
+        int rc;
+        if (dense) rc = launch_dense<FMT, 1>(d, a.T, max_active, a.st);
+        else if (wave) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, max_active, a.T, a.st);
+        else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
         return launch_combine(a.yp, a.idx, a.wts, w->down.bias, w->E, a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
     }

@@ -91,6 +91,16 @@ def tile_word_index(fmt, s, g, j):
     return 16 * s + 4 * j + g
 
 
+def interleave_nibbles(w):
+    """int32 code words with nibbles (e0 .. e7) -> (e0, e2, e4, e6, e1, e3, e5, e7), as the tile records hold
+    them (the kernels' decode pairs nibbles i and i + 4, which then are the adjacent elements 2i, 2i + 1)."""
+    u = w.to(torch.int64) & 0xFFFFFFFF
+    out = torch.zeros_like(u)
+    for i, src in enumerate((0, 2, 4, 6, 1, 3, 5, 7)):
+        out |= ((u >> (4 * src)) & 0xF) << (4 * i)
+    return torch.where(out >= 2 ** 31, out - 2 ** 32, out).to(torch.int32)
+
+
 def pack_tiles_ref(fmt, rows, K):
     """Host restatement of moe_tiles_pack: uint8 row records [E, N, row_bytes] -> uint8 [E * tile bytes].
     Test-side only (the library packs on the device); a plain loop over the documented layout."""
@@ -105,7 +115,7 @@ def pack_tiles_ref(fmt, rows, K):
     for e in range(E):
         for t in range(N // 16):
             w = words[e, 16 * t:16 * t + 16]                                  # [16 rows, K/8]
-            cw = torch.where(valid[None], w[:, wi.clamp(max=K // 8 - 1)], 0)  # [16, S, 4 g, 4 j]
+            cw = torch.where(valid[None], interleave_nibbles(w[:, wi.clamp(max=K // 8 - 1)]), 0)  # [16, S, g, j]
             out[e, t, :, :1024] = cw.permute(1, 2, 0, 3).contiguous().view(torch.uint8).reshape(S, 1024)
             meta = rows[e, 16 * t:16 * t + 16, K // 2:]
             if fmt == FMT_INT4:

@@ -299,10 +299,11 @@ def test_grouped_without_tile_copies(T):
     assert_close(y, oracle_y(s, x, idx, wts), what=("rows", T))
 
 
-@pytest.mark.parametrize("T", [2, 16, 40, 130])
+@pytest.mark.parametrize("T", [2, 16, 40, 120])
 def test_tile_copies_and_row_records_agree(T):
     """The grouped path forced with and without the tile-major copies (wave tiles vs row-major tiles): each
-    within the gate of the oracle, and of each other up to fp32 reassociation."""
+    within the gate of the oracle, and of each other up to fp32 reassociation (T * k / E <= 32 tokens per
+    expert: the wave tiles; more goes to the dense tiles, tested below)."""
     from moelab_amd.experts import drop_tiles
     sh = shape_("t", 512, 384, 16, 4)
     s = packed_state(sh, 9)
@@ -315,6 +316,50 @@ def test_tile_copies_and_row_records_agree(T):
     assert_close(y2, ref, what=("rows", T))
     rms = float(y1.pow(2).mean().sqrt())
     assert float((y1 - y2).abs().max()) <= 1e-3 * rms
+
+
+DENSE_CASES = [
+    # (name, d, F, E, k, T, routing): tokens per expert T k / E > 32 selects the dense tiles
+    ("even", 256, 384, 4, 2, 100, "uniform"),       # 50 per expert
+    ("big", 512, 1024, 8, 2, 600, "uniform"),       # 150 per expert: three passes of 64, the last partial
+    ("odd-K", 320, 448, 4, 2, 180, "zipf"),         # K % 128 == 64 both ways, N % 128 != 0, uneven counts
+    ("one-expert", 256, 384, 1, 1, 2100, "uniform"),  # 2100 tokens: more passes than the grid's z extent
+    ("k=E", 192, 256, 4, 4, 40, "uniform"),         # every token in every expert
+]
+
+
+@pytest.mark.parametrize("case", DENSE_CASES, ids=lambda c: c[0])
+def test_dense_tiles(case):
+    """Many tokens per expert: the dense tiles (exact codes on bf16 MFMA with the per-group fp32 fold, 64
+    tokens per pass, h one bf16 plane) against the oracle at the north-star gate."""
+    name, d, f, E, k, T, routing = case
+    sh = shape_(name, d, f, E, k)
+    s = packed_state(sh, 31)
+    x, idx, wts = inputs(sh, T, routing, seed=T)
+    print(f"case dense {name} T={T}", flush=True)
+    y32 = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    y = grouped(s, x, idx, wts)
+    torch.cuda.synchronize()
+    ref = oracle_y(s, x, idx, wts)
+    assert_close(y32, ref, what=("dense", name, "fp32 out"))
+    assert_close(y, ref, what=("dense", name, "bf16 out"))
+
+
+def test_dense_tiles_match_row_tiles(monkeypatch):
+    """Dense tiles vs the LDS-staged row tiles (MOE_DENSE=0) on the same inputs: both at the gate, and within
+    the dense path's bf16 rounding of h (the row tiles keep h as two bf16 planes) of each other."""
+    sh = shape_("dr", 512, 768, 8, 2)
+    s = packed_state(sh, 33)
+    x, idx, wts = inputs(sh, 400, "zipf", seed=5)
+    print("case dense-vs-rows T=400", flush=True)
+    y1 = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    monkeypatch.setenv("MOE_DENSE", "0")
+    y2 = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    ref = oracle_y(s, x, idx, wts)
+    assert_close(y1, ref, what="dense")
+    assert_close(y2, ref, what="rows")
+    rms = float(y2.pow(2).mean().sqrt())
+    assert float((y1 - y2).abs().max()) <= 1e-2 * rms
 
 
 def shared_state(d, Fs, S, seed, fmt="int4"):

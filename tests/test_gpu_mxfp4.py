@@ -128,7 +128,7 @@ def test_e8m0_scale_regimes(lo, hi, T):
     assert_close(y32, ref, what=(lo, hi))
 
 
-@pytest.mark.parametrize("T", [1, 3, 9, 32])
+@pytest.mark.parametrize("T", [1, 3, 9, 32, 100])
 @pytest.mark.parametrize("act", [0, 1])
 def test_gptoss_biases_and_clamped_glu(T, act):
     sh = shape_("g", 704, 704, 8, 4)
@@ -202,3 +202,18 @@ def test_mxfp4_tile_copies_and_row_records_agree(T):
     assert_close(y2, ref, what=("rows", T))
     rms = float(y1.pow(2).mean().sqrt())
     assert float((y1 - y2).abs().max()) <= 1e-3 * rms
+
+
+@pytest.mark.parametrize("case", [("even", 256, 384, 4, 2, 100, "uniform"), ("odd-K", 320, 448, 4, 2, 180, "zipf"),
+                                  ("big", 512, 1024, 8, 2, 600, "uniform")], ids=lambda c: c[0])
+def test_mxfp4_dense_tiles(case):
+    """MXFP4 with many tokens per expert (T k / E > 32): the dense tiles against the oracle at the gate."""
+    from moelab_amd import _lib
+    from moelab_amd.experts import run_experts
+    name, d, f, E, k, T, routing = case
+    sh = shape_(name, d, f, E, k)
+    s = packed_state(sh, 41)
+    x, idx, wts = inputs(sh, T, routing, seed=T)
+    print(f"case mxfp4 dense {name} T={T}", flush=True)
+    y = run_experts(s, x, idx, wts, path=_lib.PATH_GROUPED, out_dtype=torch.float32)
+    assert_close(y, oracle_y(s, x, idx, wts), what=("mxfp4 dense", name))

@@ -23,6 +23,38 @@ def self_describing_rows(fmt, E, N, K):
     return rows, words
 
 
+def deinterleave(w):
+    """Inverse of the stored nibble order: nibble i of the stored word is element (0,2,4,6,1,3,5,7)[i]."""
+    u = w.to(torch.int64) & 0xFFFFFFFF
+    out = torch.zeros_like(u)
+    for i, dst in enumerate((0, 2, 4, 6, 1, 3, 5, 7)):
+        out |= ((u >> (4 * i)) & 0xF) << (4 * dst)
+    return torch.where(out >= 2 ** 31, out - 2 ** 32, out).to(torch.int32)
+
+
+def decode_pairs(w):
+    """The kernels' 7-op int4 decode restated on the host: t = nibbles 0,2,4,6 and u = nibbles 1,3,5,7 in the
+    low halves of bytes; the bf16 pairs are (t.b0, t.b2), (u.b0, u.b2), (t.b1, t.b3), (u.b1, u.b3). Returns the
+    8 codes in the order the MFMA operand receives them."""
+    t = [(w >> (8 * b)) & 0xF for b in range(4)]
+    u = [(w >> (8 * b + 4)) & 0xF for b in range(4)]
+    return [t[0], t[2], u[0], u[2], t[1], t[3], u[1], u[3]]
+
+
+def test_stored_nibbles_decode_in_natural_order():
+    """A word as stored in a tile record decodes, through the kernels' pairing, to elements 0..7 in order
+    (so activations and h are used as they lie in memory)."""
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        codes = rng.integers(0, 16, 8)
+        w = int(sum(int(c) << (4 * i) for i, c in enumerate(codes)))
+        w32 = torch.tensor([w - 2 ** 32 if w >= 2 ** 31 else w], dtype=torch.int32)
+        stored = int(formats.interleave_nibbles(w32)[0]) & 0xFFFFFFFF
+        assert decode_pairs(stored) == codes.tolist()
+        assert int(deinterleave(torch.tensor([stored - 2 ** 32 if stored >= 2 ** 31 else stored],
+                                             dtype=torch.int32))[0]) & 0xFFFFFFFF == w
+
+
 @pytest.mark.parametrize("fmt", ["int4", "mxfp4"])
 @pytest.mark.parametrize("K", [128, 192, 256, 320])
 def test_every_word_moves_once_and_steps_stay_in_one_group(fmt, K):
@@ -33,7 +65,8 @@ def test_every_word_moves_once_and_steps_stay_in_one_group(fmt, K):
     sb = formats.TILE_SLICE_BYTES[fmt]
     assert t.numel() == E * (N // 16) * S * sb
     rec = t.reshape(E, N // 16, S, sb)
-    codes = rec[..., :1024].contiguous().view(torch.int32).reshape(E, N // 16, S, 4, 16, 4).numpy()  # [.., g, r, j]
+    stored = rec[..., :1024].contiguous().view(torch.int32).reshape(E, N // 16, S, 4, 16, 4)  # [.., g, r, j]
+    codes = deinterleave(stored).numpy()
     nz = codes[codes != 0]
     # bijection: every (e, n, w) word exactly once, and only zero padding besides
     assert sorted(nz.tolist()) == sorted(words.reshape(-1).tolist())
