@@ -18,7 +18,7 @@ int resolve_path(int path, int T) {
 }
 
 struct Layout {
-    size_t h, yp, counts, offsets, sorted, active, meta, total;
+    size_t h, yp, counts, offsets, sorted, active, meta, items, total;
 };
 
 Layout layout(const moe_experts_t* w, int T, int k, int path) {
@@ -39,7 +39,9 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
         L.active = off;
         off += align_up((size_t)w->E * 4);
         L.meta = off;
-        off += align_up(2 * 4);
+        off += align_up(4 * 4);
+        L.items = off;
+        off += align_up((size_t)moe::max_passes((int)nslots, w->E, 16) * 12);
     }
     L.total = off;
     return L;
@@ -199,6 +201,7 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
         a.grp.sorted = (int32_t*)(ws + L.sorted);
         a.grp.active = (int32_t*)(ws + L.active);
         a.grp.meta = (int32_t*)(ws + L.meta);
+        a.grp.items = (int32_t*)(ws + L.items);
     }
     return rpath == MOE_PATH_GROUPED ? moe::run_experts_tiles(a) : moe::run_experts_slots(a);
 }

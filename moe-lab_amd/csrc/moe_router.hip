@@ -192,9 +192,13 @@ topk_kernel(const LT* __restrict__ logits, int T, int E, int k, int norm, float 
 // are left out of every group (they contribute nothing) and counted in meta[1].
 // Outputs: counts[E], offsets[E+1], sorted[n] (valid part: offsets[E] entries), active[E] (first meta[0]
 // entries: experts with count > 0, ascending), meta[0] = number of active experts, meta[1] = bad ids.
+// With items != null (the grouped kernels' work list, pass size P): items[3w .. 3w + 2] = (expert, pass index q
+// within the expert (first token q * P), the expert's pass count) of pass w; the passes of each active expert in
+// ascending order, expert by expert; meta[2] = number of passes.
 __global__ void __launch_bounds__(256)
 group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-            int32_t* __restrict__ sorted, int32_t* __restrict__ active, int32_t* __restrict__ meta) {
+            int32_t* __restrict__ sorted, int32_t* __restrict__ active, int32_t* __restrict__ meta, int P,
+            int32_t* __restrict__ items) {
     extern __shared__ int32_t sm[];   // cnt[E], cursor[E]
     int32_t* cnt = sm;
     int32_t* cursor = sm + E;
@@ -211,17 +215,19 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
     __syncthreads();
     if (tid < 64) {   // wave 0: exclusive scan of counts and the active list, in chunks of 64 experts
         const int lane = tid;
-        int run = 0, run_act = 0;
+        int run = 0, run_act = 0, run_p = 0;
         for (int base = 0; base < E; base += 64) {
             const int e = base + lane;
             const int c = e < E ? cnt[e] : 0;
-            // inclusive wave scan of c and of (c > 0)
-            int inc = c, act = c > 0 ? 1 : 0;
+            const int np = items ? (c + P - 1) / P : 0;   // passes of expert e
+            // inclusive wave scans of c, of (c > 0) and of the pass counts
+            int inc = c, act = c > 0 ? 1 : 0, incp = np;
 #pragma unroll
             for (int s = 1; s < 64; s <<= 1) {
                 const int o = __shfl_up(inc, s, 64);
                 const int oa = __shfl_up(act, s, 64);
-                if (lane >= s) { inc += o; act += oa; }
+                const int op = __shfl_up(incp, s, 64);
+                if (lane >= s) { inc += o; act += oa; incp += op; }
             }
             if (e < E) {
                 const int excl = run + inc - c;
@@ -229,14 +235,22 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
                 cursor[e] = excl;
                 counts[e] = c;
                 if (c > 0) active[run_act + act - 1] = e;
+                const int w0 = run_p + incp - np;
+                for (int q = 0; q < np; ++q) {
+                    items[3 * (w0 + q)] = e;
+                    items[3 * (w0 + q) + 1] = q;
+                    items[3 * (w0 + q) + 2] = np;
+                }
             }
             run += __shfl(inc, 63, 64);
             run_act += __shfl(act, 63, 64);
+            run_p += __shfl(incp, 63, 64);
         }
         if (lane == 0) {
             offsets[E] = run;
             meta[0] = run_act;
             meta[1] = s_bad;
+            if (items) meta[2] = run_p;
         }
         for (int a = run_act + lane; a < E; a += 64) active[a] = -1;
     }
@@ -342,8 +356,9 @@ int launch_shared_route(const uint16_t* x, const uint16_t* gate, int T, int d, i
 }
 
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
-                 int32_t* active, int32_t* meta, hipStream_t st) {
-    group_slots<<<1, 256, 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted, active, meta);
+                 int32_t* active, int32_t* meta, hipStream_t st, int P, int32_t* items) {
+    if (items && P < 1) return MOE_ERR_ARG;
+    group_slots<<<1, 256, 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted, active, meta, P, items);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

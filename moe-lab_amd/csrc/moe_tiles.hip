@@ -53,6 +53,7 @@ struct TileArgs {
     const float* b0;       // additive row biases [E, N] (gpt-oss) or null
     const float* b1;
     const int32_t *counts, *offsets, *sorted, *active, *meta;
+    const int32_t* items;  // wave and dense tiles: pass list (expert, pass, passes), meta[2] passes
     int K, N, E, act;      // act: GLU kind (gate/up)
     int rpb;               // row tiles per block (k_tile_run)
     int kslots;            // k (slots per token)
@@ -354,8 +355,8 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     constexpr bool INT4 = FMT::XSUM;
     constexpr int HL = NPROJ == 2 ? 1 : 2;   // activation planes: x, or h = hi + lo
     constexpr int SB = tile_slice_bytes<FMT>();
-    if ((int)blockIdx.y >= a.meta[0]) return;
-    const int e = a.active[blockIdx.y];
+    if ((int)blockIdx.y >= a.meta[2]) return;   // one pass of the work list per workgroup row
+    const int e = a.items[3 * blockIdx.y], tok0 = a.items[3 * blockIdx.y + 1] * 16 * NT;
     const int n = a.counts[e], beg = a.offsets[e];
     const int lane = threadIdx.x, lr = lane & 15, lg = lane >> 4;
     const int K = a.K, N = a.N;
@@ -372,7 +373,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     const uint32_t ones = 0x3F803F80u;
     const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
 
-    for (int tok0 = 16 * NT * blockIdx.z; tok0 < n; tok0 += 16 * NT * gridDim.z) {
+    {
         // byte offset of the lane's activation row (A side: token tok0 + 16 t + lr)
         uint32_t xo[NT];
         int slotA[NT];
@@ -540,10 +541,12 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
 
 // ============================================================================ dense tiles (many tokens per expert)
 // Where an expert's token count makes the contraction dense (tens to hundreds of tokens per expert: prefill, the
-// shared experts), each block keeps its weight tiles for a whole pass of 64 tokens and multiplies them on
-// MFMA against activations staged once per block in LDS. k_dense: a block of 4 waves owns BN rows of one expert
-// (gate and up: 128 rows of each, the GLU applied in registers; down: 256 rows) and 16 * NT tokens of it (one
-// pass; further passes loop); each wave covers all the pass's tokens for its 64 rows. Per K slice of 128 inputs:
+// shared experts), each block keeps its weight tiles for a pass of 64 tokens and multiplies them on MFMA
+// against activations staged once per block in LDS. k_dense: a block of 4 waves owns BN rows of one expert (gate
+// and up: 128 rows of each, the GLU applied in registers; down: 256 rows) and one pass of the work list (up to
+// 16 * NT tokens of it); each wave covers all the pass's tokens for its 64 rows. (8-wave blocks of 128 tokens,
+// sharing each weight tile between two token halves, measured slower: one barrier domain per CU instead of two
+// independent blocks.) Per K slice of 128 inputs:
 //   activations: the pass's token rows, brought into LDS by global_load_lds_dwordx4 (16 bytes per lane, 4 token
 //     rows of 256 bytes per instruction); piece p (8 inputs) of token m lies at position p ^ (m & 15) of the
 //     token's row, so the MFMA operand reads (16 tokens x one piece) hit distinct banks. Two buffers (distinct
@@ -579,15 +582,23 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t sX1[HL * BM * 256];
     __shared__ int sSlot[BM];
 
-    if ((int)blockIdx.y >= a.meta[0]) return;   // block-uniform
-    const int e = a.active[blockIdx.y];
+    // 1-D grid over (pass list x row blocks), ordered expert by expert, and within an expert row block by row
+    // block with the expert's passes adjacent: the passes that share a weight tile run side by side (their
+    // second reads come from the caches), and the blocks in flight touch the activations of few experts
+    const int nrb = (a.N + BN - 1) / BN;
+    const int wq = blockIdx.x / nrb;               // some pass of the current expert
+    if (wq >= a.meta[2]) return;
+    const int e = a.items[3 * wq], np = a.items[3 * wq + 2];
+    const int w0 = wq - a.items[3 * wq + 1];       // the expert's first pass
+    const int local = blockIdx.x - w0 * nrb;
+    const int rb = local / np, tok0 = (local - rb * np) * BM;
     const int n = a.counts[e], beg = a.offsets[e];
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, N = a.N;
     const int nsl = (K + 127) >> 7;
     const int lastp = (K >> 3) - 1;       // last 8-input piece of an activation row
-    const int r0 = blockIdx.x * BN + wave * 16 * RT;
+    const int r0 = rb * BN + wave * 16 * RT;
     const bool wvalid = r0 < N;           // N % (16 RT) == 0: a wave's rows are all in range or all out
     const uint8_t* tb[NPROJ][RT];
 #pragma unroll
@@ -604,10 +615,9 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     const uint32_t ones = 0x3F803F80u;
     const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
 
-    for (int tok0 = BM * blockIdx.z; tok0 < n; tok0 += BM * gridDim.z) {
+    {
         const int nlive = n - tok0 < BM ? n - tok0 : BM;
         const int ntiles = (nlive + 15) >> 4;
-        __syncthreads();   // the previous pass is done with sSlot and the buffers
         if (tid < BM) sSlot[tid] = a.sorted[beg + (tok0 + tid < n ? tok0 + tid : n - 1)];
         __syncthreads();
         uint32_t xrow[NDMA];
@@ -865,27 +875,27 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 #define MOE_WAVE_RT_DN 4   // 16-row tiles per wave, down (d % 64 == 0)
 #endif
 template <class FMT, int NPROJ, int RT, int D>
-int launch_wave_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st) {
+int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st) {
     if (t.N % (16 * RT)) return MOE_ERR_ARG;
-    const int zp = (T + 16 * nt - 1) / (16 * nt);
-    dim3 grid(t.N / (16 * RT), max_active, zp < 1 ? 1 : (zp > 16 ? 16 : zp));
+    dim3 grid(t.N / (16 * RT), max_passes(nslots, t.E, 16 * nt));
+    if (grid.y > 65535) return MOE_ERR_ARG;
     if (nt == 1) k_wave_tile<FMT, NPROJ, 1, RT, D><<<grid, 64, 0, st>>>(t);
     else k_wave_tile<FMT, NPROJ, 2, RT, D><<<grid, 64, 0, st>>>(t);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-// dense tiles: DENSE_NT token tiles (64 tokens) per pass, passes over blockIdx.z. 64 tokens x 64 rows per wave
-// keep the fold's accumulators (64 VGPRs) and everything else within 256 VGPRs at 2 waves per SIMD; 128 tokens
-// would push the accumulators into AGPRs, which the fold's VALU cannot use in place.
+// dense tiles: passes of DENSE_NT token tiles (64 tokens). 64 tokens x 64 rows per wave keep the fold's
+// accumulators (64 VGPRs) and everything else within 256 VGPRs at 2 waves per SIMD; 128 tokens per wave would
+// push the accumulators into AGPRs, which the fold's VALU cannot use in place.
 constexpr int DENSE_NT = 4;
 
 template <class FMT, int NPROJ>
-int launch_dense(const TileArgs& t, int T, int max_active, hipStream_t st) {
+int launch_dense(const TileArgs& t, int nslots, hipStream_t st) {
     constexpr int BN = 64 * (4 / NPROJ);
     if (t.N % (64 / NPROJ)) return MOE_ERR_ARG;
-    const int zp = (T + 16 * DENSE_NT - 1) / (16 * DENSE_NT);   // an expert has at most T slots
-    dim3 grid((t.N + BN - 1) / BN, max_active, zp < 1 ? 1 : (zp > 32 ? 32 : zp));
-    k_dense<FMT, NPROJ, DENSE_NT><<<grid, 256, 0, st>>>(t);
+    const long nblk = (long)((t.N + BN - 1) / BN) * max_passes(nslots, t.E, 16 * DENSE_NT);
+    if (nblk > 0x7FFFFFFFL) return MOE_ERR_ARG;
+    k_dense<FMT, NPROJ, DENSE_NT><<<dim3((unsigned)nblk), 256, 0, st>>>(t);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
@@ -916,9 +926,12 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     const bool tiled = w->gate.tiles && w->up.tiles && w->down.tiles;
     const bool wave = tiled && nt <= MOE_WAVE_NT;
     const bool dense = tiled && !wave && dense_enabled();
+    t.items = a.grp.items;
+    // pass size of the work list: 16 nt tokens for the wave tiles, 16 DENSE_NT for the dense tiles
+    const int P = dense ? 16 * DENSE_NT : 16 * nt;
     if (a.stages & 1) {
         int rc = launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
-                              a.grp.meta, a.st);
+                              a.grp.meta, a.st, P, a.grp.items);
         if (rc) return rc;
         TileArgs g = t;
         g.actv = (const uint16_t*)a.x;
@@ -935,8 +948,8 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
         }
-        if (dense) rc = launch_dense<FMT, 2>(g, a.T, max_active, a.st);
-        else if (wave) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, max_active, a.T, a.st);
+        if (dense) rc = launch_dense<FMT, 2>(g, nslots, a.st);
+        else if (wave) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st);
         else rc = launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
         if (rc) return rc;
     }
@@ -951,8 +964,8 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.yp = a.yp;
         if (wave || dense) d.W0 = (const uint8_t*)w->down.tiles;
         int rc;
-        if (dense) rc = launch_dense<FMT, 1>(d, a.T, max_active, a.st);
-        else if (wave) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, max_active, a.T, a.st);
+        if (dense) rc = launch_dense<FMT, 1>(d, nslots, a.st);
+        else if (wave) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
         return launch_combine(a.yp, a.idx, a.wts, w->down.bias, w->E, a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
