@@ -59,7 +59,9 @@ struct TileArgs {
     int kslots;            // k (slots per token)
     uint16_t* hout;        // gate/up: h = hi + lo as two bf16 planes [T*k, N]
     uint16_t* hout2;
-    float* yp;             // down: [T*k, N] fp32
+    float* yp;             // down: [T*k, N] fp32 (dense tiles split over K: ksplit such planes, plane floats apart)
+    int ksplit;
+    size_t plane;
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -586,17 +588,22 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     // block with the expert's passes adjacent: the passes that share a weight tile run side by side (their
     // second reads come from the caches), and the blocks in flight touch the activations of few experts
     const int nrb = (a.N + BN - 1) / BN;
-    const int wq = blockIdx.x / nrb;               // some pass of the current expert
+    const int ks = (int)(blockIdx.x % (unsigned)a.ksplit);   // K part (down only), the fastest index
+    const int bid = (int)(blockIdx.x / (unsigned)a.ksplit);
+    const int wq = bid / nrb;                      // some pass of the current expert
     if (wq >= a.meta[2]) return;
     const int e = a.items[3 * wq], np = a.items[3 * wq + 2];
     const int w0 = wq - a.items[3 * wq + 1];       // the expert's first pass
-    const int local = blockIdx.x - w0 * nrb;
+    const int local = bid - w0 * nrb;
     const int rb = local / np, tok0 = (local - rb * np) * BM;
     const int n = a.counts[e], beg = a.offsets[e];
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, N = a.N;
     const int nsl = (K + 127) >> 7;
+    const int per = (nsl + a.ksplit - 1) / a.ksplit;
+    const int sb0 = ks * per;                                // this block's slices: sb0 .. sb0 + scnt - 1
+    const int scnt = nsl - sb0 < per ? nsl - sb0 : per;   // >= 1 (the host splits only when it is)
     const int lastp = (K >> 3) - 1;       // last 8-input piece of an activation row
     const int r0 = rb * BN + wave * 16 * RT;
     const bool wvalid = r0 < N;           // N % (16 RT) == 0: a wave's rows are all in range or all out
@@ -736,25 +743,25 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
         // slice s sits in buffer / ring slot s & 1; slice s + 1 is fetched during slice s (the last slice fetches
         // itself again into the idle slot: no branch around the loads)
         auto run = [&](auto full) __attribute__((always_inline)) {
-            dma(0, sX0);
-            wissue(0, rq[0], rm[0]);
+            dma(sb0, sX0);
+            wissue(sb0, rq[0], rm[0]);
             MOE_VMWAIT0();
             MOE_BARRIER();
-            int s = 0;
-            for (; s + 2 <= nsl; s += 2) {
-                wissue(s + 1, rq[1], rm[1]);
-                dma(s + 1, sX1);
+            int j = 0;
+            for (; j + 2 <= scnt; j += 2) {
+                wissue(sb0 + j + 1, rq[1], rm[1]);
+                dma(sb0 + j + 1, sX1);
                 compute(full, sX0, rq[0], rm[0]);
                 MOE_VMWAIT0();
                 MOE_BARRIER();
-                const int sn = s + 2 < nsl ? s + 2 : s + 1;
-                wissue(sn, rq[0], rm[0]);
-                dma(sn, sX0);
+                const int jn = sb0 + (j + 2 < scnt ? j + 2 : j + 1);
+                wissue(jn, rq[0], rm[0]);
+                dma(jn, sX0);
                 compute(full, sX1, rq[1], rm[1]);
                 MOE_VMWAIT0();
                 MOE_BARRIER();
             }
-            if (s < nsl) compute(full, sX0, rq[0], rm[0]);   // odd count: the last slice is in slot 0
+            if (j < scnt) compute(full, sX0, rq[0], rm[0]);   // odd count: the last slice is in slot 0
         };
         if (ntiles == NT) run(std::true_type{});
         else run(std::false_type{});
@@ -780,7 +787,7 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                             a.hout[(size_t)slot * N + r] = hi;
                             a.hout2[(size_t)slot * N + r] = f32_to_bf16(hv - bf16_to_f32(hi));
                         } else {
-                            a.yp[(size_t)slot * N + r] = acc[0][rt][t][v];
+                            a.yp[ks * a.plane + (size_t)slot * N + r] = acc[0][rt][t][v];
                         }
                     }
                 }
@@ -889,11 +896,19 @@ int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st) {
 // push the accumulators into AGPRs, which the fold's VALU cannot use in place.
 constexpr int DENSE_NT = 4;
 
+// K parts of the dense down projection: 2 when the row blocks x passes would leave the chip under-filled (the
+// combine adds the parts' planes); gate/up is never split (the GLU needs whole sums)
+int dense_ksplit(int N, int K, int nslots, int E) {
+    const long blocks = (long)((N + 255) / 256) * max_passes(nslots, E, 16 * DENSE_NT);
+    return blocks < 4L * 256 && (K + 127) / 128 >= 8 ? 2 : 1;
+}
+
 template <class FMT, int NPROJ>
-int launch_dense(const TileArgs& t, int nslots, hipStream_t st) {
+int launch_dense(TileArgs t, int nslots, hipStream_t st) {
     constexpr int BN = 64 * (4 / NPROJ);
     if (t.N % (64 / NPROJ)) return MOE_ERR_ARG;
-    const long nblk = (long)((t.N + BN - 1) / BN) * max_passes(nslots, t.E, 16 * DENSE_NT);
+    if (NPROJ == 2) t.ksplit = 1;
+    const long nblk = (long)((t.N + BN - 1) / BN) * max_passes(nslots, t.E, 16 * DENSE_NT) * t.ksplit;
     if (nblk > 0x7FFFFFFFL) return MOE_ERR_ARG;
     k_dense<FMT, NPROJ, DENSE_NT><<<dim3((unsigned)nblk), 256, 0, st>>>(t);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
@@ -913,6 +928,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     const int max_active = nslots < w->E ? nslots : w->E;
     const int nt = tokens_per_pass_tiles(a.T, a.k, w->E);
     TileArgs t{};
+    t.ksplit = 1;
     t.counts = a.grp.counts;
     t.offsets = a.grp.offsets;
     t.sorted = a.grp.sorted;
@@ -962,13 +978,16 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.N = w->d;
         d.W0 = (const uint8_t*)w->down.rows;
         d.yp = a.yp;
+        d.ksplit = dense ? dense_ksplit(d.N, d.K, nslots, w->E) : 1;
+        d.plane = (size_t)nslots * d.N;
         if (wave || dense) d.W0 = (const uint8_t*)w->down.tiles;
         int rc;
         if (dense) rc = launch_dense<FMT, 1>(d, nslots, a.st);
         else if (wave) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
-        return launch_combine(a.yp, a.idx, a.wts, w->down.bias, w->E, a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
+        return launch_combine(a.yp, d.ksplit > 1 ? a.yp + d.plane : nullptr, a.idx, a.wts, w->down.bias, w->E,
+                              a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
     }
     return 0;
 }

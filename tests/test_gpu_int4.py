@@ -321,10 +321,11 @@ def test_tile_copies_and_row_records_agree(T):
 DENSE_CASES = [
     # (name, d, F, E, k, T, routing): tokens per expert T k / E > 32 selects the dense tiles
     ("even", 256, 384, 4, 2, 100, "uniform"),       # 50 per expert
-    ("big", 512, 1024, 8, 2, 600, "uniform"),       # 150 per expert: three passes of 64, the last partial
+    ("big", 512, 1024, 8, 2, 600, "uniform"),       # 150 per expert: three passes of 64; down split over K
     ("odd-K", 320, 448, 4, 2, 180, "zipf"),         # K % 128 == 64 both ways, N % 128 != 0, uneven counts
     ("one-expert", 256, 384, 1, 1, 2100, "uniform"),  # 2100 tokens: more passes than the grid's z extent
     ("k=E", 192, 256, 4, 4, 40, "uniform"),         # every token in every expert
+    ("split-odd", 256, 1152, 4, 2, 200, "zipf"),    # down split over K in two parts of 5 and 4 slices
 ]
 
 
