@@ -82,6 +82,9 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU-baseline sample (0: skip)")
     ap.add_argument("--no-t32", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 4, 5a, 5b (reported beside)")
+    ap.add_argument("--only-configs", default="", metavar="NAMES",
+                    help="comma list of BASELINE config names (e.g. mixtral8x7b_int4_T512): run only those and print "
+                         "their results (for profiling runs; not the bench line)")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MIB",
                     help="finish with 3 device copies of MIB MiB (the plain-copy reference for --pmc traffic runs)")
     args = ap.parse_args()
@@ -91,6 +94,12 @@ def main():
         sys.exit(2)
 
     __graft_entry__.load_package()
+    if args.only_configs:
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        print(json.dumps(other_configs(dev, args, only=set(args.only_configs.split(",")))), flush=True)
+        copy_calibrate(dev, args.copy_calibrate)
+        return
     from moelab_amd import _lib, roofline, router
     from moelab_amd.experts import run_experts
     from moelab_amd.problem import baseline_int4_layer, baseline_x, zipf_bias
@@ -261,17 +270,23 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
-    if args.copy_calibrate > 0:
-        n = args.copy_calibrate << 20
-        a = torch.empty(n, dtype=torch.uint8, device=dev)
-        b = torch.empty_like(a)
-        for _ in range(3):
-            b.copy_(a)
-        torch.cuda.synchronize()
-        log(f"copy calibration: 3 device copies of {n} bytes")
+    copy_calibrate(dev, args.copy_calibrate)
 
 
-def other_configs(dev, args):
+def copy_calibrate(dev, mib):
+    """3 plain device copies of `mib` MiB: the reference dispatch for FETCH_SIZE / WRITE_SIZE scaling."""
+    if mib <= 0:
+        return
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 3 device copies of {n} bytes")
+
+
+def other_configs(dev, args, only=None):
     """BASELINE configs 4 (gpt-oss-20b MXFP4 + biases, clamped SwiGLU, T=1 and T=32), 5a (Mixtral-8x7B int4,
     T=512, MFMA-bound) and 5b (DeepSeek-V2-Lite int4, T=256, 2 shared experts): dependent residual chains of
     seeded layers (enough of them to exceed the 256 MB Infinity Cache), uniform router logits, timed like the
@@ -312,21 +327,29 @@ def other_configs(dev, args):
         out[name] = r
         log(f"{name}: {r}")
 
+    def want(*names):
+        return only is None or any(n in only for n in names)
+
     # config 4: gpt-oss-20b MXFP4, biases, clamped SwiGLU (act 2), softmax over the top-4
-    sh = SHAPES["gpt-oss-20b"]
-    layers = [baseline_mxfp4_layer(sh, seed=2000 + l, device=dev) for l in range(8)]
-    bias_b = 2 * (2 * sh.f + sh.d)   # bf16 gate/up/down biases per expert
-    for T in (1, 32):
-        report(f"gptoss20b_mxfp4_T{T}", sh, "mxfp4", layers, T, 2, bias_bytes=bias_b)
-    del layers
-    torch.cuda.empty_cache()
+    if want("gptoss20b_mxfp4_T1", "gptoss20b_mxfp4_T32"):
+        sh = SHAPES["gpt-oss-20b"]
+        layers = [baseline_mxfp4_layer(sh, seed=2000 + l, device=dev) for l in range(8)]
+        bias_b = 2 * (2 * sh.f + sh.d)   # bf16 gate/up/down biases per expert
+        for T in (1, 32):
+            if want(f"gptoss20b_mxfp4_T{T}"):
+                report(f"gptoss20b_mxfp4_T{T}", sh, "mxfp4", layers, T, 2, bias_bytes=bias_b)
+        del layers
+        torch.cuda.empty_cache()
     # config 5a: Mixtral-8x7B int4 T=512
-    sh = SHAPES["mixtral-8x7b"]
-    layers = [baseline_int4_layer(sh, seed=3000 + l, device=dev) for l in range(2)]
-    report("mixtral8x7b_int4_T512", sh, "int4", layers, 512, 0)
-    del layers
-    torch.cuda.empty_cache()
+    if want("mixtral8x7b_int4_T512"):
+        sh = SHAPES["mixtral-8x7b"]
+        layers = [baseline_int4_layer(sh, seed=3000 + l, device=dev) for l in range(2)]
+        report("mixtral8x7b_int4_T512", sh, "int4", layers, 512, 0)
+        del layers
+        torch.cuda.empty_cache()
     # config 5b: DeepSeek-V2-Lite int4 T=256, routed top-6 of 64 plus 2 shared experts (F=1408 each)
+    if not want("dsv2lite_int4_T256_shared2"):
+        return out
     sh = SHAPES["deepseek-v2-lite"]
     layers = []
     for l in range(8):
