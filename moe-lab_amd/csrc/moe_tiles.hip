@@ -864,9 +864,6 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-#ifndef MOE_WAVE_NT
-#define MOE_WAVE_NT 2   // token tiles per pass up to which the wave tiles run (above: LDS-staged k_tile)
-#endif
 // Wave-tile shape (measured on MI355X at the Qwen3 T = 16..64 shapes): more rows per wave share each activation
 // load across more weight bursts, more slices in flight hide more latency; both cost registers (occupancy).
 #ifndef MOE_WAVE_D_GU
@@ -914,19 +911,24 @@ int launch_dense(TileArgs t, int nslots, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-// MOE_DENSE (environment, read per call; a tuning and test knob): 0 turns the dense tiles off (the LDS-staged
-// row tiles run instead for many tokens per expert)
-bool dense_enabled() {
-    const char* v = getenv("MOE_DENSE");
-    return !(v && atoi(v) == 0);
+// Environment knobs, read per call (tuning and tests): MOE_DENSE = 0 turns the dense tiles off (the LDS-staged
+// row tiles take the calls with more than 32 tokens per expert), 1 uses them for every such call, unset chooses
+// by grid size; MOE_WAVE_NT = 1 or 2 forces the wave tiles' token tiles per pass.
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
 }
+
+#ifndef MOE_DENSE_MIN_BLOCKS
+#define MOE_DENSE_MIN_BLOCKS 256   // dense gate/up blocks below which the wave tiles fill the chip better
+#endif
 
 template <class FMT>
 int run_tiles_fmt(const ExpertsArgs& a) {
     const moe_experts_t* w = a.w;
     const int nslots = a.T * a.k;
     const int max_active = nslots < w->E ? nslots : w->E;
-    const int nt = tokens_per_pass_tiles(a.T, a.k, w->E);
+    const int avg = (nslots + w->E - 1) / w->E;   // expected slots per active expert (uniform routing)
     TileArgs t{};
     t.ksplit = 1;
     t.counts = a.grp.counts;
@@ -937,11 +939,16 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     t.E = w->E;
     t.act = a.act;
     t.kslots = a.k;
-    // tile-major weights present: wave tiles for few tokens per expert, dense tiles for many; the choice
-    // depends on (T, k, E) only, so separately launched stages agree on the layout of h between them
+    // tile-major weights present: wave tiles for few tokens per expert, dense tiles for many (unless their grid
+    // would fill only part of the chip, e.g. a few shared experts: then the wave tiles, 32-token passes). The
+    // choice depends on (T, k, E, F) only, so separately launched stages agree on the layout of h
     const bool tiled = w->gate.tiles && w->up.tiles && w->down.tiles;
-    const bool wave = tiled && nt <= MOE_WAVE_NT;
-    const bool dense = tiled && !wave && dense_enabled();
+    const int dmode = env_int("MOE_DENSE", -1);
+    const long dblocks = (long)((w->F + 127) / 128) * max_passes(nslots, w->E, 16 * DENSE_NT);
+    const bool dense = tiled && avg > 32 && (dmode == 1 || (dmode < 0 && dblocks >= MOE_DENSE_MIN_BLOCKS));
+    const bool wave = tiled && !dense && (avg <= 32 || dmode != 0);
+    const int wnt = env_int("MOE_WAVE_NT", 0);
+    const int nt = wave ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2)) : tokens_per_pass_tiles(a.T, a.k, w->E);
     t.items = a.grp.items;
     // pass size of the work list: 16 nt tokens for the wave tiles, 16 DENSE_NT for the dense tiles
     const int P = dense ? 16 * DENSE_NT : 16 * nt;

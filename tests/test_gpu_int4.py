@@ -330,9 +330,11 @@ DENSE_CASES = [
 
 
 @pytest.mark.parametrize("case", DENSE_CASES, ids=lambda c: c[0])
-def test_dense_tiles(case):
+def test_dense_tiles(case, monkeypatch):
     """Many tokens per expert: the dense tiles (exact codes on bf16 MFMA with the per-group fp32 fold, 64
-    tokens per pass, h one bf16 plane) against the oracle at the north-star gate."""
+    tokens per pass, h as two bf16 planes) against the oracle at the north-star gate. MOE_DENSE=1 keeps them on
+    at these small shapes (by default a grid this small goes to the wave tiles)."""
+    monkeypatch.setenv("MOE_DENSE", "1")
     name, d, f, E, k, T, routing = case
     sh = shape_(name, d, f, E, k)
     s = packed_state(sh, 31)
@@ -353,6 +355,7 @@ def test_dense_tiles_match_row_tiles(monkeypatch):
     s = packed_state(sh, 33)
     x, idx, wts = inputs(sh, 400, "zipf", seed=5)
     print("case dense-vs-rows T=400", flush=True)
+    monkeypatch.setenv("MOE_DENSE", "1")
     y1 = grouped(s, x, idx, wts, out_dtype=torch.float32)
     monkeypatch.setenv("MOE_DENSE", "0")
     y2 = grouped(s, x, idx, wts, out_dtype=torch.float32)
@@ -404,3 +407,17 @@ def test_shared_experts_argument_errors():
         _lib.MOE_ERR_WORKSPACE
     assert L.moe_shared_experts_run(desc, _lib.ptr(x), 2, 4, 0, None, _lib.ptr(y), 0, None, _lib.ptr(y), 1 << 20,
                                     None) == _lib.MOE_ERR_DTYPE
+
+
+@pytest.mark.parametrize("nt", ["1", "2"])
+def test_wave_tiles_for_many_tokens(nt, monkeypatch):
+    """Many tokens per expert on a grid too small for the dense tiles (a few shared-expert-like experts): the
+    wave tiles with 16- or 32-token passes, several passes per expert, against the oracle."""
+    monkeypatch.setenv("MOE_DENSE", "-1")
+    monkeypatch.setenv("MOE_WAVE_NT", nt)
+    sh = shape_("w", 256, 384, 2, 2, )
+    s = packed_state(sh, 35)
+    x, idx, wts = inputs(sh, 150, "uniform", seed=9)
+    print(f"case wave-many nt={nt}", flush=True)
+    y = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    assert_close(y, oracle_y(s, x, idx, wts), what=("wave many", nt))

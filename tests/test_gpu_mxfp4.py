@@ -206,10 +206,11 @@ def test_mxfp4_tile_copies_and_row_records_agree(T):
 
 @pytest.mark.parametrize("case", [("even", 256, 384, 4, 2, 100, "uniform"), ("odd-K", 320, 448, 4, 2, 180, "zipf"),
                                   ("big", 512, 1024, 8, 2, 600, "uniform")], ids=lambda c: c[0])
-def test_mxfp4_dense_tiles(case):
+def test_mxfp4_dense_tiles(case, monkeypatch):
     """MXFP4 with many tokens per expert (T k / E > 32): the dense tiles against the oracle at the gate."""
     from moelab_amd import _lib
     from moelab_amd.experts import run_experts
+    monkeypatch.setenv("MOE_DENSE", "1")
     name, d, f, E, k, T, routing = case
     sh = shape_(name, d, f, E, k)
     s = packed_state(sh, 41)
