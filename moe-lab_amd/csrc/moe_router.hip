@@ -195,30 +195,52 @@ topk_kernel(const LT* __restrict__ logits, int T, int E, int k, int norm, float 
 // With items != null (the grouped kernels' work list, pass size P): items[3w .. 3w + 2] = (expert, pass index q
 // within the expert (first token q * P), the expert's pass count) of pass w; the passes of each active expert in
 // ascending order, expert by expert; meta[2] = number of passes.
+// mw (the ids and 4 per-wave count arrays fit in LDS): the ids are read once into LDS, and each of the 4 waves
+// places one contiguous quarter of the slots with its own cursors (the expert's offset plus the counts of the
+// quarters before it), so the order stays ascending within every expert. Otherwise wave 0 places all slots.
 __global__ void __launch_bounds__(256)
 group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
             int32_t* __restrict__ sorted, int32_t* __restrict__ active, int32_t* __restrict__ meta, int P,
-            int32_t* __restrict__ items) {
-    extern __shared__ int32_t sm[];   // cnt[E], cursor[E]
+            int32_t* __restrict__ items, int mw) {
+    extern __shared__ int32_t sm[];   // mw: cnt[4][E], ids[n]; else cnt[E], cursor[E]
+    const int NW = mw ? 4 : 1;
     int32_t* cnt = sm;
-    int32_t* cursor = sm + E;
+    int32_t* cur1 = sm + E;
+    int32_t* sidx = sm + 4 * E;
     __shared__ int32_t s_bad;
-    const int tid = threadIdx.x;
-    for (int e = tid; e < E; e += 256) cnt[e] = 0;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    for (int i = tid; i < NW * E; i += 256) cnt[i] = 0;
     if (tid == 0) s_bad = 0;
     __syncthreads();
-    for (int p = tid; p < n; p += 256) {
-        const int e = idx[p];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-        else atomicAdd(&s_bad, 1);
+    const int q4 = (n + 3) / 4;
+    if (mw) {
+        const int b0 = wave * q4, b1 = b0 + q4 < n ? b0 + q4 : n;
+        for (int p = b0 + lane; p < b1; p += 64) {
+            const int e = idx[p];
+            sidx[p] = e;
+            if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
+            else atomicAdd(&s_bad, 1);
+        }
+    } else {
+        for (int p = tid; p < n; p += 256) {
+            const int e = idx[p];
+            if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+            else atomicAdd(&s_bad, 1);
+        }
     }
     __syncthreads();
     if (tid < 64) {   // wave 0: exclusive scan of counts and the active list, in chunks of 64 experts
-        const int lane = tid;
         int run = 0, run_act = 0, run_p = 0;
         for (int base = 0; base < E; base += 64) {
             const int e = base + lane;
-            const int c = e < E ? cnt[e] : 0;
+            int cw[4] = {0, 0, 0, 0};
+            int c = 0;
+            if (e < E) {
+                for (int w = 0; w < NW; ++w) {
+                    cw[w] = cnt[w * E + e];
+                    c += cw[w];
+                }
+            }
             const int np = items ? (c + P - 1) / P : 0;   // passes of expert e
             // inclusive wave scans of c, of (c > 0) and of the pass counts
             int inc = c, act = c > 0 ? 1 : 0, incp = np;
@@ -232,8 +254,16 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
             if (e < E) {
                 const int excl = run + inc - c;
                 offsets[e] = excl;
-                cursor[e] = excl;
                 counts[e] = c;
+                if (mw) {   // per-wave cursors: the quarters before come first
+                    int cc = excl;
+                    for (int w = 0; w < 4; ++w) {
+                        cnt[w * E + e] = cc;
+                        cc += cw[w];
+                    }
+                } else {
+                    cur1[e] = excl;
+                }
                 if (c > 0) active[run_act + act - 1] = e;
                 const int w0 = run_p + incp - np;
                 for (int q = 0; q < np; ++q) {
@@ -255,14 +285,16 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
         for (int a = run_act + lane; a < E; a += 64) active[a] = -1;
     }
     __syncthreads();
-    if (tid < 64) {   // wave 0: stable placement, 64 slots per step in ascending order
-        const int lane = tid;
+    if (mw || tid < 64) {   // stable placement, 64 slots per step in ascending order
+        int32_t* cursor = mw ? cnt + wave * E : cur1;
+        const int b0 = mw ? wave * q4 : 0;
+        const int b1 = mw ? (b0 + q4 < n ? b0 + q4 : n) : n;
         int nbits = 0;
         while ((1 << nbits) < E) ++nbits;
         const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-        for (int base = 0; base < n; base += 64) {
+        for (int base = b0; base < b1; base += 64) {
             const int p = base + lane;
-            int e = p < n ? idx[p] : -1;
+            int e = p < b1 ? (mw ? sidx[p] : idx[p]) : -1;
             const bool ok = (e >= 0 && e < E);
             // lanes holding the same valid expert: match on every bit of e
             uint64_t peers = __ballot(ok);
@@ -358,7 +390,10 @@ int launch_shared_route(const uint16_t* x, const uint16_t* gate, int T, int d, i
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
                  int32_t* active, int32_t* meta, hipStream_t st, int P, int32_t* items) {
     if (items && P < 1) return MOE_ERR_ARG;
-    group_slots<<<1, 256, 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted, active, meta, P, items);
+    const size_t mw_bytes = ((size_t)4 * E + (size_t)n) * sizeof(int32_t);
+    const int mw = mw_bytes <= 64 * 1024 ? 1 : 0;
+    group_slots<<<1, 256, mw ? mw_bytes : 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted, active,
+                                                                          meta, P, items, mw);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

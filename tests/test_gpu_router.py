@@ -96,7 +96,8 @@ def test_topk_full_softmax_weights():
 
 
 @pytest.mark.parametrize("T,k,E", [(1, 8, 128), (32, 8, 128), (256, 6, 64), (512, 2, 8), (17, 4, 16),
-                                   (5, 1, 1), (64, 8, 1024), (1024, 8, 128)])
+                                   (5, 1, 1), (64, 8, 1024), (1024, 8, 128), (3000, 8, 128), (4, 3, 8192),
+                                   (2001, 3, 7)])
 @pytest.mark.parametrize("routing", ["uniform", "one_hot"])
 def test_group_bit_exact(T, k, E, routing):
     from moelab_amd import router
