@@ -36,6 +36,8 @@
 namespace moe {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2x __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int TL_ROWS = 64;   // weight rows per block
@@ -62,6 +64,7 @@ struct TileArgs {
     float* yp;             // down: [T*k, N] fp32 (dense tiles split over K: ksplit such planes, plane floats apart)
     int ksplit;
     size_t plane;
+    size_t eslot_off;      // dense int4: per-slot exponents (int32 [slots]) at this byte offset from the exponent bytes
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -578,11 +581,15 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     constexpr int BM = 16 * NT;           // tokens per pass
     constexpr int BN = 4 * 16 * RT;       // rows per block (per projection)
     constexpr int SB = tile_slice_bytes<FMT>();
-    constexpr int HL = NPROJ == 2 ? 1 : 2;   // activation planes: x, or h = hi + lo
+    // int4: h travels as fp16 with a power-of-two exponent per (slot, 128-input slice) (H16); MXFP4 keeps the
+    // exact raw-code path on both projections (its E8M0 scales do not fit fp16), h = hi + lo
+    constexpr bool H16 = INT4;
+    constexpr int HL = (NPROJ == 2 || H16) ? 1 : 2;   // activation planes: x, h16, or h = hi + lo
     constexpr int NDMA = BM / 16;         // DMA instructions per wave per slice and plane (4 token rows each)
     __shared__ __attribute__((aligned(1024))) uint8_t sX0[HL * BM * 256];
     __shared__ __attribute__((aligned(1024))) uint8_t sX1[HL * BM * 256];
     __shared__ int sSlot[BM];
+    __shared__ float sAm[H16 && NPROJ == 2 ? 4 * BM : 1];   // gate/up epilogue: |h| max per (token, wave)
 
     // 1-D grid over (pass list x row blocks), ordered expert by expert, and within an expert row block by row
     // block with the expert's passes adjacent: the passes that share a weight tile run side by side (their
@@ -647,6 +654,10 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
         };
         uint4 rq[2][NPROJ][RT];
         uint2 rm[2][NPROJ][RT];
+        // H16 down: the exponent of lane j's token (token j of the pass): its h16 row is h 2^-E (k_h16_fix)
+        int eslot = 0;
+        if constexpr (H16 && NPROJ == 1)
+            eslot = reinterpret_cast<const int32_t*>(reinterpret_cast<const uint8_t*>(a.actv2) + a.eslot_off)[sSlot[lane]];
         auto wissue = [&](int s, uint4 (&q)[NPROJ][RT], uint2 (&m)[NPROJ][RT]) __attribute__((always_inline)) {
 #pragma unroll
             for (int p = 0; p < NPROJ; ++p)
@@ -665,10 +676,65 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
             for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[p][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // H16 down, one slice: codes dequantised exactly to fp16 pairs (v_perm puts 0x64 above each nibble: 1024 + q,
+        // exact), then q = (1024 + q) - 1024 and w = s q + b in one rounding (v_pk_add_f16, v_pk_fma_f16); the MFMA
+        // (f16 x f16, fp32 accumulate) adds the slice straight into acc.
+        auto slice_h16 = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT])
+                             __attribute__((always_inline)) {
+            const h2x off = {(_Float16)-1024.f, (_Float16)-1024.f};
+#pragma unroll
+            for (int G = 0; G < 2; ++G) {
+                __builtin_amdgcn_sched_barrier(0);   // one group at a time: bounds the live operands
+                f16x8 B[RT][2];
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const uint32_t mw = G ? m[0][rt].y : m[0][rt].x;
+                    const _Float16 s16 = (_Float16)bf16lo(mw), b16 = (_Float16)bf16hi(mw);
+                    const h2x s2 = {s16, s16}, b2 = {b16, b16};
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int j = 2 * G + u;
+                        const uint32_t w = j == 0 ? q[0][rt].x : (j == 1 ? q[0][rt].y : (j == 2 ? q[0][rt].z : q[0][rt].w));
+                        const uint32_t tq = w & 0x0F0F0F0Fu, uq = (w >> 4) & 0x0F0F0F0Fu;
+                        const uint32_t c4[4] = {__builtin_amdgcn_perm(0x64646464u, tq, 0x04020400u),
+                                                __builtin_amdgcn_perm(0x64646464u, uq, 0x04020400u),
+                                                __builtin_amdgcn_perm(0x64646464u, tq, 0x04030401u),
+                                                __builtin_amdgcn_perm(0x64646464u, uq, 0x04030401u)};
+                        h2x v[4];
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            v[c] = __builtin_elementwise_fma(__builtin_bit_cast(h2x, c4[c]) + off, s2, b2);
+                        B[rt][u] = f16x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    if (decltype(full)::value || t < ntiles) {   // wave-uniform
+                        f16x8 A[2];
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const int j = 2 * G + u;
+                            const int wi = j < 2 ? 2 * lg + j : 8 + 2 * lg + (j - 2);
+                            A[u] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(
+                                                                 xs + (16 * t + lr) * 256 + 16 * (wi ^ lr)));
+                        }
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                            for (int u = 0; u < 2; ++u)
+                                acc[0][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u], B[rt][u], acc[0][rt][t], 0, 0, 0);
+                    }
+                }
+            }
+        };
         // one slice, scale group by scale group; lane (m, g) of MFMA step j supplies word wi(j, g) of its row
         // (the record order). FULL: every token tile of the pass is live (no branch inside the slice)
-        auto compute = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT],
-                           const uint2 (&m)[NPROJ][RT]) __attribute__((always_inline)) {
+        auto compute = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT],
+                           int) __attribute__((always_inline)) {
+            if constexpr (H16 && NPROJ == 1) {
+                slice_h16(full, xs, q, m);
+                return;
+            }
 #pragma unroll
             for (int G = 0; G < 4 / SPG; ++G) {
                 __builtin_amdgcn_sched_barrier(0);   // one group at a time: bounds the live operands
@@ -751,23 +817,74 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
             for (; j + 2 <= scnt; j += 2) {
                 wissue(sb0 + j + 1, rq[1], rm[1]);
                 dma(sb0 + j + 1, sX1);
-                compute(full, sX0, rq[0], rm[0]);
+                compute(full, sX0, rq[0], rm[0], j);
                 MOE_VMWAIT0();
                 MOE_BARRIER();
                 const int jn = sb0 + (j + 2 < scnt ? j + 2 : j + 1);
                 wissue(jn, rq[0], rm[0]);
                 dma(jn, sX0);
-                compute(full, sX1, rq[1], rm[1]);
+                compute(full, sX1, rq[1], rm[1], j + 1);
                 MOE_VMWAIT0();
                 MOE_BARRIER();
             }
-            if (j < scnt) compute(full, sX0, rq[0], rm[0]);   // odd count: the last slice is in slot 0
+            if (j < scnt) compute(full, sX0, rq[0], rm[0], j);   // odd count: the last slice is in slot 0
         };
         if (ntiles == NT) run(std::true_type{});
         else run(std::false_type{});
 
         // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
-        if (wvalid) {
+        if constexpr (H16 && NPROJ == 2) {
+            // h of the block's 128 rows (one slice of the down projection's K) as fp16 h16 = h 2^-e, e per token:
+            // 0 while |h| < 2^15 on the slice, else the power of two that brings the slice's largest |h| below 2^15
+            // (so fp16 never overflows); e goes to the exponent bytes [slot, slice]
+            float hv[NT][4][RT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float am = 0.f;
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const int r = r0 + 16 * rt + lr;
+                        float g = acc[0][rt][t][v], up = acc[1][rt][t][v];
+                        if (wvalid && a.b0) g += a.b0[(size_t)e * N + r];
+                        if (wvalid && a.b1) up += a.b1[(size_t)e * N + r];
+                        hv[t][v][rt] = wvalid ? glu_act(a.act, g, up) : 0.f;
+                        am = fmaxf(am, fabsf(hv[t][v][rt]));
+                    }
+#pragma unroll
+                    for (int o = 1; o < 16; o <<= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+                    if (lr == 0) sAm[(16 * t + 4 * lg + v) * 4 + wave] = am;
+                }
+            __syncthreads();
+            uint8_t* hexp_out = reinterpret_cast<uint8_t*>(a.hout2);
+            const int nslh = (N + 127) >> 7;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int jt = 16 * t + 4 * lg + v;
+                    if (jt >= nlive) continue;
+                    const float4 m4 = *reinterpret_cast<const float4*>(&sAm[jt * 4]);
+                    const float amax = fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w));
+                    const int ex = amax >= 32768.f ? (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 141 : 0;
+                    const int slot = sSlot[jt];
+                    if (wave == 0 && lr == 0) hexp_out[(size_t)slot * nslh + rb] = (uint8_t)ex;
+                    if (wvalid) {
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt) {
+                            const _Float16 h16 = (_Float16)__builtin_ldexpf(hv[t][v][rt], -ex);
+                            a.hout[(size_t)slot * N + r0 + 16 * rt + lr] = __builtin_bit_cast(uint16_t, h16);
+                        }
+                    }
+                }
+        } else {
+            int es[NT][4];   // H16 down: the exponent of each of the lane's tokens (all lanes take part in the shuffle)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) es[t][v] = H16 ? __shfl(eslot, 16 * t + 4 * lg + v, 64) : 0;
+            if (wvalid)
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -786,12 +903,47 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                             const uint16_t hi = f32_to_bf16(hv);
                             a.hout[(size_t)slot * N + r] = hi;
                             a.hout2[(size_t)slot * N + r] = f32_to_bf16(hv - bf16_to_f32(hi));
+                        } else if (H16) {
+                            a.yp[ks * a.plane + (size_t)slot * N + r] = __builtin_ldexpf(acc[0][rt][t][v], es[t][v]);
                         } else {
                             a.yp[ks * a.plane + (size_t)slot * N + r] = acc[0][rt][t][v];
                         }
                     }
                 }
         }
+    }
+}
+
+// Dense int4, between gate/up and down: one wave per slot. The gate/up blocks wrote h16 = h 2^-e with e per (slot,
+// 128-row slice); this brings the slot's row to one exponent E = max e (slices with a smaller e are scaled by
+// 2^(e - E): exact unless a value falls into fp16's subnormal range, where it is rounded) and writes E for the
+// down projection's epilogue. A slot whose exponents are all 0 (|h| < 2^15 on the whole row, the usual case)
+// costs one load per lane.
+__global__ void __launch_bounds__(64) k_h16_fix(const uint8_t* __restrict__ hexp, uint16_t* __restrict__ h16,
+                                                int32_t* __restrict__ eslot, int nslh, int F) {
+    const int slot = blockIdx.x, lane = threadIdx.x;
+    const uint8_t* er = hexp + (size_t)slot * nslh;
+    const int e0 = lane < nslh ? er[lane] : 0, e1 = lane + 64 < nslh ? er[lane + 64] : 0;
+    int E = e0 > e1 ? e0 : e1;
+    for (int o = 32; o; o >>= 1) {
+        const int other = __shfl_xor(E, o, 64);
+        E = other > E ? other : E;
+    }
+    if (lane == 0) eslot[slot] = E;
+    if (E == 0) return;
+    uint16_t* row = h16 + (size_t)slot * F;
+    for (int s = 0; s < nslh; ++s) {
+        const int es = __shfl(s < 64 ? e0 : e1, s & 63, 64);
+        const int c = s * 128 + 2 * lane;   // two values per lane (F is even)
+        if (es == E || c >= F) continue;
+        uint32_t pr = *reinterpret_cast<const uint32_t*>(row + c);
+        uint32_t out = 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)(pr >> (16 * i)));
+            out |= (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(f, es - E)) << (16 * i);
+        }
+        *reinterpret_cast<uint32_t*>(row + c) = out;
     }
 }
 
@@ -952,6 +1104,13 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     t.items = a.grp.items;
     // pass size of the work list: 16 nt tokens for the wave tiles, 16 DENSE_NT for the dense tiles
     const int P = dense ? 16 * DENSE_NT : 16 * nt;
+    constexpr bool INT4 = FmtInt4::FMT == FMT::FMT;
+    const int nslh = (w->F + 127) / 128;
+    if (dense && INT4) {
+        // fp16 h: the second h plane holds the exponent bytes [slots, F/128], then the slot exponents int32 [slots]
+        t.eslot_off = ((size_t)nslots * nslh + 255) / 256 * 256;
+        if (t.eslot_off + (size_t)nslots * 4 > (size_t)nslots * w->F * 2) return MOE_ERR_ARG;
+    }
     if (a.stages & 1) {
         int rc = launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
                               a.grp.meta, a.st, P, a.grp.items);
@@ -971,7 +1130,14 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
         }
-        if (dense) rc = launch_dense<FMT, 2>(g, nslots, a.st);
+        if (dense) {
+            rc = launch_dense<FMT, 2>(g, nslots, a.st);
+            if (!rc && INT4) {
+                k_h16_fix<<<nslots, 64, 0, a.st>>>((const uint8_t*)a.hlo, a.hhi,
+                                                  (int32_t*)((uint8_t*)a.hlo + t.eslot_off), nslh, w->F);
+                rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+            }
+        }
         else if (wave) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st);
         else rc = launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
         if (rc) return rc;

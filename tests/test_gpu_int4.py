@@ -331,9 +331,10 @@ DENSE_CASES = [
 
 @pytest.mark.parametrize("case", DENSE_CASES, ids=lambda c: c[0])
 def test_dense_tiles(case, monkeypatch):
-    """Many tokens per expert: the dense tiles (exact codes on bf16 MFMA with the per-group fp32 fold, 64
-    tokens per pass, h as two bf16 planes) against the oracle at the north-star gate. MOE_DENSE=1 keeps them on
-    at these small shapes (by default a grid this small goes to the wave tiles)."""
+    """Many tokens per expert: the dense tiles (gate/up: exact codes on bf16 MFMA with the per-group fp32 fold;
+    h in fp16 with a power-of-two exponent per slot and 128-input slice; down: W_down dequantised to fp16 on f16
+    MFMA; 64 tokens per pass) against the oracle at the north-star gate. MOE_DENSE=1 keeps them on at these small
+    shapes (by default a grid this small goes to the wave tiles)."""
     monkeypatch.setenv("MOE_DENSE", "1")
     name, d, f, E, k, T, routing = case
     sh = shape_(name, d, f, E, k)
@@ -348,9 +349,32 @@ def test_dense_tiles(case, monkeypatch):
     assert_close(y, ref, what=("dense", name, "bf16 out"))
 
 
+def test_dense_tiles_fp16_range(monkeypatch):
+    """The dense path's fp16 h past fp16's range: 24 tokens scaled by 1000 give |h| far above 65504 (checked on
+    the oracle's own h), the other tokens stay small, so one call takes both the direct f16 accumulation and the
+    per-slice 2^e rescaling; each group of tokens meets the gate against its own RMS."""
+    monkeypatch.setenv("MOE_DENSE", "1")
+    sh = shape_("big-h", 256, 640, 4, 2)
+    s = packed_state(sh, 35)
+    x, idx, wts = inputs(sh, 150, "uniform", seed=9)
+    big = torch.zeros(150, dtype=torch.bool, device=DEV)
+    big[::6] = True
+    x = torch.where(big[:, None], x.float() * 1000.0, x.float()).to(torch.bfloat16)
+    xs = orc.bf16_bits_to_f32(np_u16(x))
+    wg, wu = deq(s, "g", experts=[int(idx[0, 0])])[0], deq(s, "u", experts=[int(idx[0, 0])])[0]
+    h0 = orc.act_fn(xs[0] @ wg.T, xs[0] @ wu.T, 0)
+    assert np.abs(h0).max() > 2 * 65504.0
+    print("case dense fp16 range T=150", flush=True)
+    y = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    ref = oracle_y(s, x, idx, wts)
+    b = big.cpu().numpy()
+    assert_close(y[big], ref[b], what="large tokens")
+    assert_close(y[~big], ref[~b], what="small tokens")
+
+
 def test_dense_tiles_match_row_tiles(monkeypatch):
     """Dense tiles vs the LDS-staged row tiles (MOE_DENSE=0) on the same inputs: both at the gate, and within
-    the dense path's bf16 rounding of h (the row tiles keep h as two bf16 planes) of each other."""
+    the gate of each other (the row tiles keep h as two bf16 planes and W_down exact)."""
     sh = shape_("dr", 512, 768, 8, 2)
     s = packed_state(sh, 33)
     x, idx, wts = inputs(sh, 400, "zipf", seed=5)
