@@ -29,7 +29,7 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
     off += align_up(nslots * (size_t)w->F * 2) * 2;   // hi and lo planes
     if (resolve_path(path, T) == MOE_PATH_GROUPED) {
         L.yp = off;
-        off += align_up(nslots * (size_t)w->d * 4 * 2);   // two planes: the dense down projection may split K
+        off += align_up(nslots * (size_t)w->d * 4 * 4);   // four planes: the dense down projection may split K
         L.counts = off;
         off += align_up((size_t)w->E * 4);
         L.offsets = off;

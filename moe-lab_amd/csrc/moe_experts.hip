@@ -468,7 +468,7 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
 // weights first, then every yp row (and bias row) load of the 8 at once (rows of skipped slots are read
 // too, then discarded by a select, so no load waits on an id), then the sums in slot order.
 __global__ void __launch_bounds__(256)
-k_combine(const float* __restrict__ yp, const float* __restrict__ yp2, const int32_t* __restrict__ idx,
+k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t* __restrict__ idx,
           const float* __restrict__ wts,
           const float* __restrict__ bd, int E, const void* __restrict__ resid, void* __restrict__ y, int T, int k,
           int D, int y32) {
@@ -490,11 +490,11 @@ k_combine(const float* __restrict__ yp, const float* __restrict__ yp2, const int
             w[j] = wts[slot];
             v[j] = reinterpret_cast<const float4*>(yp + (size_t)slot * D + n)[0];
         }
-        if (yp2) {
+        for (int pl = 1; pl < nplanes; ++pl) {   // K parts of a split down projection
 #pragma unroll
             for (int j = 0; j < KC; ++j) {
                 const int slot = t * k + (j0 + j < k ? j0 + j : k - 1);
-                const float4 u = reinterpret_cast<const float4*>(yp2 + (size_t)slot * D + n)[0];
+                const float4 u = reinterpret_cast<const float4*>(yp + pl * plane + (size_t)slot * D + n)[0];
                 v[j].x += u.x;
                 v[j].y += u.y;
                 v[j].z += u.z;
@@ -1106,12 +1106,12 @@ int run_experts_slots(const ExpertsArgs& a) {
     return run_slots_fmt<FmtMxfp4>(a);
 }
 
-int launch_combine(const float* yp, const float* yp2, const int32_t* idx, const float* wts, const float* bd, int E,
+int launch_combine(const float* yp, int nplanes, size_t plane, const int32_t* idx, const float* wts, const float* bd, int E,
                    const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st) {
     const size_t total4 = (size_t)T * d / 4;
     if (total4 == 0) return 0;
     dim3 grid((unsigned)((total4 + 255) / 256));
-    k_combine<<<grid, 256, 0, st>>>(yp, yp2, idx, wts, bd, E, residual, y, T, k, d, y32);
+    k_combine<<<grid, 256, 0, st>>>(yp, nplanes, plane, idx, wts, bd, E, residual, y, T, k, d, y32);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

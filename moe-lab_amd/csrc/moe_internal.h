@@ -58,7 +58,7 @@ int run_experts_tiles(const ExpertsArgs& a);
 // rows -> tile-major records (moe_tiles.hip; layout in include/moe_mi355x.h)
 int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tiles, hipStream_t st);
 // combine (moe_experts.hip): y[t] = residual[t] + sum_j wts[t*k + j] * (yp[t*k + j] (+ yp2[..]) + bd[idx[t*k + j]])
-int launch_combine(const float* yp, const float* yp2, const int32_t* idx, const float* wts, const float* bd, int E,
+int launch_combine(const float* yp, int nplanes, size_t plane, const int32_t* idx, const float* wts, const float* bd, int E,
                    const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);
 
 }  // namespace moe

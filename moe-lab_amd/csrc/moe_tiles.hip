@@ -679,53 +679,65 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
         // H16 down, one slice: codes dequantised exactly to fp16 pairs (v_perm puts 0x64 above each nibble: 1024 + q,
         // exact), then q = (1024 + q) - 1024 and w = s q + b in one rounding (v_pk_add_f16, v_pk_fma_f16); the MFMA
         // (f16 x f16, fp32 accumulate) adds the slice straight into acc.
-        auto slice_h16 = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT])
-                             __attribute__((always_inline)) {
+        // the B operands of row tile rt, scale group G
+        auto decode_h16 = [&](int G, int rt, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT], f16x8 (&B)[RT][2])
+                              __attribute__((always_inline)) {
             const h2x off = {(_Float16)-1024.f, (_Float16)-1024.f};
+            const uint32_t mw = G ? m[0][rt].y : m[0][rt].x;
+            const _Float16 s16 = (_Float16)bf16lo(mw), b16 = (_Float16)bf16hi(mw);
+            const h2x s2 = {s16, s16}, b2 = {b16, b16};
 #pragma unroll
-            for (int G = 0; G < 2; ++G) {
-                __builtin_amdgcn_sched_barrier(0);   // one group at a time: bounds the live operands
-                f16x8 B[RT][2];
+            for (int u = 0; u < 2; ++u) {
+                const int j = 2 * G + u;
+                const uint32_t w = j == 0 ? q[0][rt].x : (j == 1 ? q[0][rt].y : (j == 2 ? q[0][rt].z : q[0][rt].w));
+                const uint32_t tq = w & 0x0F0F0F0Fu, uq = (w >> 4) & 0x0F0F0F0Fu;
+                const uint32_t c4[4] = {__builtin_amdgcn_perm(0x64646464u, tq, 0x04020400u),
+                                        __builtin_amdgcn_perm(0x64646464u, uq, 0x04020400u),
+                                        __builtin_amdgcn_perm(0x64646464u, tq, 0x04030401u),
+                                        __builtin_amdgcn_perm(0x64646464u, uq, 0x04030401u)};
+                h2x v[4];
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
-                    const uint32_t mw = G ? m[0][rt].y : m[0][rt].x;
-                    const _Float16 s16 = (_Float16)bf16lo(mw), b16 = (_Float16)bf16hi(mw);
-                    const h2x s2 = {s16, s16}, b2 = {b16, b16};
+                for (int c = 0; c < 4; ++c) v[c] = __builtin_elementwise_fma(__builtin_bit_cast(h2x, c4[c]) + off, s2, b2);
+                B[rt][u] = f16x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+            }
+        };
+        // group G's MFMAs; after token tile t, NEXT decodes group G + 1's row tiles t * RT / NT ... (the VALU work
+        // of the next group issues while this group's MFMAs run)
+        auto mfma_h16 = [&](auto full, auto next, const uint8_t* xs, int G, const f16x8 (&B)[RT][2],
+                            const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT], f16x8 (&Bn)[RT][2])
+                            __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (decltype(full)::value || t < ntiles) {   // wave-uniform
+                    f16x8 A[2];
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
                         const int j = 2 * G + u;
-                        const uint32_t w = j == 0 ? q[0][rt].x : (j == 1 ? q[0][rt].y : (j == 2 ? q[0][rt].z : q[0][rt].w));
-                        const uint32_t tq = w & 0x0F0F0F0Fu, uq = (w >> 4) & 0x0F0F0F0Fu;
-                        const uint32_t c4[4] = {__builtin_amdgcn_perm(0x64646464u, tq, 0x04020400u),
-                                                __builtin_amdgcn_perm(0x64646464u, uq, 0x04020400u),
-                                                __builtin_amdgcn_perm(0x64646464u, tq, 0x04030401u),
-                                                __builtin_amdgcn_perm(0x64646464u, uq, 0x04030401u)};
-                        h2x v[4];
-#pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            v[c] = __builtin_elementwise_fma(__builtin_bit_cast(h2x, c4[c]) + off, s2, b2);
-                        B[rt][u] = f16x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+                        const int wi = j < 2 ? 2 * lg + j : 8 + 2 * lg + (j - 2);
+                        A[u] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(xs + (16 * t + lr) * 256 + 16 * (wi ^ lr)));
                     }
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                        for (int u = 0; u < 2; ++u)
+                            acc[0][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u], B[rt][u], acc[0][rt][t], 0, 0, 0);
                 }
+                if constexpr (decltype(next)::value) {
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    if (decltype(full)::value || t < ntiles) {   // wave-uniform
-                        f16x8 A[2];
-#pragma unroll
-                        for (int u = 0; u < 2; ++u) {
-                            const int j = 2 * G + u;
-                            const int wi = j < 2 ? 2 * lg + j : 8 + 2 * lg + (j - 2);
-                            A[u] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(
-                                                                 xs + (16 * t + lr) * 256 + 16 * (wi ^ lr)));
-                        }
-#pragma unroll
-                        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-                            for (int u = 0; u < 2; ++u)
-                                acc[0][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u], B[rt][u], acc[0][rt][t], 0, 0, 0);
-                    }
+                    for (int rt = t * RT / NT; rt < (t + 1) * RT / NT; ++rt) decode_h16(G + 1, rt, q, m, Bn);
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
+        };
+        auto slice_h16 = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT])
+                             __attribute__((always_inline)) {
+            f16x8 B0[RT][2], B1[RT][2];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) decode_h16(0, rt, q, m, B0);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_h16(full, std::true_type{}, xs, 0, B0, q, m, B1);
+            mfma_h16(full, std::false_type{}, xs, 1, B1, q, m, B0);
         };
         // one slice, scale group by scale group; lane (m, g) of MFMA step j supplies word wi(j, g) of its row
         // (the record order). FULL: every token tile of the pass is live (no branch inside the slice)
@@ -914,36 +926,64 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     }
 }
 
-// Dense int4, between gate/up and down: one wave per slot. The gate/up blocks wrote h16 = h 2^-e with e per (slot,
+// Dense int4, between gate/up and down: one block per slot. The gate/up blocks wrote h16 = h 2^-e with e per (slot,
 // 128-row slice); this brings the slot's row to one exponent E = max e (slices with a smaller e are scaled by
 // 2^(e - E): exact unless a value falls into fp16's subnormal range, where it is rounded) and writes E for the
 // down projection's epilogue. A slot whose exponents are all 0 (|h| < 2^15 on the whole row, the usual case)
-// costs one load per lane.
-__global__ void __launch_bounds__(64) k_h16_fix(const uint8_t* __restrict__ hexp, uint16_t* __restrict__ h16,
-                                                int32_t* __restrict__ eslot, int nslh, int F) {
-    const int slot = blockIdx.x, lane = threadIdx.x;
+// costs one load per lane of the first wave.
+__global__ void __launch_bounds__(256) k_h16_fix(const uint8_t* __restrict__ hexp, uint16_t* __restrict__ h16,
+                                                 int32_t* __restrict__ eslot, int nslh, int F) {
+    __shared__ int sE[128];
+    __shared__ int sMax;
+    const int slot = blockIdx.x, tid = threadIdx.x;
     const uint8_t* er = hexp + (size_t)slot * nslh;
-    const int e0 = lane < nslh ? er[lane] : 0, e1 = lane + 64 < nslh ? er[lane + 64] : 0;
-    int E = e0 > e1 ? e0 : e1;
-    for (int o = 32; o; o >>= 1) {
-        const int other = __shfl_xor(E, o, 64);
-        E = other > E ? other : E;
-    }
-    if (lane == 0) eslot[slot] = E;
-    if (E == 0) return;
-    uint16_t* row = h16 + (size_t)slot * F;
-    for (int s = 0; s < nslh; ++s) {
-        const int es = __shfl(s < 64 ? e0 : e1, s & 63, 64);
-        const int c = s * 128 + 2 * lane;   // two values per lane (F is even)
-        if (es == E || c >= F) continue;
-        uint32_t pr = *reinterpret_cast<const uint32_t*>(row + c);
-        uint32_t out = 0;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)(pr >> (16 * i)));
-            out |= (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(f, es - E)) << (16 * i);
+    if (tid < 64) {
+        const int e0 = tid < nslh ? er[tid] : 0, e1 = tid + 64 < nslh ? er[tid + 64] : 0;
+        sE[tid] = e0;
+        sE[tid + 64] = e1;
+        int E = e0 > e1 ? e0 : e1;
+        for (int o = 32; o; o >>= 1) {
+            const int other = __shfl_xor(E, o, 64);
+            E = other > E ? other : E;
         }
-        *reinterpret_cast<uint32_t*>(row + c) = out;
+        if (tid == 0) {
+            sMax = E;
+            eslot[slot] = E;
+        }
+    }
+    __syncthreads();
+    const int E = sMax;
+    if (E == 0) return;   // block-uniform
+    // 16-byte chunks (8 values, one slice each) of the row: every load first, then the rewrites
+    constexpr int CPT = 8;   // chunks per thread per round (F <= 16384: 2048 chunks, one round)
+    uint4* row = reinterpret_cast<uint4*>(h16 + (size_t)slot * F);
+    const int nch = F >> 3;
+    for (int c0 = 0; c0 < nch; c0 += 256 * CPT) {
+        uint4 v[CPT];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = c0 + i * 256 + tid;
+            if (c < nch) v[i] = row[c];
+        }
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = c0 + i * 256 + tid;
+            if (c >= nch) continue;
+            const int d = sE[c >> 4] - E;   // 16 chunks per 128-value slice
+            if (d == 0) continue;
+            uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t out = 0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] >> (16 * h)));
+                    out |= (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(f, d)) << (16 * h);
+                }
+                w[q] = out;
+            }
+            row[c] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
     }
 }
 
@@ -1045,10 +1085,20 @@ int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st) {
 // push the accumulators into AGPRs, which the fold's VALU cannot use in place.
 constexpr int DENSE_NT = 4;
 
+// Environment knobs, read per call (tuning and tests): MOE_DENSE = 0 turns the dense tiles off (the LDS-staged
+// row tiles take the calls with more than 32 tokens per expert), 1 uses them for every such call, unset chooses
+// by grid size; MOE_WAVE_NT = 1 or 2 forces the wave tiles' token tiles per pass.
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
 // K parts of the dense down projection: 2 when the row blocks x passes would leave the chip under-filled (the
 // combine adds the parts' planes); gate/up is never split (the GLU needs whole sums)
 int dense_ksplit(int N, int K, int nslots, int E) {
     const long blocks = (long)((N + 255) / 256) * max_passes(nslots, E, 16 * DENSE_NT);
+    const int ks = env_int("MOE_DENSE_KSPLIT", 0);
+    if (ks >= 1 && ks <= 4) return ks;
     return blocks < 4L * 256 && (K + 127) / 128 >= 8 ? 2 : 1;
 }
 
@@ -1063,13 +1113,6 @@ int launch_dense(TileArgs t, int nslots, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-// Environment knobs, read per call (tuning and tests): MOE_DENSE = 0 turns the dense tiles off (the LDS-staged
-// row tiles take the calls with more than 32 tokens per expert), 1 uses them for every such call, unset chooses
-// by grid size; MOE_WAVE_NT = 1 or 2 forces the wave tiles' token tiles per pass.
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
 
 #ifndef MOE_DENSE_MIN_BLOCKS
 #define MOE_DENSE_MIN_BLOCKS 256   // dense gate/up blocks below which the wave tiles fill the chip better
@@ -1133,7 +1176,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         if (dense) {
             rc = launch_dense<FMT, 2>(g, nslots, a.st);
             if (!rc && INT4) {
-                k_h16_fix<<<nslots, 64, 0, a.st>>>((const uint8_t*)a.hlo, a.hhi,
+                k_h16_fix<<<nslots, 256, 0, a.st>>>((const uint8_t*)a.hlo, a.hhi,
                                                   (int32_t*)((uint8_t*)a.hlo + t.eslot_off), nslh, w->F);
                 rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
             }
@@ -1159,7 +1202,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         else if (wave) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
-        return launch_combine(a.yp, d.ksplit > 1 ? a.yp + d.plane : nullptr, a.idx, a.wts, w->down.bias, w->E,
+        return launch_combine(a.yp, d.ksplit, d.plane, a.idx, a.wts, w->down.bias, w->E,
                               a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
     }
     return 0;
