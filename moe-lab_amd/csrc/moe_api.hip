@@ -18,7 +18,7 @@ int resolve_path(int path, int T) {
 }
 
 struct Layout {
-    size_t h, yp, counts, offsets, sorted, active, meta, items, total;
+    size_t h, yp, x16, xexp, counts, offsets, sorted, active, meta, items, total;
 };
 
 Layout layout(const moe_experts_t* w, int T, int k, int path) {
@@ -30,6 +30,10 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
     if (resolve_path(path, T) == MOE_PATH_GROUPED) {
         L.yp = off;
         off += align_up(nslots * (size_t)w->d * 4 * 4);   // four planes: the dense down projection may split K
+        L.x16 = off;
+        off += align_up((size_t)T * w->d * 2);
+        L.xexp = off;
+        off += align_up((size_t)T * 4);
         L.counts = off;
         off += align_up((size_t)w->E * 4);
         L.offsets = off;
@@ -196,6 +200,8 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     a.sync = (int32_t*)ws;
     if (rpath == MOE_PATH_GROUPED) {
         a.yp = (float*)(ws + L.yp);
+        a.x16 = (uint16_t*)(ws + L.x16);
+        a.xexp = (int32_t*)(ws + L.xexp);
         a.grp.counts = (int32_t*)(ws + L.counts);
         a.grp.offsets = (int32_t*)(ws + L.offsets);
         a.grp.sorted = (int32_t*)(ws + L.sorted);

@@ -43,7 +43,9 @@ struct ExpertsArgs {
     const void* residual; // same dtype as y, or NULL
     uint16_t* hhi;        // GLU output h = hi + lo, two bf16 planes [T*k, F]
     uint16_t* hlo;
-    float* yp;      // 2 x [T*k, d] fp32 scratch (grouped path; the second plane for a K-split down projection)
+    float* yp;      // 4 x [T*k, d] fp32 scratch (grouped path; the further planes for a K-split down projection)
+    uint16_t* x16;  // grouped path, dense int4: x as fp16 [T, d] with a power-of-two exponent per token
+    int32_t* xexp;  // [T]
     GroupBufs grp;  // grouped path
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
     int fused_t1;   // T == 1: try the single-launch kernel first
@@ -57,7 +59,8 @@ int run_experts_slots(const ExpertsArgs& a);
 int run_experts_tiles(const ExpertsArgs& a);
 // rows -> tile-major records (moe_tiles.hip; layout in include/moe_mi355x.h)
 int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tiles, hipStream_t st);
-// combine (moe_experts.hip): y[t] = residual[t] + sum_j wts[t*k + j] * (yp[t*k + j] (+ yp2[..]) + bd[idx[t*k + j]])
+// combine (moe_experts.hip): y[t] = residual[t] + sum_j wts[t*k + j] * (sum over the nplanes planes of yp[t*k + j]
+// + bd[idx[t*k + j]])
 int launch_combine(const float* yp, int nplanes, size_t plane, const int32_t* idx, const float* wts, const float* bd, int E,
                    const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);
 

@@ -64,7 +64,8 @@ struct TileArgs {
     float* yp;             // down: [T*k, N] fp32 (dense tiles split over K: ksplit such planes, plane floats apart)
     int ksplit;
     size_t plane;
-    size_t eslot_off;      // dense int4: per-slot exponents (int32 [slots]) at this byte offset from the exponent bytes
+    size_t eslot_off;      // dense int4 down: per-slot exponents (int32 [slots]) at this byte offset from the exponent bytes
+    const int32_t* xexp;   // dense int4 gate/up: per-token exponents of x16 (actv) [T]
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -581,10 +582,12 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     constexpr int BM = 16 * NT;           // tokens per pass
     constexpr int BN = 4 * 16 * RT;       // rows per block (per projection)
     constexpr int SB = tile_slice_bytes<FMT>();
-    // int4: h travels as fp16 with a power-of-two exponent per (slot, 128-input slice) (H16); MXFP4 keeps the
-    // exact raw-code path on both projections (its E8M0 scales do not fit fp16), h = hi + lo
+    // int4 (F16): activations travel as fp16 with power-of-two exponents (x16 per token; h16 per slot) and the
+    // codes are dequantised to fp16 in registers; MXFP4 keeps the exact raw-code path on bf16 MFMA with its
+    // per-group fold (its E8M0 scales do not fit fp16), h = hi + lo
+    constexpr bool F16 = INT4;
     constexpr bool H16 = INT4;
-    constexpr int HL = (NPROJ == 2 || H16) ? 1 : 2;   // activation planes: x, h16, or h = hi + lo
+    constexpr int HL = (NPROJ == 2 || H16) ? 1 : 2;   // activation planes: x, x16, h16, or h = hi + lo
     constexpr int NDMA = BM / 16;         // DMA instructions per wave per slice and plane (4 token rows each)
     __shared__ __attribute__((aligned(1024))) uint8_t sX0[HL * BM * 256];
     __shared__ __attribute__((aligned(1024))) uint8_t sX1[HL * BM * 256];
@@ -654,10 +657,15 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
         };
         uint4 rq[2][NPROJ][RT];
         uint2 rm[2][NPROJ][RT];
-        // H16 down: the exponent of lane j's token (token j of the pass): its h16 row is h 2^-E (k_h16_fix)
+        // F16: the exponent of lane j's token (token j of the pass): its activation row is x 2^-E (x16, k_x16) or
+        // h 2^-E (h16, k_h16_fix)
         int eslot = 0;
-        if constexpr (H16 && NPROJ == 1)
-            eslot = reinterpret_cast<const int32_t*>(reinterpret_cast<const uint8_t*>(a.actv2) + a.eslot_off)[sSlot[lane]];
+        if constexpr (F16) {
+            if (NPROJ == 1)
+                eslot = reinterpret_cast<const int32_t*>(reinterpret_cast<const uint8_t*>(a.actv2) + a.eslot_off)[sSlot[lane]];
+            else
+                eslot = a.xexp[sSlot[lane] / a.act_div];
+        }
         auto wissue = [&](int s, uint4 (&q)[NPROJ][RT], uint2 (&m)[NPROJ][RT]) __attribute__((always_inline)) {
 #pragma unroll
             for (int p = 0; p < NPROJ; ++p)
@@ -679,17 +687,19 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
         // H16 down, one slice: codes dequantised exactly to fp16 pairs (v_perm puts 0x64 above each nibble: 1024 + q,
         // exact), then q = (1024 + q) - 1024 and w = s q + b in one rounding (v_pk_add_f16, v_pk_fma_f16); the MFMA
         // (f16 x f16, fp32 accumulate) adds the slice straight into acc.
-        // the B operands of row tile rt, scale group G
-        auto decode_h16 = [&](int G, int rt, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT], f16x8 (&B)[RT][2])
-                              __attribute__((always_inline)) {
+        // F16 (int4): the B operands of projection p, row tile rt, scale group G: codes dequantised exactly to fp16
+        // pairs (v_perm puts 0x64 above each nibble: 1024 + q, exact), then q = (1024 + q) - 1024 and w = s q + b in
+        // one rounding (v_pk_add_f16, v_pk_fma_f16)
+        auto decode_f16 = [&](int G, int p, int rt, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT],
+                              f16x8 (&B)[NPROJ][RT][2]) __attribute__((always_inline)) {
             const h2x off = {(_Float16)-1024.f, (_Float16)-1024.f};
-            const uint32_t mw = G ? m[0][rt].y : m[0][rt].x;
+            const uint32_t mw = G ? m[p][rt].y : m[p][rt].x;
             const _Float16 s16 = (_Float16)bf16lo(mw), b16 = (_Float16)bf16hi(mw);
             const h2x s2 = {s16, s16}, b2 = {b16, b16};
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int j = 2 * G + u;
-                const uint32_t w = j == 0 ? q[0][rt].x : (j == 1 ? q[0][rt].y : (j == 2 ? q[0][rt].z : q[0][rt].w));
+                const uint32_t w = j == 0 ? q[p][rt].x : (j == 1 ? q[p][rt].y : (j == 2 ? q[p][rt].z : q[p][rt].w));
                 const uint32_t tq = w & 0x0F0F0F0Fu, uq = (w >> 4) & 0x0F0F0F0Fu;
                 const uint32_t c4[4] = {__builtin_amdgcn_perm(0x64646464u, tq, 0x04020400u),
                                         __builtin_amdgcn_perm(0x64646464u, uq, 0x04020400u),
@@ -698,14 +708,15 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                 h2x v[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) v[c] = __builtin_elementwise_fma(__builtin_bit_cast(h2x, c4[c]) + off, s2, b2);
-                B[rt][u] = f16x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+                B[p][rt][u] = f16x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
             }
         };
-        // group G's MFMAs; after token tile t, NEXT decodes group G + 1's row tiles t * RT / NT ... (the VALU work
-        // of the next group issues while this group's MFMAs run)
-        auto mfma_h16 = [&](auto full, auto next, const uint8_t* xs, int G, const f16x8 (&B)[RT][2],
-                            const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT], f16x8 (&Bn)[RT][2])
+        // group G's MFMAs (f16 x f16, fp32 accumulate, straight into acc); after token tile t, NEXT decodes group
+        // G + 1's (projection, row tile) pairs t * NPROJ * RT / NT ..., so that VALU work issues while MFMAs run
+        auto mfma_f16 = [&](auto full, auto next, const uint8_t* xs, int G, const f16x8 (&B)[NPROJ][RT][2],
+                            const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT], f16x8 (&Bn)[NPROJ][RT][2])
                             __attribute__((always_inline)) {
+            constexpr int PPT = NPROJ * RT / NT;   // pairs decoded per token tile
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 if (decltype(full)::value || t < ntiles) {   // wave-uniform
@@ -717,34 +728,37 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                         A[u] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(xs + (16 * t + lr) * 256 + 16 * (wi ^ lr)));
                     }
 #pragma unroll
-                    for (int rt = 0; rt < RT; ++rt)
+                    for (int p = 0; p < NPROJ; ++p)
 #pragma unroll
-                        for (int u = 0; u < 2; ++u)
-                            acc[0][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u], B[rt][u], acc[0][rt][t], 0, 0, 0);
+                        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                            for (int u = 0; u < 2; ++u)
+                                acc[p][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u], B[p][rt][u], acc[p][rt][t], 0, 0, 0);
                 }
                 if constexpr (decltype(next)::value) {
 #pragma unroll
-                    for (int rt = t * RT / NT; rt < (t + 1) * RT / NT; ++rt) decode_h16(G + 1, rt, q, m, Bn);
+                    for (int i = t * PPT; i < (t + 1) * PPT; ++i) decode_f16(G + 1, i / RT, i % RT, q, m, Bn);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
-        auto slice_h16 = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT])
+        auto slice_f16 = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT])
                              __attribute__((always_inline)) {
-            f16x8 B0[RT][2], B1[RT][2];
+            static_assert(NPROJ * RT % NT == 0, "decode pairs split evenly over the token tiles");
+            f16x8 B0[NPROJ][RT][2], B1[NPROJ][RT][2];
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) decode_h16(0, rt, q, m, B0);
+            for (int i = 0; i < NPROJ * RT; ++i) decode_f16(0, i / RT, i % RT, q, m, B0);
             __builtin_amdgcn_sched_barrier(0);
-            mfma_h16(full, std::true_type{}, xs, 0, B0, q, m, B1);
-            mfma_h16(full, std::false_type{}, xs, 1, B1, q, m, B0);
+            mfma_f16(full, std::true_type{}, xs, 0, B0, q, m, B1);
+            mfma_f16(full, std::false_type{}, xs, 1, B1, q, m, B0);
         };
         // one slice, scale group by scale group; lane (m, g) of MFMA step j supplies word wi(j, g) of its row
         // (the record order). FULL: every token tile of the pass is live (no branch inside the slice)
         auto compute = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT],
                            int) __attribute__((always_inline)) {
-            if constexpr (H16 && NPROJ == 1) {
-                slice_h16(full, xs, q, m);
+            if constexpr (F16) {
+                slice_f16(full, xs, q, m);
                 return;
             }
 #pragma unroll
@@ -850,6 +864,11 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
             // 0 while |h| < 2^15 on the slice, else the power of two that brings the slice's largest |h| below 2^15
             // (so fp16 never overflows); e goes to the exponent bytes [slot, slice]
             float hv[NT][4][RT];
+            int xe[NT][4];   // x16 = x 2^-E per token: the sums are scaled back before the GLU
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) xe[t][v] = __shfl(eslot, 16 * t + 4 * lg + v, 64);
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -858,7 +877,7 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) {
                         const int r = r0 + 16 * rt + lr;
-                        float g = acc[0][rt][t][v], up = acc[1][rt][t][v];
+                        float g = __builtin_ldexpf(acc[0][rt][t][v], xe[t][v]), up = __builtin_ldexpf(acc[1][rt][t][v], xe[t][v]);
                         if (wvalid && a.b0) g += a.b0[(size_t)e * N + r];
                         if (wvalid && a.b1) up += a.b1[(size_t)e * N + r];
                         hv[t][v][rt] = wvalid ? glu_act(a.act, g, up) : 0.f;
@@ -923,6 +942,50 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                     }
                 }
         }
+    }
+}
+
+// Dense int4, before gate/up: x [T, d] bf16 -> x16 = x 2^-E fp16, one block per token, E = 0 while |x| < 2^15 on the
+// row, else the power of two that brings the row's largest |x| below 2^15 (bf16 to fp16 is then exact except in
+// fp16's subnormal range, where values are rounded); E per token for the gate/up epilogue.
+__global__ void __launch_bounds__(256) k_x16(const uint16_t* __restrict__ x, uint16_t* __restrict__ x16,
+                                             int32_t* __restrict__ xexp, int d) {
+    __shared__ float sM[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const uint4* row = reinterpret_cast<const uint4*>(x + (size_t)t * d);
+    uint4* out = reinterpret_cast<uint4*>(x16 + (size_t)t * d);
+    const int nch = d >> 3;   // 16-byte chunks; d <= 2048 * 8 for one round of 8 per thread
+    constexpr int CPT = 8;
+    float am = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += 256 * CPT) {
+        uint4 v[CPT];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i)
+            if (c0 + i * 256 + tid < nch) v[i] = row[c0 + i * 256 + tid];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i)
+            if (c0 + i * 256 + tid < nch) {
+                const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) am = fmaxf(am, fmaxf(fabsf(bf16lo(w[q])), fabsf(bf16hi(w[q]))));
+            }
+    }
+    for (int o = 32; o; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    if ((tid & 63) == 0) sM[tid >> 6] = am;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(sM[0], sM[1]), fmaxf(sM[2], sM[3]));
+    const int E = amax >= 32768.f ? (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 141 : 0;
+    if (tid == 0) xexp[t] = E;
+    for (int c = tid; c < nch; c += 256) {   // the row again (cache hits)
+        const uint4 v = row[c];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const _Float16 lo = (_Float16)__builtin_ldexpf(bf16lo(w[q]), -E), hi = (_Float16)__builtin_ldexpf(bf16hi(w[q]), -E);
+            o4[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+        }
+        out[c] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
     }
 }
 
@@ -1172,6 +1235,13 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         if (wave || dense) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
+        }
+        if (dense && INT4) {
+            k_x16<<<a.T, 256, 0, a.st>>>((const uint16_t*)a.x, a.x16, a.xexp, w->d);
+            rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+            if (rc) return rc;
+            g.actv = a.x16;
+            g.xexp = a.xexp;
         }
         if (dense) {
             rc = launch_dense<FMT, 2>(g, nslots, a.st);

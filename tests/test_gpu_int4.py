@@ -350,26 +350,31 @@ def test_dense_tiles(case, monkeypatch):
 
 
 def test_dense_tiles_fp16_range(monkeypatch):
-    """The dense path's fp16 h past fp16's range: 24 tokens scaled by 1000 give |h| far above 65504 (checked on
-    the oracle's own h), the other tokens stay small, so one call takes both the direct f16 accumulation and the
-    per-slice 2^e rescaling; each group of tokens meets the gate against its own RMS."""
+    """The dense path's fp16 activations past fp16's range. Tokens scaled by 1000 give |h| far above 65504
+    (checked on the oracle's own h): their h16 rows carry exponents. Tokens scaled by 1e5 are beyond fp16
+    themselves: their x16 rows carry exponents too. The other tokens stay small, so one call mixes rows with and
+    without exponents (and slots whose slices need different exponents); each group of tokens meets the gate
+    against its own RMS."""
     monkeypatch.setenv("MOE_DENSE", "1")
     sh = shape_("big-h", 256, 640, 4, 2)
     s = packed_state(sh, 35)
     x, idx, wts = inputs(sh, 150, "uniform", seed=9)
     big = torch.zeros(150, dtype=torch.bool, device=DEV)
     big[::6] = True
-    x = torch.where(big[:, None], x.float() * 1000.0, x.float()).to(torch.bfloat16)
+    huge = torch.zeros(150, dtype=torch.bool, device=DEV)
+    huge[3::12] = True
+    x = x.float()
+    x = torch.where(big[:, None], x * 1000.0, torch.where(huge[:, None], x * 1e5, x)).to(torch.bfloat16)
     xs = orc.bf16_bits_to_f32(np_u16(x))
     wg, wu = deq(s, "g", experts=[int(idx[0, 0])])[0], deq(s, "u", experts=[int(idx[0, 0])])[0]
     h0 = orc.act_fn(xs[0] @ wg.T, xs[0] @ wu.T, 0)
-    assert np.abs(h0).max() > 2 * 65504.0
+    assert np.abs(h0).max() > 2 * 65504.0 and np.abs(xs[3]).max() > 65504.0
     print("case dense fp16 range T=150", flush=True)
     y = grouped(s, x, idx, wts, out_dtype=torch.float32)
     ref = oracle_y(s, x, idx, wts)
-    b = big.cpu().numpy()
-    assert_close(y[big], ref[b], what="large tokens")
-    assert_close(y[~big], ref[~b], what="small tokens")
+    small = ~(big | huge)
+    for sel, what in ((big, "h beyond fp16"), (huge, "x beyond fp16"), (small, "small tokens")):
+        assert_close(y[sel], ref[sel.cpu().numpy()], what=what)
 
 
 def test_dense_tiles_match_row_tiles(monkeypatch):
