@@ -149,7 +149,10 @@ int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offset
  *   path: MOE_PATH_*; nored = 1 writes the unweighted per-slot outputs y[T*k, d] instead (reference
  *   run_slots / NORED, metal_q4_moe.py:49-51; per-slot path only, residual must be NULL).
  *   Accumulation in fp32; the GLU output h is kept between the two launches as an unevaluated sum of two
- *   bf16 planes (about 16 significant bits, where the reference kernels store it in x.dtype).
+ *   bf16 planes (about 16 significant bits, where the reference kernels store it in x.dtype). Exception: int4
+ *   grouped calls with more than 32 slots per expert on average (prefill-sized T, path MOE_PATH_GROUPED with
+ *   the tile-major copies) run on fp16 MFMA: weights rounded once to fp16, x and h carried as fp16 with a
+ *   power-of-two exponent per row (no overflow); ~1e-3 of the outputs' RMS in the worst case measured.
  *   Requirements: d % 64 == 0, F % 64 == 0, F <= 16384; x, y, rows 16-byte aligned.
  *   workspace: moe_experts_workspace_bytes(...) bytes. Its first MOE_WORKSPACE_SYNC_BYTES bytes hold the
  *   fused T == 1 kernel's completion counters: zero them once when the workspace is allocated; every call
