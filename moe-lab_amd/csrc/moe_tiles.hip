@@ -1160,9 +1160,12 @@ int env_int(const char* name, int dflt) {
 // combine adds the parts' planes); gate/up is never split (the GLU needs whole sums)
 int dense_ksplit(int N, int K, int nslots, int E) {
     const long blocks = (long)((N + 255) / 256) * max_passes(nslots, E, 16 * DENSE_NT);
-    const int ks = env_int("MOE_DENSE_KSPLIT", 0);
-    if (ks >= 1 && ks <= 4) return ks;
-    return blocks < 4L * 256 && (K + 127) / 128 >= 8 ? 2 : 1;
+    const int nsl = (K + 127) / 128;
+    int ks = env_int("MOE_DENSE_KSPLIT", 0);
+    if (ks < 1 || ks > 4) ks = blocks < 4L * 256 && nsl >= 8 ? 2 : 1;
+    // parts of ceil(nsl / ks) slices: as many as are non-empty (an empty part would read past the records)
+    const int per = (nsl + ks - 1) / ks;
+    return (nsl + per - 1) / per;
 }
 
 template <class FMT, int NPROJ>

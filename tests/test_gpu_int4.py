@@ -450,3 +450,40 @@ def test_wave_tiles_for_many_tokens(nt, monkeypatch):
     print(f"case wave-many nt={nt}", flush=True)
     y = grouped(s, x, idx, wts, out_dtype=torch.float32)
     assert_close(y, oracle_y(s, x, idx, wts), what=("wave many", nt))
+
+
+@pytest.mark.parametrize("ks", [1, 2, 3, 4])
+def test_dense_down_k_parts(ks, monkeypatch):
+    """The dense down projection split into 1-4 K parts (MOE_DENSE_KSPLIT; the combine sums the parts' planes):
+    each at the gate, and every split within fp32 reassociation of the unsplit result."""
+    monkeypatch.setenv("MOE_DENSE", "1")
+    sh = shape_("ks", 256, 1152, 4, 2)   # 9 K slices: parts of 9, 5+4, 3+3+3; 4 asks for 3+3+3 as well
+    s = packed_state(sh, 41)
+    x, idx, wts = inputs(sh, 200, "zipf", seed=3)
+    print(f"case dense ksplit={ks}", flush=True)
+    monkeypatch.setenv("MOE_DENSE_KSPLIT", "1")
+    y1 = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    monkeypatch.setenv("MOE_DENSE_KSPLIT", str(ks))
+    y = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    assert_close(y, oracle_y(s, x, idx, wts), what=("ksplit", ks))
+    rms = float(y1.pow(2).mean().sqrt())
+    assert float((y - y1).abs().max()) <= 1e-5 * rms
+
+
+@pytest.mark.parametrize("T,dense", [(1, "0"), (32, "0"), (150, "1")])
+def test_stages_match_one_call(T, dense, monkeypatch):
+    """moe_experts_run_stages: GATE_UP then DOWN as two calls on one workspace gives the one-call result bit for
+    bit (the per-slot GEMVs at T=1, the wave tiles, the dense tiles with their x16 / h16 state in between)."""
+    from moelab_amd import _lib
+    from moelab_amd.experts import run_experts
+    monkeypatch.setenv("MOE_DENSE", dense)
+    sh = shape_("st", 256, 640, 4, 2)
+    s = packed_state(sh, 43)
+    x, idx, wts = inputs(sh, T, "uniform", seed=T)
+    print(f"case stages T={T} dense={dense}", flush=True)
+    y_all = run_experts(s, x, idx, wts, out_dtype=torch.float32)
+    out = torch.empty_like(y_all)
+    run_experts(s, x, idx, wts, out=out, out_dtype=torch.float32, stages=_lib.STAGE_GATE_UP)
+    run_experts(s, x, idx, wts, out=out, out_dtype=torch.float32, stages=_lib.STAGE_DOWN)
+    torch.cuda.synchronize()
+    assert torch.equal(out, y_all)
