@@ -7,6 +7,7 @@ Timing uses HIP events on the current stream around a chain of dependent calls w
 (x_{i+1} = x_i + run(x_i), reference mlx_backend.py:91-117), so host launch cost is excluded the same
 way the reference excludes its eval round-trip.
 """
+import importlib
 import importlib.util
 import platform
 
@@ -30,6 +31,12 @@ def env_info():
 
 
 def load_variant(path):
+    """A variant module by file path (reference mlx_backend.py:21-25). This package's own variants
+    (variants/*.py, relative imports) load as package modules; any other file loads on its own."""
+    import os
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "variants")
+    if os.path.dirname(os.path.abspath(path)) == here:
+        return importlib.import_module(f"{__package__}.variants.{os.path.splitext(os.path.basename(path))[0]}")
     spec = importlib.util.spec_from_file_location(f"variant_{abs(hash(path))}", path)
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
