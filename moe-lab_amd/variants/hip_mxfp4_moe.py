@@ -4,14 +4,15 @@ Variant contract and dispatch shape of the reference's MXFP4 dispatcher (referen
 moelab/variants/mlx/metal_mxfp4_moe.py:440-512): E2M1 codes with one E8M0 scale per 32 inputs,
 the scale applied in fp32 per group (exact for every byte 1..254; reference metal_mxfp4_moe.py:33-41);
     T == 1          -> one fused launch (gate/up/GLU, then down + k-reduction)
-    T > 1, load <= load_max(D, F) -> grouped expert tiles (each selected expert read once)
-    otherwise       -> gather_moe (per-slot path), like the reference's load-policy fallback (:474-477)
+    T > 1, grouped(...)  -> grouped expert tiles (each selected expert read once)
+    otherwise       -> gather_moe (per-slot path), the reference's load-policy fallback (:474-477); on MI355X
+                       it takes the small loads (fallback.grouped_from_load), not the large ones
 """
 import torch
 
 from .. import _lib, formats
 from ..experts import dims, make_state, run_experts, run_layer, unpack
-from ..fallback import gather_moe  # noqa: F401  (module attribute the dispatcher calls; tests patch it)
+from ..fallback import gather_moe, grouped_from_load  # noqa: F401  (gather_moe: tests patch the attribute)
 
 META = {"name": "hip_mxfp4_moe", "description": "gfx950 HIP MXFP4: fused T=1 launch, grouped expert tiles at T>1"}
 MODE, GS, BITS = "mxfp4", 32, 4
@@ -21,8 +22,18 @@ LOAD_MAX = None  # tests set a number to override the policy below (reference me
 
 
 def load_max(D, F):
-    """Grouped tiles up to this load (T*k/E); the reference's fitted policy (metal_mxfp4_moe.py:468-471)."""
-    return LOAD_MAX if LOAD_MAX is not None else (24 if D * F >= 3 << 19 else 8)
+    """Grouped tiles up to this load (T*k/E) (reference metal_mxfp4_moe.py:465-471). On MI355X the grouped
+    path wins at every high load measured, so there is no upper cut unless LOAD_MAX sets one."""
+    return LOAD_MAX if LOAD_MAX is not None else float("inf")
+
+
+def grouped(T, k, E, D, F):
+    """True: grouped tiles; False: the per-slot fallback. With LOAD_MAX set (tests, A/B runs) the reference's
+    rule, grouped up to LOAD_MAX; otherwise the MI355X fit, grouped from fallback.grouped_from_load."""
+    load = T * k / E
+    if LOAD_MAX is not None:
+        return load <= LOAD_MAX
+    return load >= grouped_from_load(D, F)
 
 
 def prepare(w_gate, w_up, w_down):
@@ -47,7 +58,7 @@ def run(s, x, idx, wts, act=0, residual=None, out_dtype=None):
     if T == 1:
         return run_layer(s, x, idx, wts, path=_lib.PATH_AUTO, **kw)
     E, D, F = dims(s)
-    if T * k / E > load_max(D, F):
+    if not grouped(T, k, E, D, F):
         return gather_moe(s, x, idx, wts, GS, BITS, MODE, **kw)
     return run_layer(s, x, idx, wts, path=_lib.PATH_GROUPED, **kw)
 

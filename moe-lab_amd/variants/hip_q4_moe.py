@@ -6,7 +6,8 @@ Same variant contract and dispatch shape as the reference's production int4 disp
                                (two per-slot launches when the shape does not fit the fused kernel)
     T > 1, custom_wins(...) -> grouped expert tiles: each selected expert's rows are read once and
                                applied to all of its slots (group, gate/up, down, combine)
-    otherwise               -> gather_moe (module attribute, monkeypatchable like the reference's)
+    otherwise               -> gather_moe (module attribute, monkeypatchable like the reference's); on
+                               MI355X the small loads (fallback.grouped_from_load)
 prepare / dequant keep the reference's state layout (mx.quantize affine, group 64), so `dequant(state)`
 gives the weights the fp32 reference uses.
 """
@@ -14,7 +15,7 @@ import torch
 
 from .. import _lib, formats
 from ..experts import dims, make_state, run_experts, run_layer, unpack
-from ..fallback import gather_moe  # noqa: F401  (module attribute the dispatcher calls; tests patch it)
+from ..fallback import gather_moe, grouped_from_load  # noqa: F401  (gather_moe: tests patch the attribute)
 
 META = {"name": "hip_q4_moe", "description": "gfx950 HIP: per-slot GEMV at T=1, grouped expert tiles at T>1"}
 BITS, GS = 4, 64
@@ -40,10 +41,10 @@ def dequant(s):
 
 
 def custom_wins(T, k, E, D, F):
-    """Load policy (reference metal_q4_moe.py:42-46): grouped tiles up to load = T*k/E of 24 for large
-    experts (D*F >= 1.5 * 2^20), 8 otherwise; above it the fallback runs."""
-    load = T * k / E
-    return load <= (24 if D * F >= 3 << 19 else 8)
+    """Load policy, refitted on MI355X (fallback.grouped_from_load; the reference's name and meaning,
+    metal_q4_moe.py:42-46: True runs the grouped expert tiles, False the fallback): grouped from a load
+    T*k/E of 1.0 (experts below 2.5 Mi weights per projection) or 0.27, the per-slot GEMV below."""
+    return T * k / E >= grouped_from_load(D, F)
 
 
 def run_slots(s, x, idx, act=0):

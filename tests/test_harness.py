@@ -91,3 +91,19 @@ def test_guard_verdict_history(tmp_path):
     for _ in range(30):
         guard.verdict([5000.0, 5000.0], path=path, device_key=k)
     assert len(json.load(open(path))[k]) == guard.N_HISTORY
+
+
+def test_grid_crossover_and_fitted_policy():
+    """The crossover reading of grid.py, and the MI355X load policy against the grid's boundary rows."""
+    from moelab_amd import fallback, grid
+    from moelab_amd.variants import hip_mxfp4_moe, hip_q4_moe
+    rows = [{"load": L, "slots_over_grouped": r} for L, r in ((0.1, 0.8), (1, 1.2), (4, 0.9), (8, 1.5), (16, 2.0))]
+    assert grid.crossover(rows) == 8 and grid.crossover(rows[:3]) is None
+    assert [grid.t_for_load(L, 128, 8) for L in (0.0625, 1, 32)] == [2, 16, 512]
+    # (shape D, F, E, k; T where the per-slot path won; T where grouped won)
+    for D, F, E, k, t_slots, t_grouped in ((2048, 768, 128, 8, 8, 16), (2048, 1024, 64, 8, 4, 8),
+                                           (2048, 1408, 64, 6, 2, 3), (2880, 2880, 32, 4, 2, 4)):
+        assert not hip_q4_moe.custom_wins(t_slots, k, E, D, F) and hip_q4_moe.custom_wins(t_grouped, k, E, D, F)
+        assert not hip_mxfp4_moe.grouped(t_slots, k, E, D, F) and hip_mxfp4_moe.grouped(t_grouped, k, E, D, F)
+    assert hip_q4_moe.custom_wins(2, 2, 8, 4096, 14336) and hip_q4_moe.custom_wins(512, 2, 8, 4096, 14336)
+    assert fallback.grouped_from_load(2048, 768) == 1.0 and fallback.grouped_from_load(4096, 14336) == 0.27
