@@ -18,7 +18,7 @@ int resolve_path(int path, int T) {
 }
 
 struct Layout {
-    size_t h, yp, x16, xexp, counts, offsets, sorted, active, meta, items, total;
+    size_t h, yp, x16, xexp, counts, offsets, sorted, active, meta, items, items2, total;
 };
 
 Layout layout(const moe_experts_t* w, int T, int k, int path) {
@@ -46,6 +46,8 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
         off += align_up(4 * 4);
         L.items = off;
         off += align_up((size_t)moe::max_passes((int)nslots, w->E, 16) * 12);
+        L.items2 = off;   // the dense down's list when the gate/up runs the wave tiles (64-token passes)
+        off += align_up((size_t)moe::max_passes((int)nslots, w->E, 64) * 12);
     }
     L.total = off;
     return L;
@@ -208,6 +210,7 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
         a.grp.active = (int32_t*)(ws + L.active);
         a.grp.meta = (int32_t*)(ws + L.meta);
         a.grp.items = (int32_t*)(ws + L.items);
+        a.grp.items2 = (int32_t*)(ws + L.items2);
     }
     return rpath == MOE_PATH_GROUPED ? moe::run_experts_tiles(a) : moe::run_experts_slots(a);
 }

@@ -15,7 +15,8 @@ int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, fl
                 hipStream_t st);
 // with items: also the grouped kernels' pass list for passes of P slots (items [3 * max_passes(n, E, P)], meta[2])
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
-                 int32_t* active, int32_t* meta, hipStream_t st, int P = 0, int32_t* items = nullptr);
+                 int32_t* active, int32_t* meta, hipStream_t st, int P = 0, int32_t* items = nullptr, int P2 = 0,
+                 int32_t* items2 = nullptr);
 // upper bound of the pass count: sum over experts of ceil(count / P) <= n / P + (experts with a count)
 inline int max_passes(int n, int E, int P) { return (n + P - 1) / P + (n < E ? n : E); }
 int launch_shared_route(const uint16_t* x, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
@@ -29,6 +30,7 @@ struct GroupBufs {
     int32_t* active;
     int32_t* meta;    // [4]: active experts, bad ids, passes of the work list
     int32_t* items;   // pass list, room for max_passes(n, E, 16) (expert, pass, passes) triples
+    int32_t* items2;  // second pass list (dense down after wave gate/up), room for max_passes(n, E, 64)
 };
 
 struct ExpertsArgs {

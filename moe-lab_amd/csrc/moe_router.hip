@@ -194,14 +194,15 @@ topk_kernel(const LT* __restrict__ logits, int T, int E, int k, int norm, float 
 // entries: experts with count > 0, ascending), meta[0] = number of active experts, meta[1] = bad ids.
 // With items != null (the grouped kernels' work list, pass size P): items[3w .. 3w + 2] = (expert, pass index q
 // within the expert (first token q * P), the expert's pass count) of pass w; the passes of each active expert in
-// ascending order, expert by expert; meta[2] = number of passes.
+// ascending order, expert by expert; meta[2] = number of passes. items2 (pass size P2), if given, is a second
+// such list, meta[3] its number of passes (the wave tiles' and the dense tiles' lists when a call uses both).
 // mw (the ids and 4 per-wave count arrays fit in LDS): the ids are read once into LDS, and each of the 4 waves
 // places one contiguous quarter of the slots with its own cursors (the expert's offset plus the counts of the
 // quarters before it), so the order stays ascending within every expert. Otherwise wave 0 places all slots.
 __global__ void __launch_bounds__(256)
 group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
             int32_t* __restrict__ sorted, int32_t* __restrict__ active, int32_t* __restrict__ meta, int P,
-            int32_t* __restrict__ items, int mw) {
+            int32_t* __restrict__ items, int P2, int32_t* __restrict__ items2, int mw) {
     extern __shared__ int32_t sm[];   // mw: cnt[4][E], ids[n]; else cnt[E], cursor[E]
     const int NW = mw ? 4 : 1;
     int32_t* cnt = sm;
@@ -230,7 +231,7 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
     }
     __syncthreads();
     if (tid < 64) {   // wave 0: exclusive scan of counts and the active list, in chunks of 64 experts
-        int run = 0, run_act = 0, run_p = 0;
+        int run = 0, run_act = 0, run_p = 0, run_p2 = 0;
         for (int base = 0; base < E; base += 64) {
             const int e = base + lane;
             int cw[4] = {0, 0, 0, 0};
@@ -241,15 +242,17 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
                     c += cw[w];
                 }
             }
-            const int np = items ? (c + P - 1) / P : 0;   // passes of expert e
+            const int np = items ? (c + P - 1) / P : 0;      // passes of expert e
+            const int np2 = items2 ? (c + P2 - 1) / P2 : 0;  // in the second list
             // inclusive wave scans of c, of (c > 0) and of the pass counts
-            int inc = c, act = c > 0 ? 1 : 0, incp = np;
+            int inc = c, act = c > 0 ? 1 : 0, incp = np, incp2 = np2;
 #pragma unroll
             for (int s = 1; s < 64; s <<= 1) {
                 const int o = __shfl_up(inc, s, 64);
                 const int oa = __shfl_up(act, s, 64);
                 const int op = __shfl_up(incp, s, 64);
-                if (lane >= s) { inc += o; act += oa; incp += op; }
+                const int op2 = __shfl_up(incp2, s, 64);
+                if (lane >= s) { inc += o; act += oa; incp += op; incp2 += op2; }
             }
             if (e < E) {
                 const int excl = run + inc - c;
@@ -271,16 +274,24 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
                     items[3 * (w0 + q) + 1] = q;
                     items[3 * (w0 + q) + 2] = np;
                 }
+                const int w2 = run_p2 + incp2 - np2;
+                for (int q = 0; q < np2; ++q) {
+                    items2[3 * (w2 + q)] = e;
+                    items2[3 * (w2 + q) + 1] = q;
+                    items2[3 * (w2 + q) + 2] = np2;
+                }
             }
             run += __shfl(inc, 63, 64);
             run_act += __shfl(act, 63, 64);
             run_p += __shfl(incp, 63, 64);
+            run_p2 += __shfl(incp2, 63, 64);
         }
         if (lane == 0) {
             offsets[E] = run;
             meta[0] = run_act;
             meta[1] = s_bad;
             if (items) meta[2] = run_p;
+            if (items2) meta[3] = run_p2;
         }
         for (int a = run_act + lane; a < E; a += 64) active[a] = -1;
     }
@@ -388,12 +399,12 @@ int launch_shared_route(const uint16_t* x, const uint16_t* gate, int T, int d, i
 }
 
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
-                 int32_t* active, int32_t* meta, hipStream_t st, int P, int32_t* items) {
-    if (items && P < 1) return MOE_ERR_ARG;
+                 int32_t* active, int32_t* meta, hipStream_t st, int P, int32_t* items, int P2, int32_t* items2) {
+    if ((items && P < 1) || (items2 && P2 < 1)) return MOE_ERR_ARG;
     const size_t mw_bytes = ((size_t)4 * E + (size_t)n) * sizeof(int32_t);
     const int mw = mw_bytes <= 64 * 1024 ? 1 : 0;
     group_slots<<<1, 256, mw ? mw_bytes : 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted, active,
-                                                                          meta, P, items, mw);
+                                                                          meta, P, items, P2, items2, mw);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

@@ -38,6 +38,12 @@ namespace moe {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2x __attribute__((ext_vector_type(2)));
+
+// power-of-two exponent e that keeps v 2^-e inside fp16 for |v| <= amax: 0 while amax < 2^15, else
+// floor(log2(amax)) - 14 (then amax 2^-e < 2^15; inf gives 114, and NaN, which fails the test, 0)
+__device__ __forceinline__ int h16_exponent(float amax) {
+    return amax >= 32768.f ? (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 141 : 0;
+}
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int TL_ROWS = 64;   // weight rows per block
@@ -55,7 +61,8 @@ struct TileArgs {
     const float* b0;       // additive row biases [E, N] (gpt-oss) or null
     const float* b1;
     const int32_t *counts, *offsets, *sorted, *active, *meta;
-    const int32_t* items;  // wave and dense tiles: pass list (expert, pass, passes), meta[2] passes
+    const int32_t* items;  // wave and dense tiles: pass list (expert, pass, passes), meta[nidx] passes
+    int nidx;              // 2 (first pass list) or 3 (second)
     int K, N, E, act;      // act: GLU kind (gate/up)
     int rpb;               // row tiles per block (k_tile_run)
     int kslots;            // k (slots per token)
@@ -356,12 +363,15 @@ __host__ __device__ constexpr int tile_slice_bytes() {
     return FMT::XSUM ? TILE_SLICE_INT4 : TILE_SLICE_MXFP4;
 }
 
-template <class FMT, int NPROJ, int NT, int RT, int D>
+// H16O (int4 gate/up before a dense down): h leaves as fp16 h16 = h 2^-e with e per (slot, 32-row chunk), the
+// layout the dense down reads after k_h16_fix, instead of the two bf16 planes.
+template <class FMT, int NPROJ, int NT, int RT, int D, bool H16O = false>
 __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
+    static_assert(!H16O || (NPROJ == 2 && RT % 2 == 0), "h16 output: gate/up, whole 32-row chunks per wave");
     constexpr bool INT4 = FMT::XSUM;
     constexpr int HL = NPROJ == 2 ? 1 : 2;   // activation planes: x, or h = hi + lo
     constexpr int SB = tile_slice_bytes<FMT>();
-    if ((int)blockIdx.y >= a.meta[2]) return;   // one pass of the work list per workgroup row
+    if ((int)blockIdx.y >= a.meta[a.nidx]) return;   // one pass of the work list per workgroup row
     const int e = a.items[3 * blockIdx.y], tok0 = a.items[3 * blockIdx.y + 1] * 16 * NT;
     const int n = a.counts[e], beg = a.offsets[e];
     const int lane = threadIdx.x, lr = lane & 15, lg = lane >> 4;
@@ -518,6 +528,44 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
             }
         }
         // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
+        if constexpr (H16O) {
+            uint8_t* hexp_out = reinterpret_cast<uint8_t*>(a.hout2);
+            const int nch = N >> 5;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int j = 4 * lg + v;
+                    const int slot = __shfl(slotA[t], j, 64);   // lane j (any lane group) holds token j's slot
+                    float hv[RT];
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const int r = r0 + 16 * rt + lr;
+                        float g = acc[0][rt][t][v], up = acc[1][rt][t][v];
+                        if (a.b0) g += a.b0[(size_t)e * N + r];
+                        if (a.b1) up += a.b1[(size_t)e * N + r];
+                        hv[rt] = glu_act(a.act, g, up);
+                    }
+                    int ex[RT / 2];
+#pragma unroll
+                    for (int c = 0; c < RT / 2; ++c) {   // 32-row chunk c: row tiles 2c, 2c + 1
+                        float am = fmaxf(fabsf(hv[2 * c]), fabsf(hv[2 * c + 1]));
+#pragma unroll
+                        for (int o = 1; o < 16; o <<= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+                        ex[c] = h16_exponent(am);
+                    }
+                    if (tok0 + 16 * t + j >= n) continue;
+#pragma unroll
+                    for (int c = 0; c < RT / 2; ++c)
+                        if (lr == 0) hexp_out[(size_t)slot * nch + (r0 >> 5) + c] = (uint8_t)ex[c];
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const _Float16 h16 = (_Float16)__builtin_ldexpf(hv[rt], -ex[rt >> 1]);
+                        a.hout[(size_t)slot * N + r0 + 16 * rt + lr] = __builtin_bit_cast(uint16_t, h16);
+                    }
+                }
+            return;
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -592,7 +640,6 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t sX0[HL * BM * 256];
     __shared__ __attribute__((aligned(1024))) uint8_t sX1[HL * BM * 256];
     __shared__ int sSlot[BM];
-    __shared__ float sAm[H16 && NPROJ == 2 ? 4 * BM : 1];   // gate/up epilogue: |h| max per (token, wave)
 
     // 1-D grid over (pass list x row blocks), ordered expert by expert, and within an expert row block by row
     // block with the expert's passes adjacent: the passes that share a weight tile run side by side (their
@@ -601,7 +648,7 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     const int ks = (int)(blockIdx.x % (unsigned)a.ksplit);   // K part (down only), the fastest index
     const int bid = (int)(blockIdx.x / (unsigned)a.ksplit);
     const int wq = bid / nrb;                      // some pass of the current expert
-    if (wq >= a.meta[2]) return;
+    if (wq >= a.meta[a.nidx]) return;
     const int e = a.items[3 * wq], np = a.items[3 * wq + 2];
     const int w0 = wq - a.items[3 * wq + 1];       // the expert's first pass
     const int local = bid - w0 * nrb;
@@ -860,15 +907,17 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
 
         // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
         if constexpr (H16 && NPROJ == 2) {
-            // h of the block's 128 rows (one slice of the down projection's K) as fp16 h16 = h 2^-e, e per token:
-            // 0 while |h| < 2^15 on the slice, else the power of two that brings the slice's largest |h| below 2^15
-            // (so fp16 never overflows); e goes to the exponent bytes [slot, slice]
+            // h of the wave's 32 rows as fp16 h16 = h 2^-e, e per token: 0 while |h| < 2^15 on those rows, else
+            // the power of two that brings their largest |h| below 2^15 (so fp16 never overflows); e goes to the
+            // exponent bytes [slot, F / 32] (one 32-row chunk per wave)
             float hv[NT][4][RT];
             int xe[NT][4];   // x16 = x 2^-E per token: the sums are scaled back before the GLU
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) xe[t][v] = __shfl(eslot, 16 * t + 4 * lg + v, 64);
+            uint8_t* hexp_out = reinterpret_cast<uint8_t*>(a.hout2);
+            const int nch = N >> 5;
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -885,28 +934,15 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                     }
 #pragma unroll
                     for (int o = 1; o < 16; o <<= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
-                    if (lr == 0) sAm[(16 * t + 4 * lg + v) * 4 + wave] = am;
-                }
-            __syncthreads();
-            uint8_t* hexp_out = reinterpret_cast<uint8_t*>(a.hout2);
-            const int nslh = (N + 127) >> 7;
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
+                    const int ex = h16_exponent(am);
                     const int jt = 16 * t + 4 * lg + v;
-                    if (jt >= nlive) continue;
-                    const float4 m4 = *reinterpret_cast<const float4*>(&sAm[jt * 4]);
-                    const float amax = fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w));
-                    const int ex = amax >= 32768.f ? (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 141 : 0;
+                    if (jt >= nlive || !wvalid) continue;
                     const int slot = sSlot[jt];
-                    if (wave == 0 && lr == 0) hexp_out[(size_t)slot * nslh + rb] = (uint8_t)ex;
-                    if (wvalid) {
+                    if (lr == 0) hexp_out[(size_t)slot * nch + (r0 >> 5)] = (uint8_t)ex;
 #pragma unroll
-                        for (int rt = 0; rt < RT; ++rt) {
-                            const _Float16 h16 = (_Float16)__builtin_ldexpf(hv[t][v][rt], -ex);
-                            a.hout[(size_t)slot * N + r0 + 16 * rt + lr] = __builtin_bit_cast(uint16_t, h16);
-                        }
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const _Float16 h16 = (_Float16)__builtin_ldexpf(hv[t][v][rt], -ex);
+                        a.hout[(size_t)slot * N + r0 + 16 * rt + lr] = __builtin_bit_cast(uint16_t, h16);
                     }
                 }
         } else {
@@ -974,7 +1010,7 @@ __global__ void __launch_bounds__(256) k_x16(const uint16_t* __restrict__ x, uin
     if ((tid & 63) == 0) sM[tid >> 6] = am;
     __syncthreads();
     const float amax = fmaxf(fmaxf(sM[0], sM[1]), fmaxf(sM[2], sM[3]));
-    const int E = amax >= 32768.f ? (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 141 : 0;
+    const int E = h16_exponent(amax);
     if (tid == 0) xexp[t] = E;
     for (int c = tid; c < nch; c += 256) {   // the row again (cache hits)
         const uint4 v = row[c];
@@ -989,50 +1025,47 @@ __global__ void __launch_bounds__(256) k_x16(const uint16_t* __restrict__ x, uin
     }
 }
 
-// Dense int4, between gate/up and down: one block per slot. The gate/up blocks wrote h16 = h 2^-e with e per (slot,
-// 128-row slice); this brings the slot's row to one exponent E = max e (slices with a smaller e are scaled by
-// 2^(e - E): exact unless a value falls into fp16's subnormal range, where it is rounded) and writes E for the
-// down projection's epilogue. A slot whose exponents are all 0 (|h| < 2^15 on the whole row, the usual case)
-// costs one load per lane of the first wave.
+// int4 grouped path, between gate/up and a dense down: one block per slot. The gate/up wrote h16 = h 2^-e with e
+// per (slot, 32-row chunk); this brings the slot's row to one exponent E = max e (chunks with a smaller e are
+// scaled by 2^(e - E): exact unless a value falls into fp16's subnormal range, where it is rounded) and writes
+// E for the down projection's epilogue. A slot whose exponents are all 0 (|h| < 2^15 on the whole row, the
+// usual case) costs two exponent loads per thread.
 __global__ void __launch_bounds__(256) k_h16_fix(const uint8_t* __restrict__ hexp, uint16_t* __restrict__ h16,
-                                                 int32_t* __restrict__ eslot, int nslh, int F) {
-    __shared__ int sE[128];
-    __shared__ int sMax;
-    const int slot = blockIdx.x, tid = threadIdx.x;
-    const uint8_t* er = hexp + (size_t)slot * nslh;
-    if (tid < 64) {
-        const int e0 = tid < nslh ? er[tid] : 0, e1 = tid + 64 < nslh ? er[tid + 64] : 0;
-        sE[tid] = e0;
-        sE[tid + 64] = e1;
-        int E = e0 > e1 ? e0 : e1;
-        for (int o = 32; o; o >>= 1) {
-            const int other = __shfl_xor(E, o, 64);
-            E = other > E ? other : E;
-        }
-        if (tid == 0) {
-            sMax = E;
-            eslot[slot] = E;
-        }
+                                                 int32_t* __restrict__ eslot, int F) {
+    __shared__ int sE[512];   // F <= 16384: at most 512 chunks of 32
+    __shared__ int sMax[4];
+    const int slot = blockIdx.x, tid = threadIdx.x, nch = F >> 5;
+    const uint8_t* er = hexp + (size_t)slot * nch;
+    const int e0 = tid < nch ? er[tid] : 0, e1 = tid + 256 < nch ? er[tid + 256] : 0;
+    sE[tid] = e0;
+    sE[tid + 256] = e1;
+    int m = e0 > e1 ? e0 : e1;
+    for (int o = 32; o; o >>= 1) {
+        const int other = __shfl_xor(m, o, 64);
+        m = other > m ? other : m;
     }
+    if ((tid & 63) == 0) sMax[tid >> 6] = m;
     __syncthreads();
-    const int E = sMax;
+    int E = sMax[0];
+    for (int w = 1; w < 4; ++w) E = sMax[w] > E ? sMax[w] : E;
+    if (tid == 0) eslot[slot] = E;
     if (E == 0) return;   // block-uniform
-    // 16-byte chunks (8 values, one slice each) of the row: every load first, then the rewrites
-    constexpr int CPT = 8;   // chunks per thread per round (F <= 16384: 2048 chunks, one round)
+    // 16-byte pieces (8 values; 4 per chunk) of the row: every load first, then the rewrites
+    constexpr int CPT = 8;   // pieces per thread per round (F <= 16384: 2048 pieces, one round)
     uint4* row = reinterpret_cast<uint4*>(h16 + (size_t)slot * F);
-    const int nch = F >> 3;
-    for (int c0 = 0; c0 < nch; c0 += 256 * CPT) {
+    const int np = F >> 3;
+    for (int c0 = 0; c0 < np; c0 += 256 * CPT) {
         uint4 v[CPT];
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = c0 + i * 256 + tid;
-            if (c < nch) v[i] = row[c];
+            if (c < np) v[i] = row[c];
         }
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = c0 + i * 256 + tid;
-            if (c >= nch) continue;
-            const int d = sE[c >> 4] - E;   // 16 chunks per 128-value slice
+            if (c >= np) continue;
+            const int d = sE[c >> 2] - E;
             if (d == 0) continue;
             uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
@@ -1133,13 +1166,13 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 #ifndef MOE_WAVE_RT_DN
 #define MOE_WAVE_RT_DN 4   // 16-row tiles per wave, down (d % 64 == 0)
 #endif
-template <class FMT, int NPROJ, int RT, int D>
+template <class FMT, int NPROJ, int RT, int D, bool H16O = false>
 int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st) {
     if (t.N % (16 * RT)) return MOE_ERR_ARG;
     dim3 grid(t.N / (16 * RT), max_passes(nslots, t.E, 16 * nt));
     if (grid.y > 65535) return MOE_ERR_ARG;
-    if (nt == 1) k_wave_tile<FMT, NPROJ, 1, RT, D><<<grid, 64, 0, st>>>(t);
-    else k_wave_tile<FMT, NPROJ, 2, RT, D><<<grid, 64, 0, st>>>(t);
+    if (nt == 1) k_wave_tile<FMT, NPROJ, 1, RT, D, H16O><<<grid, 64, 0, st>>>(t);
+    else k_wave_tile<FMT, NPROJ, 2, RT, D, H16O><<<grid, 64, 0, st>>>(t);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
@@ -1201,28 +1234,43 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     t.act = a.act;
     t.kslots = a.k;
     // tile-major weights present: wave tiles for few tokens per expert, dense tiles for many (unless their grid
-    // would fill only part of the chip, e.g. a few shared experts: then the wave tiles, 32-token passes). The
-    // choice depends on (T, k, E, F) only, so separately launched stages agree on the layout of h
+    // would fill only part of the chip, e.g. a few shared experts: then the wave tiles, 32-token passes). int4
+    // takes the dense down from fewer tokens per expert than the dense gate/up (the down's wave tiles read two h
+    // planes per token while the dense down shares its 64 tokens' h16 across a block): mid loads run the wave
+    // gate/up (h out as h16) and the dense down, on two pass lists. The choices depend on (T, k, E, d, F) only,
+    // so separately launched stages agree on the layout of h.
+    constexpr bool INT4 = FmtInt4::FMT == FMT::FMT;
     const bool tiled = w->gate.tiles && w->up.tiles && w->down.tiles;
     const int dmode = env_int("MOE_DENSE", -1);
-    const long dblocks = (long)((w->F + 127) / 128) * max_passes(nslots, w->E, 16 * DENSE_NT);
-    const bool dense = tiled && avg > 32 && (dmode == 1 || (dmode < 0 && dblocks >= MOE_DENSE_MIN_BLOCKS));
-    const bool wave = tiled && !dense && (avg <= 32 || dmode != 0);
+    const int dpasses = max_passes(nslots, w->E, 16 * DENSE_NT);
+    const long dblocks = (long)((w->F + 127) / 128) * dpasses;
+    const long dn_blocks = (long)((w->d + 255) / 256) * dpasses;
+    const int min_avg = env_int("MOE_DENSE_MIN_AVG", 32);
+    const int dn_min_avg = env_int("MOE_DENSE_DN_MIN_AVG", 16);
+    const bool dense_gu = tiled && avg > min_avg && (dmode == 1 || (dmode < 0 && dblocks >= MOE_DENSE_MIN_BLOCKS));
+    const bool dense_dn = dense_gu || (INT4 && tiled && dmode != 0 && avg > dn_min_avg &&
+                                       (dmode == 1 || dn_blocks >= MOE_DENSE_MIN_BLOCKS));
+    const bool wave_gu = tiled && !dense_gu && (avg <= min_avg || dmode != 0);
+    const bool wave_dn = tiled && !dense_dn && (avg <= min_avg || dmode != 0);
+    const bool h16 = INT4 && dense_dn;   // h leaves the gate/up as h16 with per-32-row exponents
     const int wnt = env_int("MOE_WAVE_NT", 0);
-    const int nt = wave ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2)) : tokens_per_pass_tiles(a.T, a.k, w->E);
+    const int nt = (wave_gu || wave_dn) ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2))
+                                        : tokens_per_pass_tiles(a.T, a.k, w->E);
+    // pass lists: 16 nt tokens per pass for the wave tiles, 16 DENSE_NT for the dense tiles; a second list
+    // when the two stages take different kernels
+    const int P_gu = dense_gu ? 16 * DENSE_NT : 16 * nt, P_dn = dense_dn ? 16 * DENSE_NT : 16 * nt;
+    const bool two_lists = P_gu != P_dn;
     t.items = a.grp.items;
-    // pass size of the work list: 16 nt tokens for the wave tiles, 16 DENSE_NT for the dense tiles
-    const int P = dense ? 16 * DENSE_NT : 16 * nt;
-    constexpr bool INT4 = FmtInt4::FMT == FMT::FMT;
-    const int nslh = (w->F + 127) / 128;
-    if (dense && INT4) {
-        // fp16 h: the second h plane holds the exponent bytes [slots, F/128], then the slot exponents int32 [slots]
-        t.eslot_off = ((size_t)nslots * nslh + 255) / 256 * 256;
+    t.nidx = 2;
+    if (h16) {
+        // the second h plane holds the exponent bytes [slots, F/32], then the slot exponents int32 [slots]
+        t.eslot_off = ((size_t)nslots * (w->F / 32) + 255) / 256 * 256;
         if (t.eslot_off + (size_t)nslots * 4 > (size_t)nslots * w->F * 2) return MOE_ERR_ARG;
     }
     if (a.stages & 1) {
         int rc = launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
-                              a.grp.meta, a.st, P, a.grp.items);
+                              a.grp.meta, a.st, P_gu, a.grp.items, two_lists ? P_dn : 0,
+                              two_lists ? a.grp.items2 : nullptr);
         if (rc) return rc;
         TileArgs g = t;
         g.actv = (const uint16_t*)a.x;
@@ -1235,27 +1283,26 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         g.b1 = w->up.bias;
         g.hout = a.hhi;
         g.hout2 = a.hlo;
-        if (wave || dense) {
+        if (wave_gu || dense_gu) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
         }
-        if (dense && INT4) {
+        if (dense_gu && INT4) {
             k_x16<<<a.T, 256, 0, a.st>>>((const uint16_t*)a.x, a.x16, a.xexp, w->d);
             rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
             if (rc) return rc;
             g.actv = a.x16;
             g.xexp = a.xexp;
         }
-        if (dense) {
-            rc = launch_dense<FMT, 2>(g, nslots, a.st);
-            if (!rc && INT4) {
-                k_h16_fix<<<nslots, 256, 0, a.st>>>((const uint8_t*)a.hlo, a.hhi,
-                                                  (int32_t*)((uint8_t*)a.hlo + t.eslot_off), nslh, w->F);
-                rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
-            }
-        }
-        else if (wave) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st);
+        if (dense_gu) rc = launch_dense<FMT, 2>(g, nslots, a.st);
+        else if (wave_gu && h16) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU, INT4>(g, nt, nslots, a.st);
+        else if (wave_gu) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st);
         else rc = launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
+        if (!rc && h16) {
+            k_h16_fix<<<nslots, 256, 0, a.st>>>((const uint8_t*)a.hlo, a.hhi,
+                                              (int32_t*)((uint8_t*)a.hlo + t.eslot_off), w->F);
+            rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+        }
         if (rc) return rc;
     }
     if (a.stages & 2) {
@@ -1267,12 +1314,16 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.N = w->d;
         d.W0 = (const uint8_t*)w->down.rows;
         d.yp = a.yp;
-        d.ksplit = dense ? dense_ksplit(d.N, d.K, nslots, w->E) : 1;
+        d.ksplit = dense_dn ? dense_ksplit(d.N, d.K, nslots, w->E) : 1;
         d.plane = (size_t)nslots * d.N;
-        if (wave || dense) d.W0 = (const uint8_t*)w->down.tiles;
+        if (two_lists) {
+            d.items = a.grp.items2;
+            d.nidx = 3;
+        }
+        if (wave_dn || dense_dn) d.W0 = (const uint8_t*)w->down.tiles;
         int rc;
-        if (dense) rc = launch_dense<FMT, 1>(d, nslots, a.st);
-        else if (wave) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
+        if (dense_dn) rc = launch_dense<FMT, 1>(d, nslots, a.st);
+        else if (wave_dn) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
         return launch_combine(a.yp, d.ksplit, d.plane, a.idx, a.wts, w->down.bias, w->E,

@@ -349,19 +349,21 @@ def test_dense_tiles(case, monkeypatch):
     assert_close(y, ref, what=("dense", name, "bf16 out"))
 
 
-def test_dense_tiles_fp16_range(monkeypatch):
+@pytest.mark.parametrize("T", [50, 150])
+def test_dense_tiles_fp16_range(T, monkeypatch):
     """The dense path's fp16 activations past fp16's range. Tokens scaled by 1000 give |h| far above 65504
     (checked on the oracle's own h): their h16 rows carry exponents. Tokens scaled by 1e5 are beyond fp16
     themselves: their x16 rows carry exponents too. The other tokens stay small, so one call mixes rows with and
     without exponents (and slots whose slices need different exponents); each group of tokens meets the gate
-    against its own RMS."""
+    against its own RMS. T=50 (25 slots per expert) runs the wave gate/up with h16 output into the dense down,
+    T=150 the dense tiles on both projections."""
     monkeypatch.setenv("MOE_DENSE", "1")
     sh = shape_("big-h", 256, 640, 4, 2)
     s = packed_state(sh, 35)
-    x, idx, wts = inputs(sh, 150, "uniform", seed=9)
-    big = torch.zeros(150, dtype=torch.bool, device=DEV)
+    x, idx, wts = inputs(sh, T, "uniform", seed=9)
+    big = torch.zeros(T, dtype=torch.bool, device=DEV)
     big[::6] = True
-    huge = torch.zeros(150, dtype=torch.bool, device=DEV)
+    huge = torch.zeros(T, dtype=torch.bool, device=DEV)
     huge[3::12] = True
     x = x.float()
     x = torch.where(big[:, None], x * 1000.0, torch.where(huge[:, None], x * 1e5, x)).to(torch.bfloat16)
@@ -369,12 +371,37 @@ def test_dense_tiles_fp16_range(monkeypatch):
     wg, wu = deq(s, "g", experts=[int(idx[0, 0])])[0], deq(s, "u", experts=[int(idx[0, 0])])[0]
     h0 = orc.act_fn(xs[0] @ wg.T, xs[0] @ wu.T, 0)
     assert np.abs(h0).max() > 2 * 65504.0 and np.abs(xs[3]).max() > 65504.0
-    print("case dense fp16 range T=150", flush=True)
+    print(f"case dense fp16 range T={T}", flush=True)
     y = grouped(s, x, idx, wts, out_dtype=torch.float32)
     ref = oracle_y(s, x, idx, wts)
     small = ~(big | huge)
     for sel, what in ((big, "h beyond fp16"), (huge, "x beyond fp16"), (small, "small tokens")):
         assert_close(y[sel], ref[sel.cpu().numpy()], what=what)
+
+
+MIXED_CASES = [
+    # (name, d, F, E, k, T, routing): 16 < T k / E <= 32 with MOE_DENSE=1: wave gate/up (h16 out) + dense down
+    ("mix", 256, 384, 4, 2, 50, "uniform"),       # 25 per expert
+    ("mix-odd", 320, 448, 4, 2, 60, "zipf"),      # K % 128 == 64 both ways, uneven counts
+    ("mix-many", 512, 1152, 16, 4, 100, "uniform"),  # 25 per expert over 16 experts; the down split over K
+]
+
+
+@pytest.mark.parametrize("case", MIXED_CASES, ids=lambda c: c[0])
+def test_wave_gate_up_dense_down(case, monkeypatch):
+    """Mid loads: the wave tiles' gate/up writes h as fp16 with per-32-row exponents, the exponent pass makes
+    one exponent per slot, the dense tiles' down reads it on its own 64-token pass list."""
+    monkeypatch.setenv("MOE_DENSE", "1")
+    name, d, f, E, k, T, routing = case
+    sh = shape_(name, d, f, E, k)
+    s = packed_state(sh, 37)
+    x, idx, wts = inputs(sh, T, routing, seed=T)
+    print(f"case mixed {name} T={T}", flush=True)
+    y32 = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    y = grouped(s, x, idx, wts)
+    ref = oracle_y(s, x, idx, wts)
+    assert_close(y32, ref, what=("mixed", name, "fp32 out"))
+    assert_close(y, ref, what=("mixed", name, "bf16 out"))
 
 
 def test_dense_tiles_match_row_tiles(monkeypatch):
@@ -470,10 +497,11 @@ def test_dense_down_k_parts(ks, monkeypatch):
     assert float((y - y1).abs().max()) <= 1e-5 * rms
 
 
-@pytest.mark.parametrize("T,dense", [(1, "0"), (32, "0"), (150, "1")])
+@pytest.mark.parametrize("T,dense", [(1, "0"), (32, "0"), (50, "1"), (150, "1")])
 def test_stages_match_one_call(T, dense, monkeypatch):
     """moe_experts_run_stages: GATE_UP then DOWN as two calls on one workspace gives the one-call result bit for
-    bit (the per-slot GEMVs at T=1, the wave tiles, the dense tiles with their x16 / h16 state in between)."""
+    bit (the per-slot GEMVs at T=1, the wave tiles, the wave gate/up into the dense down on two pass lists, the
+    dense tiles with their x16 / h16 state in between)."""
     from moelab_amd import _lib
     from moelab_amd.experts import run_experts
     monkeypatch.setenv("MOE_DENSE", dense)
