@@ -1163,6 +1163,9 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 #ifndef MOE_WAVE_RT_GU
 #define MOE_WAVE_RT_GU 2   // 16-row tiles per wave, gate/up (F % 32 == 0: F % 64 == 0 is required)
 #endif
+#ifndef MOE_WAVE_RT_DN_WIDE
+#define MOE_WAVE_RT_DN_WIDE 8   // 16-row tiles per wave, down, when d % 128 == 0 (fewer activation loads per row)
+#endif
 #ifndef MOE_WAVE_RT_DN
 #define MOE_WAVE_RT_DN 4   // 16-row tiles per wave, down (d % 64 == 0)
 #endif
@@ -1323,6 +1326,8 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         if (wave_dn || dense_dn) d.W0 = (const uint8_t*)w->down.tiles;
         int rc;
         if (dense_dn) rc = launch_dense<FMT, 1>(d, nslots, a.st);
+        else if (wave_dn && w->d % (16 * MOE_WAVE_RT_DN_WIDE) == 0)
+            rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN_WIDE, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else if (wave_dn) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
