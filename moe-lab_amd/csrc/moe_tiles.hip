@@ -1166,6 +1166,9 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 #ifndef MOE_WAVE_RT_DN_WIDE
 #define MOE_WAVE_RT_DN_WIDE 8   // 16-row tiles per wave, down, when d % 128 == 0 (fewer activation loads per row)
 #endif
+#ifndef MOE_WAVE_RT_DN_MID
+#define MOE_WAVE_RT_DN_MID 6    // next choice when d % 96 == 0 (gpt-oss, d = 2880); 0 = none
+#endif
 #ifndef MOE_WAVE_WIDE_MIN_WAVES
 #define MOE_WAVE_WIDE_MIN_WAVES 1024   // the wide down only when its grid still has this many waves (4 per CU):
 #endif                                 // a few shared experts' down (DSv2, 272 waves) ran 8% slower with it
@@ -1327,11 +1330,18 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             d.nidx = 3;
         }
         if (wave_dn || dense_dn) d.W0 = (const uint8_t*)w->down.tiles;
+        // more row tiles per down wave (fewer activation loads per weight row) where d allows and the grid
+        // keeps enough waves
+        auto wide_dn = [&](int rt) {
+            return rt > 0 && w->d % (16 * rt) == 0 &&
+                   (long)(w->d / (16 * rt)) * max_passes(nslots, w->E, 16 * nt) >= MOE_WAVE_WIDE_MIN_WAVES;
+        };
         int rc;
         if (dense_dn) rc = launch_dense<FMT, 1>(d, nslots, a.st);
-        else if (wave_dn && w->d % (16 * MOE_WAVE_RT_DN_WIDE) == 0 &&
-                 (long)(w->d / (16 * MOE_WAVE_RT_DN_WIDE)) * max_passes(nslots, w->E, 16 * nt) >= MOE_WAVE_WIDE_MIN_WAVES)
+        else if (wave_dn && wide_dn(MOE_WAVE_RT_DN_WIDE))
             rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN_WIDE, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
+        else if (MOE_WAVE_RT_DN_MID && wave_dn && wide_dn(MOE_WAVE_RT_DN_MID))
+            rc = launch_wave_tile<FMT, 1, (MOE_WAVE_RT_DN_MID ? MOE_WAVE_RT_DN_MID : 2), MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else if (wave_dn) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;

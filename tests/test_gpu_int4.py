@@ -387,6 +387,18 @@ MIXED_CASES = [
 ]
 
 
+@pytest.mark.parametrize("d,wave_rows", [(1728, 96), (2048, 128), (1472, 64)])
+def test_wave_down_row_tiles(d, wave_rows):
+    """The wave down takes 8 row tiles per wave where d % 128 == 0, 6 where d % 96 == 0, else 4 (each only while
+    its grid keeps >= 1024 waves: d / rows per wave x the pass list's bound of 72 at T=32, E=64, k=4)."""
+    assert (d // wave_rows) * (128 // 16 + 64) >= 1024 or wave_rows == 64
+    sh = shape_("wd", d, 256, 64, 4)
+    s = packed_state(sh, d)
+    x, idx, wts = inputs(sh, 32, "uniform", seed=d)
+    print(f"case wave-down d={d} rows/wave={wave_rows}", flush=True)
+    assert_close(grouped(s, x, idx, wts, out_dtype=torch.float32), oracle_y(s, x, idx, wts), what=("wave down", d))
+
+
 @pytest.mark.parametrize("case", MIXED_CASES, ids=lambda c: c[0])
 def test_wave_gate_up_dense_down(case, monkeypatch):
     """Mid loads: the wave tiles' gate/up writes h as fp16 with per-32-row exponents, the exponent pass makes
