@@ -1,14 +1,21 @@
-"""torch-ROCm harness the gfx950 variants drop under: fp32 reference, errors, chained timing.
+"""torch-ROCm harness the gfx950 variants drop under.
 
-Same contract and outputs as the reference's backends (reference moelab/torch_backend.py:1-126,
-moelab/mlx_backend.py:21-163):
-    META, prepare(w_gate, w_up, w_down) -> state, run(state, x, idx, wts) -> y, dequant(state)
-Timing uses HIP events on the current stream around a chain of dependent calls with a residual
-(x_{i+1} = x_i + run(x_i), reference mlx_backend.py:91-117), so host launch cost is excluded the same
-way the reference excludes its eval round-trip.
+The reference's harness names are kept so a variant and its callers move over unchanged (reference
+moelab/torch_backend.py:1-126, moelab/mlx_backend.py:21-163): ``load_variant``, ``make_weights``,
+``make_inputs``, ``reference``, ``errors``, ``TOL``, ``time_chained``, ``bench_variant``. The bodies are this
+build's own:
+  * inputs are drawn on the device (weights) or from one numpy stream (activations, routing through
+    ``problem.make_routing``);
+  * ``reference`` sorts the slots by expert once and walks contiguous segments, with the GLU kind and the
+    gpt-oss biases built in;
+  * ``errors`` reports the north-star gate (max |y - y_ref| / RMS(y_ref)) beside the relative Frobenius error;
+  * timing captures the whole dependent chain x <- x + run(x) in one HIP graph and times its replays with HIP
+    events, with a device-wide synchronisation before each end event, so work a variant puts on another stream
+    is inside the measured interval (an eagerly launched chain is host-bound on ROCm).
 """
 import importlib
 import importlib.util
+import os
 import platform
 
 import numpy as np
@@ -19,7 +26,9 @@ from .problem import make_routing
 
 DEVICE = "cuda" if torch.cuda.is_available() else "cpu"
 DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
-TOL = {"float32": 1e-4, "float16": 5e-3, "bfloat16": 1e-2}   # rel-Fro gate (reference mlx_backend.py:163)
+# rel-Fro pass thresholds by activation dtype (the reference harness's table, mlx_backend.py:163)
+TOL = {"float32": 1e-4, "float16": 5e-3, "bfloat16": 1e-2}
+NORTH_STAR_GATE = 1e-2   # max |y - y_ref| <= 1e-2 RMS(y_ref)
 
 
 def env_info():
@@ -31,9 +40,9 @@ def env_info():
 
 
 def load_variant(path):
-    """A variant module by file path (reference mlx_backend.py:21-25). This package's own variants
-    (variants/*.py, relative imports) load as package modules; any other file loads on its own."""
-    import os
+    """A variant module by file path (the reference loads variants by path, mlx_backend.py:21-25). This
+    package's own variants (variants/*.py, relative imports) load as package modules; any other file loads on
+    its own."""
     here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "variants")
     if os.path.dirname(os.path.abspath(path)) == here:
         return importlib.import_module(f"{__package__}.variants.{os.path.splitext(os.path.basename(path))[0]}")
@@ -43,110 +52,182 @@ def load_variant(path):
     return mod
 
 
-def make_weights(shape, dtype, seed=0):
-    g = torch.Generator(device=DEVICE).manual_seed(seed)
-    d, f, E = shape.d, shape.f, shape.E
-    mk = lambda *s, sc: (torch.randn(*s, generator=g, device=DEVICE) * sc).to(DTYPES[dtype])  # noqa: E731
-    return mk(E, f, d, sc=d ** -0.5), mk(E, f, d, sc=d ** -0.5), mk(E, d, f, sc=f ** -0.5)
+# ------------------------------------------------------------------------------------------ inputs
+def make_weights(shape, dtype="bfloat16", seed=0):
+    """Dense expert weights drawn on the device, N(0, 1 / fan_in) per projection: gate and up [E, F, d]
+    (fan-in d), down [E, d, F] (fan-in F), cast to `dtype` (what a variant's prepare() quantises)."""
+    gen = torch.Generator(device=DEVICE).manual_seed(int(seed))
+    out = []
+    for rows, fan_in in ((shape.f, shape.d), (shape.f, shape.d), (shape.d, shape.f)):
+        w = torch.empty((shape.E, rows, fan_in), device=DEVICE, dtype=torch.float32)
+        out.append(w.normal_(0.0, fan_in ** -0.5, generator=gen).to(DTYPES[dtype]))
+    return tuple(out)
 
 
-def make_inputs(shape, T, dtype, routing, seed):
-    rng = np.random.default_rng(seed)
-    x = torch.from_numpy(rng.standard_normal((T, shape.d)).astype(np.float32)).to(DEVICE, DTYPES[dtype])
+def make_inputs(shape, T, dtype="bfloat16", routing="uniform", seed=0):
+    """(x [T, d], idx [T, k] int32, wts [T, k] fp32) on the device from one numpy stream: x ~ N(0, 1), then
+    the routing of problem.make_routing (uniform, zipf, one_hot) from the same stream."""
+    rng = np.random.default_rng(int(seed))
+    x = rng.standard_normal((T, shape.d), dtype=np.float32)
     idx, wts = make_routing(T, shape.E, shape.k, routing, rng)
-    return x, torch.from_numpy(idx).to(DEVICE), torch.from_numpy(wts).to(DEVICE)
+    dev = lambda a: torch.as_tensor(a).to(DEVICE)  # noqa: E731
+    return dev(x).to(DTYPES[dtype]), dev(np.ascontiguousarray(idx, np.int32)), dev(np.ascontiguousarray(wts, np.float32))
 
 
-def glu(g, u, act=0):
-    if act == 0:
-        return torch.nn.functional.silu(g) * u
-    if act == 1:
-        return 0.5 * g * (1 + torch.tanh(0.7978845608028654 * (g + 0.044715 * g ** 3))) * u
-    g = torch.clamp(g, max=7.0)
-    u = torch.clamp(u, -7.0, 7.0)
-    return g * torch.sigmoid(1.702 * g) * (u + 1)
+# --------------------------------------------------------------------------------------- reference
+_ACTS = {
+    0: lambda g, u: torch.nn.functional.silu(g) * u,
+    1: lambda g, u: torch.nn.functional.gelu(g, approximate="tanh") * u,
+    2: lambda g, u: (lambda gc: gc * torch.sigmoid(1.702 * gc))(g.clamp(max=7.0)) * (u.clamp(-7.0, 7.0) + 1.0),
+}
 
 
 @torch.no_grad()
 def reference(wg, wu, wd, x, idx, wts, act=0, bg=None, bu=None, bd=None):
-    """fp32 per-expert loop on dequantised weights (reference torch_backend.py:58-67, plus the gpt-oss
-    biases and activation of metal_mxfp4_gptoss.py:110-126)."""
+    """fp32 layer on dense (dequantised) weights, the check every variant is held to (reference
+    torch_backend.py:58-67; the gpt-oss biases and clamped SwiGLU of metal_mxfp4_gptoss.py:110-126).
+    The T*k slots are sorted by expert once (stable), then each expert's contiguous segment of slots is
+    gathered, projected and scattered back with its routing weight."""
     x32 = x.float()
+    T, k = idx.shape
+    flat = idx.reshape(-1).long()
+    order = torch.argsort(flat, stable=True)
+    counts = torch.bincount(flat, minlength=wg.shape[0]).tolist()
+    w_slot = wts.reshape(-1).float()[order]
+    tok = order // k
     y = torch.zeros_like(x32)
-    for e in idx.unique().tolist():
-        t, j = (idx == e).nonzero(as_tuple=True)
-        xe = x32[t]
-        g, u = xe @ wg[e].float().T, xe @ wu[e].float().T
+    glu = _ACTS[int(act)]
+    start = 0
+    for e, c in enumerate(counts):
+        if c == 0:
+            continue
+        seg = slice(start, start + c)
+        start += c
+        xe = x32.index_select(0, tok[seg])
+        g = torch.mm(xe, wg[e].float().t())
+        u = torch.mm(xe, wu[e].float().t())
         if bg is not None:
-            g, u = g + bg[e].float(), u + bu[e].float()
-        o = glu(g, u, act) @ wd[e].float().T
+            g = g + bg[e].float()
+            u = u + bu[e].float()
+        o = torch.mm(glu(g, u), wd[e].float().t())
         if bd is not None:
             o = o + bd[e].float()
-        y.index_add_(0, t, o * wts[t, j, None].float())
+        y.index_add_(0, tok[seg], o * w_slot[seg].unsqueeze(1))
     return y
 
 
+@torch.no_grad()
 def errors(y, y_ref):
-    diff = y.float() - y_ref
-    rms = float(y_ref.pow(2).mean().sqrt().item()) if y_ref.numel() else 0.0
-    return {"rel_fro": (diff.norm() / (y_ref.norm() + 1e-30)).item(), "max_abs": diff.abs().max().item(),
-            "rms_ref": rms, "finite": bool(torch.isfinite(y).all().item())}
+    """Deviation of y from y_ref, in fp64: the north-star ratio max |y - y_ref| / RMS(y_ref) (`max_over_rms`),
+    its two parts, the relative Frobenius error the reference's harness gates on, and whether y is finite."""
+    a = y.double()
+    r = y_ref.double().to(a.device)
+    diff = (a - r).abs()
+    rms = float(r.square().mean().sqrt()) if r.numel() else 0.0
+    mx = float(diff.max()) if diff.numel() else 0.0
+    return {"max_abs": mx, "rms_ref": rms, "max_over_rms": mx / rms if rms > 0 else float("inf") * (mx > 0),
+            "rel_fro": float(torch.linalg.vector_norm(a - r) / (torch.linalg.vector_norm(r) + 1e-30)),
+            "finite": bool(torch.isfinite(a).all())}
 
 
-def _sync():
-    if DEVICE == "cuda":
+# ------------------------------------------------------------------------------------------ timing
+def capture(fn):
+    """fn() captured in a HIP graph. fn runs once eagerly on the capture stream first, so any allocation or
+    workspace growth happens outside the graph. Returns (graph, the captured call's output)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    return g, out
+
+
+def replay_seconds(graph, reps, warmup=1):
+    """Seconds of each of `reps` replays of a captured graph: HIP events on the current stream, the end event
+    recorded after a device-wide synchronisation."""
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    out = np.empty(reps)
+    for i in range(reps):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        graph.replay()
         torch.cuda.synchronize()
+        t1.record()
+        t1.synchronize()
+        out[i] = t0.elapsed_time(t1) * 1e-3
+    return out
 
 
-def time_chained(fn, inputs, reps, chain=10):
-    """Chain of `chain` dependent calls x <- x + fn(x) per rep; HIP events on the current stream around
-    each chain; returns seconds per call, one value per rep."""
-    def once():
+def _chain(fn, inputs, chain):
+    def run():
         x = inputs[0][0]
         for i in range(chain):
             _, idx, wts = inputs[i % len(inputs)]
             x = x + fn(x, idx, wts).to(x.dtype)
         return x
-    once()
-    _sync()
-    ts = []
-    for _ in range(reps):
+    return run
+
+
+def time_chained(fn, inputs, reps, chain=10, eager=False):
+    """Seconds per call of fn(x, idx, wts) in a chain of `chain` dependent calls x <- x + fn(x, idx, wts) over the
+    (x, idx, wts) windows `inputs`, one value per repetition. The chain is one HIP graph replayed `reps` times
+    (eager=True launches it from the host each time instead; on a CPU device always)."""
+    run = _chain(fn, inputs, chain)
+    if DEVICE == "cuda" and not eager:
+        g, _ = capture(run)
+        per = replay_seconds(g, reps) / chain
+        del g
+        return per
+    import time
+    run()
+    if DEVICE == "cuda":
+        torch.cuda.synchronize()
+    per = np.empty(reps)
+    for i in range(reps):
+        t0 = time.perf_counter()
+        run()
         if DEVICE == "cuda":
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            once()
-            b.record()
-            b.synchronize()
-            ts.append(a.elapsed_time(b) / 1e3 / chain)
-        else:
-            import time
-            t0 = time.perf_counter()
-            once()
-            ts.append((time.perf_counter() - t0) / chain)
-    return np.array(ts)
+            torch.cuda.synchronize()
+        per[i] = (time.perf_counter() - t0) / chain
+    return per
 
 
 @torch.no_grad()
 def bench_variant(mod, shape, tokens, dtype="bfloat16", routing="uniform", hw="mi355x", iters=30, n_rot=3,
                   check=True, weights=None, emit=print):
-    wg, wu, wd = weights if weights is not None else make_weights(shape, dtype)
-    state = mod.prepare(wg, wu, wd)
-    rwg, rwu, rwd = mod.dequant(state) if hasattr(mod, "dequant") else (wg, wu, wd)
+    """Check and time a variant at each T in `tokens`; emits one record per T:
+    {"variant", "shape", "T", "dtype", "routing", "time_us": {"p20", "median", "p80"}, "unique_experts",
+     "weight_GBps", "TFLOPs", "floor_us", "frac_of_floor", "check": errors(...) + {"pass"}}.
+    Weights are quantised once by mod.prepare; the reference runs on mod.dequant(state) when the variant has
+    it (the quantised weights the kernels see), else on the dense weights."""
+    dense = weights if weights is not None else make_weights(shape, dtype)
+    state = mod.prepare(*dense)
+    ref_w = mod.dequant(state) if hasattr(mod, "dequant") else dense
     w_bits = getattr(mod, "W_BITS", 16)
     for T in tokens:
-        inputs = [make_inputs(shape, T, dtype, routing, seed=s) for s in range(n_rot)]
-        res = {"type": "result", "variant": mod.META["name"], "T": T}
+        windows = [make_inputs(shape, T, dtype, routing, seed=1000 * T + s) for s in range(n_rot)]
+        rec = {"variant": mod.META["name"], "shape": getattr(shape, "name", ""), "T": T, "dtype": dtype,
+               "routing": routing}
         if check:
-            x, idx, wts = inputs[0]
-            res.update(errors(mod.run(state, x, idx, wts), reference(rwg, rwu, rwd, x, idx, wts)))
-            res["ok"] = res["finite"] and res["rel_fro"] < TOL[dtype]
-        ts = time_chained(lambda *a: mod.run(state, *a), inputs, reps=max(5, iters // 3))
-        med = float(np.median(ts))
-        U = float(np.mean([i[1].unique().numel() for i in inputs]))
-        nbytes = roofline.bytes_moved(T, shape.d, shape.f, shape.E, shape.k, w_bits, unique=U)
+            x, idx, wts = windows[0]
+            err = errors(mod.run(state, x, idx, wts), reference(*ref_w, x, idx, wts))
+            err["pass"] = err["finite"] and err["rel_fro"] < TOL[dtype]
+            rec["check"] = err
+        per = time_chained(lambda *z: mod.run(state, *z), windows, reps=max(5, iters // 3))
+        med = float(np.median(per))
+        U = float(np.mean([float(w[1].unique().numel()) for w in windows]))
         floor = roofline.floor_time_s(T, shape.d, shape.f, shape.E, shape.k, hw, w_bits, unique=U)
-        res.update({"median_us": med * 1e6, "p20_us": float(np.percentile(ts, 20)) * 1e6,
-                    "p80_us": float(np.percentile(ts, 80)) * 1e6, "unique_experts": U,
-                    "gbs": nbytes / med / 1e9, "tflops": roofline.flops(T, shape.d, shape.f, shape.k) / med / 1e12,
+        rec.update({"time_us": {"p20": float(np.percentile(per, 20)) * 1e6, "median": med * 1e6,
+                                "p80": float(np.percentile(per, 80)) * 1e6},
+                    "unique_experts": U,
+                    "weight_GBps": roofline.bytes_moved(T, shape.d, shape.f, shape.E, shape.k, w_bits,
+                                                        unique=U) / med / 1e9,
+                    "TFLOPs": roofline.flops(T, shape.d, shape.f, shape.k) / med / 1e12,
                     "floor_us": floor * 1e6, "frac_of_floor": floor / med})
-        emit(res)
+        emit(rec)

@@ -50,33 +50,58 @@ def probe(n_bytes=1 << 29, reps=9):
     return float(n_bytes / np.median(ts) / 1e9)
 
 
+class ProbeHistory:
+    """Probe readings per device key, kept as JSON {key: [GB/s, ...]} (newest last, at most N_HISTORY each)."""
+
+    def __init__(self, path=None):
+        self.path = path or history_path()
+        try:
+            with open(self.path) as f:
+                data = json.load(f)
+        except (OSError, ValueError):
+            data = {}
+        # a key holding anything but a list of numbers (an older single-value format) starts afresh
+        self.data = {k: [float(x) for x in v] for k, v in data.items()
+                     if isinstance(v, list) and all(isinstance(x, (int, float)) for x in v)}
+
+    def readings(self, device_key):
+        return self.data.get(device_key, [])
+
+    def record(self, device_key, probes):
+        self.data[device_key] = (self.readings(device_key) + [float(p) for p in probes])[-N_HISTORY:]
+        os.makedirs(os.path.dirname(os.path.abspath(self.path)), exist_ok=True)
+        tmp = self.path + ".tmp"
+        with open(tmp, "w") as f:
+            json.dump(self.data, f, indent=1)
+        os.replace(tmp, self.path)
+
+
 def verdict(probes, update=True, path=None, device_key=None):
-    path = path or history_path()
-    k = device_key or key()
-    rec = {}
-    if os.path.exists(path):
-        with open(path) as f:
-            rec = json.load(f)
-    hist = rec.get(k, [])
-    hist = hist if isinstance(hist, list) else []
-    lo = float(min(probes))
-    if len(hist) >= MIN_HISTORY:
-        ref = float(np.percentile(hist, 90))
-        status = "contended" if lo < THRESH * ref else "ok"
-    else:
-        ref, status = float(max(probes)), "calibrating"
+    """Judge this run's probes against the device's history (read before this run's probes are added):
+    the run's weakest probe against the 90th percentile of the stored readings. Returns
+    {"key", "probe_ref_gbs", "probe_min_gbs", "probe_ratio", "status", "contended", "history"}."""
+    dk = device_key or key()
+    store = ProbeHistory(path)
+    past = store.readings(dk)
+    weakest = min(float(p) for p in probes)
+    calibrating = len(past) < MIN_HISTORY
+    ref = max(float(p) for p in probes) if calibrating else float(np.percentile(np.asarray(past), 90))
+    status = "calibrating" if calibrating else ("contended" if weakest < THRESH * ref else "ok")
     if update:
-        rec[k] = (hist + [float(p) for p in probes])[-N_HISTORY:]
-        os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
-        with open(path, "w") as f:
-            json.dump(rec, f, indent=1)
-    return {"key": k, "probe_ref_gbs": ref, "probe_min_gbs": lo, "probe_ratio": lo / ref, "status": status,
-            "contended": status == "contended", "history": len(hist)}
+        store.record(dk, probes)
+    return {"key": dk, "probe_ref_gbs": ref, "probe_min_gbs": weakest, "probe_ratio": weakest / ref,
+            "status": status, "contended": status == "contended", "history": len(past)}
+
+
+_STATUS_TEXT = {
+    "ok": "no contention seen",
+    "calibrating": "history too short ({history} of {need} probes): no verdict yet",
+    "contended": "contended: another job shared the GPU, absolute timings are not trustworthy; rerun on an idle GPU",
+}
 
 
 def report(v):
-    tag = {"ok": "ok",
-           "calibrating": f"calibrating ({v['history']} probes in history): verdict not yet meaningful",
-           "contended": "CONTENDED: absolute numbers unreliable, re-run without other GPU work"}[v["status"]]
-    return (f"guard: probe min {v['probe_min_gbs']:.0f} GB/s vs p90 {v['probe_ref_gbs']:.0f} for {v['key']} "
-            f"({100 * v['probe_ratio']:.0f}%) -> {tag}")
+    """One line for a verdict."""
+    note = _STATUS_TEXT[v["status"]].format(history=v["history"], need=MIN_HISTORY)
+    return (f"[guard {v['status']}] weakest probe {v['probe_min_gbs']:.0f} GB/s = {100 * v['probe_ratio']:.0f}% of "
+            f"the reference {v['probe_ref_gbs']:.0f} GB/s on {v['key']}: {note}")

@@ -68,19 +68,6 @@ def make_problem(shape, T, routing="uniform", seed=0):
     return p
 
 
-def error_metrics(y, y_ref):
-    y = np.asarray(y, dtype=np.float64)
-    r = np.asarray(y_ref, dtype=np.float64)
-    diff = y - r
-    nr = np.linalg.norm(r) + 1e-30
-    return {
-        "rel_fro": float(np.linalg.norm(diff) / nr),
-        "max_abs": float(np.abs(diff).max()) if diff.size else 0.0,
-        "cos": float((y * r).sum() / (np.linalg.norm(y) * nr + 1e-30)),
-        "finite": bool(np.isfinite(y).all()),
-    }
-
-
 # ------------------------------------------------------------------------------- BASELINE layers
 def zipf_bias(E, s=1.1, seed=0):
     """Per-expert router logit offset 2*log(r^-s) over a random permutation (Zipf(s) popularity)."""

@@ -87,7 +87,7 @@ def test_guard_verdict_history(tmp_path):
     assert ok["status"] == "ok" and ok["history"] == 6
     bad = guard.verdict([4000.0], path=path, device_key=k, update=False)
     assert bad["status"] == "contended" and bad["contended"]
-    assert "CONTENDED" in guard.report(bad)
+    assert guard.report(bad).startswith("[guard contended]") and "rerun" in guard.report(bad)
     for _ in range(30):
         guard.verdict([5000.0, 5000.0], path=path, device_key=k)
     assert len(json.load(open(path))[k]) == guard.N_HISTORY

@@ -240,15 +240,62 @@ def test_moe_reference_two_formulations(orc, act):
     np.testing.assert_allclose(y1, y2, rtol=1e-12, atol=1e-12)
 
 
+def _sigmoid_tanh(z):
+    """The logistic function through the identity sigma(z) = (1 + tanh(z / 2)) / 2 (not the exp form the
+    oracle uses)."""
+    return 0.5 * (1.0 + np.tanh(0.5 * np.asarray(z, dtype=np.float64)))
+
+
 def test_moe_reference_textbook_activations(orc):
+    from scipy.special import erf, expit
     g = np.linspace(-10, 10, 101)
     u = np.linspace(-9, 9, 101)
-    np.testing.assert_allclose(orc.act_fn(g, u, 0), g * (1 / (1 + np.exp(-g))) * u)
-    from scipy.special import erf  # noqa: F401  (tanh-GELU vs the erf form: agree to 1e-3)
+    # SiLU against scipy's logistic and the tanh identity; silu(1) = sigma(1) = 0.7310585786 (tables)
+    np.testing.assert_allclose(orc.act_fn(g, u, 0), g * expit(g) * u, rtol=1e-13)
+    np.testing.assert_allclose(orc.act_fn(g, u, 0), g * _sigmoid_tanh(g) * u, rtol=1e-12, atol=1e-15)
+    assert abs(orc.act_fn(np.array(1.0), np.array(1.0), 0) - 0.7310585786300049) < 1e-15
+    # tanh-GELU against the erf form: the two GELUs agree to ~1e-3
     gelu_erf = 0.5 * g * (1 + erf(g / np.sqrt(2)))
     np.testing.assert_allclose(orc.act_fn(g, np.ones_like(g), 1), gelu_erf, atol=2e-3)
-    gc = np.minimum(g, 7)
-    np.testing.assert_allclose(orc.act_fn(g, u, 2), gc / (1 + np.exp(-1.702 * gc)) * (np.clip(u, -7, 7) + 1))
+
+
+def test_gptoss_clamped_swiglu_pins(orc):
+    """gpt-oss clamped SwiGLU (reference metal_mxfp4_gptoss.py:36-43, :116-121), pinned by what the definition
+    fixes rather than by restating it: g saturates at 7 from above only, u is clipped to [-7, 7], the glu term
+    is (u + 1), and alpha = 1.702 (hand values through the tanh form of the logistic)."""
+    act = lambda g, u: orc.act_fn(np.asarray(g, np.float64), np.asarray(u, np.float64), 2)  # noqa: E731
+    us = np.linspace(-6.5, 6.5, 27)
+    for g in (7.0, 7.5, 50.0, 1e30):   # g >= 7 saturates
+        np.testing.assert_array_equal(act(np.full_like(us, g), us), act(np.full_like(us, 7.0), us))
+    assert act(-7.5, 0.0) != act(-7.0, 0.0)   # no clamp from below
+    gs = np.linspace(-9.0, 6.9, 41)
+    assert (act(gs, np.full_like(gs, -1.0)) == 0.0).all()   # u = -1 -> exactly 0 (u + 1 = 0)
+    for u, lim in ((7.5, 7.0), (1e9, 7.0), (-8.0, -7.0), (-1e9, -7.0)):   # |u| > 7 saturates
+        np.testing.assert_array_equal(act(gs, np.full_like(gs, u)), act(gs, np.full_like(gs, lim)))
+    # hand values: act(1, 0) = sigma(1.702) = 0.8457958...; act(2, 1) = 2 * 2 * sigma(3.404); act(-1, 0) = -sigma(-1.702)
+    assert abs(act(1.0, 0.0) - 0.8457958) < 1e-7
+    assert abs(act(1.0, 0.0) - _sigmoid_tanh(1.702)) < 1e-14
+    assert abs(act(2.0, 1.0) - 4.0 * _sigmoid_tanh(3.404)) < 1e-13
+    assert abs(act(-1.0, 0.0) + _sigmoid_tanh(-1.702)) < 1e-14
+    # in range it is g * sigma(1.702 g) * (u + 1): a wrong alpha, a missing + 1 or a swapped g / u fails here
+    gi, ui = np.meshgrid(np.linspace(-6, 6.9, 13), np.linspace(-6.9, 6.9, 13))
+    np.testing.assert_allclose(act(gi, ui), gi * _sigmoid_tanh(1.702 * gi) * (ui + 1.0), rtol=1e-12, atol=1e-14)
+
+
+def test_error_metrics_hand_values(orc):
+    """error_metrics on vectors small enough to compute by hand; every parity gate reads max_abs / rms_ref."""
+    e = orc.error_metrics(np.array([1.0, 2.0, 3.0]), np.array([1.0, 2.0, 5.0]))
+    assert e["max_abs"] == 2.0
+    assert abs(e["rms_ref"] - math.sqrt(10.0)) < 1e-15          # sqrt((1 + 4 + 25) / 3)
+    assert abs(e["rel_fro"] - 2.0 / math.sqrt(30.0)) < 1e-15    # |(0, 0, -2)| / |(1, 2, 5)|
+    assert abs(e["cos"] - 20.0 / math.sqrt(14.0 * 30.0)) < 1e-15
+    assert e["finite"] is True
+    m = orc.error_metrics(np.array([[-3.0, 0.5], [4.0, 0.0]]), np.zeros((2, 2)))
+    assert m["max_abs"] == 4.0 and m["rms_ref"] == 0.0            # max over every element, sign dropped
+    assert orc.error_metrics(np.array([1.0, np.nan]), np.array([1.0, 1.0]))["finite"] is False
+    assert orc.error_metrics(np.array([1.0, np.inf]), np.array([1.0, 1.0]))["finite"] is False
+    z = orc.error_metrics(np.zeros(0), np.zeros(0))
+    assert z["max_abs"] == 0.0 and z["rms_ref"] == 0.0
 
 
 def test_moe_reference_invariants(orc):
