@@ -91,10 +91,17 @@ size_t moe_row_bytes(int fmt, int K);
  *         MOE_FMT_MXFP4:    16s + g, 16s + 4 + g, 16s + 8 + g, 16s + 12 + g
  *     each with its nibbles (codes e0 .. e7, low nibble first) stored as e0 e2 e4 e6 e1 e3 e5 e7
  *     then the metadata of the slice's groups, per row r:
- *         MOE_FMT_INT4_G64: 8 bytes at 1024 + 8r = group words 2s, 2s + 1   (record: 1152 bytes)
+ *         MOE_FMT_INT4_G64: 8 bytes at 1024 + 8r = group words 2s, 2s + 1, each (scale, bias) times 2^-X
+ *                           (bf16, exact), X the row's exponent below   (record: 1152 bytes)
  *         MOE_FMT_MXFP4:    4 bytes at 1024 + 4r = E8M0 bytes of groups 4s .. 4s + 3   (record: 1088 bytes)
  *     words and groups past K (K % 128 == 64) are zero.
- * moe_tile_bytes: bytes of one expert's N x K projection in this layout (0 if N % 16, K % 64 or fmt invalid).
+ *   int4 only, after the records of all E experts: row exponents int8 [E][N]. X = (biased exponent of the row's
+ *     largest bf16 |scale| or |bias|) - 137, i.e. floor(log2 of it) - 10, clamped to [-120, 120]; 0 for an
+ *     all-zero row or one holding an inf or NaN. The scaled metadata puts every row's largest at [2^10, 2^11), so
+ *     the kernels that dequantise to fp16 keep any absolute scale range (scales of 1e-8 or 1e30 alike); the tile
+ *     kernels multiply each row's sums by 2^X.
+ * moe_tile_bytes: bytes per expert of an N x K projection in this layout (int4: records + N exponent bytes;
+ *                 0 if N % 16, K % 64 or fmt invalid).
  * moe_tiles_pack: rows [E, N, moe_row_bytes(fmt, K)] -> tiles [E * moe_tile_bytes(fmt, N, K)], on `stream`.
  */
 size_t moe_tile_bytes(int fmt, int N, int K);
@@ -150,9 +157,11 @@ int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offset
  *   run_slots / NORED, metal_q4_moe.py:49-51; per-slot path only, residual must be NULL).
  *   Accumulation in fp32; the GLU output h is kept between the two launches as an unevaluated sum of two
  *   bf16 planes (about 16 significant bits, where the reference kernels store it in x.dtype). Exception: int4
- *   grouped calls with more than 32 slots per expert on average (prefill-sized T, path MOE_PATH_GROUPED with
- *   the tile-major copies) run on fp16 MFMA: weights rounded once to fp16, x and h carried as fp16 with a
- *   power-of-two exponent per row (no overflow); ~1e-3 of the outputs' RMS in the worst case measured.
+ *   grouped calls with more than 16 slots per expert on average (prefill-sized T, path MOE_PATH_GROUPED with
+ *   the tile-major copies) run the down projection, and above 32 also the gate/up, on fp16 MFMA: weights
+ *   rounded once to fp16 from the row-exponent-scaled metadata, x and h carried as fp16 with a power-of-two
+ *   exponent per row (no overflow for large rows, no flush to zero for small ones; any scale range); ~1e-3 of
+ *   the outputs' RMS in the worst case measured.
  *   Requirements: d % 64 == 0, F % 64 == 0, F <= 16384; x, y, rows 16-byte aligned.
  *   workspace: moe_experts_workspace_bytes(...) bytes. Its first MOE_WORKSPACE_SYNC_BYTES bytes hold the
  *   fused T == 1 kernel's completion counters: zero them once when the workspace is allocated; every call

@@ -90,7 +90,8 @@ size_t moe_tile_bytes(int fmt, int N, int K) {
 
 int moe_tiles_pack(int fmt, int E, int N, int K, const void* rows, void* tiles, void* stream) {
     if (fmt != MOE_FMT_INT4_G64 && fmt != MOE_FMT_MXFP4) return MOE_ERR_DTYPE;
-    if (E < 1 || N < 16 || N % 16 || K < 64 || K % 64 || N > 65535 * 16 || E > 65535) return MOE_ERR_ARG;
+    if (E < 1 || N < 16 || N % 16 || K < 64 || K % 64 || N > 65535 * 16 || E > 65535 || (long)E * N > 0x7FFFFFFFL)
+        return MOE_ERR_ARG;
     if (!rows || !tiles) return MOE_ERR_ARG;
     if (!aligned16(rows) || !aligned16(tiles)) return MOE_ERR_ALIGN;
     return moe::launch_pack_tiles(fmt, E, N, K, rows, tiles, (hipStream_t)stream);

@@ -22,9 +22,30 @@ __host__ __device__ __forceinline__ size_t rbytes(int fmt, int K) {
 // tile-major slice records (include/moe_mi355x.h: moe_tile_bytes): 16 rows x 128 inputs of codes + metadata
 constexpr int TILE_SLICE_INT4 = 1024 + 16 * 8;
 constexpr int TILE_SLICE_MXFP4 = 1024 + 16 * 4;
-__host__ __device__ __forceinline__ size_t tile_bytes(int fmt, int N, int K) {
+// one expert's slice records
+__host__ __device__ __forceinline__ size_t tile_rec_bytes(int fmt, int N, int K) {
     const size_t sb = fmt == MOE_FMT_INT4_G64 ? TILE_SLICE_INT4 : TILE_SLICE_MXFP4;
     return (size_t)(N / 16) * (size_t)((K + 127) / 128) * sb;
+}
+// per expert: its records, plus (int4) one row-exponent byte per row; the exponent bytes of all E experts follow
+// the records of all E experts
+__host__ __device__ __forceinline__ size_t tile_bytes(int fmt, int N, int K) {
+    return tile_rec_bytes(fmt, N, K) + (fmt == MOE_FMT_INT4_G64 ? (size_t)N : 0);
+}
+// int4 tile copies: the row exponents int8 [E, N] of projection base `tiles` (E experts)
+__host__ __device__ __forceinline__ const int8_t* tile_row_exps(const uint8_t* tiles, int E, int N, int K) {
+    return reinterpret_cast<const int8_t*>(tiles + (size_t)E * tile_rec_bytes(MOE_FMT_INT4_G64, N, K));
+}
+// Row exponent of an int4 row from amax, the largest bf16 magnitude bits (sign cleared) over the row's scales and
+// biases: the records hold s 2^-E and b 2^-E (exact in bf16), which puts the row's largest at [2^10, 2^11), so
+// every w = s q + b of the row stays below 2^15 in magnitude and values down to 2^-24 of the row's largest stay
+// normal fp16 numbers where the dense tiles dequantise to fp16. E = (biased exponent of amax) - 127 - 10, clamped to
+// [-120, 120] (bf16 subnormals: -120); 0 for an all-zero row or one holding an inf or NaN.
+__host__ __device__ __forceinline__ int int4_row_exponent(uint32_t amax) {
+    const int ef = (int)(amax >> 7);
+    if (amax == 0 || ef >= 0xFF) return 0;
+    const int e = ef - 137;
+    return e < -120 ? -120 : (e > 120 ? 120 : e);
 }
 
 // ============================================================================ packed row formats

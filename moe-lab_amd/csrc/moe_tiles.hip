@@ -39,10 +39,20 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2x __attribute__((ext_vector_type(2)));
 
-// power-of-two exponent e that keeps v 2^-e inside fp16 for |v| <= amax: 0 while amax < 2^15, else
-// floor(log2(amax)) - 14 (then amax 2^-e < 2^15; inf gives 114, and NaN, which fails the test, 0)
+// Power-of-two exponent e with which the int4 dense tiles store a row (x16: a token's x; h16: a slot's 32-row chunk
+// of h) of largest magnitude amax as fp16 v 2^-e: 0 while 2^-8 <= amax < 2^15 (fp16's subnormal rounding, 2^-25,
+// then stays below 2^-17 of the row's largest), else floor(log2 amax) - 14, which puts the largest at [2^14, 2^15)
+// (large rows: no overflow; small rows: no flush to zero), clamped to [-127, 127]. An all-zero row gives
+// H16_ZERO_EXP, which never wins a slot's maximum (its values are 0 under any scaling); NaN gives 0.
+constexpr int H16_ZERO_EXP = -128;
 __device__ __forceinline__ int h16_exponent(float amax) {
-    return amax >= 32768.f ? (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 141 : 0;
+    if (amax == 0.f) return H16_ZERO_EXP;
+    if (!(amax < 32768.f && amax >= 0.00390625f)) {
+        if (amax != amax) return 0;
+        const int e = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 141;
+        return e < -127 ? -127 : (e > 127 ? 127 : e);
+    }
+    return 0;
 }
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -508,6 +518,15 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
                     }
                 }
         };
+        // int4: the records hold each row's scales and biases times 2^-E (E per row, moe_tiles_pack), so the
+        // sums come back by 2^E in the epilogue; the lane's exponents are loaded before the ring starts
+        int rex[NPROJ][RT];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                rex[p][rt] = INT4 ? tile_row_exps(p ? a.W1 : a.W0, a.E, N, K)[(size_t)e * N + r0 + 16 * rt + lr] : 0;
+        __builtin_amdgcn_sched_barrier(0);
         // ring: slices s0 .. s0 + D - 1 in flight at the top of each step. The walk is rounded up to a multiple
         // of D: slices past the last re-load the last one (cache hits) and fold with scale 0, so the loop body
         // has no branch. Issued slice by slice in the steady state's order, so the vmcnt waits at the loop top
@@ -527,9 +546,19 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
                 issue(sn < nsl ? sn : nsl - 1, rq[i], rm[i], rx[i]);
             }
         }
+        if constexpr (INT4) {
+#pragma unroll
+            for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[p][rt][t][v] = __builtin_ldexpf(acc[p][rt][t][v], rex[p][rt]);
+        }
         // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
         if constexpr (H16O) {
-            uint8_t* hexp_out = reinterpret_cast<uint8_t*>(a.hout2);
+            int8_t* hexp_out = reinterpret_cast<int8_t*>(a.hout2);
             const int nch = N >> 5;
 #pragma unroll
             for (int t = 0; t < NT; ++t)
@@ -557,7 +586,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
                     if (tok0 + 16 * t + j >= n) continue;
 #pragma unroll
                     for (int c = 0; c < RT / 2; ++c)
-                        if (lr == 0) hexp_out[(size_t)slot * nch + (r0 >> 5) + c] = (uint8_t)ex[c];
+                        if (lr == 0) hexp_out[(size_t)slot * nch + (r0 >> 5) + c] = (int8_t)ex[c];
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) {
                         const _Float16 h16 = (_Float16)__builtin_ldexpf(hv[rt], -ex[rt >> 1]);
@@ -879,6 +908,13 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                 }
             }
         };
+        // int4: row exponents of the lane's rows (the records hold s 2^-E, b 2^-E; the epilogue scales by 2^E)
+        int rex[NPROJ][RT];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                rex[p][rt] = INT4 && wvalid ? tile_row_exps(p ? a.W1 : a.W0, a.E, N, K)[(size_t)e * N + r0 + 16 * rt + lr] : 0;
         // slice s sits in buffer / ring slot s & 1; slice s + 1 is fetched during slice s (the last slice fetches
         // itself again into the idle slot: no branch around the loads)
         auto run = [&](auto full) __attribute__((always_inline)) {
@@ -916,7 +952,7 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) xe[t][v] = __shfl(eslot, 16 * t + 4 * lg + v, 64);
-            uint8_t* hexp_out = reinterpret_cast<uint8_t*>(a.hout2);
+            int8_t* hexp_out = reinterpret_cast<int8_t*>(a.hout2);
             const int nch = N >> 5;
 #pragma unroll
             for (int t = 0; t < NT; ++t)
@@ -926,7 +962,8 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) {
                         const int r = r0 + 16 * rt + lr;
-                        float g = __builtin_ldexpf(acc[0][rt][t][v], xe[t][v]), up = __builtin_ldexpf(acc[1][rt][t][v], xe[t][v]);
+                        float g = __builtin_ldexpf(acc[0][rt][t][v], xe[t][v] + rex[0][rt]);
+                        float up = __builtin_ldexpf(acc[1][rt][t][v], xe[t][v] + rex[1][rt]);
                         if (wvalid && a.b0) g += a.b0[(size_t)e * N + r];
                         if (wvalid && a.b1) up += a.b1[(size_t)e * N + r];
                         hv[t][v][rt] = wvalid ? glu_act(a.act, g, up) : 0.f;
@@ -938,7 +975,7 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                     const int jt = 16 * t + 4 * lg + v;
                     if (jt >= nlive || !wvalid) continue;
                     const int slot = sSlot[jt];
-                    if (lr == 0) hexp_out[(size_t)slot * nch + (r0 >> 5)] = (uint8_t)ex;
+                    if (lr == 0) hexp_out[(size_t)slot * nch + (r0 >> 5)] = (int8_t)ex;
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) {
                         const _Float16 h16 = (_Float16)__builtin_ldexpf(hv[t][v][rt], -ex);
@@ -971,7 +1008,7 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                             a.hout[(size_t)slot * N + r] = hi;
                             a.hout2[(size_t)slot * N + r] = f32_to_bf16(hv - bf16_to_f32(hi));
                         } else if (H16) {
-                            a.yp[ks * a.plane + (size_t)slot * N + r] = __builtin_ldexpf(acc[0][rt][t][v], es[t][v]);
+                            a.yp[ks * a.plane + (size_t)slot * N + r] = __builtin_ldexpf(acc[0][rt][t][v], es[t][v] + rex[0][rt]);
                         } else {
                             a.yp[ks * a.plane + (size_t)slot * N + r] = acc[0][rt][t][v];
                         }
@@ -1026,30 +1063,41 @@ __global__ void __launch_bounds__(256) k_x16(const uint16_t* __restrict__ x, uin
 }
 
 // int4 grouped path, between gate/up and a dense down: one block per slot. The gate/up wrote h16 = h 2^-e with e
-// per (slot, 32-row chunk); this brings the slot's row to one exponent E = max e (chunks with a smaller e are
-// scaled by 2^(e - E): exact unless a value falls into fp16's subnormal range, where it is rounded) and writes
-// E for the down projection's epilogue. A slot whose exponents are all 0 (|h| < 2^15 on the whole row, the
-// usual case) costs two exponent loads per thread.
-__global__ void __launch_bounds__(256) k_h16_fix(const uint8_t* __restrict__ hexp, uint16_t* __restrict__ h16,
+// per (slot, 32-row chunk) (h16_exponent); this brings the slot's row to one exponent E = max e (chunks with a
+// smaller e are scaled by 2^(e - E): exact unless a value falls into fp16's subnormal range, where it is rounded:
+// it is then below 2^-24 of the slot's largest) and writes E for the down projection's epilogue. All-zero chunks
+// (H16_ZERO_EXP) take no part. A slot whose chunks share one exponent (the usual case: all 0) costs two exponent
+// loads per thread.
+__global__ void __launch_bounds__(256) k_h16_fix(const int8_t* __restrict__ hexp, uint16_t* __restrict__ h16,
                                                  int32_t* __restrict__ eslot, int F) {
     __shared__ int sE[512];   // F <= 16384: at most 512 chunks of 32
-    __shared__ int sMax[4];
+    __shared__ int sMax[4], sMin[4];
     const int slot = blockIdx.x, tid = threadIdx.x, nch = F >> 5;
-    const uint8_t* er = hexp + (size_t)slot * nch;
-    const int e0 = tid < nch ? er[tid] : 0, e1 = tid + 256 < nch ? er[tid + 256] : 0;
+    const int8_t* er = hexp + (size_t)slot * nch;
+    const int e0 = tid < nch ? er[tid] : H16_ZERO_EXP, e1 = tid + 256 < nch ? er[tid + 256] : H16_ZERO_EXP;
     sE[tid] = e0;
     sE[tid + 256] = e1;
     int m = e0 > e1 ? e0 : e1;
+    const int n0 = e0 == H16_ZERO_EXP ? 127 : e0, n1 = e1 == H16_ZERO_EXP ? 127 : e1;
+    int mn = n0 < n1 ? n0 : n1;
     for (int o = 32; o; o >>= 1) {
-        const int other = __shfl_xor(m, o, 64);
+        const int other = __shfl_xor(m, o, 64), omn = __shfl_xor(mn, o, 64);
         m = other > m ? other : m;
+        mn = omn < mn ? omn : mn;
     }
-    if ((tid & 63) == 0) sMax[tid >> 6] = m;
+    if ((tid & 63) == 0) {
+        sMax[tid >> 6] = m;
+        sMin[tid >> 6] = mn;
+    }
     __syncthreads();
     int E = sMax[0];
-    for (int w = 1; w < 4; ++w) E = sMax[w] > E ? sMax[w] : E;
-    if (tid == 0) eslot[slot] = E;
-    if (E == 0) return;   // block-uniform
+    mn = sMin[0];
+    for (int w = 1; w < 4; ++w) {
+        E = sMax[w] > E ? sMax[w] : E;
+        mn = sMin[w] < mn ? sMin[w] : mn;
+    }
+    if (tid == 0) eslot[slot] = E == H16_ZERO_EXP ? 0 : E;
+    if (mn >= E) return;   // block-uniform: every chunk with a non-zero value is at E already (or none has one)
     // 16-byte pieces (8 values; 4 per chunk) of the row: every load first, then the rewrites
     constexpr int CPT = 8;   // pieces per thread per round (F <= 16384: 2048 pieces, one round)
     uint4* row = reinterpret_cast<uint4*>(h16 + (size_t)slot * F);
@@ -1065,8 +1113,9 @@ __global__ void __launch_bounds__(256) k_h16_fix(const uint8_t* __restrict__ hex
         for (int i = 0; i < CPT; ++i) {
             const int c = c0 + i * 256 + tid;
             if (c >= np) continue;
-            const int d = sE[c >> 2] - E;
-            if (d == 0) continue;
+            const int ec = sE[c >> 2];
+            if (ec == E || ec == H16_ZERO_EXP) continue;
+            const int d = ec - E;
             uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -1092,7 +1141,30 @@ __device__ __forceinline__ uint32_t interleave_nibbles(uint32_t w) {
     return squeeze(w & 0x0F0F0F0Fu) | (squeeze((w >> 4) & 0x0F0F0F0Fu) << 16);
 }
 
-// rows [E, N, rbytes] -> tiles [E, N/16, ceil(K/128), slice record]; grid (slices, N/16, E), 64 lanes
+// int4 tile copies, before k_pack_tiles: the row exponent (int4_row_exponent) of each of the E * N rows, from the
+// row's largest |scale| or |bias| over all its groups, into the exponent bytes after the records. One lane per row.
+__global__ void __launch_bounds__(256) k_row_exp(const uint8_t* __restrict__ rows, int8_t* __restrict__ rexp,
+                                                 int nrows, int K) {
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= nrows) return;
+    const uint32_t* m = reinterpret_cast<const uint32_t*>(rows + (size_t)r * rbytes(MOE_FMT_INT4_G64, K) + (K >> 1));
+    uint32_t amax = 0;   // bf16 magnitude bits: ordered as the magnitudes (NaN above inf)
+    for (int g = 0; g < (K >> 6); ++g) {
+        const uint32_t w = m[g], lo = w & 0x7FFFu, hi = (w >> 16) & 0x7FFFu;
+        amax = lo > amax ? lo : amax;
+        amax = hi > amax ? hi : amax;
+    }
+    rexp[r] = (int8_t)int4_row_exponent(amax);
+}
+
+// bf16 pair word (low, high) -> both halves times 2^-e, rounded to bf16 (exact for normal results)
+__device__ __forceinline__ uint32_t scale_bf16_pair(uint32_t w, int e) {
+    return (uint32_t)f32_to_bf16(__builtin_ldexpf(bf16lo(w), -e)) |
+           ((uint32_t)f32_to_bf16(__builtin_ldexpf(bf16hi(w), -e)) << 16);
+}
+
+// rows [E, N, rbytes] -> tiles [E, N/16, ceil(K/128), slice record]; grid (slices, N/16, E), 64 lanes.
+// int4: the metadata words go in as (s 2^-E, b 2^-E) with E the row's exponent (k_row_exp, run first)
 template <class FMT>
 __global__ void __launch_bounds__(64) k_pack_tiles(const uint8_t* __restrict__ rows, uint8_t* __restrict__ tiles,
                                                    int N, int K) {
@@ -1113,10 +1185,12 @@ __global__ void __launch_bounds__(64) k_pack_tiles(const uint8_t* __restrict__ r
     }
     *reinterpret_cast<uint4*>(rec + 16 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
     if (g == 0) {
-        if (FMT::XSUM) {   // group words 2s, 2s + 1
+        if (FMT::XSUM) {   // group words 2s, 2s + 1, scaled by the row's exponent
             const int ng = K >> 6;
             const uint32_t* mw = reinterpret_cast<const uint32_t*>(row + (K >> 1));
-            const uint32_t m0 = 2 * s < ng ? mw[2 * s] : 0u, m1 = 2 * s + 1 < ng ? mw[2 * s + 1] : 0u;
+            const int er = tile_row_exps(tiles, gridDim.z, N, K)[(size_t)e * N + 16 * tile + r];
+            const uint32_t m0 = 2 * s < ng ? scale_bf16_pair(mw[2 * s], er) : 0u;
+            const uint32_t m1 = 2 * s + 1 < ng ? scale_bf16_pair(mw[2 * s + 1], er) : 0u;
             *reinterpret_cast<uint2*>(rec + 1024 + 8 * r) = make_uint2(m0, m1);
         } else {           // E8M0 bytes of groups 4s .. 4s + 3
             const int ng = K >> 5;
@@ -1308,7 +1382,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         else if (wave_gu) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st);
         else rc = launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
         if (!rc && h16) {
-            k_h16_fix<<<nslots, 256, 0, a.st>>>((const uint8_t*)a.hlo, a.hhi,
+            k_h16_fix<<<nslots, 256, 0, a.st>>>((const int8_t*)a.hlo, a.hhi,
                                               (int32_t*)((uint8_t*)a.hlo + t.eslot_off), w->F);
             rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
         }
@@ -1359,9 +1433,13 @@ int run_experts_tiles(const ExpertsArgs& a) {
 
 int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tiles, hipStream_t st) {
     dim3 grid((K + 127) / 128, N / 16, E);
-    if (fmt == MOE_FMT_INT4_G64)
+    if (fmt == MOE_FMT_INT4_G64) {
+        const int nrows = E * N;
+        k_row_exp<<<(nrows + 255) / 256, 256, 0, st>>>(
+            (const uint8_t*)rows, (int8_t*)tile_row_exps((const uint8_t*)tiles, E, N, K), nrows, K);
+        if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
         k_pack_tiles<FmtInt4><<<grid, 64, 0, st>>>((const uint8_t*)rows, (uint8_t*)tiles, N, K);
-    else
+    } else
         k_pack_tiles<FmtMxfp4><<<grid, 64, 0, st>>>((const uint8_t*)rows, (uint8_t*)tiles, N, K);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }

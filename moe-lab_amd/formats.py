@@ -101,15 +101,36 @@ def interleave_nibbles(w):
     return torch.where(out >= 2 ** 31, out - 2 ** 32, out).to(torch.int32)
 
 
+def int4_row_exponents(scales, biases):
+    """Row exponents of the int4 tile copies (include/moe_mi355x.h): amax = the largest bf16 magnitude over the
+    row's scales and biases (bf16 [..., N, K/64] each); E = (biased exponent of amax) - 137, i.e. floor(log2
+    amax) - 10, clamped to [-120, 120]; 0 for an all-zero row or one holding an inf or NaN. The records hold s 2^-E
+    and b 2^-E, putting the row's largest at [2^10, 2^11)."""
+    mag = lambda t: (t.contiguous().view(torch.int16).to(torch.int32) & 0x7FFF)  # noqa: E731
+    amax = torch.maximum(mag(scales).amax(-1), mag(biases).amax(-1))
+    ef = amax >> 7
+    e = (ef - 137).clamp(-120, 120)
+    return torch.where((amax == 0) | (ef >= 0xFF), torch.zeros_like(e), e)
+
+
 def pack_tiles_ref(fmt, rows, K):
     """Host restatement of moe_tiles_pack: uint8 row records [E, N, row_bytes] -> uint8 [E * tile bytes].
-    Test-side only (the library packs on the device); a plain loop over the documented layout."""
+    Test-side only (the library packs on the device); a plain loop over the documented layout. int4: the
+    metadata words go in scaled by each row's 2^-E, and the E * N exponent bytes follow all the records."""
     rows = rows.cpu()
     E, N, _ = rows.shape
     S = (K + 127) // 128
     sb = TILE_SLICE_BYTES[fmt]
     words = rows[..., :K // 2].contiguous().view(torch.int32).reshape(E, N, K // 8)
     out = torch.zeros((E, N // 16, S, sb), dtype=torch.uint8)
+    if fmt == FMT_INT4:
+        mw = rows[..., K // 2:K // 2 + K // 16].contiguous().view(torch.int16).reshape(E, N, K // 64, 2)
+        sc, bi = mw[..., 0].view(torch.bfloat16), mw[..., 1].view(torch.bfloat16)
+        rexp = int4_row_exponents(sc, bi)                                   # [E, N]
+        scaled = torch.stack([torch.ldexp(t.float(), -rexp[..., None].float()).to(torch.bfloat16)
+                              for t in (sc, bi)], -1)                       # [E, N, K/64, 2]
+        rows = rows.clone()
+        rows[..., K // 2:K // 2 + K // 16] = scaled.view(torch.uint8).reshape(E, N, K // 16)
     wi = torch.tensor([[[tile_word_index(fmt, s, g, j) for j in range(4)] for g in range(4)] for s in range(S)])
     valid = wi < K // 8
     for e in range(E):
@@ -127,6 +148,8 @@ def pack_tiles_ref(fmt, rows, K):
                 mb = meta[:, :K // 32]
                 mb = torch.cat([mb, torch.zeros((16, 4 * S - K // 32), dtype=torch.uint8)], 1)
                 out[e, t, :, 1024:] = mb.reshape(16, S, 4).permute(1, 0, 2).reshape(S, 64)
+    if fmt == FMT_INT4:
+        return torch.cat([out.reshape(-1), rexp.to(torch.int8).view(torch.uint8).reshape(-1)])
     return out.reshape(-1)
 
 

@@ -88,7 +88,7 @@ def test_router_argument_errors():
 def test_tile_bytes_and_pack_argument_errors():
     from moelab_amd import _lib
     L = _lib.lib()
-    assert L.moe_tile_bytes(0, 768, 2048) == 48 * 16 * 1152
+    assert L.moe_tile_bytes(0, 768, 2048) == 48 * 16 * 1152 + 768   # int4: + one row-exponent byte per row
     assert L.moe_tile_bytes(1, 2880, 2880) == 180 * 23 * 1088
     assert L.moe_tile_bytes(0, 24, 2048) == 0 and L.moe_tile_bytes(0, 32, 96) == 0 and L.moe_tile_bytes(5, 32, 64) == 0
     p, q = ctypes.c_void_p(4096), ctypes.c_void_p(8192)

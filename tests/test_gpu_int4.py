@@ -245,22 +245,59 @@ def test_fused_t1_equals_two_launch_path(T, shape_args):
     assert int(sync.abs().sum()) == 0, sync.nonzero()
 
 
-def test_small_affine_scales():
-    """Tiny scales (x1e-6 weights, x1e6 activations) stay accurate: scale and bias are applied in fp32
-    (reference tests/test_int4_small_scales.py:23-32)."""
-    from moelab_amd import formats
+def scaled_state(base, factor=None, low=None, high=None, names=("g", "u", "d"), seed=0):
+    """The packed state `base` with the int4 scales of projections `names` multiplied by `factor`, or drawn anew
+    from U(low, high); biases = -8 x scale (codes centred, as the BASELINE configs)."""
     from moelab_amd.experts import make_state, unpack
-    sh = shape_("tiny", 256, 256, 8, 2)
-    base = packed_state(sh, 10)
     parts = {n: list(unpack(base, n)) for n in ("g", "u", "d")}
-    for n in ("g", "u"):
-        parts[n][1] = (parts[n][1].float() * 1e-6).to(torch.bfloat16)
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    for n in names:
+        sc = parts[n][1].float()
+        if factor is not None:
+            sc = sc * factor
+        else:
+            sc = low + (high - low) * torch.rand(sc.shape, generator=gen, device=DEV)
+        parts[n][1] = sc.to(torch.bfloat16)
         parts[n][2] = (parts[n][1].float() * -8.0).to(torch.bfloat16)
-    s = make_state("int4", parts["g"], parts["u"], parts["d"])
+    return make_state("int4", parts["g"], parts["u"], parts["d"])
+
+
+def test_small_affine_scales():
+    """Tiny scales (x1e-6 weights, x1e6 activations) stay accurate on the per-slot GEMV (T=1) and the wave tiles
+    (T=7), which apply scale and bias in fp32 to exact-code sums (reference tests/test_int4_small_scales.py:23-32)."""
+    from moelab_amd import formats
+    sh = shape_("tiny", 256, 256, 8, 2)
+    s = scaled_state(packed_state(sh, 10), factor=1e-6, names=("g", "u"))
     for T in (1, 7):
         x, idx, wts = inputs(sh, T, seed=10, scale=1e6)
         assert_close(q4().run(s, x, idx, wts, out_dtype=torch.float32), oracle_y(s, x, idx, wts), what=T)
     assert formats.GS_INT4 == 64
+
+
+@pytest.mark.parametrize("T", [50, 200])
+@pytest.mark.parametrize("case", ["x1e-6", "qwen3-min-scale"])
+def test_small_affine_scales_dense_tiles(case, T, monkeypatch):
+    """The dense tiles dequantise weights to fp16, where raw scales below 6.1e-5 would be subnormal and below ~6e-8
+    zero: the tile records hold each row's scales and biases times 2^-E_row (largest at [2^10, 2^11)) and the
+    epilogues scale the sums back by 2^E_row. Cases: every projection's scales x1e-6 with x x1e6; scales
+    U(4e-6, 1.3e-5) around real Qwen3's smallest (8.6e-6). T=200 (100 slots per expert) runs the dense tiles on
+    both projections, T=50 (25 per expert) the wave gate/up into the dense down (reference
+    tests/test_int4_small_scales.py:21-32 runs its tiny-scale case through the MMA paths)."""
+    monkeypatch.setenv("MOE_DENSE", "1")
+    sh = shape_("tiny-dense", 256, 384, 4, 2)
+    base = packed_state(sh, 12)
+    if case == "x1e-6":
+        s, xs = scaled_state(base, factor=1e-6), 1e6
+    else:
+        s, xs = scaled_state(base, low=4e-6, high=1.3e-5, seed=T), 1.0
+    x, idx, wts = inputs(sh, T, "uniform", seed=T, scale=xs)
+    print(f"case small scales dense {case} T={T}", flush=True)
+    y32 = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    y = grouped(s, x, idx, wts)
+    ref = oracle_y(s, x, idx, wts)
+    assert np.abs(ref).max() > 0
+    assert_close(y32, ref, what=(case, T, "fp32 out"))
+    assert_close(y, ref, what=(case, T, "bf16 out"))
 
 
 @pytest.mark.parametrize("fmt", ["int4", "mxfp4"])

@@ -63,8 +63,9 @@ def test_every_word_moves_once_and_steps_stay_in_one_group(fmt, K):
     t = formats.pack_tiles_ref(fmt, rows, K)
     S = (K + 127) // 128
     sb = formats.TILE_SLICE_BYTES[fmt]
-    assert t.numel() == E * (N // 16) * S * sb
-    rec = t.reshape(E, N // 16, S, sb)
+    nrec = E * (N // 16) * S * sb
+    assert t.numel() == nrec + (E * N if fmt == "int4" else 0)   # int4: one exponent byte per row after the records
+    rec = t[:nrec].reshape(E, N // 16, S, sb)
     stored = rec[..., :1024].contiguous().view(torch.int32).reshape(E, N // 16, S, 4, 16, 4)  # [.., g, r, j]
     codes = deinterleave(stored).numpy()
     nz = codes[codes != 0]
@@ -88,29 +89,75 @@ def test_every_word_moves_once_and_steps_stay_in_one_group(fmt, K):
                         assert np.all(widx // 16 == s)
 
 
-@pytest.mark.parametrize("fmt", ["int4", "mxfp4"])
 @pytest.mark.parametrize("K", [128, 192])
-def test_metadata_follows_its_slice(fmt, K):
+def test_mxfp4_metadata_follows_its_slice(K):
     E, N = 1, 16
-    rows, _ = self_describing_rows(fmt, E, N, K)
-    t = formats.pack_tiles_ref(fmt, rows, K)
+    rows, _ = self_describing_rows("mxfp4", E, N, K)
+    t = formats.pack_tiles_ref("mxfp4", rows, K)
     S = (K + 127) // 128
-    rec = t.reshape(E, 1, S, formats.TILE_SLICE_BYTES[fmt])
+    rec = t.reshape(E, 1, S, formats.TILE_SLICE_BYTES["mxfp4"])
     meta = rows[0, :, K // 2:].numpy()
-    if fmt == "int4":
-        ng = K // 64
-        for s in range(S):
-            m = rec[0, 0, s, 1024:].reshape(16, 2, 4).numpy()
-            for r in range(16):
-                for u in range(2):
-                    grp = 2 * s + u
-                    want = meta[r, 4 * grp:4 * grp + 4] if grp < ng else np.zeros(4, np.uint8)
-                    assert np.array_equal(m[r, u], want), (s, r, u)
-    else:
-        ng = K // 32
-        for s in range(S):
-            m = rec[0, 0, s, 1024:].reshape(16, 4).numpy()
-            for r in range(16):
-                for j in range(4):
-                    grp = 4 * s + j
-                    assert m[r, j] == (meta[r, grp] if grp < ng else 0), (s, r, j)
+    ng = K // 32
+    for s in range(S):
+        m = rec[0, 0, s, 1024:].reshape(16, 4).numpy()
+        for r in range(16):
+            for j in range(4):
+                grp = 4 * s + j
+                assert m[r, j] == (meta[r, grp] if grp < ng else 0), (s, r, j)
+
+
+def int4_rows_with_meta(sc, bi, K):
+    """int4 row records [1, 16, rb] with zero codes and the given bf16 scales / biases [16, K/64]."""
+    rb = formats.row_bytes("int4", K)
+    rows = torch.zeros((1, 16, rb), dtype=torch.uint8)
+    mw = torch.stack([sc, bi], -1).contiguous().view(torch.uint8).reshape(16, K // 16)
+    rows[0, :, K // 2:K // 2 + K // 16] = mw
+    return rows
+
+
+@pytest.mark.parametrize("K", [128, 192, 320])
+def test_int4_metadata_follows_its_slice_scaled_by_the_row_exponent(K):
+    """Each slice record carries its groups' (scale, bias) of each row times 2^-E_row, exactly; E_row puts the
+    row's largest |s| or |b| at [2^10, 2^11); the exponent bytes follow the records. Rows span scales from 1e-30
+    to 1e30 (the dense tiles' fp16 dequantisation needs the scaled values, not the raw ones, inside fp16)."""
+    ng = K // 64
+    rng = np.random.default_rng(K)
+    mags = 10.0 ** rng.uniform(-30, 30, size=(16, 1)) * rng.uniform(0.5, 2.0, size=(16, ng))
+    sc = torch.tensor(mags, dtype=torch.float32).to(torch.bfloat16)
+    bi = (sc.float() * torch.tensor(rng.uniform(-12, 4, size=(16, ng)), dtype=torch.float32)).to(torch.bfloat16)
+    sc[3] = 0
+    bi[3] = 0                                  # an all-zero row: exponent 0
+    bi[5, 0] = -sc[5, 0].float() * 300         # a row whose largest is a bias
+    rows = int4_rows_with_meta(sc, bi, K)
+    t = formats.pack_tiles_ref("int4", rows, K)
+    S = (K + 127) // 128
+    nrec = S * formats.TILE_SLICE_BYTES["int4"]
+    ex = t[nrec:].view(torch.int8).to(torch.int64)
+    assert ex.numel() == 16 and int(ex[3]) == 0
+    amax = torch.maximum(sc.float().abs().amax(1), bi.float().abs().amax(1))
+    for r in range(16):
+        if r == 3:
+            continue
+        scaled = float(amax[r]) * 2.0 ** -int(ex[r])
+        assert 1024.0 <= scaled < 2048.0, (r, float(amax[r]), int(ex[r]))
+    rec = t[:nrec].reshape(S, formats.TILE_SLICE_BYTES["int4"])
+    for s in range(S):
+        m = rec[s, 1024:].reshape(16, 2, 2, 2).contiguous().view(torch.bfloat16)[..., 0]   # [row, group, s|b]
+        for u in range(2):
+            grp = 2 * s + u
+            for j, src in enumerate((sc, bi)):
+                got = torch.ldexp(m[:, u, j].float(), ex.float())
+                want = src[:, grp].float() if grp < ng else torch.zeros(16)
+                assert torch.equal(got, want), (s, u, j)
+
+
+def test_int4_row_exponent_known_answers():
+    """E = floor(log2 amax) - 10 from the bf16 bits: 0.16 (a bias of -8 x 0.02) -> -13; 1024 -> 0; 2047 -> 0 (bf16
+    rounds it to 2048 -> 1); 1e-30 -> -110; 1e-40 (bf16 subnormal) and 1e-37 -> -120 (clamped); 3e38 -> 117;
+    zero -> 0; inf and NaN -> 0."""
+    vals = [0.16, 1024.0, 2047.0, 1e-30, 1e-40, 1e-37, 3e38, 0.0, float("inf"), float("nan")]
+    want = [-13, 0, 1, -110, -120, -120, 117, 0, 0, 0]
+    b = torch.tensor(vals, dtype=torch.float32).to(torch.bfloat16)[:, None]
+    got = formats.int4_row_exponents(b, torch.zeros_like(b))
+    assert got.tolist() == want
+    assert formats.int4_row_exponents(torch.zeros_like(b), -b).tolist() == want   # sign ignored, bias side too
