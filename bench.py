@@ -14,7 +14,7 @@ roofline: the dominant kernel at T=1 is the gate/up GEMV (2/3 of the weight byte
 launches, gate/up then down). Its average launch duration is measured with HIP events on the stream it
 runs on, around replays of a graph of 48 gate/up-only launches (the same kernel the chain runs, through
 moe_experts_run_stages); achieved = algorithmic bytes per launch (k experts x gate+up packed rows) /
-duration. The single-launch fused kernel is timed beside it.
+duration.
 
 cpu_baseline: the reference's CPU torch path (torch_loop, reference variants/cuda/torch_loop.py:11-17)
 on dequantised fp32 weights of the selected experts, timed on this host for a bounded sample of layers.
@@ -116,12 +116,10 @@ def main():
     torch.cuda.synchronize()
     log(f"layers ready in {time.time() - t0:.1f}s ({L * sh.E * per_expert / 1e9:.2f} GB packed experts)")
 
-    # one workspace for every graph below (graphs keep raw pointers into it)
-    desc_probe = layers[0]
-    from moelab_amd.experts import _desc
-    need = max(_lib.lib().moe_experts_workspace_bytes(_desc(desc_probe), T, sh.k, p)
-               for T in (1, 32, 64) for p in (_lib.PATH_SLOTS, _lib.PATH_GROUPED))
-    _lib.workspace(dev, need)
+    # one workspace for every graph below (graphs keep raw pointers into it): sized before any capture
+    from moelab_amd.experts import reserve
+    reserve(layers[0], 64, sh.k)
+    router.reserve(dev, 64)
 
     # ------------------------------------------------------------------ T = 1: experts-only chain
     x1 = baseline_x(1, sh.d, seed=0, device=dev)
@@ -155,9 +153,6 @@ def main():
     g1, _ = graph_of(chain_t1())
     t_step = time_graph(g1, args.steps, args.warmup)
     log(f"T=1 experts chain (default path): {t_step * 1e6 / L:.2f} us/layer, {bytes1 / t_step / 1e9:.0f} GB/s")
-    g2, _ = graph_of(chain_t1(_lib.PATH_FUSED_T1))
-    t_step_f = time_graph(g2, args.steps, args.warmup)
-    log(f"T=1 experts chain (fused single launch): {t_step_f * 1e6 / L:.2f} us/layer")
     g1r, _ = graph_of(chain_t1_router)
     t_step_r = time_graph(g1r, args.steps, args.warmup)
     log(f"T=1 with router: {t_step_r * 1e6 / L:.2f} us/layer")
@@ -259,8 +254,7 @@ def main():
         "weight_bytes_per_step": bytes1,
         "with_router": {"us_per_layer": round(t_step_r * 1e6 / L, 3),
                         "weight_GBps": round(bytes1 / t_step_r / 1e9, 2)},
-        "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3),
-                       "fused_single_launch_us_per_layer": round(t_step_f * 1e6 / L, 3)},
+        "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3)},
         "t32": t32,
         "configs": configs,
         "roofline": {"bound": "hbm", "kernel": "k_gate_up_rows<FmtInt4, 3, 1> (T=1 gate/up GEMV + GLU)",

@@ -64,9 +64,6 @@ extern "C" {
 #define MOE_PATH_SLOTS 1      /* per-slot GEMV over all T*k slots, no grouping, two launches (the stock-style
                                  gather of the reference's pre-tile kernels) */
 #define MOE_PATH_GROUPED 2    /* grouped expert tiles: each selected expert's weights read once */
-#define MOE_PATH_FUSED_T1 3   /* T == 1 in one launch (gate/up, device-wide hand-off of h, down); falls back to
-                                 MOE_PATH_SLOTS for shapes it does not take. Measured slower than two launches
-                                 on MI355X at the Qwen3 shape: the cross-XCD hand-off costs more than a launch */
 
 /* One projection of all E experts: N output rows of K inputs. */
 typedef struct {
@@ -163,13 +160,9 @@ int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offset
  *   exponent per row (no overflow for large rows, no flush to zero for small ones; any scale range); ~1e-3 of
  *   the outputs' RMS in the worst case measured.
  *   Requirements: d % 64 == 0, F % 64 == 0, F <= 16384; x, y, rows 16-byte aligned.
- *   workspace: moe_experts_workspace_bytes(...) bytes. Its first MOE_WORKSPACE_SYNC_BYTES bytes hold the
- *   fused T == 1 kernel's completion counters: zero them once when the workspace is allocated; every call
- *   leaves them zero. The rest may hold anything. Calls sharing a workspace must be stream-ordered.
- *   The fused T == 1 kernel runs at most as many workgroups as the device holds at once and waits on the
- *   others with a bounded spin; it needs the device to itself for the duration of the launch.
+ *   workspace: moe_experts_workspace_bytes(...) bytes (any contents; every call writes what it reads). Calls
+ *   sharing a workspace must be stream-ordered.
  */
-#define MOE_WORKSPACE_SYNC_BYTES 4096
 int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T,
                     int k, int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                     size_t workspace_bytes, void* stream);
@@ -199,8 +192,7 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
  *   g_t = sigmoid(x_t . gate) (gate: bf16 [d], fp32 dot in a fixed order) or 1 when gate is NULL.
  *   ws: the S shared experts as an expert set (E = S <= 32; same formats, packing and optional tile copies).
  *   x, y, residual, dtypes, act: as moe_experts_run (path auto: per-slot GEMV at T == 1, grouped tiles above).
- *   workspace: moe_shared_experts_workspace_bytes(ws, T); its first MOE_WORKSPACE_SYNC_BYTES bytes are zero on
- *   entry and on exit, as for moe_experts_run.
+ *   workspace: moe_shared_experts_workspace_bytes(ws, T) bytes (any contents), as for moe_experts_run.
  * A layer with routed and shared experts is moe_experts_run (routed, into y) followed by this call with
  * residual = y.
  */

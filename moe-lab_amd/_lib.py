@@ -17,13 +17,12 @@ LIB_PATH = os.environ.get("MOELAB_AMD_LIB") or os.path.join(HERE, "libmoe_mi355x
 MOE_OK, MOE_ERR_ARG, MOE_ERR_DTYPE, MOE_ERR_WORKSPACE, MOE_ERR_LAUNCH, MOE_ERR_ALIGN = 0, -1, -2, -3, -4, -5
 DTYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 FMT_INT4_G64, FMT_MXFP4 = 0, 1
-PATH_AUTO, PATH_SLOTS, PATH_GROUPED, PATH_FUSED_T1 = 0, 1, 2, 3
+PATH_AUTO, PATH_SLOTS, PATH_GROUPED = 0, 1, 2
 ACT_SWIGLU, ACT_GEGLU, ACT_GPTOSS = 0, 1, 2
 
 EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
            "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_row_bytes", "moe_tile_bytes",
            "moe_tiles_pack", "moe_shared_experts_run", "moe_shared_experts_workspace_bytes", "moe_version")
-WORKSPACE_SYNC_BYTES = 4096
 STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 3
 
 _ERRORS = {
@@ -104,16 +103,31 @@ def require_device(t, name="tensor"):
         raise RuntimeError(f"{name} must be a GPU tensor (the HIP path has no CPU fallback)")
 
 
-_WS = {}
+_WS = {}        # device index -> the current scratch buffer of that device
+_RETIRED = []   # buffers replaced by larger ones: never freed (a captured HIP graph keeps their raw pointers)
+
+
+def grow(table, key, nbytes, make, what):
+    """The buffer table[key] with at least nbytes, replaced by a new one (at least twice the old size, so at
+    most log2 of the largest size is ever retired) when it is smaller. A replaced buffer is kept alive for the
+    process: a HIP graph captured with it still writes there. Growing during stream capture raises instead:
+    the new buffer would come from the graph's private pool."""
+    buf = table.get(key)
+    if buf is not None and buf.numel() >= nbytes:
+        return buf
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"{what} would grow from {0 if buf is None else buf.numel()} to {nbytes} during "
+                           f"HIP graph capture: call reserve() with the largest call's sizes before capturing")
+    if buf is not None:
+        _RETIRED.append(buf)
+    buf = make(max(int(nbytes), 2 * (0 if buf is None else buf.numel())))
+    table[key] = buf
+    return buf
 
 
 def workspace(device, nbytes):
-    """Per-device scratch buffer, grown on demand (stream-ordered reuse through torch's allocator).
-    Allocated zeroed: its first WORKSPACE_SYNC_BYTES hold the fused kernel's counters, which every
-    call leaves at zero."""
-    key = torch.device(device).index
-    buf = _WS.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(int(nbytes), WORKSPACE_SYNC_BYTES), dtype=torch.uint8, device=device)
-        _WS[key] = buf
-    return buf
+    """Per-device scratch buffer of the expert calls (uint8, at least nbytes; the calls need no particular
+    contents). Grows on demand (see grow)."""
+    device = torch.device(device)
+    return grow(_WS, device.index, max(int(nbytes), 256),
+                lambda n: torch.empty(n, dtype=torch.uint8, device=device), "the expert workspace")

@@ -13,7 +13,6 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int resolve_path(int path, int T) {
     if (path == MOE_PATH_AUTO) return T == 1 ? MOE_PATH_SLOTS : MOE_PATH_GROUPED;
-    if (path == MOE_PATH_FUSED_T1) return MOE_PATH_SLOTS;   // the fused kernel, or its per-slot fallback
     return path;
 }
 
@@ -24,7 +23,7 @@ struct Layout {
 Layout layout(const moe_experts_t* w, int T, int k, int path) {
     Layout L{};
     const size_t nslots = (size_t)T * k;
-    size_t off = MOE_WORKSPACE_SYNC_BYTES;   // fused-kernel counters live at offset 0
+    size_t off = 0;
     L.h = off;
     off += align_up(nslots * (size_t)w->F * 2) * 2;   // hi and lo planes
     if (resolve_path(path, T) == MOE_PATH_GROUPED) {
@@ -170,7 +169,7 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     if (stages < 1 || stages > MOE_STAGE_ALL) return MOE_ERR_ARG;
     int rc = check_experts(w);
     if (rc) return rc;
-    if (T < 0 || k < 1 || act < 0 || act > 2 || path < 0 || path > 3) return MOE_ERR_ARG;
+    if (T < 0 || k < 1 || act < 0 || act > 2 || path < 0 || path > 2) return MOE_ERR_ARG;
     if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;
     if (y_dtype != MOE_DTYPE_BF16 && y_dtype != MOE_DTYPE_F32) return MOE_ERR_DTYPE;
     const int rpath = resolve_path(path, T);
@@ -199,8 +198,6 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     a.hlo = a.hhi + align_up((size_t)T * k * w->F * 2) / 2;
     a.st = (hipStream_t)stream;
     a.stages = stages;
-    a.fused_t1 = path == MOE_PATH_FUSED_T1;
-    a.sync = (int32_t*)ws;
     if (rpath == MOE_PATH_GROUPED) {
         a.yp = (float*)(ws + L.yp);
         a.x16 = (uint16_t*)(ws + L.x16);

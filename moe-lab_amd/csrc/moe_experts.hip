@@ -24,8 +24,6 @@
 //   k_gate_up_slots / k_down_slots   per-slot GEMV (any T; the stock-style per-slot gather at T > 1)
 //   k_combine                        y = residual + sum over a token's slots of wts * (yp + b_down); the
 //                                    combine step of the grouped expert tiles (moe_tiles.hip)
-//   k_t1_fused                       T == 1 in one launch: gate/up for all k slots, a device-wide
-//                                    completion count, then down + k-reduction (h staged in LDS)
 #include "moe_common.h"
 #include "moe_formats.h"
 #include "moe_internal.h"
@@ -548,275 +546,8 @@ k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t
     reinterpret_cast<uint2*>(y)[i4] = o;
 }
 
-// ============================================================================ fused T == 1
-// One launch for a decode token: phase A computes gate/up/GLU for all k slots (row pairs spread over
-// every wave of the grid, NRA per wave), stores h as one 32-bit word per element (bf16 hi | bf16 lo << 16)
-// with agent-scope atomic stores, and counts the block done in one of 16 counters; phase B waits until all
-// blocks are counted, stages h slot by slot (agent-scope loads, then the pre-paired planes and chunk sums)
-// in LDS, and computes RPB = 64/LPRB down rows per block for all k slots (4 waves split the slots).
-// The XCDs' L2s are not coherent with each other; the agent-scope atomics make the hand-off coherent
-// without writing back or invalidating any L2 (see store_agent in moe_common.h).
-// The down weights of a block's first row block are loaded before the wait. The grid never exceeds the
-// number of co-resident blocks (host side), every wait is bounded by spin_limit (a timeout sets err and
-// skips the block's down rows), and the last block to finish resets the counters to zero.
-struct T1Args {
-    const uint16_t* x;
-    const uint8_t *G, *U, *Dn;
-    const float *bg, *bu, *bd;
-    const int32_t* idx;
-    const float* wts;
-    int k, d, F, E, D;
-    int rpw_a;     // row pairs per wave in phase A (<= NRA)
-    int nbtask;    // row blocks of RPB down rows
-    int y32;
-    void* y;
-    const void* resid;
-    uint32_t* h32;   // [k, F] h words (bf16 hi | bf16 lo << 16), handed between blocks
-    int32_t* sync;   // [0..15]*32: phase-A counters, 16*32: blocks finished, 17*32: timeout flag
-    int spin_limit;
-};
-constexpr int T1_SYNC_STRIDE = 32;   // one counter per 128-byte line
-
-template <class FMT, int ACT, int NRA, int LPRB, int SPW, int NCB>
-__global__ void __launch_bounds__(256, 1)
-k_t1_fused(T1Args a) {
-    extern __shared__ uint4 s_dyn[];
-    constexpr int RPB = 64 / LPRB;
-    constexpr int SL = sum_lane<LPRB>();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int gw = blockIdx.x * 4 + wave;
-    const int k = a.k, d = a.d, F = a.F, D = a.D;
-    const size_t rbA = rbytes(FMT::FMT, d), rbB = rbytes(FMT::FMT, F);
-    const int nchA = d >> 5, cpr = F >> 5;
-    const int Q = k * F;
-
-    // ---------------- phase A loads (one 64-lane pass over d: d <= 2048)
-    const bool cvA = lane < nchA;
-    const int cA = cvA ? lane : nchA - 1;
-    const int q0 = gw * a.rpw_a;
-    uint4 wg[NRA], wu[NRA];
-    uint32_t mg[NRA], mu[NRA];
-    int eq[NRA];
-#pragma unroll
-    for (int i = 0; i < NRA; ++i) {
-        const int q = min(q0 + min(i, a.rpw_a - 1), Q - 1);
-        const int j = q / F, n = q - j * F;
-        int e = a.idx[j];
-        eq[i] = e;
-        e = (unsigned)e < (unsigned)a.E ? e : 0;
-        const uint8_t* gr = a.G + ((size_t)e * F + n) * rbA;
-        const uint8_t* ur = a.U + ((size_t)e * F + n) * rbA;
-        wg[i] = *reinterpret_cast<const uint4*>(gr + 16 * cA);
-        wu[i] = *reinterpret_cast<const uint4*>(ur + 16 * cA);
-        mg[i] = FMT::meta(gr, d, cA);
-        mu[i] = FMT::meta(ur, d, cA);
-    }
-    uint32_t xw[16];
-    load_x32(a.x + 32 * cA, xw);
-
-    // ---------------- phase B prefetch: first row block of this block
-    const int rsub = lane / LPRB, psub = lane % LPRB;
-    int bt = blockIdx.x;
-    uint4 wv[SPW][NCB];
-    uint32_t mv[SPW][NCB];
-    {
-        const int n = min(bt * RPB + rsub, D - 1);
-#pragma unroll
-        for (int s = 0; s < SPW; ++s) {
-            const int j = min(wave + 4 * s, k - 1);
-            int e = a.idx[j];
-            e = (unsigned)e < (unsigned)a.E ? e : 0;
-            const uint8_t* rowp = a.Dn + ((size_t)e * D + n) * rbB;
-#pragma unroll
-            for (int m = 0; m < NCB; ++m) {
-                const int p = min(psub + m * LPRB, cpr - 1);
-                wv[s][m] = *reinterpret_cast<const uint4*>(rowp + 16 * p);
-                mv[s][m] = FMT::meta(rowp, F, p);
-            }
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---------------- phase A compute
-    {
-        uint32_t xp[16];
-        pair_x32(xw, xp);
-        const float xs = FMT::XSUM ? sum_x32(xw) : 0.f;
-        float ag[NRA], au[NRA];
-#pragma unroll
-        for (int i = 0; i < NRA; ++i) {
-            uint32_t qp[16];
-            FMT::decode(wg[i], qp);
-            ag[i] = cvA ? FMT::fold(0.f, mg[i], dot16(qp, xp, 0.f), xs) : 0.f;
-            FMT::decode(wu[i], qp);
-            au[i] = cvA ? FMT::fold(0.f, mu[i], dot16(qp, xp, 0.f), xs) : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < NRA; ++i) {
-            ag[i] = sum_lanes<64>(ag[i]);
-            au[i] = sum_lanes<64>(au[i]);
-        }
-        const int r = lane - 48;
-        if (r >= 0 && r < NRA && r < a.rpw_a && q0 + r < Q) {
-            float g = 0.f, u = 0.f;
-            int e = 0;
-#pragma unroll
-            for (int i = 0; i < NRA; ++i)
-                if (i == r) { g = ag[i]; u = au[i]; e = eq[i]; }
-            const int q = q0 + r, j = q / F, n = q - j * F;
-            float hv = 0.f;
-            if ((unsigned)e < (unsigned)a.E) {
-                if (a.bg) g += a.bg[(size_t)e * F + n];
-                if (a.bu) u += a.bu[(size_t)e * F + n];
-                hv = glu<ACT>(g, u);
-            }
-            const uint16_t hi = f32_to_bf16(hv);
-            const uint16_t lo = f32_to_bf16(hv - bf16_to_f32(hi));
-            store_agent(a.h32 + (size_t)j * F + n, (uint32_t)hi | ((uint32_t)lo << 16));
-        }
-    }
-    // publish: this wave's h stores are complete (vmcnt(0)) before the block counts itself done
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(&a.sync[(blockIdx.x & 15) * T1_SYNC_STRIDE], 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-
-    // ---------------- wait for every block's phase A (bounded)
-    __shared__ int s_ok;
-    if (wave == 0) {
-        int spins = 0, total = 0;
-        while (true) {
-            const int v = lane < 16 ? load_agent(&a.sync[lane * T1_SYNC_STRIDE]) : 0;
-            total = __builtin_amdgcn_readfirstlane((int)sum_lanes<16>((float)v));
-            if (total >= (int)gridDim.x || ++spins > a.spin_limit) break;
-            __builtin_amdgcn_s_sleep(2);
-        }
-        if (lane == 0) {
-            s_ok = total >= (int)gridDim.x;
-            if (!s_ok) __hip_atomic_store(&a.sync[17 * T1_SYNC_STRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    __syncthreads();
-    if (s_ok) {
-        // ---------------- stage h in LDS: all k*F words with coalesced agent-scope loads (32 in flight per
-        // thread), then each chunk is rewritten in place as 8 x 16 B of pre-paired (hi, lo) planes + its sum
-        uint4* s_h = s_dyn;                                                       // [k*cpr][8] (= raw words)
-        float* s_sum = reinterpret_cast<float*>(s_dyn + (size_t)8 * k * cpr);    // [k*cpr]
-        float* s_red = s_sum + k * cpr;                                           // [4][RPB]
-        uint32_t* s_raw = reinterpret_cast<uint32_t*>(s_dyn);
-        const int kf = k * F;
-        for (int base = 0; base < kf; base += 256 * 32) {
-            uint32_t v[32];
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const int o = base + i * 256 + threadIdx.x;
-                if (o < kf) v[i] = load_agent(a.h32 + o);
-            }
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const int o = base + i * 256 + threadIdx.x;
-                if (o < kf) s_raw[o] = v[i];
-            }
-        }
-        __syncthreads();
-        for (int c = threadIdx.x; c < k * cpr; c += 256) {
-            uint32_t rw[32];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const uint4 t4 = s_h[(size_t)c * 8 + q];
-                rw[4 * q] = t4.x;
-                rw[4 * q + 1] = t4.y;
-                rw[4 * q + 2] = t4.z;
-                rw[4 * q + 3] = t4.w;
-            }
-            uint32_t wh[16], wl[16];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t w0 = rw[8 * jj + i], w4 = rw[8 * jj + i + 4];
-                    wh[4 * jj + i] = __builtin_amdgcn_perm(w4, w0, 0x05040100u);   // (hi_n, hi_n+4)
-                    wl[4 * jj + i] = __builtin_amdgcn_perm(w4, w0, 0x07060302u);   // (lo_n, lo_n+4)
-                }
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                s_h[(size_t)c * 8 + q] = make_uint4(wh[4 * q], wh[4 * q + 1], wh[4 * q + 2], wh[4 * q + 3]);
-                s_h[(size_t)c * 8 + 4 + q] = make_uint4(wl[4 * q], wl[4 * q + 1], wl[4 * q + 2], wl[4 * q + 3]);
-            }
-            s_sum[c] = FMT::XSUM ? sum16(wl, sum16(wh, 0.f)) : 0.f;
-        }
-        __syncthreads();
-        // ---------------- phase B: down rows for all slots
-        for (; bt < a.nbtask; bt += gridDim.x) {
-            const bool first = bt == (int)blockIdx.x;
-            const int n = bt * RPB + rsub;
-            const int nn = min(n, D - 1);
-            float yacc = 0.f;
-#pragma unroll
-            for (int s = 0; s < SPW; ++s) {
-                const int j = wave + 4 * s;
-                if (j < k) {
-                    const int e = a.idx[j];
-                    if ((unsigned)e < (unsigned)a.E) {
-                        const uint8_t* rowp = a.Dn + ((size_t)e * D + nn) * rbB;
-                        float acc = 0.f;
-#pragma unroll
-                        for (int m = 0; m < NCB; ++m) {
-                            const int p = psub + m * LPRB;
-                            if (p < cpr) {
-                                uint4 w = wv[s][m];
-                                uint32_t mm = mv[s][m];
-                                if (!first) {
-                                    w = *reinterpret_cast<const uint4*>(rowp + 16 * p);
-                                    mm = FMT::meta(rowp, F, p);
-                                }
-                                uint32_t qp[16], wh[16], wl[16];
-                                FMT::decode(w, qp);
-                                const size_t c = (size_t)j * cpr + p;
-                                words16(&s_h[c * 8], wh);
-                                words16(&s_h[c * 8 + 4], wl);
-                                acc = FMT::fold(acc, mm, dot16(qp, wl, dot16(qp, wh, 0.f)), s_sum[c]);
-                            }
-                        }
-                        acc = sum_lanes<LPRB>(acc);
-                        if (a.bd) acc += a.bd[(size_t)e * D + nn];
-                        yacc = __builtin_fmaf(a.wts[j], acc, yacc);
-                    }
-                }
-            }
-            if (psub == SL) s_red[wave * RPB + rsub] = yacc;
-            __syncthreads();
-            if (wave == 0 && lane < RPB) {
-                const int n2 = bt * RPB + lane;
-                if (n2 < D) {
-                    const float v = ((s_red[lane] + s_red[RPB + lane]) + s_red[2 * RPB + lane]) + s_red[3 * RPB + lane];
-                    store_y(a.y, n2, a.resid ? v + load_y(a.resid, n2, a.y32) : v, a.y32);
-                }
-            }
-            __syncthreads();
-        }
-    }
-    // ---------------- the last block out resets the counters for the next launch
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int old = atomicAdd(&a.sync[16 * T1_SYNC_STRIDE], 1);
-        if (old == (int)gridDim.x - 1) {
-            for (int i = 0; i < 16; ++i) a.sync[i * T1_SYNC_STRIDE] = 0;
-            a.sync[16 * T1_SYNC_STRIDE] = 0;
-        }
-    }
-}
-
 // ============================================================================ host side
 namespace {
-
-int pick_lpr(int cpr) {
-    // lanes per down row: smallest power of two >= cpr / 3 (about three 16-byte chunks per lane), in [4, 64]
-    int l = 4;
-    while (l < 64 && l * 3 < cpr) l *= 2;
-    return l;
-}
 
 struct ProjPtrs {
     const uint8_t *G, *U, *Dn;
@@ -1007,103 +738,10 @@ int run_slots_fmt(const ExpertsArgs& a) {
     return 0;
 }
 
-// ---------------------------------------------------------------- fused T == 1
-constexpr int T1_NRA = 8;    // max row pairs per wave in phase A
-constexpr int T1_SPW = 4;    // max slots per wave in phase B (k <= 16)
-constexpr int T1_NCB = 4;    // max chunks per lane per down row
-constexpr int T1_LDS_MAX = 64 * 1024;
-
-int t1_lds_bytes(int k, int F, int rpb) { return k * (F >> 5) * (128 + 4) + 4 * rpb * 4; }
-
-template <class FMT, int ACT, int LPRB>
-int launch_t1(const ExpertsArgs& a, int32_t* sync) {
-    constexpr int RPB = 64 / LPRB;
-    auto kern = k_t1_fused<FMT, ACT, T1_NRA, LPRB, T1_SPW, T1_NCB>;
-    const moe_experts_t* w = a.w;
-    const int lds = t1_lds_bytes(a.k, w->F, RPB);
-    // co-resident capacity of this kernel on the current device (cached per device)
-    static int cap_cache[64] = {0};   // written once per device with the same value; a race is benign
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
-    if (cap_cache[dev] == 0) {
-        int per_cu = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, T1_LDS_MAX) != hipSuccess) return 1;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 1;
-        cap_cache[dev] = per_cu * cus;
-    }
-    const int cap = cap_cache[dev];
-    const int nbtask = (w->d + RPB - 1) / RPB;
-    const int Q = a.k * w->F;
-    int grid = nbtask < cap ? nbtask : cap;
-    const int need = (Q + 4 * T1_NRA - 1) / (4 * T1_NRA);   // blocks so that phase A fits NRA per wave
-    if (need > grid) grid = need;
-    if (grid > cap || grid < 1) return 1;
-    T1Args t{};
-    t.x = (const uint16_t*)a.x;
-    const ProjPtrs P = ptrs(w);
-    t.G = P.G;
-    t.U = P.U;
-    t.Dn = P.Dn;
-    t.bg = w->gate.bias;
-    t.bu = w->up.bias;
-    t.bd = w->down.bias;
-    t.idx = a.idx;
-    t.wts = a.wts;
-    t.k = a.k;
-    t.d = w->d;
-    t.F = w->F;
-    t.E = w->E;
-    t.D = w->d;
-    t.rpw_a = (Q + 4 * grid - 1) / (4 * grid);
-    t.nbtask = nbtask;
-    t.y32 = a.y32;
-    t.y = a.y;
-    t.resid = a.residual;
-    t.h32 = reinterpret_cast<uint32_t*>(a.hhi);   // the two h planes' space holds k*F words
-    t.sync = sync;
-    t.spin_limit = 1 << 22;
-    kern<<<grid, 256, lds, a.st>>>(t);
-    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
-}
-
-// returns 1 when the fused kernel cannot take this call (the caller falls back to two launches)
-template <class FMT>
-int try_t1_fused(const ExpertsArgs& a, int32_t* sync) {
-    const moe_experts_t* w = a.w;
-    const int cpr = w->F >> 5;
-    const int lprb = pick_lpr(cpr);
-    if (a.T != 1 || a.nored || a.stages != 3 || !sync || a.k > 4 * T1_SPW || w->d > 2048 ||
-        (cpr + lprb - 1) / lprb > T1_NCB || lprb > 16 || t1_lds_bytes(a.k, w->F, 64 / lprb) > T1_LDS_MAX)
-        return 1;
-    int rc;
-#define MOE_T1(ACT)                                                         \
-    switch (lprb) {                                                         \
-        case 4: rc = launch_t1<FMT, ACT, 4>(a, sync); break;                \
-        case 8: rc = launch_t1<FMT, ACT, 8>(a, sync); break;                \
-        default: rc = launch_t1<FMT, ACT, 16>(a, sync); break;              \
-    }
-    if (a.act == 0) { MOE_T1(0) }
-    else if (a.act == 1) { MOE_T1(1) }
-    else { MOE_T1(2) }
-#undef MOE_T1
-    return rc;
-}
-
 }  // namespace
 
 int run_experts_slots(const ExpertsArgs& a) {
-    if (a.w->fmt == MOE_FMT_INT4_G64) {
-        if (a.fused_t1) {
-            const int rc = try_t1_fused<FmtInt4>(a, a.sync);
-            if (rc != 1) return rc;
-        }
-        return run_slots_fmt<FmtInt4>(a);
-    }
-    if (a.fused_t1) {
-        const int rc = try_t1_fused<FmtMxfp4>(a, a.sync);
-        if (rc != 1) return rc;
-    }
-    return run_slots_fmt<FmtMxfp4>(a);
+    return a.w->fmt == MOE_FMT_INT4_G64 ? run_slots_fmt<FmtInt4>(a) : run_slots_fmt<FmtMxfp4>(a);
 }
 
 int launch_combine(const float* yp, int nplanes, size_t plane, const int32_t* idx, const float* wts, const float* bd, int E,

@@ -50,8 +50,6 @@ struct ExpertsArgs {
     int32_t* xexp;  // [T]
     GroupBufs grp;  // grouped path
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
-    int fused_t1;   // T == 1: try the single-launch kernel first
-    int32_t* sync;  // zero-initialised counters of the fused kernel (left zero after every launch)
     hipStream_t st;
 };
 

@@ -132,6 +132,21 @@ def run_experts(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, nored=False, residua
     return out
 
 
+def reserve(s, T, k, device=None):
+    """Size the per-device workspace for calls on state s of up to T tokens with k slots each, on either path
+    (and the state's shared experts): call it before capturing such calls in a HIP graph. A graph keeps the
+    workspace pointer it was captured with; the workspace never moves while it is large enough, and a buffer it
+    outgrows is kept alive, but growing it during capture raises."""
+    device = torch.device(device or s["g"].device)
+    desc = _desc(s)
+    L = _lib.lib()
+    need = max(int(L.moe_experts_workspace_bytes(desc, t, k, p)) for t in {1, int(T)}
+               for p in (_lib.PATH_SLOTS, _lib.PATH_GROUPED))
+    if "shared" in s:
+        need = max(need, int(L.moe_shared_experts_workspace_bytes(_desc(s["shared"]), int(T))))
+    return _lib.workspace(device, need)
+
+
 def run_shared(s, x, gate=None, act=0, residual=None, out=None, out_dtype=None):
     """Shared experts (always on) through moe_shared_experts_run: y = residual + g_t * sum_s expert_s(x_t),
     g_t = sigmoid(x_t . gate) for a bf16 gate vector [d] (Qwen-style gated shared expert, reference

@@ -36,13 +36,17 @@ _COUNTERS = {}
 
 
 def _counters(device, T):
-    n = _lib.lib().moe_router_counter_count(T)
-    key = torch.device(device).index
-    c = _COUNTERS.get(key)
-    if c is None or c.numel() < n:
-        c = torch.zeros(max(n, 64), dtype=torch.int32, device=device)   # the kernel leaves it zeroed
-        _COUNTERS[key] = c
-    return c
+    """The router's per-device hand-off counters (zero on entry, left zero by every call); grown like the expert
+    workspace (_lib.grow: old buffers stay alive for graphs captured with them; no growth during capture)."""
+    device = torch.device(device)
+    n = max(int(_lib.lib().moe_router_counter_count(T)), 64)
+    return _lib.grow(_COUNTERS, device.index, n, lambda m: torch.zeros(m, dtype=torch.int32, device=device),
+                     "the router counters")
+
+
+def reserve(device, T):
+    """Size the router's counters for calls of up to T tokens (before capturing them in a HIP graph)."""
+    _counters(device, T)
 
 
 def route(x, wr, k, bias=None, norm=True, scale=1.0, return_logits=False):

@@ -12,6 +12,7 @@ import torch
 
 from .. import _lib, backend
 from . import hip_mxfp4_moe as _b
+from ..experts import reserve  # noqa: F401  (workspace sizing before graph capture)
 
 META = {"name": "hip_mxfp4_gptoss",
         "description": "gfx950 HIP MXFP4 + per-expert biases + gpt-oss clamped SwiGLU"}

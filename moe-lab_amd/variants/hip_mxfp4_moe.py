@@ -3,7 +3,7 @@
 Variant contract and dispatch shape of the reference's MXFP4 dispatcher (reference
 moelab/variants/mlx/metal_mxfp4_moe.py:440-512): E2M1 codes with one E8M0 scale per 32 inputs,
 the scale applied in fp32 per group (exact for every byte 1..254; reference metal_mxfp4_moe.py:33-41);
-    T == 1          -> one fused launch (gate/up/GLU, then down + k-reduction)
+    T == 1          -> per-slot GEMV, two launches (gate/up/GLU for the k slots, then down + k-reduction)
     T > 1, grouped(...)  -> grouped expert tiles (each selected expert read once)
     otherwise       -> gather_moe (per-slot path), the reference's load-policy fallback (:474-477); on MI355X
                        it takes the small loads (fallback.grouped_from_load), not the large ones
@@ -11,10 +11,10 @@ the scale applied in fp32 per group (exact for every byte 1..254; reference meta
 import torch
 
 from .. import _lib, formats
-from ..experts import dims, make_state, run_experts, run_layer, unpack
+from ..experts import dims, make_state, reserve, run_experts, run_layer, unpack  # noqa: F401
 from ..fallback import gather_moe, grouped_from_load  # noqa: F401  (gather_moe: tests patch the attribute)
 
-META = {"name": "hip_mxfp4_moe", "description": "gfx950 HIP MXFP4: fused T=1 launch, grouped expert tiles at T>1"}
+META = {"name": "hip_mxfp4_moe", "description": "gfx950 HIP MXFP4: per-slot GEMV at T=1, grouped expert tiles at T>1"}
 MODE, GS, BITS = "mxfp4", 32, 4
 W_BITS = 4 + 8 / 32
 

@@ -2,19 +2,20 @@
 
 Same variant contract and dispatch shape as the reference's production int4 dispatcher
 (reference moelab/variants/mlx/metal_q4_moe.py:1-64):
-    T == 1                  -> one launch: gate+up+GLU for the k slots, then down + k-reduction
-                               (two per-slot launches when the shape does not fit the fused kernel)
+    T == 1                  -> per-slot GEMV, two launches: gate+up+GLU for the k slots, then down +
+                               k-reduction
     T > 1, custom_wins(...) -> grouped expert tiles: each selected expert's rows are read once and
                                applied to all of its slots (group, gate/up, down, combine)
     otherwise               -> gather_moe (module attribute, monkeypatchable like the reference's); on
                                MI355X the small loads (fallback.grouped_from_load)
 prepare / dequant keep the reference's state layout (mx.quantize affine, group 64), so `dequant(state)`
-gives the weights the fp32 reference uses.
+gives the weights the fp32 reference uses. reserve(state, T, k) sizes the per-device workspace before a caller
+captures calls in a HIP graph (graphs keep the workspace pointer they were captured with).
 """
 import torch
 
 from .. import _lib, formats
-from ..experts import dims, make_state, run_experts, run_layer, unpack
+from ..experts import dims, make_state, reserve, run_experts, run_layer, unpack  # noqa: F401
 from ..fallback import gather_moe, grouped_from_load  # noqa: F401  (gather_moe: tests patch the attribute)
 
 META = {"name": "hip_q4_moe", "description": "gfx950 HIP: per-slot GEMV at T=1, grouped expert tiles at T>1"}

@@ -109,3 +109,31 @@ def test_misaligned_tiles_rejected_before_launch():
     got = L.moe_experts_run(w, x, 0, x, x, 4, 2, 0, _lib.PATH_GROUPED, 0, x, 0, None, ctypes.c_void_p(8192), 1 << 30,
                             None)
     assert got == _lib.MOE_ERR_ALIGN
+
+
+def test_buffer_growth_keeps_old_buffers_and_refuses_growth_during_capture(monkeypatch):
+    """_lib.grow (the expert workspace and the router counters): a buffer that is large enough is returned as
+    is; a smaller one is replaced by one of at least twice its size and kept alive (a HIP graph captured with it
+    keeps its raw pointer); growing while the current stream captures raises (host-only: the capture state is
+    stubbed)."""
+    import torch
+    from moelab_amd import _lib
+    table, made = {}, []
+
+    def make(n):
+        made.append(n)
+        return torch.empty(n, dtype=torch.uint8)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    a = _lib.grow(table, 0, 1000, make, "t")
+    assert a.numel() == 1000 and _lib.grow(table, 0, 999, make, "t") is a
+    retired0 = len(_lib._RETIRED)
+    b = _lib.grow(table, 0, 1500, make, "t")
+    assert b.numel() == 2000 and made == [1000, 2000]          # at least double the old size
+    assert len(_lib._RETIRED) == retired0 + 1 and _lib._RETIRED[-1] is a
+    c = _lib.grow(table, 0, 10_000, make, "t")
+    assert c.numel() == 10_000
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    assert _lib.grow(table, 0, 10_000, make, "t") is c          # no growth needed: fine while capturing
+    with pytest.raises(RuntimeError, match="reserve"):
+        _lib.grow(table, 0, 10_001, make, "t")
+    assert table[0] is c

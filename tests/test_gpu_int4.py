@@ -225,24 +225,32 @@ def test_qwen3_full_shape(T):
     assert_close(q4().run(s, x, idx, wts), ref, what="bf16 out")
 
 
-@pytest.mark.parametrize("T", [1])
 @pytest.mark.parametrize("shape_args", [(2048, 768, 128, 8), (512, 256, 8, 1), (2048, 1408, 64, 6),
                                         (1024, 512, 16, 16), (256, 128, 4, 4)])
-def test_fused_t1_equals_two_launch_path(T, shape_args):
-    """The single-launch T=1 kernel (PATH_FUSED_T1) and the two per-slot launches agree with the oracle, and
-    the fused kernel leaves its completion counters at zero with no timeout."""
+def test_t1_paths_agree(shape_args):
+    """T=1: the default dispatch (PATH_AUTO) and the per-slot GEMV agree with the oracle, call after call (the
+    workspace's leftover contents from one call never leak into the next)."""
     from moelab_amd import _lib
     from moelab_amd.experts import run_experts
     sh = shape_("f", *shape_args)
     s = packed_state(sh, 9)
-    x, idx, wts = inputs(sh, T, seed=9)
+    x, idx, wts = inputs(sh, 1, seed=9)
     ref = oracle_y(s, x, idx, wts)
     for _ in range(3):
-        for path in (_lib.PATH_FUSED_T1, _lib.PATH_SLOTS, _lib.PATH_AUTO):
+        for path in (_lib.PATH_SLOTS, _lib.PATH_AUTO):
             assert_close(run_experts(s, x, idx, wts, path=path, out_dtype=torch.float32), ref, what=path)
-    torch.cuda.synchronize()
-    sync = _lib.workspace(x.device, 0)[:_lib.WORKSPACE_SYNC_BYTES].view(torch.int32).cpu()
-    assert int(sync.abs().sum()) == 0, sync.nonzero()
+
+
+def test_removed_fused_path_is_rejected():
+    """Path 3 (a former single-launch T=1 kernel) is no longer accepted: MOE_ERR_ARG, before any launch."""
+    from moelab_amd import _lib
+    from moelab_amd.experts import run_experts
+    sh = shape_("f", 256, 128, 4, 4)
+    s = packed_state(sh, 9)
+    x, idx, wts = inputs(sh, 1, seed=9)
+    with pytest.raises(_lib.MoeError) as ei:
+        run_experts(s, x, idx, wts, path=3)
+    assert ei.value.rc == _lib.MOE_ERR_ARG
 
 
 def scaled_state(base, factor=None, low=None, high=None, names=("g", "u", "d"), seed=0):
