@@ -169,6 +169,23 @@ int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const in
 size_t moe_experts_workspace_bytes(const moe_experts_t* w, int T, int k, int path);
 
 /*
+ * moe_experts_run without a workspace argument: no counterpart in the reference. For callers that cannot
+ * allocate (code under HIP graph capture, serving loops or harnesses that forbid allocation): the workspace is a
+ * device array inside the library, MOE_STATIC_SCRATCH_BYTES on each GPU it runs on, held until the process ends.
+ * Arguments, results and errors as moe_experts_run; calls whose workspace (moe_experts_workspace_bytes) exceeds
+ * MOE_STATIC_SCRATCH_BYTES return MOE_ERR_WORKSPACE before any launch (the Qwen3-30B-A3B shape fits calls of up
+ * to 115 tokens).
+ * It allocates nothing. Every call on one GPU uses that GPU's one array, which keeps the last call's contents (no
+ * call needs particular contents): calls that overlap on one GPU (other streams, other threads) race, and the
+ * caller must order them. The first call on each device looks up the array's address (hipGetSymbolAddress);
+ * make it outside graph capture: a call with T = 0 does only that.
+ */
+#define MOE_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
+int moe_experts_run_static(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,
+                           int T, int k, int act, int path, int nored, void* y, int y_dtype, const void* residual,
+                           void* stream);
+
+/*
  * The same call split at the one data dependency inside it, the GLU output h held in the workspace.
  * The reference dispatches these as separate kernels as well (metal_q4_decode_v4.py:177-184 _k1 gate_up,
  * _k2 down). stages = MOE_STAGE_GATE_UP: grouping (grouped path) + gate/up + GLU, h into the workspace;

@@ -2,10 +2,36 @@
 // Validates arguments before any launch, carves the caller's workspace and dispatches to the kernels.
 #include <stdint.h>
 
+#include <mutex>
+
 #include "moe_formats.h"
 #include "moe_internal.h"
 
+// Workspace of moe_experts_run_static: a file-scope device array, one copy per GPU the library runs on (held until
+// the process ends). Host code never passes its name to a kernel or a copy: the name is a host-side stand-in, and
+// the array's device address on each GPU comes from hipGetSymbolAddress (static_scratch below).
+static __device__ __align__(256) uint8_t scratch[MOE_STATIC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// the device address of `scratch` on the current device, looked up on the first call there
+int static_scratch(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return MOE_ERR_LAUNCH;
+    if (dev < 0 || dev >= kMaxDevices) return MOE_ERR_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MOE_ERR_LAUNCH;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MOE_OK;
+}
 
 constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
@@ -161,6 +187,19 @@ int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const in
                     size_t workspace_bytes, void* stream) {
     return moe_experts_run_stages(w, x, x_dtype, idx, wts, T, k, act, path, nored, y, y_dtype, residual, workspace,
                                   workspace_bytes, MOE_STAGE_ALL, stream);
+}
+
+int moe_experts_run_static(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,
+                           int T, int k, int act, int path, int nored, void* y, int y_dtype, const void* residual,
+                           void* stream) {
+    void* ws = nullptr;
+    int rc = static_scratch(&ws);   // first call on a device: the lookup; later calls: a table read
+    if (rc) return rc;
+    if (T == 0) return MOE_OK;
+    if (!w || T < 0 || k < 1) return MOE_ERR_ARG;
+    if (moe_experts_workspace_bytes(w, T, k, path) > MOE_STATIC_SCRATCH_BYTES) return MOE_ERR_WORKSPACE;
+    return moe_experts_run_stages(w, x, x_dtype, idx, wts, T, k, act, path, nored, y, y_dtype, residual, ws,
+                                  MOE_STATIC_SCRATCH_BYTES, MOE_STAGE_ALL, stream);
 }
 
 int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,
