@@ -148,8 +148,10 @@ int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offset
  * metal_mxfp4_moe.py:474-512, metal_mxfp4_gptoss.py:129-167):
  *   y[t] = residual[t] + sum_j wts[t,j] * ( down_e( act(gate_e x_t + bg_e, up_e x_t + bu_e) ) + bd_e ),
  *   e = idx[t,j]; residual optional (NULL = 0).
- *   x [T, d] of x_dtype (MOE_DTYPE_BF16); y and residual [T, d] of y_dtype (MOE_DTYPE_BF16 as the
- *   reference returns x.dtype, or MOE_DTYPE_F32 for the unrounded result); idx [T, k] int32; wts [T, k] fp32.
+ *   x [T, d] of x_dtype (MOE_DTYPE_BF16, MOE_DTYPE_F16 or MOE_DTYPE_F32: fp16 and fp32 x enter the gate/up
+ *   products exactly, as 2 or 3 bf16 planes whose sum is x; the reference's fp32 path is its exact scalar tiles,
+ *   metal_q4_moe.py:62-64); y and residual [T, d] of y_dtype (any of the three; the reference returns x.dtype,
+ *   MOE_DTYPE_F32 gives the unrounded result); idx [T, k] int32; wts [T, k] fp32.
  *   path: MOE_PATH_*; nored = 1 writes the unweighted per-slot outputs y[T*k, d] instead (reference
  *   run_slots / NORED, metal_q4_moe.py:49-51; per-slot path only, residual must be NULL).
  *   Accumulation in fp32; the GLU output h is kept between the two launches as an unevaluated sum of two
@@ -174,7 +176,7 @@ size_t moe_experts_workspace_bytes(const moe_experts_t* w, int T, int k, int pat
  * device array inside the library, MOE_STATIC_SCRATCH_BYTES on each GPU it runs on, held until the process ends.
  * Arguments, results and errors as moe_experts_run; calls whose workspace (moe_experts_workspace_bytes) exceeds
  * MOE_STATIC_SCRATCH_BYTES return MOE_ERR_WORKSPACE before any launch (the Qwen3-30B-A3B shape fits calls of up
- * to 115 tokens).
+ * to 110 tokens).
  * It allocates nothing. Every call on one GPU uses that GPU's one array, which keeps the last call's contents (no
  * call needs particular contents): calls that overlap on one GPU (other streams, other threads) race, and the
  * caller must order them. The first call on each device looks up the array's address (hipGetSymbolAddress);

@@ -43,7 +43,7 @@ int resolve_path(int path, int T) {
 }
 
 struct Layout {
-    size_t h, yp, x16, xexp, counts, offsets, sorted, active, meta, items, items2, total;
+    size_t h, xp, yp, x16, xexp, counts, offsets, sorted, active, meta, items, items2, total;
 };
 
 Layout layout(const moe_experts_t* w, int T, int k, int path) {
@@ -52,6 +52,8 @@ Layout layout(const moe_experts_t* w, int T, int k, int path) {
     size_t off = 0;
     L.h = off;
     off += align_up(nslots * (size_t)w->F * 2) * 2;   // hi and lo planes
+    L.xp = off;                                       // fp16 / fp32 x as up to 3 bf16 planes
+    off += align_up((size_t)3 * T * w->d * 2);
     if (resolve_path(path, T) == MOE_PATH_GROUPED) {
         L.yp = off;
         off += align_up(nslots * (size_t)w->d * 4 * 4);   // four planes: the dense down projection may split K
@@ -168,15 +170,14 @@ int moe_shared_experts_run(const moe_experts_t* ws, const void* x, int x_dtype, 
     if (ws->E > 32 || T < 0) return MOE_ERR_ARG;
     if (T == 0) return MOE_OK;
     if (!x || !y || !workspace) return x && y ? MOE_ERR_WORKSPACE : MOE_ERR_ARG;
-    if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;
+    if (x_dtype < MOE_DTYPE_BF16 || x_dtype > MOE_DTYPE_F32) return MOE_ERR_DTYPE;
     if (!aligned16(x) || (gate && !aligned16(gate)) || !aligned16(workspace)) return MOE_ERR_ALIGN;
     const size_t base = layout(ws, T, ws->E, MOE_PATH_AUTO).total;
     if (workspace_bytes < moe_shared_experts_workspace_bytes(ws, T)) return MOE_ERR_WORKSPACE;
     const size_t n = (size_t)T * ws->E;
     int32_t* idx = (int32_t*)((char*)workspace + base);
     float* wts = (float*)((char*)workspace + base + align_up(n * 4));
-    rc = moe::launch_shared_route((const uint16_t*)x, (const uint16_t*)gate, T, ws->d, ws->E, idx, wts,
-                                  (hipStream_t)stream);
+    rc = moe::launch_shared_route(x, x_dtype, (const uint16_t*)gate, T, ws->d, ws->E, idx, wts, (hipStream_t)stream);
     if (rc) return rc;
     return moe_experts_run_stages(ws, x, x_dtype, idx, wts, T, ws->E, act, MOE_PATH_AUTO, 0, y, y_dtype, residual,
                                   workspace, base, MOE_STAGE_ALL, stream);
@@ -209,8 +210,8 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     int rc = check_experts(w);
     if (rc) return rc;
     if (T < 0 || k < 1 || act < 0 || act > 2 || path < 0 || path > 2) return MOE_ERR_ARG;
-    if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;
-    if (y_dtype != MOE_DTYPE_BF16 && y_dtype != MOE_DTYPE_F32) return MOE_ERR_DTYPE;
+    if (x_dtype < MOE_DTYPE_BF16 || x_dtype > MOE_DTYPE_F32) return MOE_ERR_DTYPE;
+    if (y_dtype < MOE_DTYPE_BF16 || y_dtype > MOE_DTYPE_F32) return MOE_ERR_DTYPE;
     const int rpath = resolve_path(path, T);
     if (nored && (rpath != MOE_PATH_SLOTS || residual)) return MOE_ERR_ARG;
     if (T == 0) return MOE_OK;
@@ -231,7 +232,19 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     a.act = act;
     a.nored = nored;
     a.y = y;
-    a.y32 = y_dtype == MOE_DTYPE_F32;
+    a.ydt = y_dtype;
+    if (x_dtype == MOE_DTYPE_BF16) {
+        a.xb = (const uint16_t*)x;
+        a.nx = 1;
+    } else {   // fp16 / fp32: the gate/up stage reads x as 2 / 3 bf16 planes (exact)
+        a.xb = (const uint16_t*)(ws + L.xp);
+        a.nx = x_dtype == MOE_DTYPE_F16 ? 2 : 3;
+        a.xplane = (size_t)T * w->d;
+        if (stages & MOE_STAGE_GATE_UP) {
+            const int rc2 = moe::launch_x_planes(x, x_dtype, T, w->d, (uint16_t*)(ws + L.xp), (hipStream_t)stream);
+            if (rc2) return rc2;
+        }
+    }
     a.residual = residual;
     a.hhi = (uint16_t*)(ws + L.h);
     a.hlo = a.hhi + align_up((size_t)T * k * w->F * 2) / 2;

@@ -60,12 +60,64 @@ __device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t bas
     hlo[i] = f32_to_bf16(v - bf16_to_f32(hi));
 }
 
-__device__ __forceinline__ void store_y(void* y, size_t i, float v, int y32) {
-    if (y32) reinterpret_cast<float*>(y)[i] = v;
+// outputs and residuals: ydt = MOE_DTYPE_BF16, MOE_DTYPE_F16 or MOE_DTYPE_F32 (round to nearest even)
+__device__ __forceinline__ void store_y(void* y, size_t i, float v, int ydt) {
+    if (ydt == MOE_DTYPE_F32) reinterpret_cast<float*>(y)[i] = v;
+    else if (ydt == MOE_DTYPE_F16) reinterpret_cast<_Float16*>(y)[i] = (_Float16)v;
     else reinterpret_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
 }
-__device__ __forceinline__ float load_y(const void* y, size_t i, int y32) {
-    return y32 ? reinterpret_cast<const float*>(y)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
+__device__ __forceinline__ float load_y(const void* y, size_t i, int ydt) {
+    if (ydt == MOE_DTYPE_F32) return reinterpret_cast<const float*>(y)[i];
+    if (ydt == MOE_DTYPE_F16) return (float)reinterpret_cast<const _Float16*>(y)[i];
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
+}
+
+// ============================================================================ activation planes
+// fp16 and fp32 activations enter the expert kernels as NX bf16 planes whose sum is the value exactly: each plane
+// takes the next 8 significant bits by truncation (plane = the top 16 bits of the remainder's fp32 pattern;
+// the remainder after it is exact in fp32), so fp16 (11 bits) needs 2 planes and fp32 (24 bits) 3. inf and NaN
+// go whole into plane 0 (NaN quieted), the other planes 0. The kernels run one product per plane against the
+// same decoded weights and sum them in fp32, so every input bit reaches the accumulator.
+// planes [NX][n] bf16, plane = n elements apart; one thread per 8 elements (n % 8 == 0).
+template <int XDT>
+__global__ void __launch_bounds__(256) k_x_planes(const void* __restrict__ x, uint16_t* __restrict__ planes,
+                                                  size_t n8, size_t plane) {
+    constexpr int NX = XDT == MOE_DTYPE_F16 ? 2 : 3;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    float v[8];
+    if (XDT == MOE_DTYPE_F16) {
+        const uint4 r = reinterpret_cast<const uint4*>(x)[i];
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] & 0xFFFFu));
+            v[2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] >> 16));
+        }
+    } else {
+        const float4 a = reinterpret_cast<const float4*>(x)[2 * i], b = reinterpret_cast<const float4*>(x)[2 * i + 1];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    }
+    uint32_t bits[8][NX];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        float r = v[e];
+        const bool fin = __builtin_isfinite(r);
+#pragma unroll
+        for (int p = 0; p < NX; ++p) {
+            const uint32_t top = __float_as_uint(r) & 0xFFFF0000u;
+            bits[e][p] = fin ? top >> 16 : (p == 0 ? (uint32_t)f32_to_bf16(r) : 0u);
+            r = fin ? r - __uint_as_float(top) : 0.f;
+        }
+    }
+    uint32_t out[NX][4];
+#pragma unroll
+    for (int p = 0; p < NX; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) out[p][q] = bits[2 * q][p] | (bits[2 * q + 1][p] << 16);
+#pragma unroll
+    for (int p = 0; p < NX; ++p)
+        reinterpret_cast<uint4*>(planes + p * plane)[i] = make_uint4(out[p][0], out[p][1], out[p][2], out[p][3]);
 }
 
 
@@ -78,9 +130,11 @@ __device__ __forceinline__ float load_y(const void* y, size_t i, int y32) {
 // pass (L2), then every weight chunk and metadata word of the pass, all before the first use; the math then
 // runs in load order, so it overlaps with the loads still arriving. h is written as the two pre-paired bf16
 // planes hi/lo (store_h).
-template <class FMT, int R, int NCH>
+// HX activation planes (bf16 x: 1; fp16 / fp32 x: k_x_planes' 2 or 3 planes, xplane elements apart): every plane
+// is dotted with the same decoded chunk and the products add in fp32.
+template <class FMT, int R, int NCH, int HX>
 __global__ void __launch_bounds__(256)
-k_gate_up_rows(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
+k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
                const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
                int d, int F, int E, int Q, int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
     static_assert(R <= 16, "results live in lanes 48..63");
@@ -109,13 +163,14 @@ k_gate_up_rows(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, co
     for (int c0 = 0; c0 < nchunk; c0 += 64 * NCH) {
         int ch[NCH];
         bool cv[NCH];
-        uint32_t xw[NCH][16];
+        uint32_t xw[HX][NCH][16];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             ch[c] = c0 + 64 * c + lane;
             cv[c] = ch[c] < nchunk;
             ch[c] = cv[c] ? ch[c] : nchunk - 1;
-            load_x32(xr + 32 * ch[c], xw[c]);
+#pragma unroll
+            for (int h = 0; h < HX; ++h) load_x32(xr + h * xplane + 32 * ch[c], xw[h][c]);
         }
         uint4 wg[R][NCH], wu[R][NCH];
         uint32_t mg[R][NCH], mu[R][NCH];
@@ -129,22 +184,32 @@ k_gate_up_rows(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, co
                 mu[r][c] = FMT::meta(ub0 + r * rb, d, ch[c]);
             }
         __builtin_amdgcn_sched_barrier(0);   // every load of the pass is in flight before any use
-        uint32_t xp[NCH][16];
+        uint32_t xp[HX][NCH][16];
         float xs[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-            pair_x32(xw[c], xp[c]);
-            xs[c] = FMT::XSUM ? sum_x32(xw[c]) : 0.f;
+            xs[c] = 0.f;
+#pragma unroll
+            for (int h = 0; h < HX; ++h) {
+                pair_x32(xw[h][c], xp[h][c]);
+                xs[c] = FMT::XSUM ? sum_x32(xw[h][c]) + xs[c] : 0.f;
+            }
         }
+        auto dotx = [&](const uint32_t (&qp)[16], int c) __attribute__((always_inline)) {
+            float d = 0.f;
+#pragma unroll
+            for (int h = 0; h < HX; ++h) d = dot16(qp, xp[h][c], d);
+            return d;
+        };
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 uint32_t qp[16];
                 FMT::decode(wg[r][c], qp);
-                const float dg = FMT::fold(0.f, mg[r][c], dot16(qp, xp[c], 0.f), xs[c]);
+                const float dg = FMT::fold(0.f, mg[r][c], dotx(qp, c), xs[c]);
                 FMT::decode(wu[r][c], qp);
-                const float du = FMT::fold(0.f, mu[r][c], dot16(qp, xp[c], 0.f), xs[c]);
+                const float du = FMT::fold(0.f, mu[r][c], dotx(qp, c), xs[c]);
                 ag[r] += cv[c] ? dg : 0.f;
                 au[r] += cv[c] ? du : 0.f;
             }
@@ -178,7 +243,7 @@ template <class FMT, int NC, int RR, int NW>
 __global__ void __launch_bounds__(64 * NW)
 k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
             const float* __restrict__ bd, const int32_t* __restrict__ idx, const float* __restrict__ wts, int k,
-            int D, int F, int E, int lgL, int nored, int y32, const void* __restrict__ resid,
+            int D, int F, int E, int lgL, int nored, int ydt, const void* __restrict__ resid,
             void* __restrict__ y) {
     constexpr int SL = sum_lane<64>();
     constexpr int RB = NW * RR;
@@ -283,7 +348,7 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
             float v = acc[i] + bdv[i];
             // sum over the L lanes of the slot: xor butterfly within the group
             for (int s2 = 1; s2 < L; s2 <<= 1) v += __shfl_xor(v, s2, 64);
-            if (p == 0 && jv && n < D) store_y(y, (size_t)slot * D + n, v, y32);
+            if (p == 0 && jv && n < D) store_y(y, (size_t)slot * D + n, v, ydt);
         }
         return;
     }
@@ -294,7 +359,7 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
         const float v = sum_lanes<64>((acc[i] + bdv[i]) * wj);
         if (lane == SL && n < D) {
             const size_t o = (size_t)t * D + n;
-            store_y(y, o, resid ? v + load_y(resid, o, y32) : v, y32);
+            store_y(y, o, resid ? v + load_y(resid, o, ydt) : v, ydt);
         }
     }
 }
@@ -302,9 +367,9 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
 // ============================================================================ per-slot gate / up
 // grid (ceil(F / (4*NR)), T*k), block 256: wave w of block (bx, slot) computes gate and up rows
 // row0 .. row0+NR-1 of expert idx[slot]; the 64 lanes stride over the 16-byte chunks of the rows.
-template <class FMT, int ACT, int NR>
+template <class FMT, int ACT, int NR, int HX>
 __global__ void __launch_bounds__(256)
-k_gate_up_slots(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
+k_gate_up_slots(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
                 const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
                 int d, int F, int E, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -326,7 +391,7 @@ k_gate_up_slots(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, c
             const bool cv = c0 + lane < nchunk;
             const int c = cv ? c0 + lane : nchunk - 1;
             uint4 wg[NR], wu[NR];
-            uint32_t mg[NR], mu[NR], xw[16];
+            uint32_t mg[NR], mu[NR], xw[HX][16];
 #pragma unroll
             for (int r = 0; r < NR; ++r) {
                 const size_t ro = (size_t)min(r, F - 1 - row0) * rb;
@@ -335,19 +400,30 @@ k_gate_up_slots(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, c
                 mg[r] = FMT::meta(gb0 + ro, d, c);
                 mu[r] = FMT::meta(ub0 + ro, d, c);
             }
-            load_x32(xr + 32 * c, xw);
+#pragma unroll
+            for (int h = 0; h < HX; ++h) load_x32(xr + h * xplane + 32 * c, xw[h]);
             __builtin_amdgcn_sched_barrier(0);   // every load above is in flight before any use
-            uint32_t xp[16];
-            pair_x32(xw, xp);
-            const float xs = FMT::XSUM ? sum_x32(xw) : 0.f;
+            uint32_t xp[HX][16];
+            float xs = 0.f;
+#pragma unroll
+            for (int h = 0; h < HX; ++h) {
+                pair_x32(xw[h], xp[h]);
+                xs = FMT::XSUM ? sum_x32(xw[h]) + xs : 0.f;
+            }
+            auto dotx = [&](const uint32_t (&qp)[16]) __attribute__((always_inline)) {
+                float dd = 0.f;
+#pragma unroll
+                for (int h = 0; h < HX; ++h) dd = dot16(qp, xp[h], dd);
+                return dd;
+            };
             if (cv) {
 #pragma unroll
                 for (int r = 0; r < NR; ++r) {
                     uint32_t qp[16];
                     FMT::decode(wg[r], qp);
-                    ag[r] = FMT::fold(ag[r], mg[r], dot16(qp, xp, 0.f), xs);
+                    ag[r] = FMT::fold(ag[r], mg[r], dotx(qp), xs);
                     FMT::decode(wu[r], qp);
-                    au[r] = FMT::fold(au[r], mu[r], dot16(qp, xp, 0.f), xs);
+                    au[r] = FMT::fold(au[r], mu[r], dotx(qp), xs);
                 }
             }
         }
@@ -382,7 +458,7 @@ template <class FMT, int LPR, int NC>
 __global__ void __launch_bounds__(512)
 k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
              const float* __restrict__ bd, const int32_t* __restrict__ idx, const float* __restrict__ wts, int k, int D,
-             int F, int E, int nored, int y32, const void* __restrict__ resid, void* __restrict__ y) {
+             int F, int E, int nored, int ydt, const void* __restrict__ resid, void* __restrict__ y) {
     constexpr int RPW = 64 / LPR;
     constexpr int SL = sum_lane<LPR>();
     __shared__ float red[8][RPW];
@@ -400,7 +476,7 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
         const int slot = t * k + j;
         const int e = idx[slot];
         if ((unsigned)e >= (unsigned)E) {
-            if (nored && psub == SL && row_ok) store_y(y, (size_t)slot * D + n, 0.f, y32);
+            if (nored && psub == SL && row_ok) store_y(y, (size_t)slot * D + n, 0.f, ydt);
             continue;
         }
         const uint8_t* rowp = Dw + ((size_t)e * D + nn) * rb;
@@ -440,7 +516,7 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
         acc = sum_lanes<LPR>(acc);
         if (bd) acc += bd[(size_t)e * D + nn];
         if (nored) {
-            if (psub == SL && row_ok) store_y(y, (size_t)slot * D + n, acc, y32);
+            if (psub == SL && row_ok) store_y(y, (size_t)slot * D + n, acc, ydt);
         } else {
             yacc = __builtin_fmaf(wts[slot], acc, yacc);
         }
@@ -454,7 +530,7 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
             float v = red[0][lane];
             for (int w = 1; w < nw; ++w) v += red[w][lane];
             const size_t o = (size_t)t * D + n2;
-            store_y(y, o, resid ? v + load_y(resid, o, y32) : v, y32);
+            store_y(y, o, resid ? v + load_y(resid, o, ydt) : v, ydt);
         }
     }
 }
@@ -469,7 +545,7 @@ __global__ void __launch_bounds__(256)
 k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t* __restrict__ idx,
           const float* __restrict__ wts,
           const float* __restrict__ bd, int E, const void* __restrict__ resid, void* __restrict__ y, int T, int k,
-          int D, int y32) {
+          int D, int ydt) {
     constexpr int KC = 8;
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total4 = (size_t)T * D / 4;
@@ -522,7 +598,7 @@ k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t
             acc.w = ok ? __builtin_fmaf(w[j], u.w, acc.w) : acc.w;
         }
     }
-    if (y32) {
+    if (ydt == MOE_DTYPE_F32) {
         if (resid) {
             const float4 r = reinterpret_cast<const float4*>(resid)[i4];
             acc.x += r.x;
@@ -531,6 +607,18 @@ k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t
             acc.w += r.w;
         }
         reinterpret_cast<float4*>(y)[i4] = acc;
+        return;
+    }
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    if (ydt == MOE_DTYPE_F16) {
+        if (resid) {
+            const h4 r = reinterpret_cast<const h4*>(resid)[i4];
+            acc.x += (float)r[0];
+            acc.y += (float)r[1];
+            acc.z += (float)r[2];
+            acc.w += (float)r[3];
+        }
+        reinterpret_cast<h4*>(y)[i4] = h4{(_Float16)acc.x, (_Float16)acc.y, (_Float16)acc.z, (_Float16)acc.w};
         return;
     }
     if (resid) {
@@ -561,13 +649,16 @@ void launch_gu_slots(const ExpertsArgs& a, int NR) {
     const moe_experts_t* w = a.w;
     const ProjPtrs P = ptrs(w);
     const int nslots = a.T * a.k;
+    if (a.nx > 1) NR = 1;   // planes of fp16 / fp32 activations: one row pair per wave
     dim3 grid((w->F + 4 * NR - 1) / (4 * NR), nslots);
-#define MOE_GUS(R)                                                                                              \
-    k_gate_up_slots<FMT, ACT, R><<<grid, 256, 0, a.st>>>((const uint16_t*)a.x, P.G, P.U, w->gate.bias, w->up.bias, \
-                                                          a.idx, a.k, w->d, w->F, w->E, a.hhi, a.hlo)
-    if (NR == 4) MOE_GUS(4);
-    else if (NR == 2) MOE_GUS(2);
-    else MOE_GUS(1);
+#define MOE_GUS(R, H)                                                                                           \
+    k_gate_up_slots<FMT, ACT, R, H><<<grid, 256, 0, a.st>>>(a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias,  \
+                                                             a.idx, a.k, w->d, w->F, w->E, a.hhi, a.hlo)
+    if (a.nx == 3) MOE_GUS(1, 3);
+    else if (a.nx == 2) MOE_GUS(1, 2);
+    else if (NR == 4) MOE_GUS(4, 1);
+    else if (NR == 2) MOE_GUS(2, 1);
+    else MOE_GUS(1, 1);
 #undef MOE_GUS
 }
 
@@ -586,7 +677,7 @@ void launch_dn_slots(const ExpertsArgs& a) {
     dim3 grid((w->d + rpw - 1) / rpw, a.T);
 #define MOE_DNS(L, C)                                                                                           \
     k_down_slots<FMT, L, C><<<grid, 64 * nw, 0, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.idx, a.wts, a.k,      \
-                                                         w->d, w->F, w->E, a.nored, a.y32, a.residual, a.y)
+                                                         w->d, w->F, w->E, a.nored, a.ydt, a.residual, a.y)
     if (lpr == 4) MOE_DNS(4, 3);
     else if (lpr == 8) MOE_DNS(8, 3);
     else if (lpr == 16) MOE_DNS(16, 3);
@@ -597,6 +688,9 @@ void launch_dn_slots(const ExpertsArgs& a) {
 }
 
 // ---------------------------------------------------------------- balanced per-slot kernels
+#ifndef MOE_GU_MIN_WAVES
+#define MOE_GU_MIN_WAVES 2048   // gate/up: fewest waves a launch should have before rows per wave grow
+#endif
 // gate/up: R row pairs per wave (R divides F), as many as keeps >= 2048 waves in flight (2 blocks per CU on
 // 256 CUs); NCH chunks per lane per pass (2 when a row has more than 64 chunks).
 template <class FMT, int NCH>
@@ -604,25 +698,33 @@ int launch_gu_rows_n(const ExpertsArgs& a, int R) {
     const moe_experts_t* w = a.w;
     const ProjPtrs P = ptrs(w);
     const int Q = a.T * a.k * w->F;
+    if (a.nx > 1) R = w->F % 2 == 0 && Q / 2 >= MOE_GU_MIN_WAVES ? 2 : 1;   // fp16 / fp32 planes: R <= 2
     const int grid = (Q / R + 3) / 4;
-#define MOE_GUR(RR)                                                                                              \
-    k_gate_up_rows<FMT, RR, NCH><<<grid, 256, 0, a.st>>>((const uint16_t*)a.x, P.G, P.U, w->gate.bias, w->up.bias, \
-                                                        a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, a.hlo)
+#define MOE_GUR(RR, H)                                                                                           \
+    k_gate_up_rows<FMT, RR, NCH, H><<<grid, 256, 0, a.st>>>(a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias,   \
+                                                           a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, a.hlo)
+    if (a.nx > 1) {
+        if (a.nx == 3) {
+            if (R == 2) MOE_GUR(2, 3);
+            else MOE_GUR(1, 3);
+        } else {
+            if (R == 2) MOE_GUR(2, 2);
+            else MOE_GUR(1, 2);
+        }
+        return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+    }
     switch (R) {
-        case 8: MOE_GUR(8); break;
-        case 6: MOE_GUR(6); break;
-        case 4: MOE_GUR(4); break;
-        case 3: MOE_GUR(3); break;
-        case 2: MOE_GUR(2); break;
-        default: MOE_GUR(1); break;
+        case 8: MOE_GUR(8, 1); break;
+        case 6: MOE_GUR(6, 1); break;
+        case 4: MOE_GUR(4, 1); break;
+        case 3: MOE_GUR(3, 1); break;
+        case 2: MOE_GUR(2, 1); break;
+        default: MOE_GUR(1, 1); break;
     }
 #undef MOE_GUR
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-#ifndef MOE_GU_MIN_WAVES
-#define MOE_GU_MIN_WAVES 2048   // gate/up: fewest waves a launch should have before rows per wave grow
-#endif
 #ifndef MOE_GU_RMAX
 #define MOE_GU_RMAX 8
 #endif
@@ -670,7 +772,7 @@ int launch_dn_rows_k(const ExpertsArgs& a, int lgL) {
     }
     dim3 grid((w->d + NW * RR - 1) / (NW * RR), a.T);
     kern<<<grid, 64 * NW, lds, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.idx, a.wts, a.k, w->d, w->F, w->E, lgL,
-                                   a.nored, a.y32, a.residual, a.y);
+                                   a.nored, a.ydt, a.residual, a.y);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
@@ -744,12 +846,21 @@ int run_experts_slots(const ExpertsArgs& a) {
     return a.w->fmt == MOE_FMT_INT4_G64 ? run_slots_fmt<FmtInt4>(a) : run_slots_fmt<FmtMxfp4>(a);
 }
 
+int launch_x_planes(const void* x, int xdt, int T, int d, uint16_t* planes, hipStream_t st) {
+    const size_t n = (size_t)T * d, n8 = n / 8;
+    if (n8 == 0) return 0;
+    dim3 grid((unsigned)((n8 + 255) / 256));
+    if (xdt == MOE_DTYPE_F16) k_x_planes<MOE_DTYPE_F16><<<grid, 256, 0, st>>>(x, planes, n8, n);
+    else k_x_planes<MOE_DTYPE_F32><<<grid, 256, 0, st>>>(x, planes, n8, n);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
 int launch_combine(const float* yp, int nplanes, size_t plane, const int32_t* idx, const float* wts, const float* bd, int E,
-                   const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st) {
+                   const void* residual, void* y, int T, int k, int d, int ydt, hipStream_t st) {
     const size_t total4 = (size_t)T * d / 4;
     if (total4 == 0) return 0;
     dim3 grid((unsigned)((total4 + 255) / 256));
-    k_combine<<<grid, 256, 0, st>>>(yp, nplanes, plane, idx, wts, bd, E, residual, y, T, k, d, y32);
+    k_combine<<<grid, 256, 0, st>>>(yp, nplanes, plane, idx, wts, bd, E, residual, y, T, k, d, ydt);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

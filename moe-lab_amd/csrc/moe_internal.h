@@ -19,7 +19,7 @@ int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* off
                  int32_t* items2 = nullptr);
 // upper bound of the pass count: sum over experts of ceil(count / P) <= n / P + (experts with a count)
 inline int max_passes(int n, int E, int P) { return (n + P - 1) / P + (n < E ? n : E); }
-int launch_shared_route(const uint16_t* x, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
+int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
                         hipStream_t st);
 
 // grouping scratch inside an experts workspace
@@ -40,8 +40,11 @@ struct ExpertsArgs {
     const int32_t* idx;
     const float* wts;
     int T, k, act, nored;
-    void* y;              // [T, d] (or [T*k, d] when nored), fp32 when y32 else bf16
-    int y32;
+    const uint16_t* xb;   // x as bf16 planes: x itself (bf16, nx = 1) or k_x_planes' planes of fp16 / fp32 x
+    int nx;               // 1, 2 (fp16) or 3 (fp32)
+    size_t xplane;        // elements between planes (T * d)
+    void* y;              // [T, d] (or [T*k, d] when nored), of dtype ydt
+    int ydt;              // MOE_DTYPE_BF16, MOE_DTYPE_F16 or MOE_DTYPE_F32
     const void* residual; // same dtype as y, or NULL
     uint16_t* hhi;        // GLU output h = hi + lo, two bf16 planes [T*k, F]
     uint16_t* hlo;
@@ -62,6 +65,8 @@ int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tile
 // combine (moe_experts.hip): y[t] = residual[t] + sum_j wts[t*k + j] * (sum over the nplanes planes of yp[t*k + j]
 // + bd[idx[t*k + j]])
 int launch_combine(const float* yp, int nplanes, size_t plane, const int32_t* idx, const float* wts, const float* bd, int E,
-                   const void* residual, void* y, int T, int k, int d, int y32, hipStream_t st);
+                   const void* residual, void* y, int T, int k, int d, int ydt, hipStream_t st);
+// fp16 / fp32 activations x [T, d] -> bf16 planes [2 or 3][T, d] whose sum is x exactly (moe_experts.hip)
+int launch_x_planes(const void* x, int xdt, int T, int d, uint16_t* planes, hipStream_t st);
 
 }  // namespace moe

@@ -330,23 +330,37 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
 // token: lane l dots the 8-element chunks l, l + 64, ... in element order, the lane sums are added as the DPP
 // tree of sum_lanes<64>, lanes 48..63 hold the total.
 __global__ void __launch_bounds__(256)
-shared_route(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate, int T, int d, int S,
+shared_route(const void* __restrict__ x, int xdt, const uint16_t* __restrict__ gate, int T, int d, int S,
              int32_t* __restrict__ idx, float* __restrict__ wts) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + wave;
     if (t >= T) return;
     float g = 1.f;
     if (gate) {
-        const uint16_t* xr = x + (size_t)t * d;
         float acc = 0.f;
         for (int c = lane; c < (d >> 3); c += 64) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xr + 8 * c);
+            float xv[8];   // x of any of the three dtypes, as fp32 (exact)
+            if (xdt == MOE_DTYPE_F32) {
+                const float4* xr = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + (size_t)t * d);
+                const float4 a = xr[2 * c], b = xr[2 * c + 1];
+                xv[0] = a.x, xv[1] = a.y, xv[2] = a.z, xv[3] = a.w, xv[4] = b.x, xv[5] = b.y, xv[6] = b.z, xv[7] = b.w;
+            } else {
+                const uint4 r = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + (size_t)t * d)[c];
+                const uint32_t xw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    xv[2 * i] = xdt == MOE_DTYPE_F16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)(xw[i] & 0xFFFFu))
+                                                     : bf16lo(xw[i]);
+                    xv[2 * i + 1] = xdt == MOE_DTYPE_F16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)(xw[i] >> 16))
+                                                         : bf16hi(xw[i]);
+                }
+            }
             const uint4 gv = *reinterpret_cast<const uint4*>(gate + 8 * c);
-            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+            const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                acc = __builtin_fmaf(bf16lo(xw[i]), bf16lo(gw[i]), acc);
-                acc = __builtin_fmaf(bf16hi(xw[i]), bf16hi(gw[i]), acc);
+                acc = __builtin_fmaf(xv[2 * i], bf16lo(gw[i]), acc);
+                acc = __builtin_fmaf(xv[2 * i + 1], bf16hi(gw[i]), acc);
             }
         }
         acc = sum_lanes<64>(acc);
@@ -391,10 +405,10 @@ int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, fl
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-int launch_shared_route(const uint16_t* x, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
+int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
                         hipStream_t st) {
     if (T <= 0) return 0;
-    shared_route<<<(T + 3) / 4, 256, 0, st>>>(x, gate, T, d, S, idx, wts);
+    shared_route<<<(T + 3) / 4, 256, 0, st>>>(x, xdt, gate, T, d, S, idx, wts);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

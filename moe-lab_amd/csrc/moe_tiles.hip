@@ -63,8 +63,9 @@ constexpr int TL_BPAD = 4 * TL_KC + 1;   // 16-byte pieces per staged token (8 i
 constexpr int TL_GMAX = TL_KC;           // scale groups per slice at most (MXFP4: one per chunk)
 
 struct TileArgs {
-    const uint16_t* actv;  // gate/up: x [T, K]; down: h [T*k, K] (bf16; the hi plane of h = hi + lo)
+    const uint16_t* actv;  // gate/up: x [T, K] (bf16 plane 0); down: h [T*k, K] (bf16; the hi plane of h = hi + lo)
     const uint16_t* actv2; // down: the lo plane of h
+    size_t act_plane;      // gate/up with fp16 / fp32 x: elements between x's bf16 planes (k_x_planes)
     int act_div;           // activation row of slot p: p / act_div (k for gate/up, 1 for down)
     const uint8_t* W0;     // gate (or down) row records [E, N, rb]
     const uint8_t* W1;     // up row records (gate/up only)
@@ -109,12 +110,12 @@ __device__ __forceinline__ uint4 pair8(uint4 v) {
 #ifndef MOE_TILE_MINB
 #define MOE_TILE_MINB 1   // blocks per CU the register allocation must allow
 #endif
-template <class FMT, int NPROJ, int NT>
+template <class FMT, int NPROJ, int NT, int HX = 1>
 __global__ void __launch_bounds__(256, MOE_TILE_MINB)
 k_tile(TileArgs a) {
     constexpr int NTOK = 16 * NT;
     constexpr bool INT4 = FMT::XSUM;
-    constexpr int HL = NPROJ == 2 ? 1 : 2;   // activation planes
+    constexpr int HL = NPROJ == 2 ? HX : 2;   // activation planes: x's (1, or 2-3 for fp16 / fp32 x), h = hi + lo
     __shared__ uint32_t sA[NPROJ][TL_ROWS][TL_APAD];
     __shared__ float sM[NPROJ][TL_ROWS][TL_GMAX];   // int4: (s, b - 128 s) of the slice's 4 groups; MXFP4: 8 scales
     __shared__ uint4 sB[HL][NTOK][TL_BPAD];
@@ -188,7 +189,8 @@ k_tile(TileArgs a) {
                 for (int hl = 0; hl < HL; ++hl) {
                     rbv[hl][i] = make_uint4(0u, 0u, 0u, 0u);
                     if (bval[i] && k0 < K)
-                        rbv[hl][i] = *reinterpret_cast<const uint4*>((hl ? a.actv2 : a.actv) + brow[i] + k0);
+                        rbv[hl][i] = *reinterpret_cast<const uint4*>(
+                            (NPROJ == 2 ? a.actv + hl * a.act_plane : (hl ? a.actv2 : a.actv)) + brow[i] + k0);
                 }
             }
         };
@@ -375,11 +377,11 @@ __host__ __device__ constexpr int tile_slice_bytes() {
 
 // H16O (int4 gate/up before a dense down): h leaves as fp16 h16 = h 2^-e with e per (slot, 32-row chunk), the
 // layout the dense down reads after k_h16_fix, instead of the two bf16 planes.
-template <class FMT, int NPROJ, int NT, int RT, int D, bool H16O = false>
+template <class FMT, int NPROJ, int NT, int RT, int D, bool H16O = false, int HX = 1>
 __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     static_assert(!H16O || (NPROJ == 2 && RT % 2 == 0), "h16 output: gate/up, whole 32-row chunks per wave");
     constexpr bool INT4 = FMT::XSUM;
-    constexpr int HL = NPROJ == 2 ? 1 : 2;   // activation planes: x, or h = hi + lo
+    constexpr int HL = NPROJ == 2 ? HX : 2;   // activation planes: x's (1, or 2-3 for fp16 / fp32 x), h = hi + lo
     constexpr int SB = tile_slice_bytes<FMT>();
     if ((int)blockIdx.y >= a.meta[a.nidx]) return;   // one pass of the work list per workgroup row
     const int e = a.items[3 * blockIdx.y], tok0 = a.items[3 * blockIdx.y + 1] * 16 * NT;
@@ -410,8 +412,9 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
             xo[t] = (uint32_t)(slotA[t] / a.act_div) * (uint32_t)K * 2u;
         }
         const uint8_t* xbase[HL];
-        xbase[0] = reinterpret_cast<const uint8_t*>(a.actv);
-        if (HL == 2) xbase[HL - 1] = reinterpret_cast<const uint8_t*>(a.actv2);
+#pragma unroll
+        for (int hl = 0; hl < HL; ++hl)
+            xbase[hl] = reinterpret_cast<const uint8_t*>(NPROJ == 2 ? a.actv + hl * a.act_plane : (hl ? a.actv2 : a.actv));
         // register ring: code words, metadata, activation pieces of D slices
         uint4 rq[D][NPROJ][RT];
         uint2 rm[D][NPROJ][RT];
@@ -1018,29 +1021,51 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     }
 }
 
-// Dense int4, before gate/up: x [T, d] bf16 -> x16 = x 2^-E fp16, one block per token, E = 0 while |x| < 2^15 on the
-// row, else the power of two that brings the row's largest |x| below 2^15 (bf16 to fp16 is then exact except in
-// fp16's subnormal range, where values are rounded); E per token for the gate/up epilogue.
-__global__ void __launch_bounds__(256) k_x16(const uint16_t* __restrict__ x, uint16_t* __restrict__ x16,
+// Dense int4, before gate/up: x [T, d] (bf16 or fp16) -> x16 = x 2^-E fp16, one block per token, E = h16_exponent of
+// the row's largest |x| (bf16 and fp16 to fp16 are then exact except far below the row's largest, where fp16's
+// subnormal range rounds); E per token for the gate/up epilogue.
+// 8 activations of x (bf16, fp16 or fp32) starting at element 8c of row `row`, as fp32
+template <int XDT>
+__device__ __forceinline__ void load_x8(const void* row, int c, float v[8]) {
+    if (XDT == MOE_DTYPE_F32) {
+        const float4 a = reinterpret_cast<const float4*>(row)[2 * c], b = reinterpret_cast<const float4*>(row)[2 * c + 1];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+        return;
+    }
+    const uint4 r = reinterpret_cast<const uint4*>(row)[c];
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (XDT == MOE_DTYPE_F16) {
+            v[2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] & 0xFFFFu));
+            v[2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] >> 16));
+        } else {
+            v[2 * q] = bf16lo(w[q]);
+            v[2 * q + 1] = bf16hi(w[q]);
+        }
+    }
+}
+
+template <int XDT>
+__global__ void __launch_bounds__(256) k_x16(const void* __restrict__ x, uint16_t* __restrict__ x16,
                                              int32_t* __restrict__ xexp, int d) {
     __shared__ float sM[4];
     const int t = blockIdx.x, tid = threadIdx.x;
-    const uint4* row = reinterpret_cast<const uint4*>(x + (size_t)t * d);
+    const void* row = reinterpret_cast<const uint8_t*>(x) + (size_t)t * d * (XDT == MOE_DTYPE_F32 ? 4 : 2);
     uint4* out = reinterpret_cast<uint4*>(x16 + (size_t)t * d);
-    const int nch = d >> 3;   // 16-byte chunks; d <= 2048 * 8 for one round of 8 per thread
+    const int nch = d >> 3;   // 8-element chunks; d <= 2048 * 8 for one round of 8 per thread
     constexpr int CPT = 8;
     float am = 0.f;
     for (int c0 = 0; c0 < nch; c0 += 256 * CPT) {
-        uint4 v[CPT];
+        float v[CPT][8];
 #pragma unroll
         for (int i = 0; i < CPT; ++i)
-            if (c0 + i * 256 + tid < nch) v[i] = row[c0 + i * 256 + tid];
+            if (c0 + i * 256 + tid < nch) load_x8<XDT>(row, c0 + i * 256 + tid, v[i]);
 #pragma unroll
         for (int i = 0; i < CPT; ++i)
             if (c0 + i * 256 + tid < nch) {
-                const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) am = fmaxf(am, fmaxf(fabsf(bf16lo(w[q])), fabsf(bf16hi(w[q]))));
+                for (int q = 0; q < 8; ++q) am = fmaxf(am, fabsf(v[i][q]));
             }
     }
     for (int o = 32; o; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
@@ -1050,12 +1075,12 @@ __global__ void __launch_bounds__(256) k_x16(const uint16_t* __restrict__ x, uin
     const int E = h16_exponent(amax);
     if (tid == 0) xexp[t] = E;
     for (int c = tid; c < nch; c += 256) {   // the row again (cache hits)
-        const uint4 v = row[c];
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        float v[8];
+        load_x8<XDT>(row, c, v);
         uint32_t o4[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const _Float16 lo = (_Float16)__builtin_ldexpf(bf16lo(w[q]), -E), hi = (_Float16)__builtin_ldexpf(bf16hi(w[q]), -E);
+            const _Float16 lo = (_Float16)__builtin_ldexpf(v[2 * q], -E), hi = (_Float16)__builtin_ldexpf(v[2 * q + 1], -E);
             o4[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
         }
         out[c] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
@@ -1213,10 +1238,18 @@ int tokens_per_pass_tiles(int T, int k, int E) {
 }
 
 template <class FMT, int NPROJ>
-int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st) {
+int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st, int hx = 1) {
     // token passes spread over blockIdx.z: an expert has at most T slots when a token's k ids are distinct
+    if (NPROJ == 2 && hx > 1) nt = 1;   // fp16 / fp32 x planes: one 16-token tile per pass (LDS)
     const int zp = (T + 16 * nt - 1) / (16 * nt);
     dim3 grid(t.N / TL_ROWS, max_active, zp < 1 ? 1 : (zp > 16 ? 16 : zp));
+    if constexpr (NPROJ == 2) {
+        if (hx > 1) {
+            if (hx == 3) k_tile<FMT, 2, 1, 3><<<grid, 256, 0, st>>>(t);
+            else k_tile<FMT, 2, 1, 2><<<grid, 256, 0, st>>>(t);
+            return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+        }
+    }
     switch (nt) {
         case 1: k_tile<FMT, NPROJ, 1><<<grid, 256, 0, st>>>(t); break;
         case 2: k_tile<FMT, NPROJ, 2><<<grid, 256, 0, st>>>(t); break;
@@ -1250,10 +1283,18 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 #define MOE_WAVE_RT_DN 4   // 16-row tiles per wave, down (d % 64 == 0)
 #endif
 template <class FMT, int NPROJ, int RT, int D, bool H16O = false>
-int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st) {
+int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st, int hx = 1) {
     if (t.N % (16 * RT)) return MOE_ERR_ARG;
     dim3 grid(t.N / (16 * RT), max_passes(nslots, t.E, 16 * nt));
     if (grid.y > 65535) return MOE_ERR_ARG;
+    if constexpr (NPROJ == 2) {
+        if (hx > 1) {   // fp16 / fp32 x planes: one 16-token tile per pass (the host passes nt = 1)
+            if (nt != 1) return MOE_ERR_ARG;
+            if (hx == 3) k_wave_tile<FMT, 2, 1, RT, D, H16O, 3><<<grid, 64, 0, st>>>(t);
+            else k_wave_tile<FMT, 2, 1, RT, D, H16O, 2><<<grid, 64, 0, st>>>(t);
+            return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+        }
+    }
     if (nt == 1) k_wave_tile<FMT, NPROJ, 1, RT, D, H16O><<<grid, 64, 0, st>>>(t);
     else k_wave_tile<FMT, NPROJ, 2, RT, D, H16O><<<grid, 64, 0, st>>>(t);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
@@ -1330,14 +1371,20 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     const long dn_blocks = (long)((w->d + 255) / 256) * dpasses;
     const int min_avg = env_int("MOE_DENSE_MIN_AVG", 32);
     const int dn_min_avg = env_int("MOE_DENSE_DN_MIN_AVG", 16);
-    const bool dense_gu = tiled && avg > min_avg && (dmode == 1 || (dmode < 0 && dblocks >= MOE_DENSE_MIN_BLOCKS));
+    // activations as planes (fp16 / fp32 x): the dense gate/up takes only what it reads exactly, int4 with fp16 x
+    // (x16); fp32 x and MXFP4 keep the exact-operand wave / row tiles, one 16-token tile per pass (nt = 1: the
+    // planes' activation registers)
+    const bool dense_gu_x = INT4 ? a.x_dtype != MOE_DTYPE_F32 : a.nx == 1;
+    const bool dense_gu = dense_gu_x && tiled && avg > min_avg &&
+                          (dmode == 1 || (dmode < 0 && dblocks >= MOE_DENSE_MIN_BLOCKS));
     const bool dense_dn = dense_gu || (INT4 && tiled && dmode != 0 && avg > dn_min_avg &&
                                        (dmode == 1 || dn_blocks >= MOE_DENSE_MIN_BLOCKS));
     const bool wave_gu = tiled && !dense_gu && (avg <= min_avg || dmode != 0);
     const bool wave_dn = tiled && !dense_dn && (avg <= min_avg || dmode != 0);
     const bool h16 = INT4 && dense_dn;   // h leaves the gate/up as h16 with per-32-row exponents
     const int wnt = env_int("MOE_WAVE_NT", 0);
-    const int nt = (wave_gu || wave_dn) ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2))
+    const int nt = a.nx > 1 ? 1
+                 : (wave_gu || wave_dn) ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2))
                                         : tokens_per_pass_tiles(a.T, a.k, w->E);
     // pass lists: 16 nt tokens per pass for the wave tiles, 16 DENSE_NT for the dense tiles; a second list
     // when the two stages take different kernels
@@ -1356,7 +1403,8 @@ int run_tiles_fmt(const ExpertsArgs& a) {
                               two_lists ? a.grp.items2 : nullptr);
         if (rc) return rc;
         TileArgs g = t;
-        g.actv = (const uint16_t*)a.x;
+        g.actv = a.xb;
+        g.act_plane = a.xplane;
         g.act_div = a.k;
         g.K = w->d;
         g.N = w->F;
@@ -1371,16 +1419,18 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.W1 = (const uint8_t*)w->up.tiles;
         }
         if (dense_gu && INT4) {
-            k_x16<<<a.T, 256, 0, a.st>>>((const uint16_t*)a.x, a.x16, a.xexp, w->d);
+            if (a.x_dtype == MOE_DTYPE_F16) k_x16<MOE_DTYPE_F16><<<a.T, 256, 0, a.st>>>(a.x, a.x16, a.xexp, w->d);
+            else k_x16<MOE_DTYPE_BF16><<<a.T, 256, 0, a.st>>>(a.x, a.x16, a.xexp, w->d);
             rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
             if (rc) return rc;
             g.actv = a.x16;
             g.xexp = a.xexp;
         }
         if (dense_gu) rc = launch_dense<FMT, 2>(g, nslots, a.st);
-        else if (wave_gu && h16) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU, INT4>(g, nt, nslots, a.st);
-        else if (wave_gu) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st);
-        else rc = launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st);
+        else if (wave_gu && h16)
+            rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU, INT4>(g, nt, nslots, a.st, a.nx);
+        else if (wave_gu) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st, a.nx);
+        else rc = launch_tile<FMT, 2>(g, nt, max_active, a.T, a.st, a.nx);
         if (!rc && h16) {
             k_h16_fix<<<nslots, 256, 0, a.st>>>((const int8_t*)a.hlo, a.hhi,
                                               (int32_t*)((uint8_t*)a.hlo + t.eslot_off), w->F);
@@ -1420,7 +1470,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
         return launch_combine(a.yp, d.ksplit, d.plane, a.idx, a.wts, w->down.bias, w->E,
-                              a.residual, a.y, a.T, a.k, w->d, a.y32, a.st);
+                              a.residual, a.y, a.T, a.k, w->d, a.ydt, a.st);
     }
     return 0;
 }

@@ -105,12 +105,13 @@ def _desc(s):
 def run_experts(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, nored=False, residual=None, out=None, out_dtype=None,
                 stages=_lib.STAGE_ALL):
     """y [T, d] (or [T*k, d] unweighted per slot when nored) on the GPU through moe_experts_run.
-    out_dtype: x.dtype (default, as the reference) or torch.float32 for the unrounded result;
+    x: bf16, fp16 or fp32 (fp16 and fp32 reach the gate/up kernels exactly, as 2 or 3 bf16 planes).
+    out_dtype: x.dtype (default, as the reference) or another of the three (fp32: the unrounded result);
     residual, if given, is added inside the last kernel and has out_dtype.
     stages: STAGE_ALL, or STAGE_GATE_UP then STAGE_DOWN as two calls sharing the per-device workspace."""
     _lib.require_device(x, "x")
-    if x.dtype not in (torch.bfloat16,):
-        raise NotImplementedError(f"activation dtype {x.dtype}: the gfx950 expert kernels take bf16")
+    if x.dtype not in _lib.DTYPE:
+        raise TypeError(f"activation dtype {x.dtype}: the expert kernels take bf16, fp16 or fp32")
     T, d = x.shape
     k = idx.shape[1]
     x = x.contiguous()
@@ -123,7 +124,7 @@ def run_experts(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, nored=False, residua
     out_dtype = x.dtype if out_dtype is None else out_dtype
     if out is None:
         out = torch.empty((T * k if nored else T, d), dtype=out_dtype, device=x.device)
-    assert out.dtype == out_dtype and out.dtype in (torch.bfloat16, torch.float32)
+    assert out.dtype == out_dtype and out.dtype in _lib.DTYPE
     res = None if residual is None else residual.to(out_dtype).contiguous()
     rc = L.moe_experts_run_stages(desc, _lib.ptr(x), _lib.DTYPE[x.dtype], _lib.ptr(idx), _lib.ptr(wts), T, k,
                                   int(act), int(path), int(bool(nored)), _lib.ptr(out), _lib.DTYPE[out.dtype],
@@ -152,8 +153,8 @@ def run_shared(s, x, gate=None, act=0, residual=None, out=None, out_dtype=None):
     g_t = sigmoid(x_t . gate) for a bf16 gate vector [d] (Qwen-style gated shared expert, reference
     e2e.py:66-68) or 1 (DeepSeek, e2e.py:146-147). s: an expert state whose E experts are the shared ones."""
     _lib.require_device(x, "x")
-    if x.dtype != torch.bfloat16:
-        raise NotImplementedError(f"activation dtype {x.dtype}: the gfx950 expert kernels take bf16")
+    if x.dtype not in _lib.DTYPE:
+        raise TypeError(f"activation dtype {x.dtype}: the expert kernels take bf16, fp16 or fp32")
     T, d = x.shape
     x = x.contiguous()
     desc = _desc(s)
@@ -162,7 +163,7 @@ def run_shared(s, x, gate=None, act=0, residual=None, out=None, out_dtype=None):
     out_dtype = x.dtype if out_dtype is None else out_dtype
     if out is None:
         out = torch.empty((T, d), dtype=out_dtype, device=x.device)
-    assert out.dtype == out_dtype and out.dtype in (torch.bfloat16, torch.float32)
+    assert out.dtype == out_dtype and out.dtype in _lib.DTYPE
     res = None if residual is None else residual.to(out_dtype).contiguous()
     g = None if gate is None else gate.to(torch.bfloat16).contiguous()
     rc = L.moe_shared_experts_run(desc, _lib.ptr(x), _lib.DTYPE[x.dtype], T, int(act), _lib.ptr(g), _lib.ptr(out),

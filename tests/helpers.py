@@ -8,6 +8,7 @@ orc = __graft_entry__.load_oracle()
 
 TOL_MAXABS_RMS = 1e-2   # max |y - y_ref| <= 1e-2 * RMS(y_ref)  (fp32 accumulation; h kept at ~16 bits)
 BF16_HALF_ULP = 2.0 ** -8   # round-to-nearest into bf16 moves a value by at most 2^-8 of its magnitude
+F16_HALF_ULP = 2.0 ** -11   # fp16: 2^-11 (normal range)
 
 
 def np_u16(t):
@@ -58,7 +59,8 @@ def oracle_y(state, x, idx, wts, act=0):
 
 def assert_close(y, y_ref, tol=TOL_MAXABS_RMS, what=""):
     """fp32 outputs: max |y - y_ref| <= tol * RMS(y_ref) (the north-star gate).
-    bf16 outputs: the same plus the storage rounding of each element, |y - y_ref| <= tol * RMS + 2^-8 |y_ref|
+    bf16 / fp16 outputs: the same plus the storage rounding of each element, |y - y_ref| <= tol * RMS + 2^-8 |y_ref|
+    (fp16: 2^-11 |y_ref|)
     (a bf16 result cannot be closer to y_ref than its own rounding; for outputs beyond ~4 RMS that rounding
     alone exceeds 1e-2 RMS). The gate on the unrounded fp32 result is tested separately."""
     yv = y.float().cpu().numpy()
@@ -67,6 +69,7 @@ def assert_close(y, y_ref, tol=TOL_MAXABS_RMS, what=""):
     if y.dtype == torch.float32:
         assert err["max_abs"] <= tol * err["rms_ref"] + 1e-30, (what, err)
     else:
-        excess = np.abs(yv - y_ref) - (tol * err["rms_ref"] + BF16_HALF_ULP * np.abs(y_ref))
+        half_ulp = F16_HALF_ULP if y.dtype == torch.float16 else BF16_HALF_ULP
+        excess = np.abs(yv - y_ref) - (tol * err["rms_ref"] + half_ulp * np.abs(y_ref))
         assert (excess <= 1e-30).all(), (what, err, float(excess.max()))
     return err

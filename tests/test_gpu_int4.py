@@ -518,7 +518,7 @@ def test_shared_experts_argument_errors():
     desc = _desc(s)
     assert L.moe_shared_experts_run(desc, _lib.ptr(x), 0, 4, 0, None, _lib.ptr(y), 0, None, None, 0, None) == \
         _lib.MOE_ERR_WORKSPACE
-    assert L.moe_shared_experts_run(desc, _lib.ptr(x), 2, 4, 0, None, _lib.ptr(y), 0, None, _lib.ptr(y), 1 << 20,
+    assert L.moe_shared_experts_run(desc, _lib.ptr(x), 3, 4, 0, None, _lib.ptr(y), 0, None, _lib.ptr(y), 1 << 20,
                                     None) == _lib.MOE_ERR_DTYPE
 
 

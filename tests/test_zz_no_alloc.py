@@ -80,15 +80,15 @@ def test_static_entry_point_refuses_sizes_beyond_its_array():
     sh = SHAPES["qwen3-30b-a3b"]
     s = baseline_int4_layer(sh, seed=8, device=DEV, router=False)
     L = _lib.lib()
-    fits = [T for T in (1, 32, 115, 116, 256) if L.moe_experts_workspace_bytes(_desc(s), T, sh.k, 2) <=
+    fits = [T for T in (1, 32, 110, 111, 256) if L.moe_experts_workspace_bytes(_desc(s), T, sh.k, 2) <=
             _lib.STATIC_SCRATCH_BYTES]
-    assert fits == [1, 32, 115]
-    x, idx, wts = _inputs(sh, 116, seed=1)
+    assert fits == [1, 32, 110]
+    x, idx, wts = _inputs(sh, 111, seed=1)
     rc, y = run_static(s, x, idx, wts, 2)
     torch.cuda.synchronize()
     assert rc == _lib.MOE_ERR_WORKSPACE
     assert torch.isnan(y).all()   # refused before any launch: the output is untouched
-    x, idx, wts = _inputs(sh, 115, seed=2)   # the largest call that fits, at the full Qwen3 shape
+    x, idx, wts = _inputs(sh, 110, seed=2)   # the largest call that fits, at the full Qwen3 shape
     rc, y = run_static(s, x, idx, wts, 2)
     _lib.check("moe_experts_run_static", rc)
     from moelab_amd.experts import run_experts
