@@ -152,7 +152,8 @@ def main():
 
     g1, _ = graph_of(chain_t1())
     t_step = time_graph(g1, args.steps, args.warmup)
-    log(f"T=1 experts chain (default path): {t_step * 1e6 / L:.2f} us/layer, {bytes1 / t_step / 1e9:.0f} GB/s")
+    log(f"T=1 experts chain (default path: two per-slot launches): {t_step * 1e6 / L:.2f} us/layer, "
+        f"{bytes1 / t_step / 1e9:.0f} GB/s")
     g1r, _ = graph_of(chain_t1_router)
     t_step_r = time_graph(g1r, args.steps, args.warmup)
     log(f"T=1 with router: {t_step_r * 1e6 / L:.2f} us/layer")
@@ -257,7 +258,7 @@ def main():
         "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3)},
         "t32": t32,
         "configs": configs,
-        "roofline": {"bound": "hbm", "kernel": "k_gate_up_rows<FmtInt4, 3, 1> (T=1 gate/up GEMV + GLU)",
+        "roofline": {"bound": "hbm", "kernel": "k_gate_up_rows<FmtInt4, 3, 1, 1> (T=1 gate/up GEMV + GLU)",
                      "achieved": round(gu_bytes / t_gu / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_bytes / t_gu / 1e9 / HBM_PEAK_GBS, 4), "traffic": GU_T1_TRAFFIC_BYTES,
                      "launch_us": round(t_gu * 1e6, 3), "algorithmic_bytes_per_launch": gu_bytes},

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "moe_mi355x.h"
+
 #define MOE_WAVE 64
 
 typedef __bf16 moe_bf16x2 __attribute__((ext_vector_type(2)));
@@ -204,6 +206,48 @@ __device__ __forceinline__ float glu(float g, float u) {
 
 __device__ __forceinline__ float glu_act(int act, float g, float u) {
     return act == 0 ? glu<0>(g, u) : (act == 1 ? glu<1>(g, u) : glu<2>(g, u));
+}
+
+// ------------------------------------------------------------------------------------ GEMV pieces (T = 1 kernels)
+__device__ __forceinline__ float dot16(const uint32_t qp[16], const uint32_t xp[16], float acc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2_bf16(qp[i], xp[i], acc);
+    return acc;
+}
+__device__ __forceinline__ void words16(const uint4 v[4], uint32_t w[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w[4 * i + 0] = v[i].x;
+        w[4 * i + 1] = v[i].y;
+        w[4 * i + 2] = v[i].z;
+        w[4 * i + 3] = v[i].w;
+    }
+}
+__device__ __forceinline__ float sum16(const uint32_t w[16], float acc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2_bf16(w[i], 0x3f803f80u, acc);
+    return acc;
+}
+
+// h element n -> position inside its chunk so that 16-byte loads yield (n, n+4) pairs
+__device__ __forceinline__ int paired_pos(int n) { return (n & ~7) | ((n & 3) << 1) | ((n >> 2) & 1); }
+__device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t base, int n, float v) {
+    const uint16_t hi = f32_to_bf16(v);
+    const size_t i = base + paired_pos(n);
+    hhi[i] = hi;
+    hlo[i] = f32_to_bf16(v - bf16_to_f32(hi));
+}
+
+// outputs and residuals: ydt = MOE_DTYPE_BF16, MOE_DTYPE_F16 or MOE_DTYPE_F32 (round to nearest even)
+__device__ __forceinline__ void store_y(void* y, size_t i, float v, int ydt) {
+    if (ydt == MOE_DTYPE_F32) reinterpret_cast<float*>(y)[i] = v;
+    else if (ydt == MOE_DTYPE_F16) reinterpret_cast<_Float16*>(y)[i] = (_Float16)v;
+    else reinterpret_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
+}
+__device__ __forceinline__ float load_y(const void* y, size_t i, int ydt) {
+    if (ydt == MOE_DTYPE_F32) return reinterpret_cast<const float*>(y)[i];
+    if (ydt == MOE_DTYPE_F16) return (float)reinterpret_cast<const _Float16*>(y)[i];
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
 }
 
 }  // namespace moe

@@ -30,48 +30,6 @@
 
 namespace moe {
 
-// ============================================================================ shared pieces
-__device__ __forceinline__ float dot16(const uint32_t qp[16], const uint32_t xp[16], float acc) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc = dot2_bf16(qp[i], xp[i], acc);
-    return acc;
-}
-__device__ __forceinline__ void words16(const uint4 v[4], uint32_t w[16]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        w[4 * i + 0] = v[i].x;
-        w[4 * i + 1] = v[i].y;
-        w[4 * i + 2] = v[i].z;
-        w[4 * i + 3] = v[i].w;
-    }
-}
-__device__ __forceinline__ float sum16(const uint32_t w[16], float acc) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc = dot2_bf16(w[i], 0x3f803f80u, acc);
-    return acc;
-}
-
-// h element n -> position inside its chunk so that 16-byte loads yield (n, n+4) pairs
-__device__ __forceinline__ int paired_pos(int n) { return (n & ~7) | ((n & 3) << 1) | ((n >> 2) & 1); }
-__device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t base, int n, float v) {
-    const uint16_t hi = f32_to_bf16(v);
-    const size_t i = base + paired_pos(n);
-    hhi[i] = hi;
-    hlo[i] = f32_to_bf16(v - bf16_to_f32(hi));
-}
-
-// outputs and residuals: ydt = MOE_DTYPE_BF16, MOE_DTYPE_F16 or MOE_DTYPE_F32 (round to nearest even)
-__device__ __forceinline__ void store_y(void* y, size_t i, float v, int ydt) {
-    if (ydt == MOE_DTYPE_F32) reinterpret_cast<float*>(y)[i] = v;
-    else if (ydt == MOE_DTYPE_F16) reinterpret_cast<_Float16*>(y)[i] = (_Float16)v;
-    else reinterpret_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
-}
-__device__ __forceinline__ float load_y(const void* y, size_t i, int ydt) {
-    if (ydt == MOE_DTYPE_F32) return reinterpret_cast<const float*>(y)[i];
-    if (ydt == MOE_DTYPE_F16) return (float)reinterpret_cast<const _Float16*>(y)[i];
-    return bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
-}
-
 // ============================================================================ activation planes
 // fp16 and fp32 activations enter the expert kernels as NX bf16 planes whose sum is the value exactly: each plane
 // takes the next 8 significant bits by truncation (plane = the top 16 bits of the remainder's fp32 pattern;
@@ -132,16 +90,15 @@ __global__ void __launch_bounds__(256) k_x_planes(const void* __restrict__ x, ui
 // planes hi/lo (store_h).
 // HX activation planes (bf16 x: 1; fp16 / fp32 x: k_x_planes' 2 or 3 planes, xplane elements apart): every plane
 // is dotted with the same decoded chunk and the products add in fp32.
+// One wave: gate and up rows f0 .. f0 + R - 1 of slot s's expert; lanes 48..63 write h.
 template <class FMT, int R, int NCH, int HX>
-__global__ void __launch_bounds__(256)
-k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
-               const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
-               int d, int F, int E, int Q, int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
+__device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x, size_t xplane,
+                                                  const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
+                                                  const float* __restrict__ bg, const float* __restrict__ bu,
+                                                  const int32_t* __restrict__ idx, int k, int d, int F, int E,
+                                                  int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo,
+                                                  int s, int f0, int lane) {
     static_assert(R <= 16, "results live in lanes 48..63");
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int q0 = (blockIdx.x * 4 + wave) * R;
-    if (q0 >= Q) return;
-    const int s = q0 / F, f0 = q0 - s * F;
     const int e = idx[s];   // wave-uniform: a scalar load
     const size_t rb = rbytes(FMT::FMT, d);
     const int nchunk = d >> 5;
@@ -196,10 +153,10 @@ k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __r
             }
         }
         auto dotx = [&](const uint32_t (&qp)[16], int c) __attribute__((always_inline)) {
-            float d = 0.f;
+            float dd = 0.f;
 #pragma unroll
-            for (int h = 0; h < HX; ++h) d = dot16(qp, xp[h][c], d);
-            return d;
+            for (int h = 0; h < HX; ++h) dd = dot16(qp, xp[h][c], dd);
+            return dd;
         };
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -227,6 +184,18 @@ k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __r
         const float hv = valid ? glu_act(act, g + bgl, u + bul) : 0.f;
         store_h(hhi, hlo, (size_t)s * F, f0 + rl, hv);
     }
+}
+
+template <class FMT, int R, int NCH, int HX>
+__global__ void __launch_bounds__(256)
+k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
+               const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
+               int d, int F, int E, int Q, int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int q0 = (blockIdx.x * 4 + wave) * R;
+    if (q0 >= Q) return;
+    const int s = q0 / F, f0 = q0 - s * F;
+    gate_up_rows_wave<FMT, R, NCH, HX>(x, xplane, G, U, bg, bu, idx, k, d, F, E, act, hhi, hlo, s, f0, lane);
 }
 
 // ============================================================================ per-slot down, h staged in LDS
