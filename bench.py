@@ -117,7 +117,7 @@ def main():
     log(f"layers ready in {time.time() - t0:.1f}s ({L * sh.E * per_expert / 1e9:.2f} GB packed experts)")
 
     # one workspace for every graph below (graphs keep raw pointers into it): sized before any capture
-    from moelab_amd.experts import reserve
+    from moelab_amd.experts import reserve, run_routed
     reserve(layers[0], 64, sh.k)
     router.reserve(dev, 64)
 
@@ -135,11 +135,10 @@ def main():
             return x
         return f
 
-    def chain_t1_router():
+    def chain_t1_router():   # router + experts per layer in one call (moe_layer_run)
         x = x1.clone()
         for ly in layers:
-            idx, wts = router.route(x, ly["wr"], sh.k)
-            x = run_experts(ly, x, idx, wts, path=_lib.PATH_AUTO, residual=x)
+            x, _, _ = run_routed(ly, x, ly["wr"], sh.k, residual=x)
         return x
 
     def gate_up_only():

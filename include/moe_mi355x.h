@@ -203,6 +203,21 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
                            void* workspace, size_t workspace_bytes, int stages, void* stream);
 
 /*
+ * Router and experts in one call: moe_router's logits (same fixed order, so the same ids) and tail, then
+ * moe_experts_run's default path. The reference calls them one after the other, the stock gate GEMV, router.topk_norm,
+ * then the variant's run (reference e2e.py:57-64, moelab/router.py:71-80). At T == 1 the router launch computes the
+ * logits only and every gate/up wave runs the tail over the 128..1024 logits itself for its own slot (no hand-off
+ * between workgroups inside a launch: measured at 1-2 us per round trip on this part); one wave writes idx / wts.
+ *   x [T, d] bf16 (MOE_DTYPE_BF16 only: the gate GEMV reads bf16); wr [E, d] bf16, wr_bias [E] fp32 or NULL;
+ *   norm, scale: as moe_router; idx [T, k] int32 and wts [T, k] fp32 out (as moe_router's); y, residual, act,
+ *   y_dtype: as moe_experts_run. workspace: moe_layer_workspace_bytes(w, T, k) bytes (any contents).
+ */
+int moe_layer_run(const moe_experts_t* w, const void* x, int x_dtype, const void* wr, const float* wr_bias, int T,
+                  int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y, int y_dtype,
+                  const void* residual, void* workspace, size_t workspace_bytes, void* stream);
+size_t moe_layer_workspace_bytes(const moe_experts_t* w, int T, int k);
+
+/*
  * Shared experts: S always-on experts added to every token, the caller semantics of the reference's model
  * patches (reference e2e.py:66-68 Qwen-style gated shared expert, sigmoid(x . w_gate) * shared_expert(x);
  * e2e.py:146-147 DeepSeek, + shared_experts(x)). The reference runs them as stock mlx-lm modules; here they go

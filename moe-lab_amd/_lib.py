@@ -23,7 +23,7 @@ ACT_SWIGLU, ACT_GEGLU, ACT_GPTOSS = 0, 1, 2
 EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
            "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_row_bytes", "moe_tile_bytes",
            "moe_tiles_pack", "moe_shared_experts_run", "moe_shared_experts_workspace_bytes", "moe_version",
-           "moe_experts_run_static")
+           "moe_experts_run_static", "moe_layer_run", "moe_layer_workspace_bytes")
 STATIC_SCRATCH_BYTES = 32 << 20   # MOE_STATIC_SCRATCH_BYTES: the workspace array of moe_experts_run_static
 STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 3
 
@@ -71,6 +71,10 @@ def lib():
         L.moe_experts_run_static.argtypes = [ctypes.POINTER(Experts), vp, i, vp, vp, i, i, i, i, i, vp, i, vp, vp]
         L.moe_experts_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i, i, i]
         L.moe_experts_workspace_bytes.restype = sz
+        L.moe_layer_run.argtypes = [ctypes.POINTER(Experts), vp, i, vp, vp, i, i, i, f, i, vp, vp, vp, i, vp, vp, sz,
+                                    vp]
+        L.moe_layer_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i, i]
+        L.moe_layer_workspace_bytes.restype = sz
         L.moe_version.restype = ctypes.c_char_p
         L.moe_row_bytes.argtypes = [i, i]
         L.moe_row_bytes.restype = sz
@@ -81,7 +85,8 @@ def lib():
         L.moe_shared_experts_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i]
         L.moe_shared_experts_workspace_bytes.restype = sz
         for n in ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
-                  "moe_experts_run_stages", "moe_tiles_pack", "moe_shared_experts_run", "moe_experts_run_static"):
+                  "moe_experts_run_stages", "moe_tiles_pack", "moe_shared_experts_run", "moe_experts_run_static",
+                  "moe_layer_run"):
             getattr(L, n).restype = ctypes.c_int
         _lib = L
     return _lib

@@ -203,9 +203,59 @@ int moe_experts_run_static(const moe_experts_t* w, const void* x, int x_dtype, c
                                   MOE_STATIC_SCRATCH_BYTES, MOE_STAGE_ALL, stream);
 }
 
+namespace {
+int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T, int k,
+                 int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
+                 size_t workspace_bytes, int stages, void* stream, const float* route_logits, int route_norm,
+                 float route_scale);
+}  // namespace
+
+size_t moe_layer_workspace_bytes(const moe_experts_t* w, int T, int k) {
+    if (!w || T < 0 || k < 1 || w->E < 1) return 0;
+    return layout(w, T, k, MOE_PATH_AUTO).total + align_up((size_t)T * w->E * 4);   // + the router logits
+}
+
+int moe_layer_run(const moe_experts_t* w, const void* x, int x_dtype, const void* wr, const float* wr_bias, int T,
+                  int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y, int y_dtype,
+                  const void* residual, void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_experts(w);
+    if (rc) return rc;
+    if (T < 0 || k < 1 || k > w->E || k > 32 || w->E > 1024 || act < 0 || act > 2) return MOE_ERR_ARG;
+    if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;   // the router GEMV reads bf16 x
+    if (y_dtype < MOE_DTYPE_BF16 || y_dtype > MOE_DTYPE_F32) return MOE_ERR_DTYPE;
+    if (T == 0) return MOE_OK;
+    if (!x || !wr || !idx || !wts || !y) return MOE_ERR_ARG;
+    if (!aligned16(x) || !aligned16(wr) || !aligned16(y) || (residual && !aligned16(residual))) return MOE_ERR_ALIGN;
+    if (!workspace || workspace_bytes < moe_layer_workspace_bytes(w, T, k)) return MOE_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return MOE_ERR_ALIGN;
+    const size_t base = layout(w, T, k, MOE_PATH_AUTO).total;
+    float* logits = (float*)((char*)workspace + base);
+    hipStream_t st = (hipStream_t)stream;
+    rc = moe::launch_router_logits((const uint16_t*)x, (const uint16_t*)wr, wr_bias, T, w->d, w->E, logits, st);
+    if (rc) return rc;
+    if (T == 1 && moe::slots_route_in_gate_up(k, w->F))   // the gate/up waves run the tail themselves
+        return experts_call(w, x, x_dtype, idx, wts, T, k, act, MOE_PATH_AUTO, 0, y, y_dtype, residual, workspace,
+                            base, MOE_STAGE_ALL, stream, logits, norm, scale);
+    rc = moe::launch_topk(logits, MOE_DTYPE_F32, T, w->E, k, norm, scale, idx, wts, st);
+    if (rc) return rc;
+    return experts_call(w, x, x_dtype, idx, wts, T, k, act, MOE_PATH_AUTO, 0, y, y_dtype, residual, workspace, base,
+                        MOE_STAGE_ALL, stream, nullptr, 1, 1.f);
+}
+
 int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,
                            int T, int k, int act, int path, int nored, void* y, int y_dtype, const void* residual,
                            void* workspace, size_t workspace_bytes, int stages, void* stream) {
+    return experts_call(w, x, x_dtype, idx, wts, T, k, act, path, nored, y, y_dtype, residual, workspace,
+                        workspace_bytes, stages, stream, nullptr, 1, 1.f);
+}
+
+}  // extern "C"
+
+namespace {
+int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T, int k,
+                 int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
+                 size_t workspace_bytes, int stages, void* stream, const float* route_logits, int route_norm,
+                 float route_scale) {
     if (stages < 1 || stages > MOE_STAGE_ALL) return MOE_ERR_ARG;
     int rc = check_experts(w);
     if (rc) return rc;
@@ -250,6 +300,9 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     a.hlo = a.hhi + align_up((size_t)T * k * w->F * 2) / 2;
     a.st = (hipStream_t)stream;
     a.stages = stages;
+    a.route_logits = route_logits;
+    a.route_norm = route_norm;
+    a.route_scale = route_scale;
     if (rpath == MOE_PATH_GROUPED) {
         a.yp = (float*)(ws + L.yp);
         a.x16 = (uint16_t*)(ws + L.x16);
@@ -265,4 +318,4 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
     return rpath == MOE_PATH_GROUPED ? moe::run_experts_tiles(a) : moe::run_experts_slots(a);
 }
 
-}  // extern "C"
+}  // namespace

@@ -250,4 +250,81 @@ __device__ __forceinline__ float load_y(const void* y, size_t i, int ydt) {
     return bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
 }
 
+// ------------------------------------------------------------------------------------ router tail
+constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024
+
+// One wave: router tail for one token (reference moelab/router.py:15-66). `lg(e)` yields logit e as fp32. Lane r < k
+// ends with round r's expert id (*id) and routing weight (*w): NaN counts as -inf, k rounds of arg-max with the lowest
+// id winning ties, fewer than k finite logits -> the lowest unused ids with weight 0; norm: softmax over the top-k
+// logits, !norm: full-softmax probabilities; weights times scale. rounds <= k stops after that many rounds (a caller
+// that needs only round r passes r + 1; the weights are then not computed).
+template <typename F>
+__device__ __forceinline__ void wave_topk_lanes(F lg, int E, int k, int norm, float scale, int rounds, uint32_t* id,
+                                                float* w) {
+    const int lane = threadIdx.x & 63;
+    const int J = (E + 63) / 64;
+    float v[TOPK_MAX_J];
+#pragma unroll
+    for (int j = 0; j < TOPK_MAX_J; ++j) {
+        const int e = j * 64 + lane;
+        float l = (j < J && e < E) ? lg(e) : -INFINITY;
+        v[j] = __builtin_isnan(l) ? -INFINITY : l;
+    }
+    const bool weights = rounds >= k;
+    float m0 = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < TOPK_MAX_J; ++j) m0 = fmaxf(m0, v[j]);
+    if (weights) m0 = wave_max_dpp(m0);
+    float den = 0.f;
+    if (weights && !norm) {
+#pragma unroll
+        for (int j = 0; j < TOPK_MAX_J; ++j) den += (v[j] == -INFINITY) ? 0.f : expf(v[j] - m0);
+        den = wave_sum_dpp(den);
+    }
+    float myv = -INFINITY;   // lane r < k holds round r's value and id
+    uint32_t myi = 0;
+    float top0 = -INFINITY;
+    for (int r = 0; r < rounds; ++r) {
+        float b = -INFINITY;
+        uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = 0; j < TOPK_MAX_J; ++j)
+            if (v[j] > b) { b = v[j]; bi = (uint32_t)(j * 64 + lane); }
+        float m = wave_max_dpp(b);
+        uint32_t sel = wave_min_dpp(b == m ? bi : 0xFFFFFFFFu);
+        if (sel == 0xFFFFFFFFu) {   // no finite candidate left: lowest id not chosen yet, weight 0
+            sel = 0;
+            while (__ballot(lane < r && myi == sel) != 0ull) ++sel;
+            m = -INFINITY;
+        } else if ((int)(sel & 63u) == lane) {
+#pragma unroll
+            for (int j = 0; j < TOPK_MAX_J; ++j)
+                if (j == (int)(sel >> 6)) v[j] = -INFINITY;
+        }
+        if (r == 0) top0 = m;
+        if (lane == r) { myv = m; myi = sel; }
+    }
+    *id = myi;
+    *w = 0.f;
+    if (!weights) return;
+    float s;
+    if (norm) s = wave_sum_dpp(lane < k ? expf(myv - top0) : 0.f);
+    else s = den;
+    const float off = norm ? top0 : m0;
+    *w = expf(myv - off) / s * scale;
+}
+
+// One wave: router tail for one token, written to idx[k], wts[k].
+template <typename F>
+__device__ void wave_topk(F lg, int E, int k, int norm, float scale, int32_t* idx, float* wts) {
+    uint32_t id;
+    float w;
+    wave_topk_lanes(lg, E, k, norm, scale, k, &id, &w);
+    const int lane = threadIdx.x & 63;
+    if (lane < k) {
+        idx[lane] = (int32_t)id;
+        wts[lane] = w;
+    }
+}
+
 }  // namespace moe

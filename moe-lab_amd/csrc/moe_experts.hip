@@ -91,15 +91,40 @@ __global__ void __launch_bounds__(256) k_x_planes(const void* __restrict__ x, ui
 // HX activation planes (bf16 x: 1; fp16 / fp32 x: k_x_planes' 2 or 3 planes, xplane elements apart): every plane
 // is dotted with the same decoded chunk and the products add in fp32.
 // One wave: gate and up rows f0 .. f0 + R - 1 of slot s's expert; lanes 48..63 write h.
+// Routed (rt.logits != null): the expert is round s % k of the router tail over token s / k's logits, run by the
+// wave itself (as many rounds as it needs); the wave with s % k == 0 and f0 == 0 runs all k and writes the token's
+// idx / wts for the down kernel and the caller.
+struct RouteArgs {
+    const float* logits;   // [T, E] fp32, or null: the expert ids come from idx
+    int norm;
+    float scale;
+    int32_t* idx;          // outputs when routed
+    float* wts;
+};
 template <class FMT, int R, int NCH, int HX>
 __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x, size_t xplane,
                                                   const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
                                                   const float* __restrict__ bg, const float* __restrict__ bu,
                                                   const int32_t* __restrict__ idx, int k, int d, int F, int E,
                                                   int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo,
-                                                  int s, int f0, int lane) {
+                                                  int s, int f0, int lane, const RouteArgs& rt = RouteArgs{}) {
     static_assert(R <= 16, "results live in lanes 48..63");
-    const int e = idx[s];   // wave-uniform: a scalar load
+    int e;
+    if (rt.logits) {
+        const int t = s / k, r = s - t * k;
+        const bool writer = r == 0 && f0 == 0;
+        const float* lrow = rt.logits + (size_t)t * E;
+        uint32_t id;
+        float w;
+        wave_topk_lanes([&](int ee) { return lrow[ee]; }, E, k, rt.norm, rt.scale, writer ? k : r + 1, &id, &w);
+        e = __builtin_amdgcn_readlane((int)id, r);
+        if (writer && lane < k) {
+            rt.idx[(size_t)t * k + lane] = (int32_t)id;
+            rt.wts[(size_t)t * k + lane] = w;
+        }
+    } else {
+        e = idx[s];   // wave-uniform: a scalar load
+    }
     const size_t rb = rbytes(FMT::FMT, d);
     const int nchunk = d >> 5;
     const uint16_t* xr = x + (size_t)(s / k) * d;
@@ -190,12 +215,13 @@ template <class FMT, int R, int NCH, int HX>
 __global__ void __launch_bounds__(256)
 k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
                const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
-               int d, int F, int E, int Q, int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo) {
+               int d, int F, int E, int Q, int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo,
+               RouteArgs rt) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int q0 = (blockIdx.x * 4 + wave) * R;
     if (q0 >= Q) return;
     const int s = q0 / F, f0 = q0 - s * F;
-    gate_up_rows_wave<FMT, R, NCH, HX>(x, xplane, G, U, bg, bu, idx, k, d, F, E, act, hhi, hlo, s, f0, lane);
+    gate_up_rows_wave<FMT, R, NCH, HX>(x, xplane, G, U, bg, bu, idx, k, d, F, E, act, hhi, hlo, s, f0, lane, rt);
 }
 
 // ============================================================================ per-slot down, h staged in LDS
@@ -669,9 +695,10 @@ int launch_gu_rows_n(const ExpertsArgs& a, int R) {
     const int Q = a.T * a.k * w->F;
     if (a.nx > 1) R = w->F % 2 == 0 && Q / 2 >= MOE_GU_MIN_WAVES ? 2 : 1;   // fp16 / fp32 planes: R <= 2
     const int grid = (Q / R + 3) / 4;
+    RouteArgs rt{a.route_logits, a.route_norm, a.route_scale, const_cast<int32_t*>(a.idx), const_cast<float*>(a.wts)};
 #define MOE_GUR(RR, H)                                                                                           \
     k_gate_up_rows<FMT, RR, NCH, H><<<grid, 256, 0, a.st>>>(a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias,   \
-                                                           a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, a.hlo)
+                                                           a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, a.hlo, rt)
     if (a.nx > 1) {
         if (a.nx == 3) {
             if (R == 2) MOE_GUR(2, 3);
@@ -810,6 +837,8 @@ int run_slots_fmt(const ExpertsArgs& a) {
 }
 
 }  // namespace
+
+bool slots_route_in_gate_up(int k, int F) { return down_rows_fits(k, F); }
 
 int run_experts_slots(const ExpertsArgs& a) {
     return a.w->fmt == MOE_FMT_INT4_G64 ? run_slots_fmt<FmtInt4>(a) : run_slots_fmt<FmtMxfp4>(a);

@@ -11,6 +11,9 @@ namespace moe {
 int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
                   float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st);
 int router_counter_slots(int T);
+// logits only (x . wr^T + bias in the router's fixed order), no tail
+int launch_router_logits(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, float* logits,
+                         hipStream_t st);
 int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
                 hipStream_t st);
 // with items: also the grouped kernels' pass list for passes of P slots (items [3 * max_passes(n, E, P)], meta[2])
@@ -53,11 +56,18 @@ struct ExpertsArgs {
     int32_t* xexp;  // [T]
     GroupBufs grp;  // grouped path
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
+    // moe_layer_run at T == 1: the gate/up waves take their experts from the top-k of these router logits [T, E] (and
+    // write idx / wts, which the down kernel reads); null: idx / wts are inputs
+    const float* route_logits;
+    int route_norm;
+    float route_scale;
     hipStream_t st;
 };
 
 // expert kernels, both formats (moe_experts.hip)
 int run_experts_slots(const ExpertsArgs& a);
+// whether the per-slot gate/up takes its experts from router logits (ExpertsArgs::route_logits) at this (k, F)
+bool slots_route_in_gate_up(int k, int F);
 // grouped expert tiles on MFMA (moe_tiles.hip): grouping, gate/up + GLU, down, combine
 int run_experts_tiles(const ExpertsArgs& a);
 // rows -> tile-major records (moe_tiles.hip; layout in include/moe_mi355x.h)

@@ -21,7 +21,6 @@ namespace moe {
 
 constexpr int ROUTER_WAVES = 4;   // waves per block
 constexpr int ROUTER_TPW = 4;     // tokens per wave for T > 1 (the Wr row chunk is reused across them)
-constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024
 
 
 template <typename LT>
@@ -33,74 +32,21 @@ __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return bf16_to_f
 template <>
 __device__ __forceinline__ float to_f32<_Float16>(_Float16 v) { return (float)v; }
 
-// One wave: router tail for one token. `lg(e)` yields logit e as fp32. Writes idx[k], wts[k].
-template <typename F>
-__device__ void wave_topk(F lg, int E, int k, int norm, float scale, int32_t* idx, float* wts) {
-    const int lane = threadIdx.x & 63;
-    const int J = (E + 63) / 64;
-    float v[TOPK_MAX_J];
-#pragma unroll
-    for (int j = 0; j < TOPK_MAX_J; ++j) {
-        const int e = j * 64 + lane;
-        float l = (j < J && e < E) ? lg(e) : -INFINITY;
-        v[j] = __builtin_isnan(l) ? -INFINITY : l;
-    }
-    float m0 = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < TOPK_MAX_J; ++j) m0 = fmaxf(m0, v[j]);
-    m0 = wave_max_dpp(m0);
-    float den = 0.f;
-    if (!norm) {
-#pragma unroll
-        for (int j = 0; j < TOPK_MAX_J; ++j) den += (v[j] == -INFINITY) ? 0.f : expf(v[j] - m0);
-        den = wave_sum_dpp(den);
-    }
-    float myv = -INFINITY;   // lane r < k holds round r's value and id
-    uint32_t myi = 0;
-    float top0 = -INFINITY;
-    for (int r = 0; r < k; ++r) {
-        float b = -INFINITY;
-        uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-        for (int j = 0; j < TOPK_MAX_J; ++j)
-            if (v[j] > b) { b = v[j]; bi = (uint32_t)(j * 64 + lane); }
-        float m = wave_max_dpp(b);
-        uint32_t sel = wave_min_dpp(b == m ? bi : 0xFFFFFFFFu);
-        if (sel == 0xFFFFFFFFu) {   // no finite candidate left: lowest id not chosen yet, weight 0
-            sel = 0;
-            while (__ballot(lane < r && myi == sel) != 0ull) ++sel;
-            m = -INFINITY;
-        } else if ((int)(sel & 63u) == lane) {
-#pragma unroll
-            for (int j = 0; j < TOPK_MAX_J; ++j)
-                if (j == (int)(sel >> 6)) v[j] = -INFINITY;
-        }
-        if (r == 0) top0 = m;
-        if (lane == r) { myv = m; myi = sel; }
-    }
-    float s;
-    if (norm) s = wave_sum_dpp(lane < k ? expf(myv - top0) : 0.f);
-    else s = den;
-    const float off = norm ? top0 : m0;
-    if (lane < k) {
-        idx[lane] = (int32_t)myi;
-        wts[lane] = expf(myv - off) / s * scale;
-    }
-}
-
 // grid (ceil(E / (ROUTER_WAVES * EPW)), ceil(T / TPW)), block 64 * ROUTER_WAVES.
 // counters[ty] must be 0 on entry; the last block of token group ty resets it to 0. Logits pass between
 // blocks through agent-scope atomic stores / loads (no L2 write-back or invalidation).
 constexpr int ROUTER_MAXC = 4;   // 16-byte chunks per lane held in registers per pass (2048 inputs)
 
-template <int TPW, int EPW>
-__global__ void __launch_bounds__(64 * ROUTER_WAVES)
+// TAIL = false: logits only (plain stores, no counters), for callers that run the tail elsewhere (moe_layer_run: the
+// T = 1 gate/up waves, or topk_kernel).
+template <int TPW, int EPW, bool TAIL = true, int WPB = ROUTER_WAVES>
+__global__ void __launch_bounds__(64 * WPB)
 router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, const float* __restrict__ bias,
                    int T, int d, int E, int k, int norm, float scale, float* __restrict__ logits,
                    int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* __restrict__ counters) {
     const int bx = blockIdx.x, nbx = gridDim.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int e0 = (bx * ROUTER_WAVES + wave) * EPW;
+    const int e0 = (bx * WPB + wave) * EPW;
     const int t0 = blockIdx.y * TPW;
     const int nt = min(TPW, T - t0);
     const int nchunk = d >> 3;
@@ -153,10 +99,12 @@ router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ 
                 const int e = e0 + q;
                 if (lane == 63 && i < nt && e < E) {
                     if (bias) a = a + bias[e];
-                    store_agent(&logits[(size_t)(t0 + i) * E + e], a);
+                    if (TAIL) store_agent(&logits[(size_t)(t0 + i) * E + e], a);
+                    else logits[(size_t)(t0 + i) * E + e] = a;
                 }
             }
     }
+    if (!TAIL) return;
     // the last block of this token group runs the tail
     __shared__ int s_last;
     wait_stores();
@@ -385,6 +333,20 @@ int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int 
         dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, (T + ROUTER_TPW - 1) / ROUTER_TPW);
         router_logits_topk<ROUTER_TPW, 1><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, k, norm, scale,
                                                                                logits, idx, wts, counters);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+int launch_router_logits(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, float* logits,
+                         hipStream_t st) {
+    if (T == 1) {   // one expert per wave (one wave per workgroup, spread over E CUs, measured no faster)
+        dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, 1);
+        router_logits_topk<1, 1, false><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, 1, 1, 1.f, logits,
+                                                                             nullptr, nullptr, nullptr);
+    } else {
+        dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, (T + ROUTER_TPW - 1) / ROUTER_TPW);
+        router_logits_topk<ROUTER_TPW, 1, false><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, 1, 1, 1.f,
+                                                                                      logits, nullptr, nullptr, nullptr);
     }
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }

@@ -141,11 +141,40 @@ def reserve(s, T, k, device=None):
     device = torch.device(device or s["g"].device)
     desc = _desc(s)
     L = _lib.lib()
-    need = max(int(L.moe_experts_workspace_bytes(desc, t, k, p)) for t in {1, int(T)}
-               for p in (_lib.PATH_SLOTS, _lib.PATH_GROUPED))
+    need = max([int(L.moe_experts_workspace_bytes(desc, t, k, p)) for t in {1, int(T)}
+                for p in (_lib.PATH_SLOTS, _lib.PATH_GROUPED)] +
+               [int(L.moe_layer_workspace_bytes(desc, t, k)) for t in {1, int(T)}])
     if "shared" in s:
         need = max(need, int(L.moe_shared_experts_workspace_bytes(_desc(s["shared"]), int(T))))
     return _lib.workspace(device, need)
+
+
+def run_routed(s, x, wr, k, bias=None, norm=True, scale=1.0, act=0, residual=None, out=None, out_dtype=None):
+    """Router + experts in one call (moe_layer_run): the fused router's logits x . wr^T (+ bias) and tail (the same
+    ids as router.route), then the experts on the default path. x [T, d] bf16, wr [E, d] bf16.
+    Returns (y [T, d], idx [T, k] int32, wts [T, k] fp32). The state's shared experts are not included."""
+    _lib.require_device(x, "x")
+    if x.dtype != torch.bfloat16 or wr.dtype != torch.bfloat16:
+        raise TypeError("run_routed takes bf16 x and router weights (the gate GEMV reads bf16)")
+    T, d = x.shape
+    x = x.contiguous()
+    wr = wr.contiguous()
+    b = None if bias is None else bias.to(torch.float32).contiguous()
+    desc = _desc(s)
+    L = _lib.lib()
+    ws = _lib.workspace(x.device, L.moe_layer_workspace_bytes(desc, T, k))
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((T, d), dtype=out_dtype, device=x.device)
+    assert out.dtype == out_dtype and out.dtype in _lib.DTYPE
+    idx = torch.empty((T, k), dtype=torch.int32, device=x.device)
+    wts = torch.empty((T, k), dtype=torch.float32, device=x.device)
+    res = None if residual is None else residual.to(out_dtype).contiguous()
+    rc = L.moe_layer_run(desc, _lib.ptr(x), _lib.DTYPE[x.dtype], _lib.ptr(wr), _lib.ptr(b), T, k, int(bool(norm)),
+                         float(scale), int(act), _lib.ptr(idx), _lib.ptr(wts), _lib.ptr(out), _lib.DTYPE[out.dtype],
+                         _lib.ptr(res), _lib.ptr(ws), ws.numel(), _lib.stream_of(x.device))
+    _lib.check("moe_layer_run", rc)
+    return out, idx, wts
 
 
 def run_shared(s, x, gate=None, act=0, residual=None, out=None, out_dtype=None):
