@@ -104,6 +104,18 @@ __device__ __forceinline__ float sum_lanes(float v) {
     if (G >= 64) v = dpp_add<0x143, 0xC>(v);
     return v;
 }
+// Inclusive prefix sum over the 64 lanes: row_shr steps inside each row of 16 lanes, then the row totals
+// (lanes 15, 31, 47) read as scalars and added to the rows after them.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+              r2 = __builtin_amdgcn_readlane(v, 47);
+    const int row = (threadIdx.x & 63) >> 4;
+    return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
 template <int G>
 __host__ __device__ constexpr int sum_lane() { return G <= 16 ? 0 : (G == 32 ? 16 : 48); }
 

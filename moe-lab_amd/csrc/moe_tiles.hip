@@ -84,7 +84,74 @@ struct TileArgs {
     size_t plane;
     size_t eslot_off;      // dense int4 down: per-slot exponents (int32 [slots]) at this byte offset from the exponent bytes
     const int32_t* xexp;   // dense int4 gate/up: per-token exponents of x16 (actv) [T]
+    const int32_t* gidx;   // wave tiles: when set, each workgroup finds its pass from these raw ids (gn = T k of them)
+    int gn, gfirst;        // instead of the grouping kernel's pass list (gfirst: expert-major first passes)
 };
+
+// In-kernel grouping, one wave: pass y of the wave tiles' pass list (passes of P slots; an expert's slots in
+// ascending slot id, the grouping kernel's order within each expert) from the raw ids idx[0 .. n)
+// (n <= 64 * GW_MAXJ). With first = 1 the list is expert-major: pass y < E is the first pass (ranks 0 .. P-1) of
+// expert y, found from the ids alone (a ballot per 64 ids); passes E, E + 1, ... are the further passes (q >= 1)
+// expert by expert. With first = 0 every pass is in the second, compact part (passes expert by expert from y = 0).
+// The compact part takes an LDS histogram (sCnt [E]) and a wave scan of the per-expert pass counts.
+// Returns false when pass y is empty (expert without slots, or past the last pass); else e, the pass's first
+// rank tok0 within the expert, the expert's slot count cnt, and sSlot[0 .. min(P, cnt - tok0)) the pass's slots.
+// Slots whose id is outside [0, E) join no pass. Called by whole one-wave workgroups.
+constexpr int GW_MAXJ = 16;
+__device__ __forceinline__ bool wave_find_pass(const int32_t* __restrict__ idx, int n, int E, int P, int first,
+                                               int y, int* sCnt, int* sSlot, int& e, int& tok0, int& cnt) {
+    const int lane = threadIdx.x & 63;
+    int id[GW_MAXJ];
+#pragma unroll
+    for (int j = 0; j < GW_MAXJ; ++j) {
+        const int p = lane + 64 * j;
+        id[j] = p < n ? idx[p] : -1;
+    }
+    if (first && y < E) {
+        e = y;
+        tok0 = 0;
+    } else {
+        const int w = first ? y - E : y;
+        for (int i = lane; i < E; i += 64) sCnt[i] = 0;
+        __syncthreads();   // one-wave workgroup: orders the LDS accesses
+#pragma unroll
+        for (int j = 0; j < GW_MAXJ; ++j)
+            if ((unsigned)id[j] < (unsigned)E) atomicAdd(&sCnt[id[j]], 1);
+        __syncthreads();
+        int run = 0;
+        bool found = false;
+        for (int base = 0; base < E && !found; base += 64) {
+            const int ee = base + lane;
+            const int c = ee < E ? sCnt[ee] : 0;
+            const int np = c > 0 ? (c - 1) / P + 1 - first : 0;   // the expert's passes in this part
+            const int inc = wave_incl_scan(np);
+            const int excl = run + inc - np;
+            const uint64_t hit = __ballot(np > 0 && excl <= w && w < excl + np);
+            if (hit) {   // wave-uniform results: scalar registers for the tile bases
+                const int src = __builtin_ctzll(hit);
+                e = __builtin_amdgcn_readlane(ee, src);
+                tok0 = (first + w - __builtin_amdgcn_readlane(excl, src)) * P;
+                found = true;
+            }
+            run += __builtin_amdgcn_readlane(inc, 63);
+        }
+        if (!found) return false;
+    }
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+    int seen = 0;
+#pragma unroll
+    for (int j = 0; j < GW_MAXJ; ++j) {
+        const bool m = id[j] == e;
+        const uint64_t mask = __ballot(m);
+        const int rank = seen + __popcll(mask & lt);
+        if (m && rank >= tok0 && rank < tok0 + P) sSlot[rank - tok0] = lane + 64 * j;
+        seen += __popcll(mask);
+    }
+    cnt = __builtin_amdgcn_readfirstlane(seen);
+    if (tok0 >= cnt) return false;
+    __syncthreads();
+    return true;
+}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -383,9 +450,21 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     constexpr bool INT4 = FMT::XSUM;
     constexpr int HL = NPROJ == 2 ? HX : 2;   // activation planes: x's (1, or 2-3 for fp16 / fp32 x), h = hi + lo
     constexpr int SB = tile_slice_bytes<FMT>();
-    if ((int)blockIdx.y >= a.meta[a.nidx]) return;   // one pass of the work list per workgroup row
-    const int e = a.items[3 * blockIdx.y], tok0 = a.items[3 * blockIdx.y + 1] * 16 * NT;
-    const int n = a.counts[e], beg = a.offsets[e];
+    __shared__ int sCnt[1024];            // in-kernel grouping: counts per expert (E <= 1024)
+    __shared__ int sSlot[16 * NT];        // and the pass's slots
+    int e, tok0, n, beg = 0;
+    if (a.gidx) {
+        if (!wave_find_pass(a.gidx, a.gn, a.E, 16 * NT, a.gfirst, (int)blockIdx.y, sCnt, sSlot, e, tok0, n))
+            return;
+        e = __builtin_amdgcn_readfirstlane(e);
+        tok0 = __builtin_amdgcn_readfirstlane(tok0);
+    } else {
+        if ((int)blockIdx.y >= a.meta[a.nidx]) return;   // one pass of the work list per workgroup row
+        e = a.items[3 * blockIdx.y];
+        tok0 = a.items[3 * blockIdx.y + 1] * 16 * NT;
+        n = a.counts[e];
+        beg = a.offsets[e];
+    }
     const int lane = threadIdx.x, lr = lane & 15, lg = lane >> 4;
     const int K = a.K, N = a.N;
     const int nsl = (K + 127) >> 7;
@@ -408,7 +487,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int m = tok0 + 16 * t + lr;
-            slotA[t] = a.sorted[beg + (m < n ? m : n - 1)];
+            slotA[t] = a.gidx ? sSlot[(m < n ? m : n - 1) - tok0] : a.sorted[beg + (m < n ? m : n - 1)];
             xo[t] = (uint32_t)(slotA[t] / a.act_div) * (uint32_t)K * 2u;
         }
         const uint8_t* xbase[HL];
@@ -1285,7 +1364,10 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 template <class FMT, int NPROJ, int RT, int D, bool H16O = false>
 int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st, int hx = 1) {
     if (t.N % (16 * RT)) return MOE_ERR_ARG;
-    dim3 grid(t.N / (16 * RT), max_passes(nslots, t.E, 16 * nt));
+    // in-kernel grouping, expert-major: E first passes and at most ceil(n / P) further ones (an expert with c
+    // slots has ceil(c / P) - 1 <= (c - 1) / P of them)
+    dim3 grid(t.N / (16 * RT), t.gidx && t.gfirst ? t.E + (nslots + 16 * nt - 1) / (16 * nt)
+                                                   : max_passes(nslots, t.E, 16 * nt));
     if (grid.y > 65535) return MOE_ERR_ARG;
     if constexpr (NPROJ == 2) {
         if (hx > 1) {   // fp16 / fp32 x planes: one 16-token tile per pass (the host passes nt = 1)
@@ -1392,15 +1474,27 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     const bool two_lists = P_gu != P_dn;
     t.items = a.grp.items;
     t.nidx = 2;
+    // both stages on the wave tiles with few slots: each workgroup finds its pass from the raw ids itself (an LDS
+    // histogram and a wave scan, the grouping launch's order), so the call has no grouping launch
+    if (wave_gu && wave_dn && nslots <= 64 * GW_MAXJ && w->E <= 1024 && env_int("MOE_INGROUP", 1)) {
+        t.gidx = a.idx;
+        t.gn = nslots;
+        // the compact pass list by default: its live passes come first in dispatch order whatever the skew. The
+        // expert-major list (MOE_INGROUP_FIRST=1) spares most workgroups the histogram and scan; measured at
+        // Qwen3 T=32 it gains ~1.3 us/layer with uniform routing but loses ~6 with Zipf routing, where the hot
+        // experts' further passes sit behind ~100 empty rows
+        t.gfirst = env_int("MOE_INGROUP_FIRST", 0) ? 1 : 0;
+    }
     if (h16) {
         // the second h plane holds the exponent bytes [slots, F/32], then the slot exponents int32 [slots]
         t.eslot_off = ((size_t)nslots * (w->F / 32) + 255) / 256 * 256;
         if (t.eslot_off + (size_t)nslots * 4 > (size_t)nslots * w->F * 2) return MOE_ERR_ARG;
     }
     if (a.stages & 1) {
-        int rc = launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
-                              a.grp.meta, a.st, P_gu, a.grp.items, two_lists ? P_dn : 0,
-                              two_lists ? a.grp.items2 : nullptr);
+        int rc = t.gidx ? 0
+                        : launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
+                                       a.grp.meta, a.st, P_gu, a.grp.items, two_lists ? P_dn : 0,
+                                       two_lists ? a.grp.items2 : nullptr);
         if (rc) return rc;
         TileArgs g = t;
         g.actv = a.xb;
