@@ -7,8 +7,9 @@ Cache). A step is one token through the 48 layers: x <- x + moe_l(x) for l = 0..
 HIP graph and replayed. `value` is expert weight-byte GB/s of that chain: the packed bytes of the unique
 selected experts of all 48 layers divided by the step time, the reference's `run(state, x, idx, wts)`
 contract (routing precomputed per layer, reference mlx_backend.py:91-117). The same chain with the
-fused router inside each layer is reported as `with_router`. BASELINE config 3 (T=32, uniform and
-Zipf(1.1) routing) reports the grouped expert path against the per-slot stock-style gather.
+router inside each layer (moe_layer_run) is reported as `with_router`. BASELINE config 3 (T=16, 32 and 64,
+uniform and Zipf(1.1) routing) reports the grouped expert path against the per-slot stock-style gather under
+`batched`; configs 4, 5a and 5b under `configs`.
 
 roofline: the dominant kernel at T=1 is the gate/up GEMV (2/3 of the weight bytes; the layer is two
 launches, gate/up then down). Its average launch duration is measured with HIP events on the stream it
@@ -18,6 +19,7 @@ duration.
 
 cpu_baseline: the reference's CPU torch path (torch_loop, reference variants/cuda/torch_loop.py:11-17)
 on dequantised fp32 weights of the selected experts, timed on this host for a bounded sample of layers.
+cpu_points: the same path at config 3's T=32 (one layer) and on 32-token samples of configs 5a and 5b.
 """
 import argparse
 import json
@@ -165,57 +167,21 @@ def main():
     log(f"gate/up kernel {t_gu * 1e6:.2f} us ({gu_bytes / t_gu / 1e9:.0f} GB/s), down kernel {t_dn * 1e6:.2f} us "
         f"({dn_bytes / t_dn / 1e9:.0f} GB/s)")
 
-    # ------------------------------------------------------------------ T = 32: grouped vs per-slot
-    t32 = {}
+    # ------------------------------------------------------------------ T = 16, 32, 64: grouped vs per-slot
+    # (uniform and Zipf(1.1) routing; T=16 and T=64 locate the per-slot / grouped crossover)
+    batched = {}
+    routes_b = {}
     if not args.no_t32:
-        for dist in ("uniform", "zipf"):
-            T = 32
-            x32 = baseline_x(T, sh.d, seed=32, device=dev)
-            bias = torch.from_numpy(zipf_bias(sh.E, 1.1, seed=3)).to(dev) if dist == "zipf" else None
-            routes = [router.route(x32, ly["wr"], sh.k, bias=bias) for ly in layers]
-            U = [int(torch.unique(r[0]).numel()) for r in routes]
-
-            def chain(path):
-                def f():
-                    x = x32.clone()
-                    for ly, (idx, wts) in zip(layers, routes):
-                        x = run_experts(ly, x, idx, wts, path=path, residual=x)
-                    return x
-                return f
-            res = {}
-            for name, path in (("grouped", _lib.PATH_GROUPED), ("per_slot", _lib.PATH_SLOTS)):
-                g, _ = graph_of(chain(path))
-                t = time_graph(g, max(5, args.steps // 5), max(2, args.warmup // 5))
-                res[name] = t
-                del g
-
-            def stage(st):   # one stage of the grouped path over the 48 layers (x fixed: timing only)
-                def f():
-                    for ly, (idx, wts) in zip(layers, routes):
-                        run_experts(ly, x32, idx, wts, path=_lib.PATH_GROUPED, stages=st)
-                return f
-            for name, st in (("gate_up", _lib.STAGE_GATE_UP), ("down", _lib.STAGE_DOWN)):
-                g, _ = graph_of(stage(st))
-                res[name] = time_graph(g, max(5, args.steps // 5), max(2, args.warmup // 5))
-                del g
-            ub = sum(U) * per_expert
-            t32[dist] = {
-                "us_per_layer_grouped": res["grouped"] * 1e6 / L,
-                "us_per_layer_per_slot": res["per_slot"] * 1e6 / L,
-                "speedup_per_token": res["per_slot"] / res["grouped"],
-                "unique_experts_mean": float(np.mean(U)),
-                "weight_GBps_grouped": ub / res["grouped"] / 1e9,
-                "slot_weight_GBps_per_slot": L * T * sh.k * per_expert / res["per_slot"] / 1e9,
-                # stage split of the grouped path: grouping + gate/up wave tiles (2/3 of the bytes), then
-                # down wave tiles + combine (1/3)
-                "gate_up_stage_us": res["gate_up"] * 1e6 / L,
-                "down_stage_us": res["down"] * 1e6 / L,
-                "gate_up_stage_GBps": ub * 2 / 3 / res["gate_up"] / 1e9,
-                "down_stage_GBps": ub / 3 / res["down"] / 1e9,
-            }
-            log(f"T=32 {dist}: grouped {t32[dist]['us_per_layer_grouped']:.1f} us/layer, per-slot "
-                f"{t32[dist]['us_per_layer_per_slot']:.1f} us/layer, speedup {t32[dist]['speedup_per_token']:.2f}x, "
-                f"U={t32[dist]['unique_experts_mean']:.1f}")
+        for T in (16, 32, 64):
+            for dist in ("uniform", "zipf"):
+                xT = baseline_x(T, sh.d, seed=T, device=dev)
+                bias = torch.from_numpy(zipf_bias(sh.E, 1.1, seed=3)).to(dev) if dist == "zipf" else None
+                routes = [router.route(xT, ly["wr"], sh.k, bias=bias) for ly in layers]
+                routes_b[(T, dist)] = (xT, routes)
+                batched.setdefault(f"T{T}", {})[dist] = r = time_batched(layers, xT, routes, T, sh, args)
+                log(f"T={T} {dist}: grouped {r['us_per_layer_grouped']:.1f} us/layer "
+                    f"({r['weight_GBps_grouped']:.0f} GB/s), per-slot {r['us_per_layer_per_slot']:.1f} us/layer, "
+                    f"speedup {r['speedup_per_token']:.2f}x, U={r['unique_experts_mean']:.1f}")
 
     # ------------------------------------------------------------------ BASELINE configs 4, 5a, 5b
     configs = {}
@@ -224,12 +190,19 @@ def main():
         torch.cuda.empty_cache()
         configs = other_configs(dev, args)
 
-    # ------------------------------------------------------------------ CPU baseline (bounded sample)
+    # ------------------------------------------------------------------ CPU baseline (bounded samples)
     cpu = None
+    cpu_points = {}
     if args.cpu_layers > 0:
         cpu_layers = [baseline_int4_layer(sh, seed=1000 + l, device=dev) for l in range(args.cpu_layers)]
         cpu = cpu_baseline(cpu_layers, routes1[:args.cpu_layers], x1, sh)
         log(f"CPU baseline: {cpu['value']:.1f} us/layer on {cpu['cores']} threads")
+        if (32, "uniform") in routes_b:   # config 3 at T=32 (the first seeded layer of the GPU chain)
+            xT, routes = routes_b[(32, "uniform")]
+            cpu_points["qwen3_T32_uniform"] = cpu_point([cpu_layers[0]], [routes[0]], xT, sh, "T=32 uniform", 4.0)
+        cpu_points.update(cpu_large_points(dev))
+        for name, r in cpu_points.items():
+            log(f"CPU {name}: {r['value']:.1f} {r['unit']} ({r['sample']})")
 
     value = bytes1 / t_step / 1e9
     out = {
@@ -255,16 +228,64 @@ def main():
         "with_router": {"us_per_layer": round(t_step_r * 1e6 / L, 3),
                         "weight_GBps": round(bytes1 / t_step_r / 1e9, 2)},
         "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3)},
-        "t32": t32,
+        "batched": batched,
         "configs": configs,
         "roofline": {"bound": "hbm", "kernel": "k_gate_up_rows<FmtInt4, 3, 1, 1> (T=1 gate/up GEMV + GLU)",
                      "achieved": round(gu_bytes / t_gu / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_bytes / t_gu / 1e9 / HBM_PEAK_GBS, 4), "traffic": GU_T1_TRAFFIC_BYTES,
                      "launch_us": round(t_gu * 1e6, 3), "algorithmic_bytes_per_launch": gu_bytes},
         "cpu_baseline": cpu,
+        "cpu_points": cpu_points,
     }
     print(json.dumps(out), flush=True)
     copy_calibrate(dev, args.copy_calibrate)
+
+
+def time_batched(layers, x, routes, T, sh, args):
+    """One BASELINE config 3 point: the 48-layer residual chain on the grouped path and on the per-slot path
+    (graph replays), plus the grouped path's two stages timed alone (x fixed: timing only)."""
+    from moelab_amd import _lib, roofline
+    from moelab_amd.experts import run_experts
+    L = len(layers)
+    per_expert = roofline.expert_bytes(sh.d, sh.f, "int4")
+    U = [int(torch.unique(r[0]).numel()) for r in routes]
+    steps, warm = max(5, args.steps // 5), max(2, args.warmup // 5)
+
+    def chain(path):
+        def f():
+            y = x.clone()
+            for ly, (idx, wts) in zip(layers, routes):
+                y = run_experts(ly, y, idx, wts, path=path, residual=y)
+            return y
+        return f
+
+    def stage(st):
+        def f():
+            for ly, (idx, wts) in zip(layers, routes):
+                run_experts(ly, x, idx, wts, path=_lib.PATH_GROUPED, stages=st)
+        return f
+    res = {}
+    for name, fn in (("grouped", chain(_lib.PATH_GROUPED)), ("per_slot", chain(_lib.PATH_SLOTS)),
+                     ("gate_up", stage(_lib.STAGE_GATE_UP)), ("down", stage(_lib.STAGE_DOWN))):
+        g, _ = graph_of(fn)
+        res[name] = time_graph(g, steps, warm)
+        del g
+    ub = sum(U) * per_expert
+    return {
+        "T": T,
+        "us_per_layer_grouped": round(res["grouped"] * 1e6 / L, 2),
+        "us_per_layer_per_slot": round(res["per_slot"] * 1e6 / L, 2),
+        "speedup_per_token": round(res["per_slot"] / res["grouped"], 3),
+        "tokens_per_s_grouped": round(T * L / res["grouped"], 1),
+        "unique_experts_mean": round(float(np.mean(U)), 2),
+        "weight_GBps_grouped": round(ub / res["grouped"] / 1e9, 1),
+        "slot_weight_GBps_per_slot": round(L * T * sh.k * per_expert / res["per_slot"] / 1e9, 1),
+        # stage split of the grouped path: gate/up (2/3 of the bytes), then down + combine (1/3)
+        "gate_up_stage_us": round(res["gate_up"] * 1e6 / L, 2),
+        "down_stage_us": round(res["down"] * 1e6 / L, 2),
+        "gate_up_stage_GBps": round(ub * 2 / 3 / res["gate_up"] / 1e9, 1),
+        "down_stage_GBps": round(ub / 3 / res["down"] / 1e9, 1),
+    }
 
 
 def copy_calibrate(dev, mib):
@@ -359,11 +380,21 @@ def other_configs(dev, args, only=None):
 
 
 def cpu_baseline(layers, routes, x, sh):
-    """torch_loop (the reference's CPU torch path) on fp32 dense weights of the selected experts only."""
+    """torch_loop (the reference's CPU torch path) on fp32 dense weights of the selected experts only: the
+    bench line's cpu_baseline, at T=1 on the first layers of the GPU chain."""
+    r = cpu_point(layers, routes, x, sh, "T=1", 10.0)
+    dt = r["value"] * 1e-6
+    r["unit"] = "us/layer (T=1, expert path)"
+    r["weight_GBps_equiv"] = round(sh.k * roofline_bytes(sh) / dt / 1e9, 2)
+    return r
+
+
+def cpu_point(layers, routes, x, sh, what, budget_s):
+    """torch_loop (the reference's CPU torch path) on fp32 dense copies of the selected experts of int4 SwiGLU
+    layers: a residual chain over `layers`, repeated for about budget_s seconds; microseconds per layer-call."""
     from moelab_amd import formats
     from moelab_amd.experts import unpack
     orc = __graft_entry__.load_oracle()
-    cores = torch.get_num_threads()
     xs = x.float().cpu()
     dense = []
     for ly, (idx, wts) in zip(layers, routes):
@@ -382,14 +413,35 @@ def cpu_baseline(layers, routes, x, sh):
     once()
     t0 = time.perf_counter()
     reps = 0
-    while time.perf_counter() - t0 < 10.0 and reps < 2000:
+    while time.perf_counter() - t0 < budget_s and reps < 2000:
         once()
         reps += 1
     dt = (time.perf_counter() - t0) / reps / len(dense)
-    return {"value": round(dt * 1e6, 2), "unit": "us/layer (T=1, expert path)", "cores": cores, "kind": "port",
-            "sample": f"{len(dense)} Qwen3 int4 layers at T=1 (k=8 experts each, dequantised to fp32), "
-                      f"{reps} reps of the residual chain, ~10 s",
-            "weight_GBps_equiv": round(sh.k * roofline_bytes(sh) / dt / 1e9, 2)}
+    T = x.shape[0]
+    return {"value": round(dt * 1e6, 1), "unit": "us/layer", "tokens_per_s": round(T / dt, 1),
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(dense)} {sh.name} int4 layer(s) at {what} (T={T}, k={sh.k}, selected experts "
+                      f"dequantised to fp32), {reps} reps, ~{budget_s:.0f} s"}
+
+
+def cpu_large_points(dev):
+    """BASELINE configs 5a and 5b on the CPU torch path, on a bounded sample: the first 32 tokens of the T=512 /
+    T=256 batch (uniform router logits) through one seeded layer; 5b's routed experts only (the shared experts
+    are two dense SwiGLU MLPs on every token, left out of this sample). Reported as us per layer-call of 32
+    tokens and tokens/s."""
+    from moelab_amd import router
+    from moelab_amd.problem import baseline_int4_layer, baseline_x
+    from moelab_amd.shapes import SHAPES
+    out = {}
+    for key, name, T in (("mixtral8x7b_int4_T512_32tok", "mixtral-8x7b", 512),
+                         ("dsv2lite_int4_T256_32tok_routed", "deepseek-v2-lite", 256)):
+        sh = SHAPES[name]
+        ly = baseline_int4_layer(sh, seed=3000, device=dev)
+        x = baseline_x(T, sh.d, seed=T, device=dev)[:32].contiguous()
+        out[key] = cpu_point([ly], [router.route(x, ly["wr"], sh.k)], x, sh, f"a 32-token sample of T={T}", 3.0)
+        del ly
+        torch.cuda.empty_cache()
+    return out
 
 
 def roofline_bytes(sh):
