@@ -733,13 +733,27 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
 // workgroup barrier without a memory fence; the "memory" clobber keeps LDS accesses on their side of it
 #define MOE_BARRIER() asm volatile("s_barrier" ::: "memory")
 
+// Dense tile shapes (measured at the Mixtral T=512 shape). int4 down (operands decoded to fp16 with the scale
+// applied, no fold): 128-token passes and 32 rows per wave, so each decoded operand feeds 8 MFMAs (the decode's
+// 15 VALU instructions per code word come to ~2 per MFMA) and the 64 accumulators stay in VGPRs at 2 waves per
+// SIMD: 234 -> 214 us against 64-token passes. int4 gate/up keeps 64-token passes with 32 rows of each
+// projection per wave: with 128 tokens and 16 rows each, every activation slice staged in LDS serves half as many
+// rows (K = d is long, the L2 -> LDS traffic doubles) and the kernel slowed 440 -> 509 us. MXFP4 (raw codes on
+// bf16 MFMA, fp32 fold per group): 64-token passes, 32 / 64 rows per wave.
+template <class FMT, int NPROJ>
+__host__ __device__ constexpr int dense_nt() { return FMT::XSUM && NPROJ == 1 ? 8 : 4; }
+template <class FMT, int NPROJ>
+__host__ __device__ constexpr int dense_rt() { return FMT::XSUM ? 2 : 4 / NPROJ; }
+template <class FMT, int NPROJ>
+__host__ __device__ constexpr int dense_bn() { return 4 * 16 * dense_rt<FMT, NPROJ>(); }
+
 template <class FMT, int NPROJ, int NT>
 __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     constexpr bool INT4 = FMT::XSUM;
     constexpr int SPG = INT4 ? 2 : 1;     // MFMA steps (32 inputs) per scale group
-    constexpr int RT = 4 / NPROJ;         // 16-row tiles per projection per wave
+    constexpr int RT = dense_rt<FMT, NPROJ>();   // 16-row tiles per projection per wave
     constexpr int BM = 16 * NT;           // tokens per pass
-    constexpr int BN = 4 * 16 * RT;       // rows per block (per projection)
+    constexpr int BN = dense_bn<FMT, NPROJ>();   // rows per block (per projection)
     constexpr int SB = tile_slice_bytes<FMT>();
     // int4 (F16): activations travel as fp16 with power-of-two exponents (x16 per token; h16 per slot) and the
     // codes are dequantised to fp16 in registers; MXFP4 keeps the exact raw-code path on bf16 MFMA with its
@@ -752,14 +766,21 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t sX1[HL * BM * 256];
     __shared__ int sSlot[BM];
 
-    // 1-D grid over (pass list x row blocks), ordered expert by expert, and within an expert row block by row
-    // block with the expert's passes adjacent: the passes that share a weight tile run side by side (their
-    // second reads come from the caches), and the blocks in flight touch the activations of few experts
+    // Work items (pass list x row blocks x K parts), ordered expert by expert, within an expert row block by row
+    // block with the expert's passes adjacent, K part fastest. The launch hands workgroups to the 8 XCDs round
+    // robin (workgroup b to XCD (b + c) mod 8, c fixed per launch), so XCD slot b & 7 takes the contiguous
+    // eighth of the live items, in order: each XCD's L2 then holds the activations of few experts, and the
+    // passes that share a weight tile run side by side on one XCD (their second reads hit its L2). The grid is
+    // a multiple of 8 covering the largest possible item count.
     const int nrb = (a.N + BN - 1) / BN;
-    const int ks = (int)(blockIdx.x % (unsigned)a.ksplit);   // K part (down only), the fastest index
-    const int bid = (int)(blockIdx.x / (unsigned)a.ksplit);
+    const int nitems = a.meta[a.nidx] * nrb * a.ksplit;
+    const int chunk = (nitems + 7) >> 3;
+    const int rank = (int)(blockIdx.x >> 3);
+    const int item = (int)(blockIdx.x & 7u) * chunk + rank;
+    if (rank >= chunk || item >= nitems) return;
+    const int ks = item % a.ksplit;               // K part (down only), the fastest index
+    const int bid = item / a.ksplit;
     const int wq = bid / nrb;                      // some pass of the current expert
-    if (wq >= a.meta[a.nidx]) return;
     const int e = a.items[3 * wq], np = a.items[3 * wq + 2];
     const int w0 = wq - a.items[3 * wq + 1];       // the expert's first pass
     const int local = bid - w0 * nrb;
@@ -815,14 +836,20 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
         };
         uint4 rq[2][NPROJ][RT];
         uint2 rm[2][NPROJ][RT];
-        // F16: the exponent of lane j's token (token j of the pass): its activation row is x 2^-E (x16, k_x16) or
-        // h 2^-E (h16, k_h16_fix)
-        int eslot = 0;
-        if constexpr (F16) {
-            if (NPROJ == 1)
-                eslot = reinterpret_cast<const int32_t*>(reinterpret_cast<const uint8_t*>(a.actv2) + a.eslot_off)[sSlot[lane]];
-            else
-                eslot = a.xexp[sSlot[lane] / a.act_div];
+        // F16: entry h of lane j holds the exponent E of token 64 h + j of the pass: its activation row is x 2^-E
+        // (x16, k_x16) or h 2^-E (h16, k_h16_fix)
+        constexpr int NE = (BM + 63) / 64;   // lane j of entry h: token 64 h + j
+        int eslot[NE];
+#pragma unroll
+        for (int h = 0; h < NE; ++h) {
+            eslot[h] = 0;
+            const int j = 64 * h + lane;
+            if (F16 && j < BM) {
+                if (NPROJ == 1)
+                    eslot[h] = reinterpret_cast<const int32_t*>(reinterpret_cast<const uint8_t*>(a.actv2) + a.eslot_off)[sSlot[j]];
+                else
+                    eslot[h] = a.xexp[sSlot[j] / a.act_div];
+            }
         }
         auto wissue = [&](int s, uint4 (&q)[NPROJ][RT], uint2 (&m)[NPROJ][RT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -874,35 +901,47 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
         auto mfma_f16 = [&](auto full, auto next, const uint8_t* xs, int G, const f16x8 (&B)[NPROJ][RT][2],
                             const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT], f16x8 (&Bn)[NPROJ][RT][2])
                             __attribute__((always_inline)) {
-            constexpr int PPT = NPROJ * RT / NT;   // pairs decoded per token tile
+            // pairs decoded after each token tile (PPT >= 1), or one pair after every TPP-th token tile
+            constexpr int PPT = NPROJ * RT >= NT ? NPROJ * RT / NT : 1;
+            constexpr int TPP = NPROJ * RT >= NT ? 1 : NT / (NPROJ * RT);
+            // the A operands of token tile t + 2 are read from LDS while tile t's MFMAs run (three register sets:
+            // one token tile's MFMAs alone do not cover the LDS latency when a wave has only 2 row tiles)
+            auto load_a = [&](int t, f16x8 (&A)[2]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int j = 2 * G + u;
+                    const int wi = j < 2 ? 2 * lg + j : 8 + 2 * lg + (j - 2);
+                    A[u] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(xs + (16 * t + lr) * 256 + 16 * (wi ^ lr)));
+                }
+            };
+            f16x8 Ab[3][2];
+            if (decltype(full)::value || 0 < ntiles) load_a(0, Ab[0]);
+            if (NT > 1 && (decltype(full)::value || 1 < ntiles)) load_a(1, Ab[1]);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
+                if (t + 2 < NT && (decltype(full)::value || t + 2 < ntiles)) load_a(t + 2, Ab[(t + 2) % 3]);
+                __builtin_amdgcn_sched_barrier(0);
                 if (decltype(full)::value || t < ntiles) {   // wave-uniform
-                    f16x8 A[2];
 #pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const int j = 2 * G + u;
-                        const int wi = j < 2 ? 2 * lg + j : 8 + 2 * lg + (j - 2);
-                        A[u] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(xs + (16 * t + lr) * 256 + 16 * (wi ^ lr)));
-                    }
+                    for (int u = 0; u < 2; ++u)
 #pragma unroll
-                    for (int p = 0; p < NPROJ; ++p)
+                        for (int p = 0; p < NPROJ; ++p)
 #pragma unroll
-                        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-                            for (int u = 0; u < 2; ++u)
-                                acc[p][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u], B[p][rt][u], acc[p][rt][t], 0, 0, 0);
+                            for (int rt = 0; rt < RT; ++rt)
+                                acc[p][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab[t % 3][u], B[p][rt][u], acc[p][rt][t], 0, 0, 0);
                 }
                 if constexpr (decltype(next)::value) {
+                    if (t % TPP == TPP - 1) {
 #pragma unroll
-                    for (int i = t * PPT; i < (t + 1) * PPT; ++i) decode_f16(G + 1, i / RT, i % RT, q, m, Bn);
+                        for (int i = (t / TPP) * PPT; i < (t / TPP + 1) * PPT; ++i) decode_f16(G + 1, i / RT, i % RT, q, m, Bn);
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
         auto slice_f16 = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT])
                              __attribute__((always_inline)) {
-            static_assert(NPROJ * RT % NT == 0, "decode pairs split evenly over the token tiles");
+            static_assert(NPROJ * RT % NT == 0 || NT % (NPROJ * RT) == 0, "decode pairs spread evenly over the token tiles");
             f16x8 B0[NPROJ][RT][2], B1[NPROJ][RT][2];
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1028,12 +1067,13 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
             // h of the wave's 32 rows as fp16 h16 = h 2^-e, e per token: 0 while |h| < 2^15 on those rows, else
             // the power of two that brings their largest |h| below 2^15 (so fp16 never overflows); e goes to the
             // exponent bytes [slot, F / 32] (one 32-row chunk per wave)
+            static_assert(RT == 2, "one 32-row chunk per wave");
             float hv[NT][4][RT];
             int xe[NT][4];   // x16 = x 2^-E per token: the sums are scaled back before the GLU
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) xe[t][v] = __shfl(eslot, 16 * t + 4 * lg + v, 64);
+                for (int v = 0; v < 4; ++v) xe[t][v] = __shfl(eslot[(16 * t) >> 6], (16 * t + 4 * lg + v) & 63, 64);
             int8_t* hexp_out = reinterpret_cast<int8_t*>(a.hout2);
             const int nch = N >> 5;
 #pragma unroll
@@ -1069,7 +1109,7 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) es[t][v] = H16 ? __shfl(eslot, 16 * t + 4 * lg + v, 64) : 0;
+                for (int v = 0; v < 4; ++v) es[t][v] = H16 ? __shfl(eslot[(16 * t) >> 6], (16 * t + 4 * lg + v) & 63, 64) : 0;
             if (wvalid)
 #pragma unroll
             for (int t = 0; t < NT; ++t)
@@ -1382,11 +1422,6 @@ int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st, int 
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-// dense tiles: passes of DENSE_NT token tiles (64 tokens). 64 tokens x 64 rows per wave keep the fold's
-// accumulators (64 VGPRs) and everything else within 256 VGPRs at 2 waves per SIMD; 128 tokens per wave would
-// push the accumulators into AGPRs, which the fold's VALU cannot use in place.
-constexpr int DENSE_NT = 4;
-
 // Environment knobs, read per call (tuning and tests): MOE_DENSE = 0 turns the dense tiles off (the LDS-staged
 // row tiles take the calls with more than 32 tokens per expert), 1 uses them for every such call, unset chooses
 // by grid size; MOE_WAVE_NT = 1 or 2 forces the wave tiles' token tiles per pass.
@@ -1397,8 +1432,8 @@ int env_int(const char* name, int dflt) {
 
 // K parts of the dense down projection: 2 when the row blocks x passes would leave the chip under-filled (the
 // combine adds the parts' planes); gate/up is never split (the GLU needs whole sums)
-int dense_ksplit(int N, int K, int nslots, int E) {
-    const long blocks = (long)((N + 255) / 256) * max_passes(nslots, E, 16 * DENSE_NT);
+int dense_ksplit(int N, int K, int nslots, int E, int BN, int P) {
+    const long blocks = (long)((N + BN - 1) / BN) * max_passes(nslots, E, P);
     const int nsl = (K + 127) / 128;
     int ks = env_int("MOE_DENSE_KSPLIT", 0);
     if (ks < 1 || ks > 4) ks = blocks < 4L * 256 && nsl >= 8 ? 2 : 1;
@@ -1409,12 +1444,13 @@ int dense_ksplit(int N, int K, int nslots, int E) {
 
 template <class FMT, int NPROJ>
 int launch_dense(TileArgs t, int nslots, hipStream_t st) {
-    constexpr int BN = 64 * (4 / NPROJ);
-    if (t.N % (64 / NPROJ)) return MOE_ERR_ARG;
+    constexpr int BN = dense_bn<FMT, NPROJ>(), NT = dense_nt<FMT, NPROJ>();
+    if (t.N % (16 * dense_rt<FMT, NPROJ>())) return MOE_ERR_ARG;   // whole row tiles per wave
     if (NPROJ == 2) t.ksplit = 1;
-    const long nblk = (long)((t.N + BN - 1) / BN) * max_passes(nslots, t.E, 16 * DENSE_NT) * t.ksplit;
-    if (nblk > 0x7FFFFFFFL) return MOE_ERR_ARG;
-    k_dense<FMT, NPROJ, DENSE_NT><<<dim3((unsigned)nblk), 256, 0, st>>>(t);
+    // rounded up to a multiple of 8: every XCD slot then has a workgroup for each of its ceil(items / 8) items
+    const long nblk = ((long)((t.N + BN - 1) / BN) * max_passes(nslots, t.E, 16 * NT) * t.ksplit + 7) / 8 * 8;
+    if (nblk > 0x7FFFFFF8L) return MOE_ERR_ARG;
+    k_dense<FMT, NPROJ, NT><<<dim3((unsigned)nblk), 256, 0, st>>>(t);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
@@ -1448,9 +1484,10 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     constexpr bool INT4 = FmtInt4::FMT == FMT::FMT;
     const bool tiled = w->gate.tiles && w->up.tiles && w->down.tiles;
     const int dmode = env_int("MOE_DENSE", -1);
-    const int dpasses = max_passes(nslots, w->E, 16 * DENSE_NT);
-    const long dblocks = (long)((w->F + 127) / 128) * dpasses;
-    const long dn_blocks = (long)((w->d + 255) / 256) * dpasses;
+    constexpr int DP_GU = 16 * dense_nt<FMT, 2>(), DP_DN = 16 * dense_nt<FMT, 1>();
+    constexpr int BN_GU = dense_bn<FMT, 2>(), BN_DN = dense_bn<FMT, 1>();
+    const long dblocks = (long)((w->F + BN_GU - 1) / BN_GU) * max_passes(nslots, w->E, DP_GU);
+    const long dn_blocks = (long)((w->d + BN_DN - 1) / BN_DN) * max_passes(nslots, w->E, DP_DN);
     const int min_avg = env_int("MOE_DENSE_MIN_AVG", 32);
     const int dn_min_avg = env_int("MOE_DENSE_DN_MIN_AVG", 16);
     // activations as planes (fp16 / fp32 x): the dense gate/up takes only what it reads exactly, int4 with fp16 x
@@ -1468,9 +1505,9 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     const int nt = a.nx > 1 ? 1
                  : (wave_gu || wave_dn) ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2))
                                         : tokens_per_pass_tiles(a.T, a.k, w->E);
-    // pass lists: 16 nt tokens per pass for the wave tiles, 16 DENSE_NT for the dense tiles; a second list
+    // pass lists: 16 nt tokens per pass for the wave tiles, DP_GU / DP_DN for the dense tiles; a second list
     // when the two stages take different kernels
-    const int P_gu = dense_gu ? 16 * DENSE_NT : 16 * nt, P_dn = dense_dn ? 16 * DENSE_NT : 16 * nt;
+    const int P_gu = dense_gu ? DP_GU : 16 * nt, P_dn = dense_dn ? DP_DN : 16 * nt;
     const bool two_lists = P_gu != P_dn;
     t.items = a.grp.items;
     t.nidx = 2;
@@ -1541,7 +1578,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.N = w->d;
         d.W0 = (const uint8_t*)w->down.rows;
         d.yp = a.yp;
-        d.ksplit = dense_dn ? dense_ksplit(d.N, d.K, nslots, w->E) : 1;
+        d.ksplit = dense_dn ? dense_ksplit(d.N, d.K, nslots, w->E, BN_DN, DP_DN) : 1;
         d.plane = (size_t)nslots * d.N;
         if (two_lists) {
             d.items = a.grp.items2;
