@@ -869,30 +869,27 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
             for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[p][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        // H16 down, one slice: codes dequantised exactly to fp16 pairs (v_perm puts 0x64 above each nibble: 1024 + q,
-        // exact), then q = (1024 + q) - 1024 and w = s q + b in one rounding (v_pk_add_f16, v_pk_fma_f16); the MFMA
-        // (f16 x f16, fp32 accumulate) adds the slice straight into acc.
-        // F16 (int4): the B operands of projection p, row tile rt, scale group G: codes dequantised exactly to fp16
-        // pairs (v_perm puts 0x64 above each nibble: 1024 + q, exact), then q = (1024 + q) - 1024 and w = s q + b in
-        // one rounding (v_pk_add_f16, v_pk_fma_f16)
+        // F16 (int4): the B operands of projection p, row tile rt, scale group G, as fp16 w' = (s q + b) 2^-16 in
+        // one rounding: each code pair (q_k, q_{k+4}) is masked into bits 4-7 of two fp16 halves with exponent 0,
+        // which makes them the exact subnormals q 2^-20 (one shift and one mask), and one v_pk_fma_f16 takes
+        // q 2^-20 (s 16) + b 2^-16. The records' row scaling keeps |s|, |b| below 2^11, so s 16 < 2^15 fits fp16
+        // and |w'| < 2^-1; the epilogue adds 16 to the row exponent. 11 VALU per code word (the 1024 + q magic
+        // and its v_pk_add_f16 took 15).
+        constexpr int DEC_EXP = 16;
         auto decode_f16 = [&](int G, int p, int rt, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT],
                               f16x8 (&B)[NPROJ][RT][2]) __attribute__((always_inline)) {
-            const h2x off = {(_Float16)-1024.f, (_Float16)-1024.f};
             const uint32_t mw = G ? m[p][rt].y : m[p][rt].x;
-            const _Float16 s16 = (_Float16)bf16lo(mw), b16 = (_Float16)bf16hi(mw);
+            const _Float16 s16 = (_Float16)(bf16lo(mw) * 16.0f), b16 = (_Float16)(bf16hi(mw) * 0x1p-16f);
             const h2x s2 = {s16, s16}, b2 = {b16, b16};
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int j = 2 * G + u;
                 const uint32_t w = j == 0 ? q[p][rt].x : (j == 1 ? q[p][rt].y : (j == 2 ? q[p][rt].z : q[p][rt].w));
-                const uint32_t tq = w & 0x0F0F0F0Fu, uq = (w >> 4) & 0x0F0F0F0Fu;
-                const uint32_t c4[4] = {__builtin_amdgcn_perm(0x64646464u, tq, 0x04020400u),
-                                        __builtin_amdgcn_perm(0x64646464u, uq, 0x04020400u),
-                                        __builtin_amdgcn_perm(0x64646464u, tq, 0x04030401u),
-                                        __builtin_amdgcn_perm(0x64646464u, uq, 0x04030401u)};
+                const uint32_t c4[4] = {(w << 4) & 0x00F000F0u, w & 0x00F000F0u, (w >> 4) & 0x00F000F0u,
+                                        (w >> 8) & 0x00F000F0u};
                 h2x v[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) v[c] = __builtin_elementwise_fma(__builtin_bit_cast(h2x, c4[c]) + off, s2, b2);
+                for (int c = 0; c < 4; ++c) v[c] = __builtin_elementwise_fma(__builtin_bit_cast(h2x, c4[c]), s2, b2);
                 B[p][rt][u] = f16x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
             }
         };
@@ -1035,7 +1032,7 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
         for (int p = 0; p < NPROJ; ++p)
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
-                rex[p][rt] = INT4 && wvalid ? tile_row_exps(p ? a.W1 : a.W0, a.E, N, K)[(size_t)e * N + r0 + 16 * rt + lr] : 0;
+                rex[p][rt] = INT4 && wvalid ? tile_row_exps(p ? a.W1 : a.W0, a.E, N, K)[(size_t)e * N + r0 + 16 * rt + lr] + DEC_EXP : 0;
         // slice s sits in buffer / ring slot s & 1; slice s + 1 is fetched during slice s (the last slice fetches
         // itself again into the idle slot: no branch around the loads)
         auto run = [&](auto full) __attribute__((always_inline)) {
