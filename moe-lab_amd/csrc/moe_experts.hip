@@ -229,11 +229,14 @@ k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __r
 // k slots of token t. Lane l of a wave: chunk phase p = l % L, slot j = l / L (64 / L >= k slot lanes, L a
 // power of two), so one wave covers every (slot, chunk) pair of its RR rows, and the k-reduction is an
 // in-wave DPP sum. A lane handles chunks p, p + L, ..., p + (NC-1) L of rows n .. n + RR - 1 and reuses
-// each h chunk for the RR rows. The pre-paired h planes of the k slots are copied once per block into LDS,
-// with each chunk's sum (the int4 fold needs it). Order of memory operations: the lane's expert id and
-// routing weight, the first h chunks (L2), every weight chunk and metadata word of the lane (branch-free:
-// chunk indices past the row are clamped into it and masked out of the math), the LDS staging, then the
-// math in load order.
+// each h chunk for the RR rows. The pre-paired h planes of the k slots are copied once per block into LDS
+// (coalesced: consecutive lanes load consecutive 16-byte words), with each chunk's sum (the int4 fold needs it)
+// in a ninth 16-byte word: a chunk record is 144 bytes, so the records of 16 consecutive chunks start on 16
+// distinct 16-byte bank groups (144 = 9 x 16, 9 odd) and the math's ds_read_b128 of 16 lanes on consecutive
+// chunks is free of bank conflicts (a 128-byte record puts every second chunk on the same 4 banks: an 8-way
+// conflict). Order of memory operations: the lane's expert id and routing weight, the first staged h words
+// (L2), every weight chunk and metadata word of the lane (branch-free: chunk indices past the row are clamped
+// into it and masked out of the math), the LDS staging, then the math in load order.
 template <class FMT, int NC, int RR, int NW>
 __global__ void __launch_bounds__(64 * NW)
 k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
@@ -249,26 +252,25 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     const int p = lane & (L - 1), j = lane >> lgL;
     const int cpr = F >> 5;
     const int nch = k * cpr;   // chunks of h to stage
-    uint4* s_h = s_dyn;                                                 // [nch][8]: hi pairs x4, lo pairs x4
-    float* s_sum = reinterpret_cast<float*>(s_dyn + (size_t)8 * nch);   // [nch]
+    uint4* s_h = s_dyn;   // [nch][9]: hi pairs x4, lo pairs x4, {chunk sum, pad}
     // ---- expert id and routing weight of this lane's slot
     const bool jv = j < k;
     const int slot = t * k + (jv ? j : k - 1);
     const int e = idx[slot];
     const float wraw = wts[slot];
-    // ---- first staging chunk of this thread (L2)
+    // ---- first staged words of this thread (L2): 16-byte word u of the token's hi and lo planes, u = thread +
+    // m * block size, consecutive lanes on consecutive words (word u is quarter u & 3 of chunk u >> 2)
+    constexpr int PF = 4;
     const size_t hbase = (size_t)t * k * F;
-    const int c_st = threadIdx.x;
-    uint4 hv[8];
-    {
-        const int c = min(c_st, nch - 1);
-        const uint4* sh = reinterpret_cast<const uint4*>(hhi + hbase + 32 * (size_t)c);
-        const uint4* sl = reinterpret_cast<const uint4*>(hlo + hbase + 32 * (size_t)c);
+    const uint4* h4 = reinterpret_cast<const uint4*>(hhi + hbase);
+    const uint4* l4 = reinterpret_cast<const uint4*>(hlo + hbase);
+    const int nu = nch * 4;
+    uint4 hv[2 * PF];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            hv[q] = sh[q];
-            hv[4 + q] = sl[q];
-        }
+    for (int m = 0; m < PF; ++m) {
+        const int u = min((int)threadIdx.x + m * 64 * NW, nu - 1);
+        hv[2 * m] = h4[u];
+        hv[2 * m + 1] = l4[u];
     }
     // ---- weights of this lane
     const bool ev = jv && (unsigned)e < (unsigned)E;
@@ -293,27 +295,34 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // ---- stage h: this thread's first chunk, then any further chunks (only when k * cpr > 64 * NW)
-    for (int c = c_st; c < nch; c += 64 * NW) {
-        if (c != c_st) {
-            const uint4* sh = reinterpret_cast<const uint4*>(hhi + hbase + 32 * (size_t)c);
-            const uint4* sl = reinterpret_cast<const uint4*>(hlo + hbase + 32 * (size_t)c);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                hv[q] = sh[q];
-                hv[4 + q] = sl[q];
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) s_h[(size_t)c * 8 + q] = hv[q];
+    // ---- stage h: the prefetched words, then any further ones (only when k * F > 32 * PF * block size). The
+    // four lanes of a chunk are consecutive lanes of one wave and always active together (nu and the block size
+    // are multiples of 4), so the chunk sum (int4 fold) is a quad reduction.
+    auto put = [&](int u, const uint4& a, const uint4& b) __attribute__((always_inline)) {
+        uint4* r = s_h + (size_t)(u >> 2) * 9;
+        r[u & 3] = a;
+        r[4 + (u & 3)] = b;
         if (FMT::XSUM) {
-            uint32_t w[16];
-            words16(hv, w);
-            const float sm = sum16(w, 0.f);
-            words16(hv + 4, w);
-            s_sum[c] = sum16(w, sm);
+            float sm = 0.f;
+            sm = dot2_bf16(a.x, 0x3f803f80u, sm);
+            sm = dot2_bf16(a.y, 0x3f803f80u, sm);
+            sm = dot2_bf16(a.z, 0x3f803f80u, sm);
+            sm = dot2_bf16(a.w, 0x3f803f80u, sm);
+            sm = dot2_bf16(b.x, 0x3f803f80u, sm);
+            sm = dot2_bf16(b.y, 0x3f803f80u, sm);
+            sm = dot2_bf16(b.z, 0x3f803f80u, sm);
+            sm = dot2_bf16(b.w, 0x3f803f80u, sm);
+            sm += __shfl_xor(sm, 1, 64);
+            sm += __shfl_xor(sm, 2, 64);
+            if ((u & 3) == 0) reinterpret_cast<float*>(r + 8)[0] = sm;
         }
+    };
+#pragma unroll
+    for (int m = 0; m < PF; ++m) {
+        const int u = (int)threadIdx.x + m * 64 * NW;
+        if (u < nu) put(u, hv[2 * m], hv[2 * m + 1]);
     }
+    for (int u = (int)threadIdx.x + PF * 64 * NW; u < nu; u += 64 * NW) put(u, h4[u], l4[u]);
     __syncthreads();
     // ---- math
     float acc[RR];
@@ -325,9 +334,9 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
         const bool cv = ev && chk < cpr;
         const size_t hc = (size_t)(jv ? j : 0) * cpr + min(chk, cpr - 1);
         uint32_t wh[16], wl[16];
-        words16(&s_h[hc * 8], wh);
-        words16(&s_h[hc * 8 + 4], wl);
-        const float hs = FMT::XSUM ? s_sum[hc] : 0.f;
+        words16(&s_h[hc * 9], wh);
+        words16(&s_h[hc * 9 + 4], wl);
+        const float hs = FMT::XSUM ? reinterpret_cast<const float*>(s_h + hc * 9 + 8)[0] : 0.f;
 #pragma unroll
         for (int i = 0; i < RR; ++i) {
             uint32_t qp[16];
@@ -742,7 +751,7 @@ int launch_gu_rows(const ExpertsArgs& a) {
 // lane. Returns 1 when the shape does not fit (k > 64, or k * F too large for LDS): the caller falls back.
 constexpr int DR_LDS_MAX = 150 * 1024;
 
-int down_rows_lds(int k, int F) { return k * (F >> 5) * (128 + 4); }
+int down_rows_lds(int k, int F) { return k * (F >> 5) * 144; }   // 144-byte chunk records
 
 #ifndef MOE_DN_NW
 #define MOE_DN_NW 4   // waves per down block
@@ -801,8 +810,8 @@ int launch_dn_rows(const ExpertsArgs& a) {
         case 2: return launch_dn_rows_k<FMT, 2, (2 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
         case 3: return launch_dn_rows_k<FMT, 3, (3 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
         case 4: return launch_dn_rows_k<FMT, 4, (4 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
-        case 6: return launch_dn_rows_k<FMT, 6, 1>(a, lgL);
-        case 8: return launch_dn_rows_k<FMT, 8, 1>(a, lgL);
+        case 6: return launch_dn_rows_k<FMT, 6, (6 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
+        case 8: return launch_dn_rows_k<FMT, 8, (8 <= MOE_DN_RR2_NC ? 2 : 1)>(a, lgL);
         case 12: return launch_dn_rows_k<FMT, 12, 1>(a, lgL);
         case 16: return launch_dn_rows_k<FMT, 16, 1>(a, lgL);
         default: return MOE_ERR_ARG;

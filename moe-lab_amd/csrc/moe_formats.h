@@ -80,18 +80,19 @@ struct FmtMxfp4 {
     static constexpr int FMT = MOE_FMT_MXFP4;
     static constexpr bool XSUM = false;
     __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) { return row[(K >> 1) + c]; }
-    // E2M1 magnitude index m (0..7) -> bf16 bytes of {0, .5, 1, 1.5, 2, 3, 4, 6}: low bytes {00,00,80,C0,00,40,
-    // 80,C0}, high bytes {00,3F,3F,3F,40,40,40,40}; v_perm_b32 looks up four indices (one per byte) at once.
+    // gfx950's v_cvt_scalef32_pk_bf16_fp4 turns the two E2M1 codes of one byte (low nibble first) into two bf16
+    // (scale 1: exact), giving (e0, e1), (e2, e3), (e4, e5), (e6, e7); one v_perm_b32 per pair word regroups them
+    // into the (n, n + 4) pairs the activations are laid out in. 8 VALU per code word, bit-identical to a
+    // table decode of {0, .5, 1, 1.5, 2, 3, 4, 6} x sign for every byte value.
     __device__ static __forceinline__ void decode_word(uint32_t v, uint32_t q[4]) {
-        const uint32_t me = v & 0x07070707u, mo = (v >> 4) & 0x07070707u;   // nibbles 0,2,4,6 / 1,3,5,7
-        const uint32_t lo_e = __builtin_amdgcn_perm(0xC0804000u, 0xC0800000u, me);
-        const uint32_t hi_e = __builtin_amdgcn_perm(0x40404040u, 0x3F3F3F00u, me) | ((v & 0x08080808u) << 4);
-        const uint32_t lo_o = __builtin_amdgcn_perm(0xC0804000u, 0xC0800000u, mo);
-        const uint32_t hi_o = __builtin_amdgcn_perm(0x40404040u, 0x3F3F3F00u, mo) | (v & 0x80808080u);
-        q[0] = __builtin_amdgcn_perm(hi_e, lo_e, 0x06020400u);   // (e0, e4)
-        q[1] = __builtin_amdgcn_perm(hi_o, lo_o, 0x06020400u);   // (e1, e5)
-        q[2] = __builtin_amdgcn_perm(hi_e, lo_e, 0x07030501u);   // (e2, e6)
-        q[3] = __builtin_amdgcn_perm(hi_o, lo_o, 0x07030501u);   // (e3, e7)
+        const uint32_t p0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0));
+        const uint32_t p1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1));
+        const uint32_t p2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2));
+        const uint32_t p3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3));
+        q[0] = __builtin_amdgcn_perm(p2, p0, 0x05040100u);   // (e0, e4)
+        q[1] = __builtin_amdgcn_perm(p2, p0, 0x07060302u);   // (e1, e5)
+        q[2] = __builtin_amdgcn_perm(p3, p1, 0x05040100u);   // (e2, e6)
+        q[3] = __builtin_amdgcn_perm(p3, p1, 0x07060302u);   // (e3, e7)
     }
     __device__ static __forceinline__ void decode(uint4 w, uint32_t qp[16]) {
         decode_word(w.x, qp);
