@@ -307,6 +307,7 @@ int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32
         a.yp = (float*)(ws + L.yp);
         a.x16 = (uint16_t*)(ws + L.x16);
         a.xexp = (int32_t*)(ws + L.xexp);
+        a.xterm = x_dtype == MOE_DTYPE_BF16 ? (uint8_t*)(ws + L.xp) : nullptr;
         a.grp.counts = (int32_t*)(ws + L.counts);
         a.grp.offsets = (int32_t*)(ws + L.offsets);
         a.grp.sorted = (int32_t*)(ws + L.sorted);

@@ -54,6 +54,7 @@ struct ExpertsArgs {
     float* yp;      // 4 x [T*k, d] fp32 scratch (grouped path; the further planes for a K-split down projection)
     uint16_t* x16;  // grouped path, dense int4: x as fp16 [T, d] with a power-of-two exponent per token
     int32_t* xexp;  // [T]
+    uint8_t* xterm; // grouped path, MXFP4 block-scaled MFMA: x's fp8 term records (the x-planes region when x is bf16)
     GroupBufs grp;  // grouped path
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
     // moe_layer_run at T == 1: the gate/up waves take their experts from the top-k of these router logits [T, E] (and

@@ -1137,6 +1137,307 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     }
 }
 
+// ============================================================================ MXFP4 dense tiles on the block-scaled MFMA
+// gfx950's v_mfma_scale_f32_16x16x128_f8f6f4 multiplies fp8 (E4M3) A by fp4 (E2M1) B over 128 inputs, each
+// operand's 32-input blocks (lane group g of the B operand: block g) times its own E8M0 power of two. The weights
+// go in undecoded and unfolded from the tile-major records: lane (r, g) loads its 16 bytes of the slice record
+// (row r's code words g, 4 + g, 8 + g, 12 + g), a 4 x 4 transpose across the lane groups (two v_permlane32_swap,
+// two v_permlane16_swap) leaves it words 4 g .. 4 g + 3 = block g, and byte g of row r's E8M0 word is its scale.
+// The words keep the records' nibble order (e0 e2 e4 e6 e1 e3 e5 e7); the activation terms are written in that
+// order instead. The activations enter as a sum of fp8 terms, each with an E8M0 byte per (token, 32 inputs): term t of a block
+// has scale 2^e, e = floor(log2 max |r|) - 7 (|r / 2^e| < 256, inside E4M3's range), q = E4M3(r / 2^e) and
+// r -= q 2^e (exact). Two terms hold bf16 x, three hold h = hi + lo; measured on this part, the instruction's own
+// accumulation keeps ~2e-5 of the outputs' RMS (two to four terms give the same result), against the 1e-2 RMS gate.
+
+// Activation rows -> per (row, 128-input slice) records of REC = 16 (8 NTERM + 1) bytes: NTERM x 128 bytes of terms
+// in the A operand's order (bytes 32 g .. 32 g + 15 = inputs 16 g .. 16 g + 15, bytes 32 g + 16 .. 32 g + 31 =
+// inputs 64 + 16 g .. 64 + 16 g + 15), then the E8M0 byte of term t, block b at 128 NTERM + 4 t + b. Inputs past K
+// (K % 128 == 64) are zero codes with scale byte 127. One thread per 32-input block; HL: rows are h = hi + lo.
+template <int NTERM>
+__host__ __device__ constexpr int mx_rec() { return 16 * (8 * NTERM + 1); }
+
+template <int NTERM, bool HL>
+__global__ void __launch_bounds__(256) k_mx_terms(const uint16_t* __restrict__ src, const uint16_t* __restrict__ src2,
+                                                 int rows, int K, uint8_t* __restrict__ out) {
+    constexpr int REC = mx_rec<NTERM>();
+    const int nsl = (K + 127) >> 7, nb = 4 * nsl;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)rows * nb) return;
+    const int row = (int)(i / nb), blk = (int)(i - (long)row * nb);
+    const int s = blk >> 2, b = blk & 3;
+    uint8_t* rec = out + ((size_t)row * nsl + s) * REC;
+    float r[32];
+    if (32 * blk < K) {
+        const uint4* p = reinterpret_cast<const uint4*>(src + (size_t)row * K + 32 * blk);
+        const uint4* p2 = HL ? reinterpret_cast<const uint4*>(src2 + (size_t)row * K + 32 * blk) : p;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = p[q];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                r[8 * q + 2 * u] = bf16lo(w[u]);
+                r[8 * q + 2 * u + 1] = bf16hi(w[u]);
+            }
+            if (HL) {
+                const uint4 v2 = p2[q];
+                const uint32_t w2[4] = {v2.x, v2.y, v2.z, v2.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    r[8 * q + 2 * u] += bf16lo(w2[u]);
+                    r[8 * q + 2 * u + 1] += bf16hi(w2[u]);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) r[j] = 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < NTERM; ++t) {
+        float am = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) am = fmaxf(am, fabsf(r[j]));
+        int e = am > 0.f ? (int)((__float_as_uint(am) >> 23) & 0xFFu) - 127 - 7 : -127;
+        e = e < -127 ? -127 : (e > 127 ? 127 : e);
+        const float inv = __builtin_ldexpf(1.f, -e);
+        // byte j of the block's 32 = input 8 (j / 8) + (0 2 4 6 1 3 5 7)[j % 8]: the order of the codes in the tile
+        // records' words (nibbles e0 e2 e4 e6 e1 e3 e5 e7)
+        uint32_t qw[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i0 = 8 * (j >> 1) + (j & 1);
+            uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(r[i0] * inv, r[i0 + 2] * inv, 0, false);
+            w = __builtin_amdgcn_cvt_pk_fp8_f32(r[i0 + 4] * inv, r[i0 + 6] * inv, (int)w, true);
+            qw[j] = w;
+            r[i0] -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 0), e);
+            r[i0 + 2] -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 1), e);
+            r[i0 + 4] -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 2), e);
+            r[i0 + 6] -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 3), e);
+        }
+        uint8_t* tq = rec + 128 * t + 64 * (b & 1) + 16 * (b >> 1);
+        *reinterpret_cast<uint4*>(tq) = uint4{qw[0], qw[1], qw[2], qw[3]};        // code words 0, 1 of the block
+        *reinterpret_cast<uint4*>(tq + 32) = uint4{qw[4], qw[5], qw[6], qw[7]};   // code words 2, 3
+        rec[128 * NTERM + 4 * t + b] = (uint8_t)(32 * blk < K ? e + 127 : 127);
+    }
+}
+
+// k_mxd: blocks of 4 waves own BN = 64 RT rows of one expert (per projection) and one pass of up to 64 of its slots
+// (the dense tiles' work list, XCD-chunked the same way); each wave covers the pass's 4 token tiles for its RT row
+// tiles. Per 128-input slice: the pass's activation records (64 x REC bytes) come into LDS by
+// global_load_lds_dwordx4 (records of 17 or 25 16-byte pieces, an odd count, so the 16 lanes of a token tile read
+// 16 distinct bank groups), double-buffered; each wave loads its row tiles' slice records (1 KB of codes + the
+// E8M0 words) one slice ahead; NTERM x 4 x NPROJ x RT MFMAs per slice.
+#ifndef MOE_MXD_RT_DN
+#define MOE_MXD_RT_DN 4
+#endif
+#ifndef MOE_MXD_MINB_GU
+#define MOE_MXD_MINB_GU 2
+#endif
+#ifndef MOE_MXD_MINB_DN
+#define MOE_MXD_MINB_DN 2
+#endif
+template <int NPROJ>
+__host__ __device__ constexpr int mxd_rt() { return NPROJ == 2 ? 2 : MOE_MXD_RT_DN; }
+
+template <int NPROJ, int NTERM>
+__global__ void __launch_bounds__(256, NPROJ == 2 ? MOE_MXD_MINB_GU : MOE_MXD_MINB_DN) k_mxd(TileArgs a) {
+    constexpr int NT = 4, BM = 64;
+    constexpr int RT = mxd_rt<NPROJ>();
+    constexpr int BN = 64 * RT;
+    constexpr int REC = mx_rec<NTERM>();
+    constexpr int NPC = REC / 16;                     // 16-byte pieces per record
+    constexpr int NCH = (BM * NPC + 63) / 64;         // 64-piece DMA chunks per slice
+    constexpr int NDMA = (NCH + 3) / 4;               // DMA instructions per wave per slice (the last partial)
+    typedef int v8i __attribute__((ext_vector_type(8)));
+    __shared__ __attribute__((aligned(1024))) uint8_t sX0[NCH * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t sX1[NCH * 1024];
+    __shared__ int sSlot[BM];
+
+    const int nrb = (a.N + BN - 1) / BN;
+    const int nitems = a.meta[a.nidx] * nrb;
+    const int chunk = (nitems + 7) >> 3;
+    const int rank = (int)(blockIdx.x >> 3);
+    const int item = (int)(blockIdx.x & 7u) * chunk + rank;
+    if (rank >= chunk || item >= nitems) return;
+    const int wq = item / nrb;
+    const int e = a.items[3 * wq], np = a.items[3 * wq + 2];
+    const int w0 = wq - a.items[3 * wq + 1];
+    const int local = item - w0 * nrb;
+    const int rb = local / np, tok0 = (local - rb * np) * BM;
+    const int n = a.counts[e], beg = a.offsets[e];
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int K = a.K, N = a.N;
+    const int nsl = (K + 127) >> 7;
+    const int r0 = rb * BN + wave * 16 * RT;
+    const bool wvalid = r0 < N;                        // N % (16 RT) == 0
+    constexpr int SB = TILE_SLICE_MXFP4;
+    const uint8_t* tb[NPROJ][RT];
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            tb[p][rt] = (p ? a.W1 : a.W0) + ((size_t)e * (N >> 4) + (wvalid ? (r0 >> 4) + rt : 0)) * (size_t)nsl * SB;
+    const uint8_t* recs = reinterpret_cast<const uint8_t*>(a.actv);
+
+    const int nlive = n - tok0 < BM ? n - tok0 : BM;
+    const int ntiles = (nlive + 15) >> 4;
+    if (tid < BM) sSlot[tid] = a.sorted[beg + (tok0 + tid < n ? tok0 + tid : n - 1)];
+    __syncthreads();
+    // DMA lanes: chunk c = 4 i + wave of the slice's BM * NPC pieces; piece q = 64 c + lane -> record of token
+    // q / NPC, piece q % NPC (pieces past the last record re-read the last piece into the buffer's tail)
+    uint32_t xoff[NDMA];
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+        int q = 64 * (4 * i + wave) + lane;
+        q = q < BM * NPC ? q : BM * NPC - 1;
+        const int tok = q / NPC, pc = q - tok * NPC;
+        xoff[i] = ((uint32_t)(sSlot[tok] / a.act_div) * (uint32_t)nsl) * (uint32_t)REC + 16u * (uint32_t)pc;
+    }
+    auto dma = [&](int s, uint8_t* buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NDMA; ++i)
+            if (4 * i + wave < NCH) {   // wave-uniform
+                uint32_t o = xoff[i] + (uint32_t)s * (uint32_t)REC;
+                asm volatile("" : "+v"(o));
+                __builtin_amdgcn_global_load_lds((const void*)(recs + o), MOE_LDSP(buf + (4 * i + wave) * 1024), 16, 0, 0);
+            }
+    };
+    // weights of slice s: the lane's 16 bytes of each row tile's record and its row's E8M0 word (words and groups
+    // past K are zero in the records: zero codes, scale 2^-127)
+    auto wissue = [&](int s, uint4 (&q)[NPROJ][RT], uint32_t (&m)[NPROJ][RT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint8_t* sl = tb[p][rt] + (uint32_t)s * (uint32_t)SB;
+                q[p][rt] = *reinterpret_cast<const uint4*>(sl + 16 * lane);
+                m[p][rt] = *reinterpret_cast<const uint32_t*>(sl + 1024 + 4 * lr);
+            }
+    };
+    // lane group g: words (g, 4 + g, 8 + g, 12 + g) -> (4 g, 4 g + 1, 4 g + 2, 4 g + 3)
+    auto transpose = [](const uint4& v) __attribute__((always_inline)) {
+        const auto s0 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+        const auto t0 = __builtin_amdgcn_permlane16_swap(s0[0], s1[0], false, false);
+        const auto t1 = __builtin_amdgcn_permlane16_swap(s0[1], s1[1], false, false);
+        return uint4{t0[0], t0[1], t1[0], t1[1]};
+    };
+    f32x4 acc[NPROJ][RT][NT];
+#pragma unroll
+    for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[p][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // token tile by token tile (live tiles only): the tile's NTERM A operands from LDS, then its MFMAs
+    auto compute = [&](const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint32_t (&m)[NPROJ][RT])
+                       __attribute__((always_inline)) {
+        v8i B[NPROJ][RT];
+        int sb[NPROJ][RT];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint4 w = transpose(q[p][rt]);
+                B[p][rt] = v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                sb[p][rt] = (int)(m[p][rt] >> (8 * lg));
+            }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t < ntiles) {   // wave-uniform
+                const uint8_t* ra = xs + (16 * t + lr) * REC;
+                v8i A[NTERM];
+                int sa[NTERM];
+#pragma unroll
+                for (int tm = 0; tm < NTERM; ++tm) {
+                    const uint4 a0 = *reinterpret_cast<const uint4*>(ra + 128 * tm + 32 * lg);
+                    const uint4 a1 = *reinterpret_cast<const uint4*>(ra + 128 * tm + 32 * lg + 16);
+                    A[tm] = v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                    sa[tm] = ra[128 * NTERM + 4 * tm + lg];
+                }
+#pragma unroll
+                for (int tm = 0; tm < NTERM; ++tm)
+#pragma unroll
+                    for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt)
+                            acc[p][rt][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                                A[tm], B[p][rt], acc[p][rt][t], 0, 4, 0, sa[tm], 0, sb[p][rt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    uint4 rq[2][NPROJ][RT];
+    uint32_t rm[2][NPROJ][RT];
+    // slice s in buffer / register set s & 1; slice s + 1 is fetched while slice s is multiplied (the last slice
+    // fetches itself again into the idle set: no branch around the loads)
+    dma(0, sX0);
+    wissue(0, rq[0], rm[0]);
+    MOE_VMWAIT0();
+    MOE_BARRIER();
+    int j = 0;
+    for (; j + 2 <= nsl; j += 2) {
+        wissue(j + 1, rq[1], rm[1]);
+        dma(j + 1, sX1);
+        compute(sX0, rq[0], rm[0]);
+        MOE_VMWAIT0();
+        MOE_BARRIER();
+        const int jn = j + 2 < nsl ? j + 2 : j + 1;
+        wissue(jn, rq[0], rm[0]);
+        dma(jn, sX0);
+        compute(sX1, rq[1], rm[1]);
+        MOE_VMWAIT0();
+        MOE_BARRIER();
+    }
+    if (j < nsl) compute(sX0, rq[0], rm[0]);   // odd count: the last slice is in buffer 0
+
+    // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
+    if (!wvalid) return;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int jt = 16 * t + 4 * lg + v;
+            if (jt >= nlive) continue;
+            const int slot = sSlot[jt];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int r = r0 + 16 * rt + lr;
+                if (NPROJ == 2) {
+                    float g = acc[0][rt][t][v], up = acc[NPROJ - 1][rt][t][v];
+                    if (a.b0) g += a.b0[(size_t)e * N + r];
+                    if (a.b1) up += a.b1[(size_t)e * N + r];
+                    const float hv = glu_act(a.act, g, up);
+                    const uint16_t hi = f32_to_bf16(hv);
+                    a.hout[(size_t)slot * N + r] = hi;
+                    a.hout2[(size_t)slot * N + r] = f32_to_bf16(hv - bf16_to_f32(hi));
+                } else {
+                    a.yp[(size_t)slot * N + r] = acc[0][rt][t][v];
+                }
+            }
+        }
+}
+
+template <int NPROJ, int NTERM>
+int launch_mxd(const TileArgs& t, int nslots, hipStream_t st) {
+    constexpr int BN = 64 * mxd_rt<NPROJ>();
+    if (t.N % (16 * mxd_rt<NPROJ>())) return MOE_ERR_ARG;
+    const long nblk = ((long)((t.N + BN - 1) / BN) * max_passes(nslots, t.E, 64) + 7) / 8 * 8;
+    if (nblk > 0x7FFFFFF8L) return MOE_ERR_ARG;
+    k_mxd<NPROJ, NTERM><<<dim3((unsigned)nblk), 256, 0, st>>>(t);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+template <int NTERM, bool HL>
+int launch_mx_terms(const uint16_t* src, const uint16_t* src2, int rows, int K, uint8_t* out, hipStream_t st) {
+    const long n = (long)rows * 4 * ((K + 127) >> 7);
+    if (n <= 0 || (n + 255) / 256 > 0x7FFFFFFFL) return MOE_ERR_ARG;
+    k_mx_terms<NTERM, HL><<<dim3((unsigned)((n + 255) / 256)), 256, 0, st>>>(src, src2, rows, K, out);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
 // Dense int4, before gate/up: x [T, d] (bf16 or fp16) -> x16 = x 2^-E fp16, one block per token, E = h16_exponent of
 // the row's largest |x| (bf16 and fp16 to fp16 are then exact except far below the row's largest, where fp16's
 // subnormal range rounds); E per token for the gate/up epilogue.
@@ -1495,6 +1796,14 @@ int run_tiles_fmt(const ExpertsArgs& a) {
                           (dmode == 1 || (dmode < 0 && dblocks >= MOE_DENSE_MIN_BLOCKS));
     const bool dense_dn = dense_gu || (INT4 && tiled && dmode != 0 && avg > dn_min_avg &&
                                        (dmode == 1 || dn_blocks >= MOE_DENSE_MIN_BLOCKS));
+    // MXFP4 with bf16 x on the dense tiles: the block-scaled MFMA kernels instead (MOE_MXMFMA=0: the bf16-MFMA
+    // dense tiles). x's terms go to the x-planes region, h's terms to the yp planes the split down would use; both
+    // must fit there, with 32-bit record offsets
+    const size_t mx_xb = (size_t)a.T * ((w->d + 127) / 128) * mx_rec<2>();
+    const size_t mx_hb = (size_t)nslots * ((w->F + 127) / 128) * mx_rec<3>();
+    const bool mxd = !INT4 && dense_gu && a.nx == 1 && env_int("MOE_MXMFMA", 1) && a.xterm &&
+                     mx_xb <= (size_t)6 * a.T * w->d && mx_hb <= (size_t)12 * nslots * w->d && mx_hb < (1ull << 32) &&
+                     w->F % (16 * mxd_rt<2>()) == 0 && w->d % (16 * mxd_rt<1>()) == 0;
     const bool wave_gu = tiled && !dense_gu && (avg <= min_avg || dmode != 0);
     const bool wave_dn = tiled && !dense_dn && (avg <= min_avg || dmode != 0);
     const bool h16 = INT4 && dense_dn;   // h leaves the gate/up as h16 with per-32-row exponents
@@ -1546,7 +1855,14 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
         }
-        if (dense_gu && INT4) {
+        if (mxd) {
+            g.W0 = (const uint8_t*)w->gate.tiles;
+            g.W1 = (const uint8_t*)w->up.tiles;
+            rc = launch_mx_terms<2, false>(a.xb, nullptr, a.T, w->d, a.xterm, a.st);
+            g.actv = reinterpret_cast<const uint16_t*>(a.xterm);
+            if (!rc) rc = launch_mxd<2, 2>(g, nslots, a.st);
+            if (rc) return rc;
+        } else if (dense_gu && INT4) {
             if (a.x_dtype == MOE_DTYPE_F16) k_x16<MOE_DTYPE_F16><<<a.T, 256, 0, a.st>>>(a.x, a.x16, a.xexp, w->d);
             else k_x16<MOE_DTYPE_BF16><<<a.T, 256, 0, a.st>>>(a.x, a.x16, a.xexp, w->d);
             rc = hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
@@ -1554,7 +1870,8 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.actv = a.x16;
             g.xexp = a.xexp;
         }
-        if (dense_gu) rc = launch_dense<FMT, 2>(g, nslots, a.st);
+        if (mxd) rc = 0;
+        else if (dense_gu) rc = launch_dense<FMT, 2>(g, nslots, a.st);
         else if (wave_gu && h16)
             rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU, INT4>(g, nt, nslots, a.st, a.nx);
         else if (wave_gu) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st, a.nx);
@@ -1575,7 +1892,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.N = w->d;
         d.W0 = (const uint8_t*)w->down.rows;
         d.yp = a.yp;
-        d.ksplit = dense_dn ? dense_ksplit(d.N, d.K, nslots, w->E, BN_DN, DP_DN) : 1;
+        d.ksplit = dense_dn && !mxd ? dense_ksplit(d.N, d.K, nslots, w->E, BN_DN, DP_DN) : 1;
         d.plane = (size_t)nslots * d.N;
         if (two_lists) {
             d.items = a.grp.items2;
@@ -1589,7 +1906,13 @@ int run_tiles_fmt(const ExpertsArgs& a) {
                    (long)(w->d / (16 * rt)) * max_passes(nslots, w->E, 16 * nt) >= MOE_WAVE_WIDE_MIN_WAVES;
         };
         int rc;
-        if (dense_dn) rc = launch_dense<FMT, 1>(d, nslots, a.st);
+        if (mxd) {
+            uint8_t* hterm = reinterpret_cast<uint8_t*>(a.yp + d.plane);   // the yp planes after the first
+            d.W0 = (const uint8_t*)w->down.tiles;
+            rc = launch_mx_terms<3, true>(a.hhi, a.hlo, nslots, w->F, hterm, a.st);
+            d.actv = reinterpret_cast<const uint16_t*>(hterm);
+            if (!rc) rc = launch_mxd<1, 3>(d, nslots, a.st);
+        } else if (dense_dn) rc = launch_dense<FMT, 1>(d, nslots, a.st);
         else if (wave_dn && wide_dn(MOE_WAVE_RT_DN_WIDE))
             rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN_WIDE, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
         else if (MOE_WAVE_RT_DN_MID && wave_dn && wide_dn(MOE_WAVE_RT_DN_MID))
