@@ -162,19 +162,43 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
     if (tid == 0) s_bad = 0;
     __syncthreads();
     const int q4 = (n + 3) / 4;
+    // ids are read GB per lane at a time (one memory round trip per batch, not one per id)
+    constexpr int GB = 8;
     if (mw) {
         const int b0 = wave * q4, b1 = b0 + q4 < n ? b0 + q4 : n;
-        for (int p = b0 + lane; p < b1; p += 64) {
-            const int e = idx[p];
-            sidx[p] = e;
-            if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
-            else atomicAdd(&s_bad, 1);
+        for (int base = b0; base < b1; base += 64 * GB) {
+            int ev[GB];
+#pragma unroll
+            for (int j = 0; j < GB; ++j) {
+                const int p = base + 64 * j + lane;
+                ev[j] = p < b1 ? idx[p] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < GB; ++j) {
+                const int p = base + 64 * j + lane;
+                if (p < b1) {
+                    sidx[p] = ev[j];
+                    if (ev[j] >= 0 && ev[j] < E) atomicAdd(&cnt[wave * E + ev[j]], 1);
+                    else atomicAdd(&s_bad, 1);
+                }
+            }
         }
     } else {
-        for (int p = tid; p < n; p += 256) {
-            const int e = idx[p];
-            if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-            else atomicAdd(&s_bad, 1);
+        for (int base = 0; base < n; base += 256 * GB) {
+            int ev[GB];
+#pragma unroll
+            for (int j = 0; j < GB; ++j) {
+                const int p = base + 256 * j + tid;
+                ev[j] = p < n ? idx[p] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < GB; ++j) {
+                const int p = base + 256 * j + tid;
+                if (p < n) {
+                    if (ev[j] >= 0 && ev[j] < E) atomicAdd(&cnt[ev[j]], 1);
+                    else atomicAdd(&s_bad, 1);
+                }
+            }
         }
     }
     __syncthreads();
@@ -251,9 +275,21 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
         int nbits = 0;
         while ((1 << nbits) < E) ++nbits;
         const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        int ev[GB];
         for (int base = b0; base < b1; base += 64) {
+            const int j = ((base - b0) >> 6) % GB;
+            if (j == 0) {   // the next GB steps' ids
+#pragma unroll
+                for (int i = 0; i < GB; ++i) {
+                    const int q = base + 64 * i + lane;
+                    ev[i] = q < b1 ? (mw ? sidx[q] : idx[q]) : -1;
+                }
+            }
             const int p = base + lane;
-            int e = p < b1 ? (mw ? sidx[p] : idx[p]) : -1;
+            int e = -1;
+#pragma unroll
+            for (int i = 0; i < GB; ++i)
+                if (i == j) e = ev[i];
             const bool ok = (e >= 0 && e < E);
             // lanes holding the same valid expert: match on every bit of e
             uint64_t peers = __ballot(ok);
