@@ -62,6 +62,10 @@ constexpr int TL_APAD = 4 * TL_KC + 4;   // words per staged row: [g 0..3][chunk
 constexpr int TL_BPAD = 4 * TL_KC + 1;   // 16-byte pieces per staged token (8 inputs each) + 1 of padding
 constexpr int TL_GMAX = TL_KC;           // scale groups per slice at most (MXFP4: one per chunk)
 
+// block-scaled MXFP4 tiles: bytes of one (activation row, 128-input slice) record of NTERM fp8 terms + scales
+template <int NTERM>
+__host__ __device__ constexpr int mx_rec() { return 16 * (8 * NTERM + 1); }
+
 struct TileArgs {
     const uint16_t* actv;  // gate/up: x [T, K] (bf16 plane 0); down: h [T*k, K] (bf16; the hi plane of h = hi + lo)
     const uint16_t* actv2; // down: the lo plane of h
@@ -444,9 +448,12 @@ __host__ __device__ constexpr int tile_slice_bytes() {
 
 // H16O (int4 gate/up before a dense down): h leaves as fp16 h16 = h 2^-e with e per (slot, 32-row chunk), the
 // layout the dense down reads after k_h16_fix, instead of the two bf16 planes.
-template <class FMT, int NPROJ, int NT, int RT, int D, bool H16O = false, int HX = 1>
+// MXT > 0 (MXFP4, bf16 x): the activations are fp8 term records (k_mx_terms, MXT terms) and the products run on
+// the block-scaled MFMA (the weights undecoded, as in k_mxd)
+template <class FMT, int NPROJ, int NT, int RT, int D, bool H16O = false, int HX = 1, int MXT = 0>
 __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     static_assert(!H16O || (NPROJ == 2 && RT % 2 == 0), "h16 output: gate/up, whole 32-row chunks per wave");
+    static_assert(MXT == 0 || (!FMT::XSUM && HX == 1 && !H16O), "block-scaled: MXFP4, one activation source");
     constexpr bool INT4 = FMT::XSUM;
     constexpr int HL = NPROJ == 2 ? HX : 2;   // activation planes: x's (1, or 2-3 for fp16 / fp32 x), h = hi + lo
     constexpr int SB = tile_slice_bytes<FMT>();
@@ -490,6 +497,94 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
             slotA[t] = a.gidx ? sSlot[(m < n ? m : n - 1) - tok0] : a.sorted[beg + (m < n ? m : n - 1)];
             xo[t] = (uint32_t)(slotA[t] / a.act_div) * (uint32_t)K * 2u;
         }
+        f32x4 acc[NPROJ][RT][NT];
+#pragma unroll
+        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[p][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (MXT > 0) {
+            typedef int v8i __attribute__((ext_vector_type(8)));
+            constexpr int REC = mx_rec<MXT>();
+            const uint8_t* xrec = reinterpret_cast<const uint8_t*>(a.actv);
+            uint32_t ro[NT];   // byte offset of the lane's token's records
+#pragma unroll
+            for (int t = 0; t < NT; ++t) ro[t] = (uint32_t)(slotA[t] / a.act_div) * (uint32_t)nsl * (uint32_t)REC;
+            // register ring: code words, E8M0 words, the lane's 32 bytes of each term and the terms' scale words
+            uint4 rq[D][NPROJ][RT];
+            uint32_t rm[D][NPROJ][RT];
+            uint4 ra[D][MXT][NT][2];
+            uint32_t rs[D][MXT][NT];
+            auto issue = [&](int s, uint4 (&q)[NPROJ][RT], uint32_t (&m)[NPROJ][RT], uint4 (&x)[MXT][NT][2],
+                             uint32_t (&xs)[MXT][NT]) {
+#pragma unroll
+                for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const uint8_t* sl = tb[p][rt] + (uint32_t)s * (uint32_t)SB;
+                        q[p][rt] = *reinterpret_cast<const uint4*>(sl + 16 * lane);
+                        m[p][rt] = *reinterpret_cast<const uint32_t*>(sl + 1024 + 4 * lr);
+                    }
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int tm = 0; tm < MXT; ++tm) {
+                        const uint8_t* r = xrec + (ro[t] + (uint32_t)s * (uint32_t)REC);
+                        x[tm][t][0] = *reinterpret_cast<const uint4*>(r + 128 * tm + 32 * lg);
+                        x[tm][t][1] = *reinterpret_cast<const uint4*>(r + 128 * tm + 32 * lg + 16);
+                        xs[tm][t] = *reinterpret_cast<const uint32_t*>(r + 128 * MXT + 4 * tm);
+                    }
+            };
+            auto compute = [&](bool live, const uint4 (&q)[NPROJ][RT], const uint32_t (&m)[NPROJ][RT],
+                               const uint4 (&x)[MXT][NT][2], const uint32_t (&xs)[MXT][NT]) {
+                if (!live) return;   // wave-uniform: slices past the last (the ring's rounding)
+                v8i B[NPROJ][RT];
+                int sb[NPROJ][RT];
+#pragma unroll
+                for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        // lane group g: words (g, 4 + g, 8 + g, 12 + g) -> (4 g .. 4 g + 3), i.e. block g
+                        const uint4 v = q[p][rt];
+                        const auto s0 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+                        const auto s1 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+                        const auto t0 = __builtin_amdgcn_permlane16_swap(s0[0], s1[0], false, false);
+                        const auto t1 = __builtin_amdgcn_permlane16_swap(s0[1], s1[1], false, false);
+                        B[p][rt] = v8i{(int)t0[0], (int)t0[1], (int)t1[0], (int)t1[1], 0, 0, 0, 0};
+                        sb[p][rt] = (int)(m[p][rt] >> (8 * lg));
+                    }
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int tm = 0; tm < MXT; ++tm) {
+                        const uint4 a0 = x[tm][t][0], a1 = x[tm][t][1];
+                        const v8i A = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                        const int sa = (int)(xs[tm][t] >> (8 * lg));
+#pragma unroll
+                        for (int p = 0; p < NPROJ; ++p)
+#pragma unroll
+                            for (int rt = 0; rt < RT; ++rt)
+                                acc[p][rt][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                                    A, B[p][rt], acc[p][rt][t], 0, 4, 0, sa, 0, sb[p][rt]);
+                    }
+            };
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                issue(i < nsl ? i : nsl - 1, rq[i], rm[i], ra[i], rs[i]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            for (int s0 = 0; s0 < nsl; s0 += D) {
+#pragma unroll
+                for (int i = 0; i < D; ++i) {
+                    compute(s0 + i < nsl, rq[i], rm[i], ra[i], rs[i]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    const int sn = s0 + i + D;
+                    issue(sn < nsl ? sn : nsl - 1, rq[i], rm[i], ra[i], rs[i]);
+                }
+            }
+        } else {
         const uint8_t* xbase[HL];
 #pragma unroll
         for (int hl = 0; hl < HL; ++hl)
@@ -519,13 +614,6 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
                         x[hl][t][j] = *reinterpret_cast<const uint4*>(xbase[hl] + (xo[t] + 16u * piece));
                     }
         };
-        f32x4 acc[NPROJ][RT][NT];
-#pragma unroll
-        for (int p = 0; p < NPROJ; ++p)
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-                for (int t = 0; t < NT; ++t) acc[p][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
         auto compute = [&](bool live, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT],
                            const uint4 (&x)[HL][NT][4]) {
             bf16x8 X[HL][NT][4];
@@ -638,6 +726,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
 #pragma unroll
                         for (int v = 0; v < 4; ++v) acc[p][rt][t][v] = __builtin_ldexpf(acc[p][rt][t][v], rex[p][rt]);
         }
+        }   // MXT == 0
         // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
         if constexpr (H16O) {
             int8_t* hexp_out = reinterpret_cast<int8_t*>(a.hout2);
@@ -1153,9 +1242,6 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
 // in the A operand's order (bytes 32 g .. 32 g + 15 = inputs 16 g .. 16 g + 15, bytes 32 g + 16 .. 32 g + 31 =
 // inputs 64 + 16 g .. 64 + 16 g + 15), then the E8M0 byte of term t, block b at 128 NTERM + 4 t + b. Inputs past K
 // (K % 128 == 64) are zero codes with scale byte 127. One thread per 32-input block; HL: rows are h = hi + lo.
-template <int NTERM>
-__host__ __device__ constexpr int mx_rec() { return 16 * (8 * NTERM + 1); }
-
 template <int NTERM, bool HL>
 __global__ void __launch_bounds__(256) k_mx_terms(const uint16_t* __restrict__ src, const uint16_t* __restrict__ src2,
                                                  int rows, int K, uint8_t* __restrict__ out) {
@@ -1700,13 +1786,23 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 #define MOE_WAVE_RT_DN 4   // 16-row tiles per wave, down (d % 64 == 0)
 #endif
 template <class FMT, int NPROJ, int RT, int D, bool H16O = false>
-int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st, int hx = 1) {
+int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st, int hx = 1, int mxt = 0) {
     if (t.N % (16 * RT)) return MOE_ERR_ARG;
     // in-kernel grouping, expert-major: E first passes and at most ceil(n / P) further ones (an expert with c
     // slots has ceil(c / P) - 1 <= (c - 1) / P of them)
     dim3 grid(t.N / (16 * RT), t.gidx && t.gfirst ? t.E + (nslots + 16 * nt - 1) / (16 * nt)
                                                    : max_passes(nslots, t.E, 16 * nt));
     if (grid.y > 65535) return MOE_ERR_ARG;
+    if constexpr (!FMT::XSUM && !H16O) {   // MXFP4 on the block-scaled MFMA: x 2 terms, h 3
+        if (mxt) {
+            constexpr int MT = NPROJ == 2 ? 2 : 3;
+            if (hx != 1 || mxt != MT) return MOE_ERR_ARG;
+            if (nt == 1) k_wave_tile<FMT, NPROJ, 1, RT, D, false, 1, MT><<<grid, 64, 0, st>>>(t);
+            else k_wave_tile<FMT, NPROJ, 2, RT, D, false, 1, MT><<<grid, 64, 0, st>>>(t);
+            return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+        }
+    }
+    if (mxt) return MOE_ERR_ARG;
     if constexpr (NPROJ == 2) {
         if (hx > 1) {   // fp16 / fp32 x planes: one 16-token tile per pass (the host passes nt = 1)
             if (nt != 1) return MOE_ERR_ARG;
@@ -1801,11 +1897,13 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     // must fit there, with 32-bit record offsets
     const size_t mx_xb = (size_t)a.T * ((w->d + 127) / 128) * mx_rec<2>();
     const size_t mx_hb = (size_t)nslots * ((w->F + 127) / 128) * mx_rec<3>();
-    const bool mxd = !INT4 && dense_gu && a.nx == 1 && env_int("MOE_MXMFMA", 1) && a.xterm &&
-                     mx_xb <= (size_t)6 * a.T * w->d && mx_hb <= (size_t)12 * nslots * w->d && mx_hb < (1ull << 32) &&
-                     w->F % (16 * mxd_rt<2>()) == 0 && w->d % (16 * mxd_rt<1>()) == 0;
+    const bool mx_fit = !INT4 && a.nx == 1 && env_int("MOE_MXMFMA", 1) && a.xterm && mx_xb <= (size_t)6 * a.T * w->d &&
+                        mx_hb <= (size_t)12 * nslots * w->d && mx_hb < (1ull << 32);
+    const bool mxd = mx_fit && dense_gu && w->F % (16 * mxd_rt<2>()) == 0 && w->d % (16 * mxd_rt<1>()) == 0;
     const bool wave_gu = tiled && !dense_gu && (avg <= min_avg || dmode != 0);
     const bool wave_dn = tiled && !dense_dn && (avg <= min_avg || dmode != 0);
+    // the wave tiles of MXFP4 with bf16 x on the block-scaled MFMA too (terms as for the dense kernels)
+    const bool mxw = mx_fit && wave_gu && wave_dn;
     const bool h16 = INT4 && dense_dn;   // h leaves the gate/up as h16 with per-32-row exponents
     const int wnt = env_int("MOE_WAVE_NT", 0);
     const int nt = a.nx > 1 ? 1
@@ -1870,7 +1968,11 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.actv = a.x16;
             g.xexp = a.xexp;
         }
-        if (mxd) rc = 0;
+        if (mxw) {
+            rc = launch_mx_terms<2, false>(a.xb, nullptr, a.T, w->d, a.xterm, a.st);
+            g.actv = reinterpret_cast<const uint16_t*>(a.xterm);
+            if (!rc) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st, 1, 2);
+        } else if (mxd) rc = 0;
         else if (dense_gu) rc = launch_dense<FMT, 2>(g, nslots, a.st);
         else if (wave_gu && h16)
             rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU, INT4>(g, nt, nslots, a.st, a.nx);
@@ -1905,7 +2007,14 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             return rt > 0 && w->d % (16 * rt) == 0 &&
                    (long)(w->d / (16 * rt)) * max_passes(nslots, w->E, 16 * nt) >= MOE_WAVE_WIDE_MIN_WAVES;
         };
-        int rc;
+        int rc = 0;
+        if (mxw) {   // h's terms for the wave down
+            uint8_t* hterm = reinterpret_cast<uint8_t*>(a.yp + d.plane);
+            rc = launch_mx_terms<3, true>(a.hhi, a.hlo, nslots, w->F, hterm, a.st);
+            d.actv = reinterpret_cast<const uint16_t*>(hterm);
+            if (rc) return rc;
+        }
+        const int mxt = mxw ? 3 : 0;
         if (mxd) {
             uint8_t* hterm = reinterpret_cast<uint8_t*>(a.yp + d.plane);   // the yp planes after the first
             d.W0 = (const uint8_t*)w->down.tiles;
@@ -1914,10 +2023,10 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             if (!rc) rc = launch_mxd<1, 3>(d, nslots, a.st);
         } else if (dense_dn) rc = launch_dense<FMT, 1>(d, nslots, a.st);
         else if (wave_dn && wide_dn(MOE_WAVE_RT_DN_WIDE))
-            rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN_WIDE, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
+            rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN_WIDE, MOE_WAVE_D_DN>(d, nt, nslots, a.st, 1, mxt);
         else if (MOE_WAVE_RT_DN_MID && wave_dn && wide_dn(MOE_WAVE_RT_DN_MID))
-            rc = launch_wave_tile<FMT, 1, (MOE_WAVE_RT_DN_MID ? MOE_WAVE_RT_DN_MID : 2), MOE_WAVE_D_DN>(d, nt, nslots, a.st);
-        else if (wave_dn) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st);
+            rc = launch_wave_tile<FMT, 1, (MOE_WAVE_RT_DN_MID ? MOE_WAVE_RT_DN_MID : 2), MOE_WAVE_D_DN>(d, nt, nslots, a.st, 1, mxt);
+        else if (wave_dn) rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN, MOE_WAVE_D_DN>(d, nt, nslots, a.st, 1, mxt);
         else rc = launch_tile<FMT, 1>(d, nt, max_active, a.T, a.st);
         if (rc) return rc;
         return launch_combine(a.yp, d.ksplit, d.plane, a.idx, a.wts, w->down.bias, w->E,

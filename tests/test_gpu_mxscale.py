@@ -1,10 +1,10 @@
-"""MXFP4 dense tiles on gfx950's block-scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4): the row records' raw E2M1
-codes and E8M0 bytes go in as the B operand, the activations as fp8 E4M3 terms with an E8M0 byte per 32 inputs
-(x: two terms, h = hi + lo: three) as A. Taken by default wherever MXFP4 with bf16 x runs the dense tiles;
-MOE_MXMFMA=0 selects the bf16-MFMA dense tiles (decoded codes, per-group fp32 fold) for comparison.
+"""MXFP4 grouped tiles on gfx950's block-scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4): the tile records' raw
+E2M1 codes and E8M0 bytes go in as the B operand, the activations as fp8 E4M3 terms with an E8M0 byte per 32
+inputs (x: two terms, h = hi + lo: three) as A. Taken by default wherever MXFP4 with bf16 x runs the dense or
+the wave tiles; MOE_MXMFMA=0 selects the bf16-MFMA tiles (decoded codes, per-group fp32 fold) for comparison.
 
 Checked against the oracle at the north-star gate and, tighter, within 2e-3 RMS (the instruction's own
-accumulation keeps ~1e-4 RMS on these cases); against the bf16-MFMA dense tiles; on ragged passes, K % 128 == 64
+accumulation keeps ~1e-4 RMS on these cases); against the bf16-MFMA tiles; on ragged passes, K % 128 == 64
 (the last slice's second half is padding), gpt-oss biases and the clamped GLU, E8M0 scale regimes (reference
 tests/test_mxfp4_large_scales.py:22-34), the stages as separate calls, and config 4's gpt-oss-20b shape at
 T = 512 on sampled token rows (reference metal_mxfp4_moe.py:155-308 is the T >= 8 path this replaces).
@@ -47,11 +47,13 @@ def inputs(sh, T, routing, seed, scale=1.0):
     return x, torch.from_numpy(idx).to(DEV), torch.from_numpy(wts).to(DEV)
 
 
-def both(monkeypatch, s, x, idx, wts, act=0):
-    """(block-scaled MFMA, bf16-MFMA dense tiles) on the same call, MOE_DENSE=1."""
+def both(monkeypatch, s, x, idx, wts, act=0, dense="1"):
+    """(block-scaled MFMA, bf16-MFMA tiles) on the same call; dense: MOE_DENSE ("1": the dense tiles above 32
+    tokens per expert; None: the default choice, the wave tiles up to 32)."""
     from moelab_amd import _lib
     from moelab_amd.experts import run_experts
-    monkeypatch.setenv("MOE_DENSE", "1")
+    if dense is not None:
+        monkeypatch.setenv("MOE_DENSE", dense)
     monkeypatch.setenv("MOE_MXMFMA", "1")
     y1 = run_experts(s, x, idx, wts, act=act, path=_lib.PATH_GROUPED, out_dtype=torch.float32)
     monkeypatch.setenv("MOE_MXMFMA", "0")
@@ -147,3 +149,44 @@ def test_mxscale_gptoss20b_T512_sampled():
     ref = oracle_y(s, x[sel], idx[sel], wts[sel], act=2)
     e = assert_close(y[sel], ref, what="gpt-oss-20b T=512")
     assert e["max_abs"] <= 2e-3 * e["rms_ref"], e
+
+
+WAVE_CASES = [
+    # (name, d, F, E, k, T, routing, act, biases): at most 32 tokens per expert, the wave tiles
+    ("w-uniform", 512, 512, 32, 4, 24, "uniform", 0, False),    # 16-token passes, in-kernel grouping
+    ("w-zipf-gptoss", 704, 704, 16, 4, 64, "zipf", 2, True),    # K = 64 mod 128, hot experts over several passes
+    ("w-32tok", 384, 448, 8, 2, 100, "uniform", 1, False),      # 25 per expert: 32-token passes
+    ("w-grouping-launch", 256, 384, 64, 4, 300, "uniform", 0, False),   # 1200 slots: the grouping launch
+]
+
+
+@pytest.mark.parametrize("case", WAVE_CASES, ids=lambda c: c[0])
+def test_mxscale_wave_tiles(case, monkeypatch):
+    name, d, f, E, k, T, routing, act, biases = case
+    sh, s = state(name, d, f, E, k, seed=400 + T, biases=biases)
+    x, idx, wts = inputs(sh, T, routing, seed=T, scale=3.0 if act == 2 else 1.0)
+    print(f"case mxscale wave {name} T={T}", flush=True)
+    y1, y0 = both(monkeypatch, s, x, idx, wts, act=act, dense=None)
+    ref = oracle_y(s, x, idx, wts, act=act)
+    e1 = assert_close(y1, ref, what=("block-scaled wave", name))
+    assert_close(y0, ref, what=("bf16 wave", name))
+    assert e1["max_abs"] <= 2e-3 * e1["rms_ref"], (name, e1)
+    assert not torch.equal(y1, y0), "MOE_MXMFMA made no difference: the block-scaled wave tiles did not run"
+
+
+def test_mxscale_wave_stages_split_and_ingroup(monkeypatch):
+    """Wave tiles: the stages as two calls, and the grouping launch (MOE_INGROUP=0) against the in-kernel
+    grouping, all bit for bit."""
+    from moelab_amd import _lib
+    from moelab_amd.experts import run_experts
+    sh, s = state("ws", 512, 384, 16, 4, seed=13)
+    x, idx, wts = inputs(sh, 40, "zipf", seed=13)
+    g = _lib.PATH_GROUPED
+    y = run_experts(s, x, idx, wts, path=g, out_dtype=torch.float32)
+    run_experts(s, x, idx, wts, path=g, out_dtype=torch.float32, stages=_lib.STAGE_GATE_UP)
+    y2 = run_experts(s, x, idx, wts, path=g, out_dtype=torch.float32, stages=_lib.STAGE_DOWN)
+    monkeypatch.setenv("MOE_INGROUP", "0")
+    y3 = run_experts(s, x, idx, wts, path=g, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    assert torch.equal(y, y3)
