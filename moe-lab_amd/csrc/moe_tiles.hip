@@ -66,6 +66,48 @@ constexpr int TL_GMAX = TL_KC;           // scale groups per slice at most (MXFP
 template <int NTERM>
 __host__ __device__ constexpr int mx_rec() { return 16 * (8 * NTERM + 1); }
 
+// Byte of record-term position of input k (0..127) of a slice: the code order of the tile records within each
+// word (inputs 8 i + (0 2 4 6 1 3 5 7)), then the A operand's lane order (bytes 32 g .. 32 g + 15: logical inputs
+// 16 g .. 16 g + 15, bytes 32 g + 16 .. 32 g + 31: 64 + 16 g .. 64 + 16 g + 15)
+__device__ __forceinline__ int mx_pos(int k) {
+    const int e = k & 7;
+    const int l = (k & ~7) | ((e >> 1) + 4 * (e & 1));
+    return 32 * ((l & 63) >> 4) + 16 * (l >> 6) + (l & 15);
+}
+
+// One token's h on the 32 rows of a wave's block b of slice s (lane lr of its lane group: rows 16 rt + lr of
+// the block, values h0 (rt 0) and h1 (rt 1)) -> the NTERM term bytes and scale bytes of that block in the token's
+// record rec (the layout k_mx_terms writes). The 16 lanes of the group take part in the max reductions; only
+// `write` lanes store. pad: also the zero blocks 2, 3 of a slice that ends at input 64 (K % 128 == 64).
+template <int NTERM>
+__device__ __forceinline__ void mx_h_block(float h0, float h1, bool write, uint8_t* rec, int b, int lr, bool pad) {
+    const int p0 = mx_pos(32 * b + lr), p1 = mx_pos(32 * b + 16 + lr);
+#pragma unroll
+    for (int t = 0; t < NTERM; ++t) {
+        float am = fmaxf(fabsf(h0), fabsf(h1));
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+        int e = am > 0.f ? (int)((__float_as_uint(am) >> 23) & 0xFFu) - 127 - 7 : -127;
+        e = e < -127 ? -127 : (e > 127 ? 127 : e);
+        const float inv = __builtin_ldexpf(1.f, -e);
+        const uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(h0 * inv, h1 * inv, 0, false);
+        h0 -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 0), e);
+        h1 -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 1), e);
+        if (write) {
+            rec[128 * t + p0] = (uint8_t)(w & 0xFFu);
+            rec[128 * t + p1] = (uint8_t)((w >> 8) & 0xFFu);
+            if (lr == 0) rec[128 * NTERM + 4 * t + b] = (uint8_t)(e + 127);
+        }
+    }
+    if (pad && write && lr < 2 * NTERM) {   // blocks 2 and 3: lane lr zeroes term lr >> 1's block 2 + (lr & 1)
+        const int t = lr >> 1, bz = 2 + (lr & 1);
+        uint8_t* z = rec + 128 * t + 64 * (bz & 1) + 16 * (bz >> 1);
+        *reinterpret_cast<uint4*>(z) = uint4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<uint4*>(z + 32) = uint4{0u, 0u, 0u, 0u};
+        rec[128 * NTERM + 4 * t + bz] = 127;
+    }
+}
+
 struct TileArgs {
     const uint16_t* actv;  // gate/up: x [T, K] (bf16 plane 0); down: h [T*k, K] (bf16; the hi plane of h = hi + lo)
     const uint16_t* actv2; // down: the lo plane of h
@@ -90,6 +132,7 @@ struct TileArgs {
     const int32_t* xexp;   // dense int4 gate/up: per-token exponents of x16 (actv) [T]
     const int32_t* gidx;   // wave tiles: when set, each workgroup finds its pass from these raw ids (gn = T k of them)
     int gn, gfirst;        // instead of the grouping kernel's pass list (gfirst: expert-major first passes)
+    uint8_t* hterm;        // block-scaled MXFP4 gate/up: h leaves as 3-term records [T*k][ceil(N/128)] (no planes)
 };
 
 // In-kernel grouping, one wave: pass y of the wave tiles' pass list (passes of P slots; an expert's slots in
@@ -728,6 +771,32 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
         }
         }   // MXT == 0
         // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
+        if constexpr (MXT > 0 && NPROJ == 2) {   // h as the down's 3-term records: this wave's 32 rows = one block
+            static_assert(RT == 2, "one 32-row block of h per wave");
+            if (a.hterm) {
+                const int nslN = (N + 127) >> 7, bk = (r0 & 127) >> 5;
+                const bool pad = (N & 127) == 64 && (r0 >> 7) == nslN - 1 && bk == 1;
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int j = 4 * lg + v;
+                        const int slot = __shfl(slotA[t], j, 64);   // lane j (any lane group) holds token j's slot
+                        float hv[RT];
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt) {
+                            const int r = r0 + 16 * rt + lr;
+                            float g = acc[0][rt][t][v], up = acc[1][rt][t][v];
+                            if (a.b0) g += a.b0[(size_t)e * N + r];
+                            if (a.b1) up += a.b1[(size_t)e * N + r];
+                            hv[rt] = glu_act(a.act, g, up);
+                        }
+                        mx_h_block<3>(hv[0], hv[1], tok0 + 16 * t + j < n,
+                                      a.hterm + ((size_t)slot * nslN + (r0 >> 7)) * mx_rec<3>(), bk, lr, pad);
+                    }
+                return;
+            }
+        }
         if constexpr (H16O) {
             int8_t* hexp_out = reinterpret_cast<int8_t*>(a.hout2);
             const int nch = N >> 5;
@@ -1238,13 +1307,13 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
 // r -= q 2^e (exact). Two terms hold bf16 x, three hold h = hi + lo; measured on this part, the instruction's own
 // accumulation keeps ~2e-5 of the outputs' RMS (two to four terms give the same result), against the 1e-2 RMS gate.
 
-// Activation rows -> per (row, 128-input slice) records of REC = 16 (8 NTERM + 1) bytes: NTERM x 128 bytes of terms
-// in the A operand's order (bytes 32 g .. 32 g + 15 = inputs 16 g .. 16 g + 15, bytes 32 g + 16 .. 32 g + 31 =
-// inputs 64 + 16 g .. 64 + 16 g + 15), then the E8M0 byte of term t, block b at 128 NTERM + 4 t + b. Inputs past K
-// (K % 128 == 64) are zero codes with scale byte 127. One thread per 32-input block; HL: rows are h = hi + lo.
-template <int NTERM, bool HL>
-__global__ void __launch_bounds__(256) k_mx_terms(const uint16_t* __restrict__ src, const uint16_t* __restrict__ src2,
-                                                 int rows, int K, uint8_t* __restrict__ out) {
+// x rows (bf16) -> per (row, 128-input slice) records of REC = 16 (8 NTERM + 1) bytes: NTERM x 128 bytes of terms
+// at mx_pos (the records' code order, then the A operand's lane order), then the E8M0 byte of term t, block b at
+// 128 NTERM + 4 t + b. Inputs past K (K % 128 == 64) are zero codes with scale byte 127. One thread per 32-input
+// block. (h's records come from the gate/up epilogues, mx_h_block.)
+template <int NTERM>
+__global__ void __launch_bounds__(256) k_mx_terms(const uint16_t* __restrict__ src, int rows, int K,
+                                                 uint8_t* __restrict__ out) {
     constexpr int REC = mx_rec<NTERM>();
     const int nsl = (K + 127) >> 7, nb = 4 * nsl;
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
@@ -1255,7 +1324,6 @@ __global__ void __launch_bounds__(256) k_mx_terms(const uint16_t* __restrict__ s
     float r[32];
     if (32 * blk < K) {
         const uint4* p = reinterpret_cast<const uint4*>(src + (size_t)row * K + 32 * blk);
-        const uint4* p2 = HL ? reinterpret_cast<const uint4*>(src2 + (size_t)row * K + 32 * blk) : p;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint4 v = p[q];
@@ -1264,15 +1332,6 @@ __global__ void __launch_bounds__(256) k_mx_terms(const uint16_t* __restrict__ s
             for (int u = 0; u < 4; ++u) {
                 r[8 * q + 2 * u] = bf16lo(w[u]);
                 r[8 * q + 2 * u + 1] = bf16hi(w[u]);
-            }
-            if (HL) {
-                const uint4 v2 = p2[q];
-                const uint32_t w2[4] = {v2.x, v2.y, v2.z, v2.w};
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    r[8 * q + 2 * u] += bf16lo(w2[u]);
-                    r[8 * q + 2 * u + 1] += bf16hi(w2[u]);
-                }
             }
         }
     } else {
@@ -1481,6 +1540,30 @@ __global__ void __launch_bounds__(256, NPROJ == 2 ? MOE_MXD_MINB_GU : MOE_MXD_MI
 
     // ---- epilogue: lane holds row r0 + 16 rt + lr of tokens tok0 + 16 t + 4 lg + v
     if (!wvalid) return;
+    if constexpr (NPROJ == 2) {   // h as the down's 3-term records: this wave's 32 rows = one block
+        static_assert(RT == 2, "one 32-row block of h per wave");
+        const int nslN = (N + 127) >> 7, bk = (r0 & 127) >> 5;
+        const bool pad = (N & 127) == 64 && (r0 >> 7) == nslN - 1 && bk == 1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int jt = 16 * t + 4 * lg + v;
+                const int slot = sSlot[jt];
+                float hv[RT];
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const int r = r0 + 16 * rt + lr;
+                    float g = acc[0][rt][t][v], up = acc[1][rt][t][v];
+                    if (a.b0) g += a.b0[(size_t)e * N + r];
+                    if (a.b1) up += a.b1[(size_t)e * N + r];
+                    hv[rt] = glu_act(a.act, g, up);
+                }
+                mx_h_block<3>(hv[0], hv[1], jt < nlive, a.hterm + ((size_t)slot * nslN + (r0 >> 7)) * mx_rec<3>(), bk,
+                              lr, pad);
+            }
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -1489,20 +1572,7 @@ __global__ void __launch_bounds__(256, NPROJ == 2 ? MOE_MXD_MINB_GU : MOE_MXD_MI
             if (jt >= nlive) continue;
             const int slot = sSlot[jt];
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                const int r = r0 + 16 * rt + lr;
-                if (NPROJ == 2) {
-                    float g = acc[0][rt][t][v], up = acc[NPROJ - 1][rt][t][v];
-                    if (a.b0) g += a.b0[(size_t)e * N + r];
-                    if (a.b1) up += a.b1[(size_t)e * N + r];
-                    const float hv = glu_act(a.act, g, up);
-                    const uint16_t hi = f32_to_bf16(hv);
-                    a.hout[(size_t)slot * N + r] = hi;
-                    a.hout2[(size_t)slot * N + r] = f32_to_bf16(hv - bf16_to_f32(hi));
-                } else {
-                    a.yp[(size_t)slot * N + r] = acc[0][rt][t][v];
-                }
-            }
+            for (int rt = 0; rt < RT; ++rt) a.yp[(size_t)slot * N + r0 + 16 * rt + lr] = acc[0][rt][t][v];
         }
 }
 
@@ -1516,11 +1586,11 @@ int launch_mxd(const TileArgs& t, int nslots, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
-template <int NTERM, bool HL>
-int launch_mx_terms(const uint16_t* src, const uint16_t* src2, int rows, int K, uint8_t* out, hipStream_t st) {
+template <int NTERM>
+int launch_mx_terms(const uint16_t* src, int rows, int K, uint8_t* out, hipStream_t st) {
     const long n = (long)rows * 4 * ((K + 127) >> 7);
     if (n <= 0 || (n + 255) / 256 > 0x7FFFFFFFL) return MOE_ERR_ARG;
-    k_mx_terms<NTERM, HL><<<dim3((unsigned)((n + 255) / 256)), 256, 0, st>>>(src, src2, rows, K, out);
+    k_mx_terms<NTERM><<<dim3((unsigned)((n + 255) / 256)), 256, 0, st>>>(src, rows, K, out);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
@@ -1953,10 +2023,11 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
         }
+        if (mxd || mxw) g.hterm = reinterpret_cast<uint8_t*>(a.yp + (size_t)nslots * w->d);   // h's records
         if (mxd) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
-            rc = launch_mx_terms<2, false>(a.xb, nullptr, a.T, w->d, a.xterm, a.st);
+            rc = launch_mx_terms<2>(a.xb, a.T, w->d, a.xterm, a.st);
             g.actv = reinterpret_cast<const uint16_t*>(a.xterm);
             if (!rc) rc = launch_mxd<2, 2>(g, nslots, a.st);
             if (rc) return rc;
@@ -1969,7 +2040,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.xexp = a.xexp;
         }
         if (mxw) {
-            rc = launch_mx_terms<2, false>(a.xb, nullptr, a.T, w->d, a.xterm, a.st);
+            rc = launch_mx_terms<2>(a.xb, a.T, w->d, a.xterm, a.st);
             g.actv = reinterpret_cast<const uint16_t*>(a.xterm);
             if (!rc) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st, 1, 2);
         } else if (mxd) rc = 0;
@@ -2008,19 +2079,12 @@ int run_tiles_fmt(const ExpertsArgs& a) {
                    (long)(w->d / (16 * rt)) * max_passes(nslots, w->E, 16 * nt) >= MOE_WAVE_WIDE_MIN_WAVES;
         };
         int rc = 0;
-        if (mxw) {   // h's terms for the wave down
-            uint8_t* hterm = reinterpret_cast<uint8_t*>(a.yp + d.plane);
-            rc = launch_mx_terms<3, true>(a.hhi, a.hlo, nslots, w->F, hterm, a.st);
-            d.actv = reinterpret_cast<const uint16_t*>(hterm);
-            if (rc) return rc;
-        }
+        // block-scaled: h's 3-term records, written by the gate/up epilogue into the yp planes after the first
+        if (mxw || mxd) d.actv = reinterpret_cast<const uint16_t*>(a.yp + d.plane);
         const int mxt = mxw ? 3 : 0;
         if (mxd) {
-            uint8_t* hterm = reinterpret_cast<uint8_t*>(a.yp + d.plane);   // the yp planes after the first
             d.W0 = (const uint8_t*)w->down.tiles;
-            rc = launch_mx_terms<3, true>(a.hhi, a.hlo, nslots, w->F, hterm, a.st);
-            d.actv = reinterpret_cast<const uint16_t*>(hterm);
-            if (!rc) rc = launch_mxd<1, 3>(d, nslots, a.st);
+            rc = launch_mxd<1, 3>(d, nslots, a.st);
         } else if (dense_dn) rc = launch_dense<FMT, 1>(d, nslots, a.st);
         else if (wave_dn && wide_dn(MOE_WAVE_RT_DN_WIDE))
             rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN_WIDE, MOE_WAVE_D_DN>(d, nt, nslots, a.st, 1, mxt);
