@@ -307,7 +307,7 @@ def other_configs(dev, args, only=None):
     seeded layers (enough of them to exceed the 256 MB Infinity Cache), uniform router logits, timed like the
     headline. Reported beside `value`."""
     from moelab_amd import _lib, roofline, router
-    from moelab_amd.experts import make_state, run_layer
+    from moelab_amd.experts import make_state, merge_shared, run_layer
     from moelab_amd import formats
     from moelab_amd.problem import baseline_int4_layer, baseline_mxfp4_layer, baseline_x
     from moelab_amd.shapes import SHAPES
@@ -372,7 +372,8 @@ def other_configs(dev, args, only=None):
         g = torch.Generator(device=dev).manual_seed(4100 + l)
         ly["shared"] = make_state("int4", *(formats.random_int4(sh.shared, n, k, generator=g, device=dev)
                                             for n, k in ((sh.f, sh.d), (sh.f, sh.d), (sh.d, sh.f))))
-        layers.append(ly)
+        layers.append(merge_shared(ly))   # shared experts as experts 64, 65: one call per layer
+        del ly
     report("dsv2lite_int4_T256_shared2", sh, "int4", layers, 256, 0, shared_f=sh.shared * sh.f)
     del layers
     torch.cuda.empty_cache()

@@ -235,6 +235,24 @@ int moe_shared_experts_run(const moe_experts_t* ws, const void* x, int x_dtype, 
                            void* stream);
 size_t moe_shared_experts_workspace_bytes(const moe_experts_t* ws, int T);
 
+/*
+ * Routed and shared experts in one call (no counterpart in the reference, whose model patches run the shared
+ * experts as a separate module after the routed ones, e2e.py:66-68 and 146-147): w holds E = E_r + S experts,
+ * experts E_r .. E_r + S - 1 being the shared ones (same d, F, format and packing as the routed ones: the two
+ * sets' rows concatenated, with tile copies packed over all E). Token t's slots are its k routed slots (idx, wts
+ * as moe_experts_run; ids outside [0, E_r) join no group) followed by the S shared slots, expert E_r + s with
+ * weight g_t = sigmoid(x_t . gate) (gate: bf16 [d]) or 1 when gate is NULL:
+ *   y[t] = residual[t] + sum_j wts[t,j] * expert_{idx[t,j]}(x_t) + g_t * sum_s expert_{E_r + s}(x_t),
+ * the experts and path as in moe_experts_run. One grouping, one combine, and the shared experts' work inside
+ * the routed launches (the two-call form costs a second grouping, combine and slot-list launch, and runs the few
+ * shared experts on grids too small to fill the chip). Limits: 1 <= S < E, k >= 1, k + S <= 64.
+ *   workspace: moe_experts_shared_workspace_bytes(w, S, T, k, path) bytes (any contents).
+ */
+int moe_experts_run_shared(const moe_experts_t* w, int S, const void* x, int x_dtype, const int32_t* idx,
+                           const float* wts, int T, int k, int act, int path, const void* gate, void* y, int y_dtype,
+                           const void* residual, void* workspace, size_t workspace_bytes, void* stream);
+size_t moe_experts_shared_workspace_bytes(const moe_experts_t* w, int S, int T, int k, int path);
+
 /* Library version and build target, for logs. */
 const char* moe_version(void);
 

@@ -183,6 +183,38 @@ int moe_shared_experts_run(const moe_experts_t* ws, const void* x, int x_dtype, 
                                   workspace, base, MOE_STAGE_ALL, stream);
 }
 
+size_t moe_experts_shared_workspace_bytes(const moe_experts_t* w, int S, int T, int k, int path) {
+    if (!w || T < 0 || k < 1 || S < 1 || k + S > 64) return 0;
+    const size_t n = (size_t)T * (k + S);
+    return layout(w, T, k + S, path).total + 2 * align_up(n * 4);
+}
+
+// routed + shared in one call: the slot lists [T, k + S] (routed ids outside [0, E - S) become -1, so they join no
+// group as in moe_experts_run), then the expert call on them
+int moe_experts_run_shared(const moe_experts_t* w, int S, const void* x, int x_dtype, const int32_t* idx,
+                           const float* wts, int T, int k, int act, int path, const void* gate, void* y, int y_dtype,
+                           const void* residual, void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_experts(w);
+    if (rc) return rc;
+    if (S < 1 || k < 1 || k + S > 64 || S >= w->E || T < 0 || path < MOE_PATH_AUTO || path > MOE_PATH_GROUPED)
+        return MOE_ERR_ARG;
+    if (T == 0) return MOE_OK;
+    if (!x || !y || !idx || !wts) return MOE_ERR_ARG;
+    if (!workspace) return MOE_ERR_WORKSPACE;
+    if (x_dtype < MOE_DTYPE_BF16 || x_dtype > MOE_DTYPE_F32) return MOE_ERR_DTYPE;
+    if (!aligned16(x) || (gate && !aligned16(gate)) || !aligned16(workspace)) return MOE_ERR_ALIGN;
+    if (workspace_bytes < moe_experts_shared_workspace_bytes(w, S, T, k, path)) return MOE_ERR_WORKSPACE;
+    const size_t base = layout(w, T, k + S, path).total;
+    const size_t n = (size_t)T * (k + S);
+    int32_t* idx2 = (int32_t*)((char*)workspace + base);
+    float* wts2 = (float*)((char*)workspace + base + align_up(n * 4));
+    rc = moe::launch_shared_route(x, x_dtype, (const uint16_t*)gate, T, w->d, S, idx2, wts2, (hipStream_t)stream, k,
+                                  w->E - S, idx, wts);
+    if (rc) return rc;
+    return moe_experts_run_stages(w, x, x_dtype, idx2, wts2, T, k + S, act, path, 0, y, y_dtype, residual, workspace,
+                                  base, MOE_STAGE_ALL, stream);
+}
+
 int moe_experts_run(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T,
                     int k, int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                     size_t workspace_bytes, void* stream) {

@@ -23,7 +23,7 @@ int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* off
 // upper bound of the pass count: sum over experts of ceil(count / P) <= n / P + (experts with a count)
 inline int max_passes(int n, int E, int P) { return (n + P - 1) / P + (n < E ? n : E); }
 int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
-                        hipStream_t st);
+                        hipStream_t st, int k = 0, int E0 = 0, const int32_t* ridx = nullptr, const float* rwts = nullptr);
 
 // grouping scratch inside an experts workspace
 struct GroupBufs {

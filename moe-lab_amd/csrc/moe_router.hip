@@ -310,12 +310,14 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
     }
 }
 
-// shared experts: the slots of token t are (t, s) for s < S, weight g_t = sigmoid(x_t . gate) or 1. One wave per
-// token: lane l dots the 8-element chunks l, l + 64, ... in element order, the lane sums are added as the DPP
-// tree of sum_lanes<64>, lanes 48..63 hold the total.
+// shared experts: token t's slot list is its k routed slots (copied from ridx / rwts [T, k]; none when k = 0)
+// followed by S shared slots, expert E0 + s with weight g_t = sigmoid(x_t . gate) or 1, written as idx / wts
+// [T, k + S] (k + S <= 64). One wave per token: lane l dots the 8-element chunks l, l + 64, ... in element
+// order, the lane sums are added as the DPP tree of sum_lanes<64>, lanes 48..63 hold the total.
 __global__ void __launch_bounds__(256)
-shared_route(const void* __restrict__ x, int xdt, const uint16_t* __restrict__ gate, int T, int d, int S,
-             int32_t* __restrict__ idx, float* __restrict__ wts) {
+shared_route(const void* __restrict__ x, int xdt, const uint16_t* __restrict__ gate, int T, int d, int S, int k,
+             int E0, const int32_t* __restrict__ ridx, const float* __restrict__ rwts, int32_t* __restrict__ idx,
+             float* __restrict__ wts) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + wave;
     if (t >= T) return;
@@ -351,9 +353,14 @@ shared_route(const void* __restrict__ x, int xdt, const uint16_t* __restrict__ g
         acc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 63));
         g = 1.f / (1.f + expf(-acc));
     }
-    if (lane < S) {
-        idx[(size_t)t * S + lane] = lane;
-        wts[(size_t)t * S + lane] = g;
+    const int w = k + S;
+    if (lane < k) {   // routed ids outside [0, E0) join no group (E0 .. E0 + S - 1 are the shared experts)
+        const int id = ridx[(size_t)t * k + lane];
+        idx[(size_t)t * w + lane] = (unsigned)id < (unsigned)E0 ? id : -1;
+        wts[(size_t)t * w + lane] = rwts[(size_t)t * k + lane];
+    } else if (lane < w) {
+        idx[(size_t)t * w + lane] = E0 + lane - k;
+        wts[(size_t)t * w + lane] = g;
     }
 }
 
@@ -404,9 +411,10 @@ int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, fl
 }
 
 int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
-                        hipStream_t st) {
+                        hipStream_t st, int k, int E0, const int32_t* ridx, const float* rwts) {
     if (T <= 0) return 0;
-    shared_route<<<(T + 3) / 4, 256, 0, st>>>(x, xdt, gate, T, d, S, idx, wts);
+    if (k < 0 || S < 0 || k + S > 64 || (k > 0 && (!ridx || !rwts))) return MOE_ERR_ARG;
+    shared_route<<<(T + 3) / 4, 256, 0, st>>>(x, xdt, gate, T, d, S, k, E0, ridx, rwts, idx, wts);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

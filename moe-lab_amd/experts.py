@@ -146,6 +146,9 @@ def reserve(s, T, k, device=None):
                [int(L.moe_layer_workspace_bytes(desc, t, k)) for t in {1, int(T)}])
     if "shared" in s:
         need = max(need, int(L.moe_shared_experts_workspace_bytes(_desc(s["shared"]), int(T))))
+    if "n_shared" in s:
+        need = max([need] + [int(L.moe_experts_shared_workspace_bytes(desc, int(s["n_shared"]), t, k, p))
+                             for t in {1, int(T)} for p in (_lib.PATH_AUTO, _lib.PATH_SLOTS, _lib.PATH_GROUPED)])
     return _lib.workspace(device, need)
 
 
@@ -202,9 +205,71 @@ def run_shared(s, x, gate=None, act=0, residual=None, out=None, out_dtype=None):
     return out
 
 
+def merge_shared(s):
+    """The state with its shared experts (s["shared"]) appended to the routed ones as experts E .. E + S - 1, for
+    one call per layer (moe_experts_run_shared: one grouping, one combine, the shared experts' work inside the
+    routed launches). Needs the same format, d and F in both sets; additive biases are concatenated (zeros where a
+    set has none). Routed ids keep their meaning. Returns a new state (its weights a copy; s is left as it is)."""
+    sh = s["shared"]
+    E, d, F = dims(s)
+    S, d2, F2 = dims(sh)
+    if sh["fmt"] != s["fmt"] or (d2, F2) != (d, F):
+        raise ValueError(f"shared experts ({sh['fmt']}, d={d2}, F={F2}) do not match the routed ones "
+                         f"({s['fmt']}, d={d}, F={F}): run them with run_shared")
+    if S + 1 > 64:
+        raise ValueError("at most 63 shared experts")
+    m = {k: v for k, v in s.items()
+         if k not in ("g", "u", "d", "bg", "bu", "bd", "gt", "ut", "dt", "_c", "_tiles_of", "shared", "shape")}
+    m["shape"] = (E + S, d, F)
+    for n in ("g", "u", "d"):
+        m[n] = torch.cat([s[n], sh[n]], 0).contiguous()
+    for b, N in (("bg", F), ("bu", F), ("bd", d)):
+        if b in s or b in sh:
+            parts = [t[b] if b in t else torch.zeros((n, N), dtype=torch.float32, device=s["g"].device)
+                     for t, n in ((s, E), (sh, S))]
+            m[b] = torch.cat(parts, 0).contiguous()
+    m["n_shared"] = S
+    if "gt" in s:
+        add_tiles(m)
+    return m
+
+
+def run_experts_shared(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, residual=None, out=None, out_dtype=None):
+    """Routed and shared experts of a merge_shared state in one call (moe_experts_run_shared): idx, wts [T, k]
+    the routed slots (ids < E - S); every token also takes the S shared experts with weight
+    sigmoid(x . s["shared_gate"]) or 1."""
+    _lib.require_device(x, "x")
+    if x.dtype not in _lib.DTYPE:
+        raise TypeError(f"activation dtype {x.dtype}: the expert kernels take bf16, fp16 or fp32")
+    T, d = x.shape
+    k = int(idx.shape[1])
+    S = int(s["n_shared"])
+    x = x.contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    wts = wts.to(torch.float32).contiguous()
+    desc = _desc(s)
+    L = _lib.lib()
+    ws = _lib.workspace(x.device, L.moe_experts_shared_workspace_bytes(desc, S, T, k, int(path)))
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((T, d), dtype=out_dtype, device=x.device)
+    assert out.dtype == out_dtype and out.dtype in _lib.DTYPE
+    res = None if residual is None else residual.to(out_dtype).contiguous()
+    g = s.get("shared_gate")
+    g = None if g is None else g.to(torch.bfloat16).contiguous()
+    rc = L.moe_experts_run_shared(desc, S, _lib.ptr(x), _lib.DTYPE[x.dtype], _lib.ptr(idx), _lib.ptr(wts), T, k,
+                                  int(act), int(path), _lib.ptr(g), _lib.ptr(out), _lib.DTYPE[out.dtype],
+                                  _lib.ptr(res), _lib.ptr(ws), ws.numel(), _lib.stream_of(x.device))
+    _lib.check("moe_experts_run_shared", rc)
+    return out
+
+
 def run_layer(s, x, idx, wts, act=0, path=_lib.PATH_AUTO, residual=None, out_dtype=None):
     """Routed experts, then the state's shared experts if it has them (s["shared"], optional
-    s["shared_gate"]): the routed sum stays fp32 until the shared call adds to it."""
+    s["shared_gate"]): the routed sum stays fp32 until the shared call adds to it. A merge_shared state runs
+    both in one call."""
+    if "n_shared" in s:
+        return run_experts_shared(s, x, idx, wts, act=act, path=path, residual=residual, out_dtype=out_dtype)
     if "shared" not in s:
         return run_experts(s, x, idx, wts, act=act, path=path, residual=residual, out_dtype=out_dtype)
     y = run_experts(s, x, idx, wts, act=act, path=path, residual=residual, out_dtype=torch.float32)

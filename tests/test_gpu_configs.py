@@ -111,11 +111,12 @@ def test_config5a_mixtral_full_size():
 
 
 def test_config5b_dsv2_lite_shared_full_size():
-    """Config 5b: DeepSeek-V2-Lite int4 g64 (d=2048, F=1408, E=64, k=6) at T=256 (24 slots per routed expert:
-    wave gate/up into the dense down) plus 2 always-on shared experts of F=1408 (256 tokens each: the wave tiles
-    on the small shared grid), built as bench.py builds it; 64 sampled token rows."""
+    """Config 5b: DeepSeek-V2-Lite int4 g64 (d=2048, F=1408, E=64, k=6) at T=256 plus 2 always-on shared experts of
+    F=1408, built as bench.py builds it: the shared experts merged into the routed set (experts 64, 65; one call
+    of 8 slots per token, 31 per expert: wave gate/up into the dense down). The two-call form (routed, then
+    shared on its own small grid) is checked too; 64 sampled token rows against the oracle on the unmerged layer."""
     from moelab_amd import formats
-    from moelab_amd.experts import make_state
+    from moelab_amd.experts import make_state, merge_shared
     from moelab_amd.problem import baseline_int4_layer, baseline_x
     from moelab_amd.shapes import SHAPES
     from moelab_amd.variants import hip_q4_moe as q4
@@ -129,9 +130,12 @@ def test_config5b_dsv2_lite_shared_full_size():
     print("case config5b dsv2-lite T=256 + 2 shared", flush=True)
     idx, wts = route_checked(x, layer["wr"], sh.k)
     grouping_checked(idx, sh.E)
-    y32 = q4.run(layer, x, idx, wts, out_dtype=torch.float32)
-    y = q4.run(layer, x, idx, wts)
+    merged = merge_shared(layer)
+    y32 = q4.run(merged, x, idx, wts, out_dtype=torch.float32)
+    y = q4.run(merged, x, idx, wts)
+    y2 = q4.run(layer, x, idx, wts, out_dtype=torch.float32)
     torch.cuda.synchronize()
     rows = sample_rows(T, seed=52)
     check_rows(y32, layer, x, idx, wts, rows, ("config5b", "fp32"))
     check_rows(y, layer, x, idx, wts, rows, ("config5b", "bf16"))
+    check_rows(y2, layer, x, idx, wts, rows, ("config5b", "two calls"))
