@@ -757,7 +757,7 @@ int down_rows_lds(int k, int F) { return k * (F >> 5) * 144; }   // 144-byte chu
 #define MOE_DN_NW 4   // waves per down block
 #endif
 #ifndef MOE_DN_RR2_NC
-#define MOE_DN_RR2_NC 4   // two rows per lane while NC <= this
+#define MOE_DN_RR2_NC 2   // two rows per lane while NC <= this (at NC = 3, Qwen3: twice the blocks, 4.95 -> 4.68 us)
 #endif
 template <class FMT, int NC, int RR>
 int launch_dn_rows_k(const ExpertsArgs& a, int lgL) {
@@ -782,7 +782,7 @@ int launch_dn_rows_k(const ExpertsArgs& a, int lgL) {
 }
 
 // lanes per down row L = 64 / KP (KP = the power of two >= k); chunks per lane NC >= cpr / L, from a fixed
-// menu; two rows per lane while NC <= 4
+// menu; two rows per lane while NC <= MOE_DN_RR2_NC
 int down_rows_plan(int k, int F, int* lgL) {
     if (k > 32 || k < 1) return 0;
     int kp = 1;
