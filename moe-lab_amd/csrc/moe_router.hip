@@ -147,21 +147,22 @@ topk_kernel(const LT* __restrict__ logits, int T, int E, int k, int norm, float 
 // mw (the ids and 4 per-wave count arrays fit in LDS): the ids are read once into LDS, and each of the 4 waves
 // places one contiguous quarter of the slots with its own cursors (the expert's offset plus the counts of the
 // quarters before it), so the order stays ascending within every expert. Otherwise wave 0 places all slots.
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(1024)
 group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
             int32_t* __restrict__ sorted, int32_t* __restrict__ active, int32_t* __restrict__ meta, int P,
             int32_t* __restrict__ items, int P2, int32_t* __restrict__ items2, int mw) {
-    extern __shared__ int32_t sm[];   // mw: cnt[4][E], ids[n]; else cnt[E], cursor[E]
-    const int NW = mw ? 4 : 1;
+    extern __shared__ int32_t sm[];   // mw: cnt[NW][E], ids[n] (NW = the block's waves); else cnt[E], cursor[E]
+    const int NT = (int)blockDim.x;
+    const int NW = mw ? NT >> 6 : 1;
     int32_t* cnt = sm;
     int32_t* cur1 = sm + E;
-    int32_t* sidx = sm + 4 * E;
+    int32_t* sidx = sm + NW * E;
     __shared__ int32_t s_bad;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int i = tid; i < NW * E; i += 256) cnt[i] = 0;
+    for (int i = tid; i < NW * E; i += NT) cnt[i] = 0;
     if (tid == 0) s_bad = 0;
     __syncthreads();
-    const int q4 = (n + 3) / 4;
+    const int q4 = (n + NW - 1) / NW;   // mw: wave w takes slots [w q4, (w + 1) q4)
     // ids are read GB per lane at a time (one memory round trip per batch, not one per id)
     constexpr int GB = 8;
     if (mw) {
@@ -184,16 +185,16 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
             }
         }
     } else {
-        for (int base = 0; base < n; base += 256 * GB) {
+        for (int base = 0; base < n; base += NT * GB) {
             int ev[GB];
 #pragma unroll
             for (int j = 0; j < GB; ++j) {
-                const int p = base + 256 * j + tid;
+                const int p = base + NT * j + tid;
                 ev[j] = p < n ? idx[p] : 0;
             }
 #pragma unroll
             for (int j = 0; j < GB; ++j) {
-                const int p = base + 256 * j + tid;
+                const int p = base + NT * j + tid;
                 if (p < n) {
                     if (ev[j] >= 0 && ev[j] < E) atomicAdd(&cnt[ev[j]], 1);
                     else atomicAdd(&s_bad, 1);
@@ -206,14 +207,9 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
         int run = 0, run_act = 0, run_p = 0, run_p2 = 0;
         for (int base = 0; base < E; base += 64) {
             const int e = base + lane;
-            int cw[4] = {0, 0, 0, 0};
             int c = 0;
-            if (e < E) {
-                for (int w = 0; w < NW; ++w) {
-                    cw[w] = cnt[w * E + e];
-                    c += cw[w];
-                }
-            }
+            if (e < E)
+                for (int w = 0; w < NW; ++w) c += cnt[w * E + e];
             const int np = items ? (c + P - 1) / P : 0;      // passes of expert e
             const int np2 = items2 ? (c + P2 - 1) / P2 : 0;  // in the second list
             // inclusive wave scans of c, of (c > 0) and of the pass counts
@@ -230,11 +226,12 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
                 const int excl = run + inc - c;
                 offsets[e] = excl;
                 counts[e] = c;
-                if (mw) {   // per-wave cursors: the quarters before come first
+                if (mw) {   // per-wave cursors: the earlier waves' slots come first
                     int cc = excl;
-                    for (int w = 0; w < 4; ++w) {
+                    for (int w = 0; w < NW; ++w) {
+                        const int cw = cnt[w * E + e];
                         cnt[w * E + e] = cc;
-                        cc += cw[w];
+                        cc += cw;
                     }
                 } else {
                     cur1[e] = excl;
@@ -421,10 +418,15 @@ int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
                  int32_t* active, int32_t* meta, hipStream_t st, int P, int32_t* items, int P2, int32_t* items2) {
     if ((items && P < 1) || (items2 && P2 < 1)) return MOE_ERR_ARG;
-    const size_t mw_bytes = ((size_t)4 * E + (size_t)n) * sizeof(int32_t);
+    // one block: 16 waves (1024 threads) each placing a sixteenth of the slots from 1024 slots, else 4 waves; the
+    // per-wave counts and the ids in LDS (at most 64 KB), else wave 0 places all of them
+    int nw = n >= 1024 ? 16 : 4;
+    if (((size_t)nw * E + (size_t)n) * sizeof(int32_t) > 64 * 1024) nw = 4;
+    const size_t mw_bytes = ((size_t)nw * E + (size_t)n) * sizeof(int32_t);
     const int mw = mw_bytes <= 64 * 1024 ? 1 : 0;
-    group_slots<<<1, 256, mw ? mw_bytes : 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted, active,
-                                                                          meta, P, items, P2, items2, mw);
+    if (!mw) nw = 4;
+    group_slots<<<1, 64 * nw, mw ? mw_bytes : 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted,
+                                                                              active, meta, P, items, P2, items2, mw);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
