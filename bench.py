@@ -9,7 +9,8 @@ selected experts of all 48 layers divided by the step time, the reference's `run
 contract (routing precomputed per layer, reference mlx_backend.py:91-117). The same chain with the
 router inside each layer (moe_layer_run) is reported as `with_router`. BASELINE config 3 (T=16, 32 and 64,
 uniform and Zipf(1.1) routing) reports the grouped expert path against the per-slot stock-style gather under
-`batched`; configs 4, 5a and 5b under `configs`.
+`batched`; configs 4, 5a and 5b under `configs`; gpt-oss-20b at T=512 (not a BASELINE config: the MXFP4 tiles
+on the block-scaled MFMA) under `mxfp4_prefill`.
 
 roofline: the dominant kernel at T=1 is the gate/up GEMV (2/3 of the weight bytes; the layer is two
 launches, gate/up then down). Its average launch duration is measured with HIP events on the stream it
@@ -185,10 +186,11 @@ def main():
 
     # ------------------------------------------------------------------ BASELINE configs 4, 5a, 5b
     configs = {}
+    prefill = {}   # beside the configs: gpt-oss-20b at T=512 (block-scaled MXFP4 tiles)
     if not args.no_configs:
         del layers
         torch.cuda.empty_cache()
-        configs = other_configs(dev, args)
+        configs = other_configs(dev, args, extra=prefill)
 
     # ------------------------------------------------------------------ CPU baseline (bounded samples)
     cpu = None
@@ -230,6 +232,7 @@ def main():
         "kernels_t1": {"gate_up_us": round(t_gu * 1e6, 3), "down_us": round(t_dn * 1e6, 3)},
         "batched": batched,
         "configs": configs,
+        "mxfp4_prefill": prefill,
         "roofline": {"bound": "hbm", "kernel": "k_gate_up_rows<FmtInt4, 3, 1, 1> (T=1 gate/up GEMV + GLU)",
                      "achieved": round(gu_bytes / t_gu / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_bytes / t_gu / 1e9 / HBM_PEAK_GBS, 4), "traffic": GU_T1_TRAFFIC_BYTES,
@@ -301,7 +304,7 @@ def copy_calibrate(dev, mib):
     log(f"copy calibration: 3 device copies of {n} bytes")
 
 
-def other_configs(dev, args, only=None):
+def other_configs(dev, args, only=None, extra=None):
     """BASELINE configs 4 (gpt-oss-20b MXFP4 + biases, clamped SwiGLU, T=1 and T=32), 5a (Mixtral-8x7B int4,
     T=512, MFMA-bound) and 5b (DeepSeek-V2-Lite int4, T=256, 2 shared experts): dependent residual chains of
     seeded layers (enough of them to exceed the 256 MB Infinity Cache), uniform router logits, timed like the
@@ -324,7 +327,7 @@ def other_configs(dev, args, only=None):
         del g
         return t
 
-    def report(name, sh, fmt, layers, T, act, shared_f=0, bias_bytes=0.0):
+    def report(name, sh, fmt, layers, T, act, shared_f=0, bias_bytes=0.0, into=None):
         x = baseline_x(T, sh.d, seed=T, device=dev)
         routes = [router.route(x, ly["wr"], sh.k) for ly in layers]
         U = [int(torch.unique(r[0]).numel()) for r in routes]
@@ -339,7 +342,7 @@ def other_configs(dev, args, only=None):
              "weight_GBps": round(wb / t / 1e9, 1), "TFLOPs": round(fl / t / 1e12, 2),
              "bound": "mfma" if mfma_floor > hbm_floor else "hbm",
              "frac_of_roofline": round(max(hbm_floor, mfma_floor) / t, 4), "layers": len(layers)}
-        out[name] = r
+        (out if into is None else into)[name] = r
         log(f"{name}: {r}")
 
     def want(*names):
@@ -353,6 +356,10 @@ def other_configs(dev, args, only=None):
         for T in (1, 32):
             if want(f"gptoss20b_mxfp4_T{T}"):
                 report(f"gptoss20b_mxfp4_T{T}", sh, "mxfp4", layers, T, 2, bias_bytes=bias_b)
+        # beside the configs (not a BASELINE config): the same layers at a prefill size, where the MXFP4 tiles
+        # run on the block-scaled MFMA (64 slots per expert: the dense tiles)
+        if extra is not None:
+            report("gptoss20b_mxfp4_T512", sh, "mxfp4", layers, 512, 2, bias_bytes=bias_b, into=extra)
         del layers
         torch.cuda.empty_cache()
     # config 5a: Mixtral-8x7B int4 T=512
