@@ -269,28 +269,29 @@ constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024
 // ends with round r's expert id (*id) and routing weight (*w): NaN counts as -inf, k rounds of arg-max with the lowest
 // id winning ties, fewer than k finite logits -> the lowest unused ids with weight 0; norm: softmax over the top-k
 // logits, !norm: full-softmax probabilities; weights times scale. rounds <= k stops after that many rounds (a caller
-// that needs only round r passes r + 1; the weights are then not computed).
-template <typename F>
-__device__ __forceinline__ void wave_topk_lanes(F lg, int E, int k, int norm, float scale, int rounds, uint32_t* id,
-                                                float* w) {
+// that needs only round r passes r + 1; the weights are then not computed). JM >= ceil(E / 64) logits per lane
+// (logit j * 64 + lane in v[j]); a round is one DPP max over the lanes' best values, then the lowest id holding it
+// from one ballot per j (the lowest j with a lane at the maximum, then the lowest such lane).
+template <int JM, typename F>
+__device__ __forceinline__ void topk_lanes(F lg, int E, int k, int norm, float scale, int rounds, uint32_t* id,
+                                           float* w) {
     const int lane = threadIdx.x & 63;
-    const int J = (E + 63) / 64;
-    float v[TOPK_MAX_J];
+    float v[JM];
 #pragma unroll
-    for (int j = 0; j < TOPK_MAX_J; ++j) {
+    for (int j = 0; j < JM; ++j) {
         const int e = j * 64 + lane;
-        float l = (j < J && e < E) ? lg(e) : -INFINITY;
+        float l = e < E ? lg(e) : -INFINITY;
         v[j] = __builtin_isnan(l) ? -INFINITY : l;
     }
     const bool weights = rounds >= k;
     float m0 = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < TOPK_MAX_J; ++j) m0 = fmaxf(m0, v[j]);
+    for (int j = 0; j < JM; ++j) m0 = fmaxf(m0, v[j]);
     if (weights) m0 = wave_max_dpp(m0);
     float den = 0.f;
     if (weights && !norm) {
 #pragma unroll
-        for (int j = 0; j < TOPK_MAX_J; ++j) den += (v[j] == -INFINITY) ? 0.f : expf(v[j] - m0);
+        for (int j = 0; j < JM; ++j) den += (v[j] == -INFINITY) ? 0.f : expf(v[j] - m0);
         den = wave_sum_dpp(den);
     }
     float myv = -INFINITY;   // lane r < k holds round r's value and id
@@ -298,19 +299,24 @@ __device__ __forceinline__ void wave_topk_lanes(F lg, int E, int k, int norm, fl
     float top0 = -INFINITY;
     for (int r = 0; r < rounds; ++r) {
         float b = -INFINITY;
-        uint32_t bi = 0xFFFFFFFFu;
+        int bj = -1;   // the lane's lowest j holding its maximum; -1: nothing above -inf
 #pragma unroll
-        for (int j = 0; j < TOPK_MAX_J; ++j)
-            if (v[j] > b) { b = v[j]; bi = (uint32_t)(j * 64 + lane); }
+        for (int j = 0; j < JM; ++j)
+            if (v[j] > b) { b = v[j]; bj = j; }
         float m = wave_max_dpp(b);
-        uint32_t sel = wave_min_dpp(b == m ? bi : 0xFFFFFFFFu);
+        uint32_t sel = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = 0; j < JM; ++j) {
+            const uint64_t hit = __ballot(bj == j && b == m);
+            if (sel == 0xFFFFFFFFu && hit) sel = (uint32_t)(j * 64 + __builtin_ctzll(hit));
+        }
         if (sel == 0xFFFFFFFFu) {   // no finite candidate left: lowest id not chosen yet, weight 0
             sel = 0;
             while (__ballot(lane < r && myi == sel) != 0ull) ++sel;
             m = -INFINITY;
         } else if ((int)(sel & 63u) == lane) {
 #pragma unroll
-            for (int j = 0; j < TOPK_MAX_J; ++j)
+            for (int j = 0; j < JM; ++j)
                 if (j == (int)(sel >> 6)) v[j] = -INFINITY;
         }
         if (r == 0) top0 = m;
@@ -324,6 +330,14 @@ __device__ __forceinline__ void wave_topk_lanes(F lg, int E, int k, int norm, fl
     else s = den;
     const float off = norm ? top0 : m0;
     *w = expf(myv - off) / s * scale;
+}
+template <typename F>
+__device__ __forceinline__ void wave_topk_lanes(F lg, int E, int k, int norm, float scale, int rounds, uint32_t* id,
+                                                float* w) {
+    if (E <= 64) topk_lanes<1>(lg, E, k, norm, scale, rounds, id, w);
+    else if (E <= 128) topk_lanes<2>(lg, E, k, norm, scale, rounds, id, w);
+    else if (E <= 256) topk_lanes<4>(lg, E, k, norm, scale, rounds, id, w);
+    else topk_lanes<TOPK_MAX_J>(lg, E, k, norm, scale, rounds, id, w);
 }
 
 // One wave: router tail for one token, written to idx[k], wts[k].

@@ -109,6 +109,22 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
                                                   int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo,
                                                   int s, int f0, int lane, const RouteArgs& rt = RouteArgs{}) {
     static_assert(R <= 16, "results live in lanes 48..63");
+    const int nchunk = d >> 5;
+    const uint16_t* xr = x + (size_t)(s / k) * d;
+    int ch[NCH];
+    bool cv[NCH];
+    uint32_t xw[HX][NCH][16];
+    auto load_x = [&](int c0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            ch[c] = c0 + 64 * c + lane;
+            cv[c] = ch[c] < nchunk;
+            ch[c] = cv[c] ? ch[c] : nchunk - 1;
+#pragma unroll
+            for (int h = 0; h < HX; ++h) load_x32(xr + h * xplane + 32 * ch[c], xw[h][c]);
+        }
+    };
+    load_x(0);   // x does not depend on the expert: its first loads go out before the expert id or router tail
     int e;
     if (rt.logits) {
         const int t = s / k, r = s - t * k;
@@ -126,8 +142,6 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
         e = idx[s];   // wave-uniform: a scalar load
     }
     const size_t rb = rbytes(FMT::FMT, d);
-    const int nchunk = d >> 5;
-    const uint16_t* xr = x + (size_t)(s / k) * d;
     float ag[R], au[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) ag[r] = au[r] = 0.f;
@@ -143,17 +157,7 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
         if (bu) bul = bu[(size_t)e * F + f0 + rl];
     }
     for (int c0 = 0; c0 < nchunk; c0 += 64 * NCH) {
-        int ch[NCH];
-        bool cv[NCH];
-        uint32_t xw[HX][NCH][16];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            ch[c] = c0 + 64 * c + lane;
-            cv[c] = ch[c] < nchunk;
-            ch[c] = cv[c] ? ch[c] : nchunk - 1;
-#pragma unroll
-            for (int h = 0; h < HX; ++h) load_x32(xr + h * xplane + 32 * ch[c], xw[h][c]);
-        }
+        if (c0) load_x(c0);
         uint4 wg[R][NCH], wu[R][NCH];
         uint32_t mg[R][NCH], mu[R][NCH];
 #pragma unroll
