@@ -281,6 +281,11 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     const int ee = ev ? e : 0;
     const size_t rb = rbytes(FMT::FMT, F);
     const int n0 = blockIdx.x * RB + wave * RR;
+    // the residual of the wave's output rows (added by the storing lane at the end), loaded with the first
+    // loads so that no memory round trip follows the reduction
+    float rres[RR];
+#pragma unroll
+    for (int i = 0; i < RR; ++i) rres[i] = resid ? load_y(resid, (size_t)t * D + min(n0 + i, D - 1), ydt) : 0.f;
     const uint8_t* rows[RR];
 #pragma unroll
     for (int i = 0; i < RR; ++i) rows[i] = Dw + ((size_t)ee * D + min(n0 + i, D - 1)) * rb;
@@ -365,10 +370,7 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     for (int i = 0; i < RR; ++i) {
         const int n = n0 + i;
         const float v = sum_lanes<64>((acc[i] + bdv[i]) * wj);
-        if (lane == SL && n < D) {
-            const size_t o = (size_t)t * D + n;
-            store_y(y, o, resid ? v + load_y(resid, o, ydt) : v, ydt);
-        }
+        if (lane == SL && n < D) store_y(y, (size_t)t * D + n, resid ? v + rres[i] : v, ydt);
     }
 }
 
@@ -479,6 +481,9 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
     const int nn = row_ok ? n : D - 1;
     const size_t rb = rbytes(FMT::FMT, F);
     const int cpr = F >> 5;
+    // the residual of the output row wave 0's lane stores at the end, loaded before the slots' loads
+    const int nr = blockIdx.x * RPW + lane;
+    const float rres = resid && !nored && wave == 0 && lane < RPW && nr < D ? load_y(resid, (size_t)t * D + nr, ydt) : 0.f;
     float yacc = 0.f;
     for (int j = wave; j < k; j += nw) {
         const int slot = t * k + j;
@@ -537,8 +542,7 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
         if (n2 < D) {
             float v = red[0][lane];
             for (int w = 1; w < nw; ++w) v += red[w][lane];
-            const size_t o = (size_t)t * D + n2;
-            store_y(y, o, resid ? v + load_y(resid, o, ydt) : v, ydt);
+            store_y(y, (size_t)t * D + n2, resid ? v + rres : v, ydt);
         }
     }
 }
@@ -560,6 +564,20 @@ k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t
     if (i4 >= total4) return;
     const size_t i = i4 * 4;
     const int t = (int)(i / D), n = (int)(i % D);
+    // the residual first: its load goes out with the slots' loads (one memory round trip for the kernel)
+    float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (resid) {
+        if (ydt == MOE_DTYPE_F32) {
+            rv = reinterpret_cast<const float4*>(resid)[i4];
+        } else if (ydt == MOE_DTYPE_F16) {
+            typedef _Float16 h4r __attribute__((ext_vector_type(4)));
+            const h4r r = reinterpret_cast<const h4r*>(resid)[i4];
+            rv = make_float4((float)r[0], (float)r[1], (float)r[2], (float)r[3]);
+        } else {
+            const uint2 r = reinterpret_cast<const uint2*>(resid)[i4];
+            rv = make_float4(bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y));
+        }
+    }
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j0 = 0; j0 < k; j0 += KC) {
         int e[KC];
@@ -606,35 +624,20 @@ k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t
             acc.w = ok ? __builtin_fmaf(w[j], u.w, acc.w) : acc.w;
         }
     }
+    if (resid) {
+        acc.x += rv.x;
+        acc.y += rv.y;
+        acc.z += rv.z;
+        acc.w += rv.w;
+    }
     if (ydt == MOE_DTYPE_F32) {
-        if (resid) {
-            const float4 r = reinterpret_cast<const float4*>(resid)[i4];
-            acc.x += r.x;
-            acc.y += r.y;
-            acc.z += r.z;
-            acc.w += r.w;
-        }
         reinterpret_cast<float4*>(y)[i4] = acc;
         return;
     }
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
     if (ydt == MOE_DTYPE_F16) {
-        if (resid) {
-            const h4 r = reinterpret_cast<const h4*>(resid)[i4];
-            acc.x += (float)r[0];
-            acc.y += (float)r[1];
-            acc.z += (float)r[2];
-            acc.w += (float)r[3];
-        }
         reinterpret_cast<h4*>(y)[i4] = h4{(_Float16)acc.x, (_Float16)acc.y, (_Float16)acc.z, (_Float16)acc.w};
         return;
-    }
-    if (resid) {
-        const uint2 r = reinterpret_cast<const uint2*>(resid)[i4];
-        acc.x += bf16lo(r.x);
-        acc.y += bf16hi(r.x);
-        acc.z += bf16lo(r.y);
-        acc.w += bf16hi(r.y);
     }
     uint2 o;
     o.x = (uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16);
