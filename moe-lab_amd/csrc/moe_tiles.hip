@@ -1053,17 +1053,27 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                 B[p][rt][u] = f16x8{v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
             }
         };
-        // group G's MFMAs (f16 x f16, fp32 accumulate, straight into acc); after token tile t, NEXT decodes group
-        // G + 1's (projection, row tile) pairs t * NPROJ * RT / NT ..., so that VALU work issues while MFMAs run
-        auto mfma_f16 = [&](auto full, auto next, const uint8_t* xs, int G, const f16x8 (&B)[NPROJ][RT][2],
-                            const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT], f16x8 (&Bn)[NPROJ][RT][2])
-                            __attribute__((always_inline)) {
+        // one slice as 2 NT steps f = G NT + t (scale group G, token tile t): group G's MFMAs (f16 x f16, fp32
+        // accumulate, straight into acc) for token tile t; after each of group 0's steps, group 1's (projection,
+        // row tile) pairs t * NPROJ * RT / NT ... are decoded, so that VALU work issues while MFMAs run. The A
+        // operands of step f + 2 are read from LDS while step f's MFMAs run, across the group boundary (three
+        // register sets; one step's MFMAs alone do not cover the LDS latency when a wave has only 2 row tiles), so
+        // a slice waits for LDS reads once, before its first step.
+        auto slice_f16 = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT])
+                             __attribute__((always_inline)) {
+            static_assert(NPROJ * RT % NT == 0 || NT % (NPROJ * RT) == 0, "decode pairs spread evenly over the token tiles");
             // pairs decoded after each token tile (PPT >= 1), or one pair after every TPP-th token tile
             constexpr int PPT = NPROJ * RT >= NT ? NPROJ * RT / NT : 1;
             constexpr int TPP = NPROJ * RT >= NT ? 1 : NT / (NPROJ * RT);
-            // the A operands of token tile t + 2 are read from LDS while tile t's MFMAs run (three register sets:
-            // one token tile's MFMAs alone do not cover the LDS latency when a wave has only 2 row tiles)
-            auto load_a = [&](int t, f16x8 (&A)[2]) __attribute__((always_inline)) {
+            constexpr int NS = 2 * NT;
+            f16x8 B0[NPROJ][RT][2], B1[NPROJ][RT][2];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < NPROJ * RT; ++i) decode_f16(0, i / RT, i % RT, q, m, B0);
+            __builtin_amdgcn_sched_barrier(0);
+            auto live = [&](int f) __attribute__((always_inline)) { return decltype(full)::value || f % NT < ntiles; };
+            auto load_a = [&](int f, f16x8 (&A)[2]) __attribute__((always_inline)) {
+                const int G = f / NT, t = f % NT;
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const int j = 2 * G + u;
@@ -1072,40 +1082,29 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
                 }
             };
             f16x8 Ab[3][2];
-            if (decltype(full)::value || 0 < ntiles) load_a(0, Ab[0]);
-            if (NT > 1 && (decltype(full)::value || 1 < ntiles)) load_a(1, Ab[1]);
+            if (live(0)) load_a(0, Ab[0]);
+            if (live(1)) load_a(1, Ab[1]);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                if (t + 2 < NT && (decltype(full)::value || t + 2 < ntiles)) load_a(t + 2, Ab[(t + 2) % 3]);
+            for (int f = 0; f < NS; ++f) {
+                const int G = f / NT, t = f % NT;
+                if (f + 2 < NS && live(f + 2)) load_a(f + 2, Ab[(f + 2) % 3]);
                 __builtin_amdgcn_sched_barrier(0);
-                if (decltype(full)::value || t < ntiles) {   // wave-uniform
+                if (live(f)) {   // wave-uniform
 #pragma unroll
                     for (int u = 0; u < 2; ++u)
 #pragma unroll
                         for (int p = 0; p < NPROJ; ++p)
 #pragma unroll
                             for (int rt = 0; rt < RT; ++rt)
-                                acc[p][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab[t % 3][u], B[p][rt][u], acc[p][rt][t], 0, 0, 0);
+                                acc[p][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    Ab[f % 3][u], G ? B1[p][rt][u] : B0[p][rt][u], acc[p][rt][t], 0, 0, 0);
                 }
-                if constexpr (decltype(next)::value) {
-                    if (t % TPP == TPP - 1) {
+                if (G == 0 && t % TPP == TPP - 1) {
 #pragma unroll
-                        for (int i = (t / TPP) * PPT; i < (t / TPP + 1) * PPT; ++i) decode_f16(G + 1, i / RT, i % RT, q, m, Bn);
-                    }
+                    for (int i = (t / TPP) * PPT; i < (t / TPP + 1) * PPT; ++i) decode_f16(1, i / RT, i % RT, q, m, B1);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-        };
-        auto slice_f16 = [&](auto full, const uint8_t* xs, const uint4 (&q)[NPROJ][RT], const uint2 (&m)[NPROJ][RT])
-                             __attribute__((always_inline)) {
-            static_assert(NPROJ * RT % NT == 0 || NT % (NPROJ * RT) == 0, "decode pairs spread evenly over the token tiles");
-            f16x8 B0[NPROJ][RT][2], B1[NPROJ][RT][2];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < NPROJ * RT; ++i) decode_f16(0, i / RT, i % RT, q, m, B0);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_f16(full, std::true_type{}, xs, 0, B0, q, m, B1);
-            mfma_f16(full, std::false_type{}, xs, 1, B1, q, m, B0);
         };
         // one slice, scale group by scale group; lane (m, g) of MFMA step j supplies word wi(j, g) of its row
         // (the record order). FULL: every token tile of the pass is live (no branch inside the slice)
