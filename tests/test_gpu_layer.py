@@ -82,3 +82,22 @@ def test_layer_ties_pick_lowest_ids():
     x = baseline_x(1, sh.d, seed=9, device=DEV)
     idx = check_layer(s, x, wr, sh.k, what="ties")
     assert idx.cpu().numpy().tolist() == [[0, 1, 2, 3]]
+
+
+@pytest.mark.parametrize("E", [200, 1000])
+def test_layer_ties_across_logit_groups(E):
+    """The router tail in the gate/up waves with E > 128 (4 and 16 logits per lane): three router rows set equal so
+    that experts 9, 67 and E - 50 (lanes 9, 3 and (E - 50) % 64 of logit groups 0, 1 and (E - 50) // 64) tie for
+    the top; the rounds must take them lowest id first, as the oracle does, and the rest of the layer must match."""
+    from moelab_amd.problem import baseline_int4_layer, baseline_x
+    from moelab_amd.shapes import MoEShape
+    sh = MoEShape("tiesJ", d=256, f=256, E=E, k=4)
+    s = baseline_int4_layer(sh, seed=11, device=DEV)
+    x = baseline_x(1, sh.d, seed=11, device=DEV)
+    wr = s["wr"].clone()
+    top = (torch.sign(x[0].float()) * 0.05).to(torch.bfloat16)   # logit 0.05 sum |x|: above every random row's
+    for e in (9, 67, E - 50):
+        wr[e] = top
+    print(f"case layer ties across groups E={E}", flush=True)
+    idx = check_layer(s, x, wr, sh.k, what=("tiesJ", E))
+    assert idx.cpu().numpy()[0, :3].tolist() == [9, 67, E - 50]
