@@ -124,7 +124,7 @@ int moe_tiles_pack(int fmt, int E, int N, int K, const void* rows, void* tiles, 
     return moe::launch_pack_tiles(fmt, E, N, K, rows, tiles, (hipStream_t)stream);
 }
 
-int moe_router_counter_count(int T) { return T < 1 ? 1 : moe::router_counter_slots(T); }
+int moe_router_counter_count(int T) { return moe::router_counter_slots(T < 1 ? 1 : T); }
 
 int moe_router(const void* x, const void* wr, const float* bias, int T, int d, int E, int k, int norm, float scale,
                float* logits, int32_t* idx, float* wts, int32_t* counters, void* stream) {
@@ -135,6 +135,24 @@ int moe_router(const void* x, const void* wr, const float* bias, int T, int d, i
     return moe::launch_router((const uint16_t*)x, (const uint16_t*)wr, bias, T, d, E, k, norm, scale, logits, idx, wts,
                               counters, (hipStream_t)stream);
 }
+
+int moe_router_group(const void* x, const void* wr, const float* bias, int T, int d, int E, int k, int norm,
+                     float scale, float* logits, int32_t* idx, float* wts, int32_t* counts, int32_t* offsets,
+                     int32_t* sorted, int32_t* active, int32_t* meta, int32_t* counters, void* stream) {
+    if (T < 0 || d < 8 || d % 8 || E < 1 || E > 1024 || k < 1 || k > E || k > 32) return MOE_ERR_ARG;
+    if (T == 0) return MOE_OK;
+    if (!x || !wr || !logits || !idx || !wts || !counters || !counts || !offsets || !sorted || !active || !meta)
+        return MOE_ERR_ARG;
+    if (!aligned16(x) || !aligned16(wr)) return MOE_ERR_ALIGN;
+    if (!moe::route_groups_inline(T * k, E)) return MOE_ERR_ARG;
+    moe::RouterArgs a{};
+    a.x = (const uint16_t*)x, a.wr = (const uint16_t*)wr, a.bias = bias, a.T = T, a.d = d, a.E = E, a.k = k;
+    a.norm = norm, a.scale = scale, a.logits = logits, a.lstride = E, a.idx = idx, a.wts = wts, a.counters = counters;
+    a.grp = moe::GroupBufs{counts, offsets, sorted, active, meta, nullptr, nullptr};
+    return moe::launch_route(a, true, (hipStream_t)stream);
+}
+
+int moe_router_group_max_slots(int E) { return E < 1 || E > 1024 ? 0 : moe::route_groups_max_slots(E); }
 
 int moe_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
              void* stream) {
@@ -239,7 +257,11 @@ namespace {
 int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T, int k,
                  int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                  size_t workspace_bytes, int stages, void* stream, const float* route_logits, int route_norm,
-                 float route_scale);
+                 float route_scale, int pregrouped = 0);
+int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const void* wr, const float* wr_bias,
+               const void* gate, int T, int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y,
+               int y_dtype, const void* residual, int32_t* counters, void* workspace, size_t workspace_bytes,
+               void* stream);
 }  // namespace
 
 size_t moe_layer_workspace_bytes(const moe_experts_t* w, int T, int k) {
@@ -247,31 +269,27 @@ size_t moe_layer_workspace_bytes(const moe_experts_t* w, int T, int k) {
     return layout(w, T, k, MOE_PATH_AUTO).total + align_up((size_t)T * w->E * 4);   // + the router logits
 }
 
+size_t moe_layer_shared_workspace_bytes(const moe_experts_t* w, int S, int T, int k) {
+    if (!w || T < 0 || k < 1 || S < 1 || S >= w->E || k + S > 64) return 0;
+    const size_t n = (size_t)T * (k + S);
+    // the experts' workspace for k + S slots, the router logits with the gate row, the merged slot lists
+    return layout(w, T, k + S, MOE_PATH_AUTO).total + align_up((size_t)T * (w->E - S + 1) * 4) + 2 * align_up(n * 4);
+}
+
 int moe_layer_run(const moe_experts_t* w, const void* x, int x_dtype, const void* wr, const float* wr_bias, int T,
                   int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y, int y_dtype,
-                  const void* residual, void* workspace, size_t workspace_bytes, void* stream) {
-    int rc = check_experts(w);
-    if (rc) return rc;
-    if (T < 0 || k < 1 || k > w->E || k > 32 || w->E > 1024 || act < 0 || act > 2) return MOE_ERR_ARG;
-    if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;   // the router GEMV reads bf16 x
-    if (y_dtype < MOE_DTYPE_BF16 || y_dtype > MOE_DTYPE_F32) return MOE_ERR_DTYPE;
-    if (T == 0) return MOE_OK;
-    if (!x || !wr || !idx || !wts || !y) return MOE_ERR_ARG;
-    if (!aligned16(x) || !aligned16(wr) || !aligned16(y) || (residual && !aligned16(residual))) return MOE_ERR_ALIGN;
-    if (!workspace || workspace_bytes < moe_layer_workspace_bytes(w, T, k)) return MOE_ERR_WORKSPACE;
-    if (!aligned16(workspace)) return MOE_ERR_ALIGN;
-    const size_t base = layout(w, T, k, MOE_PATH_AUTO).total;
-    float* logits = (float*)((char*)workspace + base);
-    hipStream_t st = (hipStream_t)stream;
-    rc = moe::launch_router_logits((const uint16_t*)x, (const uint16_t*)wr, wr_bias, T, w->d, w->E, logits, st);
-    if (rc) return rc;
-    if (T == 1 && moe::slots_route_in_gate_up(k, w->F))   // the gate/up waves run the tail themselves
-        return experts_call(w, x, x_dtype, idx, wts, T, k, act, MOE_PATH_AUTO, 0, y, y_dtype, residual, workspace,
-                            base, MOE_STAGE_ALL, stream, logits, norm, scale);
-    rc = moe::launch_topk(logits, MOE_DTYPE_F32, T, w->E, k, norm, scale, idx, wts, st);
-    if (rc) return rc;
-    return experts_call(w, x, x_dtype, idx, wts, T, k, act, MOE_PATH_AUTO, 0, y, y_dtype, residual, workspace, base,
-                        MOE_STAGE_ALL, stream, nullptr, 1, 1.f);
+                  const void* residual, int32_t* counters, void* workspace, size_t workspace_bytes, void* stream) {
+    return layer_call(w, 0, x, x_dtype, wr, wr_bias, nullptr, T, k, norm, scale, act, idx, wts, y, y_dtype, residual,
+                      counters, workspace, workspace_bytes, stream);
+}
+
+int moe_layer_run_shared(const moe_experts_t* w, int S, const void* x, int x_dtype, const void* wr,
+                         const float* wr_bias, const void* gate, int T, int k, int norm, float scale, int act,
+                         int32_t* idx, float* wts, void* y, int y_dtype, const void* residual, int32_t* counters,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    if (S < 1) return MOE_ERR_ARG;
+    return layer_call(w, S, x, x_dtype, wr, wr_bias, gate, T, k, norm, scale, act, idx, wts, y, y_dtype, residual,
+                      counters, workspace, workspace_bytes, stream);
 }
 
 int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,
@@ -287,7 +305,7 @@ namespace {
 int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T, int k,
                  int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                  size_t workspace_bytes, int stages, void* stream, const float* route_logits, int route_norm,
-                 float route_scale) {
+                 float route_scale, int pregrouped) {
     if (stages < 1 || stages > MOE_STAGE_ALL) return MOE_ERR_ARG;
     int rc = check_experts(w);
     if (rc) return rc;
@@ -347,8 +365,75 @@ int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32
         a.grp.meta = (int32_t*)(ws + L.meta);
         a.grp.items = (int32_t*)(ws + L.items);
         a.grp.items2 = (int32_t*)(ws + L.items2);
+        a.pregrouped = pregrouped;
     }
     return rpath == MOE_PATH_GROUPED ? moe::run_experts_tiles(a) : moe::run_experts_slots(a);
+}
+
+
+// Router and experts of one layer (S > 0: w's last S experts are shared ones, appended to every token's slots).
+// T == 1 (no shared experts, k and F the per-slot gate/up can route at): a logits-only router launch, the tail in the
+// gate/up waves. Otherwise one router launch computes the logits and the tail, writes the merged slot lists (S > 0),
+// and, on the grouped path when the slots fit its LDS, the grouping and the pass lists the expert kernels read; the
+// expert call then has no top-k or grouping launch. (MOE_LAYER_INGROUP=1: calls whose wave tiles can group in-kernel
+// leave it to them.)
+int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const void* wr, const float* wr_bias,
+               const void* gate, int T, int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y,
+               int y_dtype, const void* residual, int32_t* counters, void* workspace, size_t workspace_bytes,
+               void* stream) {
+    int rc = check_experts(w);
+    if (rc) return rc;
+    const int Er = w->E - S;   // routed experts
+    if (T < 0 || S < 0 || Er < 1 || k < 1 || k > Er || k > 32 || Er > 1024 || k + S > 64 || act < 0 || act > 2)
+        return MOE_ERR_ARG;
+    if (S == 0 && gate) return MOE_ERR_ARG;
+    if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;   // the router GEMV reads bf16 x
+    if (y_dtype < MOE_DTYPE_BF16 || y_dtype > MOE_DTYPE_F32) return MOE_ERR_DTYPE;
+    if (T == 0) return MOE_OK;
+    if (!x || !wr || !idx || !wts || !y || !counters) return MOE_ERR_ARG;
+    if (!aligned16(x) || !aligned16(wr) || !aligned16(y) || (residual && !aligned16(residual)) ||
+        (gate && !aligned16(gate)))
+        return MOE_ERR_ALIGN;
+    const size_t need = S ? moe_layer_shared_workspace_bytes(w, S, T, k) : moe_layer_workspace_bytes(w, T, k);
+    if (!workspace || workspace_bytes < need) return MOE_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return MOE_ERR_ALIGN;
+    const int ks = k + S;   // slots per token
+    const Layout L = layout(w, T, ks, MOE_PATH_AUTO);
+    char* ws = (char*)workspace;
+    hipStream_t st = (hipStream_t)stream;
+    moe::RouterArgs ra{};
+    ra.x = (const uint16_t*)x, ra.wr = (const uint16_t*)wr, ra.bias = wr_bias, ra.gate = (const uint16_t*)gate;
+    ra.T = T, ra.d = w->d, ra.E = Er, ra.k = k, ra.norm = norm, ra.scale = scale;
+    ra.logits = (float*)(ws + L.total), ra.lstride = Er + (gate ? 1 : 0);
+    ra.idx = idx, ra.wts = wts, ra.counters = counters, ra.S = S;
+    const int32_t* eidx = idx;   // the slot lists the experts read
+    const float* ewts = wts;
+    if (S) {
+        ra.sidx = (int32_t*)(ws + L.total + align_up((size_t)T * (Er + 1) * 4));
+        ra.swts = (float*)((char*)ra.sidx + align_up((size_t)T * ks * 4));
+        eidx = ra.sidx, ewts = ra.swts;
+    }
+    if (T == 1 && S == 0 && moe::slots_route_in_gate_up(k, w->F)) {   // the gate/up waves run the tail themselves
+        rc = moe::launch_route(ra, false, st);
+        if (rc) return rc;
+        return experts_call(w, x, x_dtype, idx, wts, T, k, act, MOE_PATH_AUTO, 0, y, y_dtype, residual, workspace,
+                            L.total, MOE_STAGE_ALL, stream, ra.logits, norm, scale);
+    }
+    int pregrouped = 0;
+    if (resolve_path(MOE_PATH_AUTO, T) == MOE_PATH_GROUPED && moe::route_groups_inline(T * ks, w->E)) {
+        const moe::TilePasses tp = moe::tile_passes(w, T, ks, x_dtype);
+        if (!(tp.ingroup && moe::env_int("MOE_LAYER_INGROUP", 0))) {
+            ra.grp = moe::GroupBufs{(int32_t*)(ws + L.counts), (int32_t*)(ws + L.offsets), (int32_t*)(ws + L.sorted),
+                                    (int32_t*)(ws + L.active), (int32_t*)(ws + L.meta), (int32_t*)(ws + L.items),
+                                    tp.P2 ? (int32_t*)(ws + L.items2) : nullptr};
+            ra.P = tp.P, ra.P2 = tp.P2;
+            pregrouped = 1;
+        }
+    }
+    rc = moe::launch_route(ra, true, st);
+    if (rc) return rc;
+    return experts_call(w, x, x_dtype, eidx, ewts, T, ks, act, MOE_PATH_AUTO, 0, y, y_dtype, residual, workspace,
+                        L.total, MOE_STAGE_ALL, stream, nullptr, 1, 1.f, pregrouped);
 }
 
 }  // namespace

@@ -2,12 +2,48 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "moe_mi355x.h"
 
 namespace moe {
 
-// router / grouping (moe_router.hip)
+// grouping scratch inside an experts workspace
+struct GroupBufs {
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* sorted;
+    int32_t* active;
+    int32_t* meta;    // [4]: active experts, bad ids, passes of the work list, passes of the second list
+    int32_t* items;   // pass list, room for max_passes(n, E, 16) (expert, pass, passes) triples
+    int32_t* items2;  // second pass list (dense down after wave gate/up), room for max_passes(n, E, 64)
+};
+
+// One router launch (moe_router.hip): the logits, then (tail) the top-k tail per token, the merged slot lists with
+// shared experts, and the slot grouping.
+struct RouterArgs {
+    const uint16_t* x;     // [T, d] bf16
+    const uint16_t* wr;    // [E, d] bf16
+    const float* bias;     // [E] or null
+    const uint16_t* gate;  // [d] bf16 or null: one more logit row (index E), the shared experts' gate
+    int T, d, E, k, norm;
+    float scale;
+    float* logits;         // [T, lstride]
+    int lstride;           // E, or E + 1 with the gate row
+    int32_t* idx;          // [T, k] routed ids
+    float* wts;            // [T, k] routed weights
+    int32_t* counters;     // [router_counter_slots(T)], zero on entry; the launch leaves them zero
+    int S;                 // shared experts appended to every token's slots (0: none)
+    int32_t* sidx;         // S > 0: [T, k + S] the k routed ids, then E .. E + S - 1
+    float* swts;           // S > 0: [T, k + S] the routed weights, then sigmoid(gate logit) or 1
+    GroupBufs grp;         // grp.counts null: no grouping; else the grouping of the slots (sidx when S > 0, else idx)
+    int P, P2;             // pass sizes of grp.items / grp.items2 (unused when null)
+    int mw;                // set by launch_route
+};
+// tail = false: logits only (no counters needed)
+int launch_route(RouterArgs a, bool tail, hipStream_t st);
+// whether launch_route can group n slots over E experts in its own launch (else: launch_group after it)
+bool route_groups_inline(int n, int E);
 int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
                   float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st);
 int router_counter_slots(int T);
@@ -20,21 +56,24 @@ int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, fl
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
                  int32_t* active, int32_t* meta, hipStream_t st, int P = 0, int32_t* items = nullptr, int P2 = 0,
                  int32_t* items2 = nullptr);
+// tuning and test knobs from the environment, read per call
+inline int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+// how many slots launch_route can group over E experts in its own launch
+int route_groups_max_slots(int E);
 // upper bound of the pass count: sum over experts of ceil(count / P) <= n / P + (experts with a count)
 inline int max_passes(int n, int E, int P) { return (n + P - 1) / P + (n < E ? n : E); }
 int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,
                         hipStream_t st, int k = 0, int E0 = 0, const int32_t* ridx = nullptr, const float* rwts = nullptr);
 
-// grouping scratch inside an experts workspace
-struct GroupBufs {
-    int32_t* counts;
-    int32_t* offsets;
-    int32_t* sorted;
-    int32_t* active;
-    int32_t* meta;    // [4]: active experts, bad ids, passes of the work list
-    int32_t* items;   // pass list, room for max_passes(n, E, 16) (expert, pass, passes) triples
-    int32_t* items2;  // second pass list (dense down after wave gate/up), room for max_passes(n, E, 64)
+// The grouped path's pass sizes for a call (the same choice run_experts_tiles makes): P the gate/up list's, P2 the
+// down list's when it differs (else 0); ingroup: the wave tiles group the slots in-kernel (no list needed).
+struct TilePasses {
+    int P, P2, ingroup;
 };
+TilePasses tile_passes(const moe_experts_t* w, int T, int k, int x_dtype);
 
 struct ExpertsArgs {
     const moe_experts_t* w;
@@ -56,6 +95,7 @@ struct ExpertsArgs {
     int32_t* xexp;  // [T]
     uint8_t* xterm; // grouped path, MXFP4 block-scaled MFMA: x's fp8 term records (the x-planes region when x is bf16)
     GroupBufs grp;  // grouped path
+    int pregrouped; // grouped path: grp already holds the grouping and pass lists of idx (written by the router)
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
     // moe_layer_run at T == 1: the gate/up waves take their experts from the top-k of these router logits [T, E] (and
     // write idx / wts, which the down kernel reads); null: idx / wts are inputs

@@ -1,7 +1,8 @@
 // Router and slot grouping kernels for gfx950.
 //
-// router_logits_topk: logits[t, e] = x[t] . Wr[e] (+ b[e]) in fp32, one wave per EPW experts x TPW tokens,
-// then the last block to finish a token group runs the router tail (top-k, softmax) for its tokens.
+// router_kernel: logits[t, e] = x[t] . Wr[e] (+ b[e]) in fp32, one wave per EPW experts x TPW tokens; then the last
+// block to finish a token group runs the router tail (top-k, softmax) for its tokens, and, when the call asks for the
+// grouping, the last token group to finish sorts all T*k slots by expert in the same launch (group_block).
 // The logit reduction order is fixed, so a CPU restatement reproduces every logit bit for bit and top-k ids
 // match exactly: lane l takes the 8-element chunks l, l+64, ... in order with fused multiply-adds in
 // element order, starting from +0; the 64 lane partials a[0..63] are combined by the DPP tree of
@@ -12,8 +13,9 @@
 // with the lowest expert id winning ties, fewer than k finite logits -> lowest unused ids with weight 0,
 // norm: softmax over the top-k logits, !norm: full-softmax probabilities; weights times `scale`.
 //
-// group_slots: stable grouping of the T*k slots by expert (reference metal_q4_tiles_v2.py:362-373 lists a
-// tile's slots in ascending slot id; closed form = stable argsort, reference triton_fused_moe.py:56-70).
+// Grouping (group_block, run by the router's last block or by the group_slots launch): stable grouping of the
+// T*k slots by expert (reference metal_q4_tiles_v2.py:362-373 lists a tile's slots in ascending slot id; closed
+// form = stable argsort, reference triton_fused_moe.py:56-70), offsets from a wave prefix sum of the counts.
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -32,129 +34,24 @@ __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return bf16_to_f
 template <>
 __device__ __forceinline__ float to_f32<_Float16>(_Float16 v) { return (float)v; }
 
-// grid (ceil(E / (ROUTER_WAVES * EPW)), ceil(T / TPW)), block 64 * ROUTER_WAVES.
-// counters[ty] must be 0 on entry; the last block of token group ty resets it to 0. Logits pass between
-// blocks through agent-scope atomic stores / loads (no L2 write-back or invalidation).
 constexpr int ROUTER_MAXC = 4;   // 16-byte chunks per lane held in registers per pass (2048 inputs)
 
-// TAIL = false: logits only (plain stores, no counters), for callers that run the tail elsewhere (moe_layer_run: the
-// T = 1 gate/up waves, or topk_kernel).
-template <int TPW, int EPW, bool TAIL = true, int WPB = ROUTER_WAVES>
-__global__ void __launch_bounds__(64 * WPB)
-router_logits_topk(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, const float* __restrict__ bias,
-                   int T, int d, int E, int k, int norm, float scale, float* __restrict__ logits,
-                   int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* __restrict__ counters) {
-    const int bx = blockIdx.x, nbx = gridDim.x;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int e0 = (bx * WPB + wave) * EPW;
-    const int t0 = blockIdx.y * TPW;
-    const int nt = min(TPW, T - t0);
-    const int nchunk = d >> 3;
-    if (e0 < E) {
-        float acc[EPW][TPW];
-#pragma unroll
-        for (int q = 0; q < EPW; ++q)
-#pragma unroll
-            for (int i = 0; i < TPW; ++i) acc[q][i] = 0.f;
-        for (int c0 = 0; c0 < nchunk; c0 += 64 * ROUTER_MAXC) {
-            // all loads of this pass first (chunks c0 + lane + 64m), then the fma chains in chunk order
-            uint4 w[EPW][ROUTER_MAXC], xv[TPW][ROUTER_MAXC];
-#pragma unroll
-            for (int m = 0; m < ROUTER_MAXC; ++m) {
-                const int c = min(c0 + lane + 64 * m, nchunk - 1);
-#pragma unroll
-                for (int q = 0; q < EPW; ++q)
-                    w[q][m] = reinterpret_cast<const uint4*>(wr + (size_t)min(e0 + q, E - 1) * d)[c];
-#pragma unroll
-                for (int i = 0; i < TPW; ++i)
-                    xv[i][m] = reinterpret_cast<const uint4*>(x + (size_t)(t0 + min(i, nt - 1)) * d)[c];
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int m = 0; m < ROUTER_MAXC; ++m) {
-                if (c0 + lane + 64 * m < nchunk) {
-#pragma unroll
-                    for (int q = 0; q < EPW; ++q) {
-                        const uint32_t ww[4] = {w[q][m].x, w[q][m].y, w[q][m].z, w[q][m].w};
-#pragma unroll
-                        for (int i = 0; i < TPW; ++i) {
-                            const uint32_t xx[4] = {xv[i][m].x, xv[i][m].y, xv[i][m].z, xv[i][m].w};
-                            float a = acc[q][i];
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                a = __builtin_fmaf(bf16lo(xx[r]), bf16lo(ww[r]), a);
-                                a = __builtin_fmaf(bf16hi(xx[r]), bf16hi(ww[r]), a);
-                            }
-                            acc[q][i] = a;
-                        }
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < EPW; ++q)
-#pragma unroll
-            for (int i = 0; i < TPW; ++i) {
-                float a = sum_lanes<64>(acc[q][i]);   // lanes 48..63 hold the total
-                const int e = e0 + q;
-                if (lane == 63 && i < nt && e < E) {
-                    if (bias) a = a + bias[e];
-                    if (TAIL) store_agent(&logits[(size_t)(t0 + i) * E + e], a);
-                    else logits[(size_t)(t0 + i) * E + e] = a;
-                }
-            }
-    }
-    if (!TAIL) return;
-    // the last block of this token group runs the tail
-    __shared__ int s_last;
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(&counters[blockIdx.y], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == nbx - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    for (int i = wave; i < nt; i += ROUTER_WAVES) {
-        const int t = t0 + i;
-        const float* lrow = logits + (size_t)t * E;
-        wave_topk([&](int ee) { return load_agent(lrow + ee); }, E, k, norm, scale, idx + (size_t)t * k,
-                  wts + (size_t)t * k);
-    }
-    if (threadIdx.x == 0) counters[blockIdx.y] = 0;
-}
-
-// Router tail on given logits [T, E] (fp32, bf16 or fp16): one wave per token.
-template <typename LT>
-__global__ void __launch_bounds__(256)
-topk_kernel(const LT* __restrict__ logits, int T, int E, int k, int norm, float scale, int32_t* __restrict__ idx,
-            float* __restrict__ wts) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T) return;
-    const LT* lrow = logits + (size_t)t * E;
-    wave_topk([&](int ee) { return to_f32<LT>(lrow[ee]); }, E, k, norm, scale, idx + (size_t)t * k,
-              wts + (size_t)t * k);
-}
-
-// Stable slot grouping by expert, one block of 256 threads. Slots p = t*k + j with ids outside [0, E)
-// are left out of every group (they contribute nothing) and counted in meta[1].
-// Outputs: counts[E], offsets[E+1], sorted[n] (valid part: offsets[E] entries), active[E] (first meta[0]
+// Stable slot grouping by one block (blockDim.x a multiple of 64). ld(p) yields the expert id of slot p = t*k + j;
+// ids outside [0, E) are left out of every group (they contribute nothing) and counted in meta[1].
+// Outputs (o): counts[E], offsets[E+1], sorted[n] (valid part: offsets[E] entries), active[E] (first meta[0]
 // entries: experts with count > 0, ascending), meta[0] = number of active experts, meta[1] = bad ids.
-// With items != null (the grouped kernels' work list, pass size P): items[3w .. 3w + 2] = (expert, pass index q
-// within the expert (first token q * P), the expert's pass count) of pass w; the passes of each active expert in
-// ascending order, expert by expert; meta[2] = number of passes. items2 (pass size P2), if given, is a second
-// such list, meta[3] its number of passes (the wave tiles' and the dense tiles' lists when a call uses both).
-// mw (the ids and 4 per-wave count arrays fit in LDS): the ids are read once into LDS, and each of the 4 waves
-// places one contiguous quarter of the slots with its own cursors (the expert's offset plus the counts of the
-// quarters before it), so the order stays ascending within every expert. Otherwise wave 0 places all slots.
-__global__ void __launch_bounds__(1024)
-group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-            int32_t* __restrict__ sorted, int32_t* __restrict__ active, int32_t* __restrict__ meta, int P,
-            int32_t* __restrict__ items, int P2, int32_t* __restrict__ items2, int mw) {
-    extern __shared__ int32_t sm[];   // mw: cnt[NW][E], ids[n] (NW = the block's waves); else cnt[E], cursor[E]
+// With o.items (the grouped kernels' work list, pass size P): items[3w .. 3w + 2] = (expert, pass index q within the
+// expert (first token q * P), the expert's pass count) of pass w; the passes of each active expert in ascending
+// order, expert by expert; meta[2] = number of passes. o.items2 (pass size P2), if given, is a second such list,
+// meta[3] its number of passes (the wave tiles' and the dense tiles' lists when a call uses both).
+// sm: dynamic LDS. mw (the ids and one count array per wave fit there): the ids are read once into LDS, and each
+// wave places one contiguous share of the slots with its own cursors (the expert's offset plus the counts of the
+// shares before it), so the order stays ascending within every expert. Otherwise wave 0 places all slots.
+template <typename LD>
+__device__ void group_block(LD ld, int n, int E, const GroupBufs& o, int P, int P2, int32_t* sm, int mw) {
     const int NT = (int)blockDim.x;
     const int NW = mw ? NT >> 6 : 1;
-    int32_t* cnt = sm;
+    int32_t* cnt = sm;            // mw: cnt[NW][E], ids[n]; else cnt[E], cursor[E]
     int32_t* cur1 = sm + E;
     int32_t* sidx = sm + NW * E;
     __shared__ int32_t s_bad;
@@ -172,7 +69,7 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
 #pragma unroll
             for (int j = 0; j < GB; ++j) {
                 const int p = base + 64 * j + lane;
-                ev[j] = p < b1 ? idx[p] : 0;
+                ev[j] = p < b1 ? ld(p) : 0;
             }
 #pragma unroll
             for (int j = 0; j < GB; ++j) {
@@ -190,7 +87,7 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
 #pragma unroll
             for (int j = 0; j < GB; ++j) {
                 const int p = base + NT * j + tid;
-                ev[j] = p < n ? idx[p] : 0;
+                ev[j] = p < n ? ld(p) : 0;
             }
 #pragma unroll
             for (int j = 0; j < GB; ++j) {
@@ -210,22 +107,15 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
             int c = 0;
             if (e < E)
                 for (int w = 0; w < NW; ++w) c += cnt[w * E + e];
-            const int np = items ? (c + P - 1) / P : 0;      // passes of expert e
-            const int np2 = items2 ? (c + P2 - 1) / P2 : 0;  // in the second list
+            const int np = o.items ? (c + P - 1) / P : 0;      // passes of expert e
+            const int np2 = o.items2 ? (c + P2 - 1) / P2 : 0;  // in the second list
             // inclusive wave scans of c, of (c > 0) and of the pass counts
-            int inc = c, act = c > 0 ? 1 : 0, incp = np, incp2 = np2;
-#pragma unroll
-            for (int s = 1; s < 64; s <<= 1) {
-                const int o = __shfl_up(inc, s, 64);
-                const int oa = __shfl_up(act, s, 64);
-                const int op = __shfl_up(incp, s, 64);
-                const int op2 = __shfl_up(incp2, s, 64);
-                if (lane >= s) { inc += o; act += oa; incp += op; incp2 += op2; }
-            }
+            const int inc = wave_incl_scan(c), act = wave_incl_scan(c > 0 ? 1 : 0);
+            const int incp = wave_incl_scan(np), incp2 = wave_incl_scan(np2);
             if (e < E) {
                 const int excl = run + inc - c;
-                offsets[e] = excl;
-                counts[e] = c;
+                o.offsets[e] = excl;
+                o.counts[e] = c;
                 if (mw) {   // per-wave cursors: the earlier waves' slots come first
                     int cc = excl;
                     for (int w = 0; w < NW; ++w) {
@@ -236,33 +126,33 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
                 } else {
                     cur1[e] = excl;
                 }
-                if (c > 0) active[run_act + act - 1] = e;
+                if (c > 0) o.active[run_act + act - 1] = e;
                 const int w0 = run_p + incp - np;
                 for (int q = 0; q < np; ++q) {
-                    items[3 * (w0 + q)] = e;
-                    items[3 * (w0 + q) + 1] = q;
-                    items[3 * (w0 + q) + 2] = np;
+                    o.items[3 * (w0 + q)] = e;
+                    o.items[3 * (w0 + q) + 1] = q;
+                    o.items[3 * (w0 + q) + 2] = np;
                 }
                 const int w2 = run_p2 + incp2 - np2;
                 for (int q = 0; q < np2; ++q) {
-                    items2[3 * (w2 + q)] = e;
-                    items2[3 * (w2 + q) + 1] = q;
-                    items2[3 * (w2 + q) + 2] = np2;
+                    o.items2[3 * (w2 + q)] = e;
+                    o.items2[3 * (w2 + q) + 1] = q;
+                    o.items2[3 * (w2 + q) + 2] = np2;
                 }
             }
-            run += __shfl(inc, 63, 64);
-            run_act += __shfl(act, 63, 64);
-            run_p += __shfl(incp, 63, 64);
-            run_p2 += __shfl(incp2, 63, 64);
+            run += __builtin_amdgcn_readlane(inc, 63);
+            run_act += __builtin_amdgcn_readlane(act, 63);
+            run_p += __builtin_amdgcn_readlane(incp, 63);
+            run_p2 += __builtin_amdgcn_readlane(incp2, 63);
         }
         if (lane == 0) {
-            offsets[E] = run;
-            meta[0] = run_act;
-            meta[1] = s_bad;
-            if (items) meta[2] = run_p;
-            if (items2) meta[3] = run_p2;
+            o.offsets[E] = run;
+            o.meta[0] = run_act;
+            o.meta[1] = s_bad;
+            if (o.items) o.meta[2] = run_p;
+            if (o.items2) o.meta[3] = run_p2;
         }
-        for (int a = run_act + lane; a < E; a += 64) active[a] = -1;
+        for (int a = run_act + lane; a < E; a += 64) o.active[a] = -1;
     }
     __syncthreads();
     if (mw || tid < 64) {   // stable placement, 64 slots per step in ascending order
@@ -279,7 +169,7 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
 #pragma unroll
                 for (int i = 0; i < GB; ++i) {
                     const int q = base + 64 * i + lane;
-                    ev[i] = q < b1 ? (mw ? sidx[q] : idx[q]) : -1;
+                    ev[i] = q < b1 ? (mw ? sidx[q] : ld(q)) : -1;
                 }
             }
             const int p = base + lane;
@@ -299,12 +189,159 @@ group_slots(const int32_t* __restrict__ idx, int n, int E, int32_t* __restrict__
             if (ok) pos = cursor[e] + __popcll(peers & lt_mask);
             __builtin_amdgcn_wave_barrier();
             if (ok) {
-                sorted[pos] = p;
+                o.sorted[pos] = p;
                 if ((peers & lt_mask) == 0ull) cursor[e] += __popcll(peers);   // lowest lane of the group
             }
             __builtin_amdgcn_wave_barrier();
         }
     }
+}
+
+// grid (ceil(rows / (ROUTER_WAVES * EPW)), ceil(T / TPW)), block 64 * ROUTER_WAVES; rows = a.lstride (the E router
+// rows, plus the shared experts' gate row when a.gate is given).
+// TAIL: a.counters[ty] must be 0 on entry; the last block of token group ty runs the tail for its tokens and resets it
+// to 0. With a.grp.counts, the last token group to finish (counter a.counters[gridDim.y], reset to 0 likewise) groups
+// the slots in the same launch. Logits and ids pass between blocks through agent-scope atomic stores / loads (no L2
+// write-back or invalidation). !TAIL: logits only (plain stores, no counters), for callers that run the tail
+// elsewhere (moe_layer_run at T = 1: the gate/up waves).
+template <int TPW, int EPW, bool TAIL>
+__global__ void __launch_bounds__(64 * ROUTER_WAVES) router_kernel(RouterArgs a) {
+    const int nbx = gridDim.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int rows = a.lstride;
+    const int e0 = (blockIdx.x * ROUTER_WAVES + wave) * EPW;
+    const int t0 = blockIdx.y * TPW;
+    const int nt = min(TPW, a.T - t0);
+    const int d = a.d;
+    const int nchunk = d >> 3;
+    if (e0 < rows) {
+        const uint16_t* wrow[EPW];   // row e < E of Wr, row E the gate
+#pragma unroll
+        for (int q = 0; q < EPW; ++q) {
+            const int e = min(e0 + q, rows - 1);
+            wrow[q] = e < a.E ? a.wr + (size_t)e * d : a.gate;
+        }
+        float acc[EPW][TPW];
+#pragma unroll
+        for (int q = 0; q < EPW; ++q)
+#pragma unroll
+            for (int i = 0; i < TPW; ++i) acc[q][i] = 0.f;
+        for (int c0 = 0; c0 < nchunk; c0 += 64 * ROUTER_MAXC) {
+            // all loads of this pass first (chunks c0 + lane + 64m), then the fma chains in chunk order
+            uint4 w[EPW][ROUTER_MAXC], xv[TPW][ROUTER_MAXC];
+#pragma unroll
+            for (int m = 0; m < ROUTER_MAXC; ++m) {
+                const int c = min(c0 + lane + 64 * m, nchunk - 1);
+#pragma unroll
+                for (int q = 0; q < EPW; ++q) w[q][m] = reinterpret_cast<const uint4*>(wrow[q])[c];
+#pragma unroll
+                for (int i = 0; i < TPW; ++i)
+                    xv[i][m] = reinterpret_cast<const uint4*>(a.x + (size_t)(t0 + min(i, nt - 1)) * d)[c];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int m = 0; m < ROUTER_MAXC; ++m) {
+                if (c0 + lane + 64 * m < nchunk) {
+#pragma unroll
+                    for (int q = 0; q < EPW; ++q) {
+                        const uint32_t ww[4] = {w[q][m].x, w[q][m].y, w[q][m].z, w[q][m].w};
+#pragma unroll
+                        for (int i = 0; i < TPW; ++i) {
+                            const uint32_t xx[4] = {xv[i][m].x, xv[i][m].y, xv[i][m].z, xv[i][m].w};
+                            float s = acc[q][i];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                s = __builtin_fmaf(bf16lo(xx[r]), bf16lo(ww[r]), s);
+                                s = __builtin_fmaf(bf16hi(xx[r]), bf16hi(ww[r]), s);
+                            }
+                            acc[q][i] = s;
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < EPW; ++q)
+#pragma unroll
+            for (int i = 0; i < TPW; ++i) {
+                float s = sum_lanes<64>(acc[q][i]);   // lanes 48..63 hold the total
+                const int e = e0 + q;
+                if (lane == 63 && i < nt && e < rows) {
+                    if (a.bias && e < a.E) s = s + a.bias[e];
+                    if (TAIL) store_agent(&a.logits[(size_t)(t0 + i) * rows + e], s);
+                    else a.logits[(size_t)(t0 + i) * rows + e] = s;
+                }
+            }
+    }
+    if (!TAIL) return;
+    // the last block of this token group runs the tail
+    __shared__ int s_last;
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(&a.counters[blockIdx.y], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == nbx - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const bool grouping = a.grp.counts != nullptr;
+    const int k = a.k, ws = a.k + a.S;
+    for (int i = wave; i < nt; i += ROUTER_WAVES) {
+        const int t = t0 + i;
+        const float* lrow = a.logits + (size_t)t * rows;
+        uint32_t id;
+        float w;
+        wave_topk_lanes([&](int ee) { return load_agent(lrow + ee); }, a.E, k, a.norm, a.scale, k, &id, &w);
+        if (lane < k) {
+            if (grouping && !a.S) store_agent(&a.idx[(size_t)t * k + lane], (int32_t)id);
+            else a.idx[(size_t)t * k + lane] = (int32_t)id;
+            a.wts[(size_t)t * k + lane] = w;
+        }
+        if (a.S) {   // merged slot list: the k routed slots, then the S shared experts E .. E + S - 1
+            const float g = a.gate ? 1.f / (1.f + expf(-load_agent(lrow + a.E))) : 1.f;
+            if (lane < ws) {
+                const int32_t sid = lane < k ? (int32_t)id : a.E + lane - k;
+                if (grouping) store_agent(&a.sidx[(size_t)t * ws + lane], sid);
+                else a.sidx[(size_t)t * ws + lane] = sid;
+                a.swts[(size_t)t * ws + lane] = lane < k ? w : g;
+            }
+        }
+    }
+    if (threadIdx.x == 0) a.counters[blockIdx.y] = 0;
+    if (!grouping) return;
+    // the last token group to finish groups every slot (its ids pass by agent-scope stores and loads, as the logits)
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int ng = gridDim.y;
+        const int old = __hip_atomic_fetch_add(&a.counters[ng], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == ng - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    extern __shared__ int32_t sm[];
+    const int32_t* ids = a.S ? a.sidx : a.idx;
+    group_block([&](int p) { return load_agent(ids + p); }, a.T * ws, a.E + a.S, a.grp, a.P, a.P2, sm, a.mw);
+    if (threadIdx.x == 0) a.counters[gridDim.y] = 0;
+}
+
+// Router tail on given logits [T, E] (fp32, bf16 or fp16): one wave per token.
+template <typename LT>
+__global__ void __launch_bounds__(256)
+topk_kernel(const LT* __restrict__ logits, int T, int E, int k, int norm, float scale, int32_t* __restrict__ idx,
+            float* __restrict__ wts) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const LT* lrow = logits + (size_t)t * E;
+    wave_topk([&](int ee) { return to_f32<LT>(lrow[ee]); }, E, k, norm, scale, idx + (size_t)t * k,
+              wts + (size_t)t * k);
+}
+
+// Stable slot grouping by expert in a launch of its own (group_block): one block.
+__global__ void __launch_bounds__(1024)
+group_slots(const int32_t* __restrict__ idx, int n, int E, GroupBufs o, int P, int P2, int mw) {
+    extern __shared__ int32_t sm[];
+    group_block([&](int p) { return idx[p]; }, n, E, o, P, P2, sm, mw);
 }
 
 // shared experts: token t's slot list is its k routed slots (copied from ridx / rwts [T, k]; none when k = 0)
@@ -362,36 +399,72 @@ shared_route(const void* __restrict__ x, int xdt, const uint16_t* __restrict__ g
 }
 
 // ------------------------------------------------------------------------------------ host launchers
-int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
-                  float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st) {
-    if (T == 1) {   // one expert per wave (fewer, larger waves measured slower)
-        constexpr int EPW = 1;
-        dim3 grid((E + ROUTER_WAVES * EPW - 1) / (ROUTER_WAVES * EPW), 1);
-        router_logits_topk<1, EPW><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, k, norm, scale, logits,
-                                                                        idx, wts, counters);
+// The router groups the slots in its own launch (its last block) when its LDS holds what the grouping needs; every
+// router block reserves that LDS, so more than ROUTER_GROUP_LDS would cost the logit blocks occupancy. Either the ids
+// and one count array per wave (the 4 waves place the slots in parallel), or, for many experts and up to
+// ROUTER_GROUP_WAVE0 slots, the counts and cursors only (wave 0 places every slot). Larger calls group in a launch
+// of their own (launch_group, up to 16 waves).
+constexpr size_t ROUTER_GROUP_LDS = 16 * 1024;
+constexpr int ROUTER_GROUP_WAVE0 = 2048;
+
+size_t route_group_lds(int n, int E, int* mw) {
+    const size_t per_wave = ((size_t)ROUTER_WAVES * E + (size_t)n) * 4;
+    if (per_wave <= ROUTER_GROUP_LDS) {
+        *mw = 1;
+        return per_wave;
+    }
+    *mw = 0;
+    return n <= ROUTER_GROUP_WAVE0 && (size_t)E * 8 <= ROUTER_GROUP_LDS ? (size_t)E * 8 : 0;
+}
+
+bool route_groups_inline(int n, int E) {
+    int mw;
+    return route_group_lds(n, E, &mw) > 0;
+}
+
+int route_groups_max_slots(int E) {
+    const long n = (long)(ROUTER_GROUP_LDS / 4) - (long)ROUTER_WAVES * E;
+    const long w0 = (size_t)E * 8 <= ROUTER_GROUP_LDS ? ROUTER_GROUP_WAVE0 : 0;
+    return (int)(n > w0 ? n : w0);
+}
+
+int launch_route(RouterArgs a, bool tail, hipStream_t st) {
+    size_t lds = 0;
+    if (tail && a.grp.counts) {
+        lds = route_group_lds(a.T * (a.k + a.S), a.E + a.S, &a.mw);
+        if (!lds) return MOE_ERR_ARG;
+    }
+    // T == 1: one expert per wave and token (fewer, larger waves, or one wave per workgroup spread over E CUs,
+    // measured no faster); T > 1: ROUTER_TPW tokens per wave share each loaded Wr chunk
+    const dim3 grid((a.lstride + ROUTER_WAVES - 1) / ROUTER_WAVES, a.T == 1 ? 1 : (a.T + ROUTER_TPW - 1) / ROUTER_TPW);
+    if (a.T == 1) {
+        if (tail) router_kernel<1, 1, true><<<grid, 64 * ROUTER_WAVES, lds, st>>>(a);
+        else router_kernel<1, 1, false><<<grid, 64 * ROUTER_WAVES, 0, st>>>(a);
     } else {
-        dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, (T + ROUTER_TPW - 1) / ROUTER_TPW);
-        router_logits_topk<ROUTER_TPW, 1><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, k, norm, scale,
-                                                                               logits, idx, wts, counters);
+        if (tail) router_kernel<ROUTER_TPW, 1, true><<<grid, 64 * ROUTER_WAVES, lds, st>>>(a);
+        else router_kernel<ROUTER_TPW, 1, false><<<grid, 64 * ROUTER_WAVES, 0, st>>>(a);
     }
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+
+int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
+                  float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st) {
+    RouterArgs a{};
+    a.x = x, a.wr = wr, a.bias = bias, a.T = T, a.d = d, a.E = E, a.k = k, a.norm = norm, a.scale = scale;
+    a.logits = logits, a.lstride = E, a.idx = idx, a.wts = wts, a.counters = counters;
+    return launch_route(a, true, st);
 }
 
 int launch_router_logits(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, float* logits,
                          hipStream_t st) {
-    if (T == 1) {   // one expert per wave (one wave per workgroup, spread over E CUs, measured no faster)
-        dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, 1);
-        router_logits_topk<1, 1, false><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, 1, 1, 1.f, logits,
-                                                                             nullptr, nullptr, nullptr);
-    } else {
-        dim3 grid((E + ROUTER_WAVES - 1) / ROUTER_WAVES, (T + ROUTER_TPW - 1) / ROUTER_TPW);
-        router_logits_topk<ROUTER_TPW, 1, false><<<grid, 64 * ROUTER_WAVES, 0, st>>>(x, wr, bias, T, d, E, 1, 1, 1.f,
-                                                                                      logits, nullptr, nullptr, nullptr);
-    }
-    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+    RouterArgs a{};
+    a.x = x, a.wr = wr, a.bias = bias, a.T = T, a.d = d, a.E = E, a.k = 1, a.norm = 1, a.scale = 1.f;
+    a.logits = logits, a.lstride = E;
+    return launch_route(a, false, st);
 }
 
-int router_counter_slots(int T) { return (T + ROUTER_TPW - 1) / ROUTER_TPW; }
+// token groups + the grouping's counter
+int router_counter_slots(int T) { return (T + ROUTER_TPW - 1) / ROUTER_TPW + 1; }
 
 int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
                 hipStream_t st) {
@@ -425,8 +498,8 @@ int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* off
     const size_t mw_bytes = ((size_t)nw * E + (size_t)n) * sizeof(int32_t);
     const int mw = mw_bytes <= 64 * 1024 ? 1 : 0;
     if (!mw) nw = 4;
-    group_slots<<<1, 64 * nw, mw ? mw_bytes : 2 * E * sizeof(int32_t), st>>>(idx, n, E, counts, offsets, sorted,
-                                                                              active, meta, P, items, P2, items2, mw);
+    const GroupBufs o{counts, offsets, sorted, active, meta, items, items2};
+    group_slots<<<1, 64 * nw, mw ? mw_bytes : 2 * E * sizeof(int32_t), st>>>(idx, n, E, o, P, P2, mw);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 

@@ -1890,10 +1890,6 @@ int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st, int 
 // Environment knobs, read per call (tuning and tests): MOE_DENSE = 0 turns the dense tiles off (the LDS-staged
 // row tiles take the calls with more than 32 tokens per expert), 1 uses them for every such call, unset chooses
 // by grid size; MOE_WAVE_NT = 1 or 2 forces the wave tiles' token tiles per pass.
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
 
 // K parts of the dense down projection: 2 when the row blocks x passes would leave the chip under-filled (the
 // combine adds the parts' planes); gate/up is never split (the GLU needs whole sums)
@@ -1924,30 +1920,26 @@ int launch_dense(TileArgs t, int nslots, hipStream_t st) {
 #define MOE_DENSE_MIN_BLOCKS 256   // dense gate/up blocks below which the wave tiles fill the chip better
 #endif
 
+// The kernels a grouped call runs, from (w, T, k, x dtype) and the tuning environment only, so separately launched
+// stages (and the router, which writes the pass lists in moe_layer_run) agree on the layout of h and the passes.
+// Tile-major weights present: wave tiles for few tokens per expert, dense tiles for many (unless their grid would fill
+// only part of the chip, e.g. a few shared experts: then the wave tiles, 32-token passes). int4 takes the dense down
+// from fewer tokens per expert than the dense gate/up (the down's wave tiles read two h planes per token while the
+// dense down shares its 64 tokens' h16 across a block): mid loads run the wave gate/up (h out as h16) and the dense
+// down, on two pass lists.
+struct Plan {
+    bool tiled, dense_gu, dense_dn, mxd, wave_gu, wave_dn, mxw, h16, two_lists, ingroup;
+    int nt, P_gu, P_dn;
+};
+
 template <class FMT>
-int run_tiles_fmt(const ExpertsArgs& a) {
-    const moe_experts_t* w = a.w;
-    const int nslots = a.T * a.k;
-    const int max_active = nslots < w->E ? nslots : w->E;
+Plan make_plan(const moe_experts_t* w, int T, int k, int x_dtype) {
+    Plan p{};
+    const int nslots = T * k;
     const int avg = (nslots + w->E - 1) / w->E;   // expected slots per active expert (uniform routing)
-    TileArgs t{};
-    t.ksplit = 1;
-    t.counts = a.grp.counts;
-    t.offsets = a.grp.offsets;
-    t.sorted = a.grp.sorted;
-    t.active = a.grp.active;
-    t.meta = a.grp.meta;
-    t.E = w->E;
-    t.act = a.act;
-    t.kslots = a.k;
-    // tile-major weights present: wave tiles for few tokens per expert, dense tiles for many (unless their grid
-    // would fill only part of the chip, e.g. a few shared experts: then the wave tiles, 32-token passes). int4
-    // takes the dense down from fewer tokens per expert than the dense gate/up (the down's wave tiles read two h
-    // planes per token while the dense down shares its 64 tokens' h16 across a block): mid loads run the wave
-    // gate/up (h out as h16) and the dense down, on two pass lists. The choices depend on (T, k, E, d, F) only,
-    // so separately launched stages agree on the layout of h.
+    const int nx = x_dtype == MOE_DTYPE_BF16 ? 1 : (x_dtype == MOE_DTYPE_F16 ? 2 : 3);
     constexpr bool INT4 = FmtInt4::FMT == FMT::FMT;
-    const bool tiled = w->gate.tiles && w->up.tiles && w->down.tiles;
+    p.tiled = w->gate.tiles && w->up.tiles && w->down.tiles;
     const int dmode = env_int("MOE_DENSE", -1);
     constexpr int DP_GU = 16 * dense_nt<FMT, 2>(), DP_DN = 16 * dense_nt<FMT, 1>();
     constexpr int BN_GU = dense_bn<FMT, 2>(), BN_DN = dense_bn<FMT, 1>();
@@ -1958,37 +1950,65 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     // activations as planes (fp16 / fp32 x): the dense gate/up takes only what it reads exactly, int4 with fp16 x
     // (x16); fp32 x and MXFP4 keep the exact-operand wave / row tiles, one 16-token tile per pass (nt = 1: the
     // planes' activation registers)
-    const bool dense_gu_x = INT4 ? a.x_dtype != MOE_DTYPE_F32 : a.nx == 1;
-    const bool dense_gu = dense_gu_x && tiled && avg > min_avg &&
-                          (dmode == 1 || (dmode < 0 && dblocks >= MOE_DENSE_MIN_BLOCKS));
-    const bool dense_dn = dense_gu || (INT4 && tiled && dmode != 0 && avg > dn_min_avg &&
-                                       (dmode == 1 || dn_blocks >= MOE_DENSE_MIN_BLOCKS));
+    const bool dense_gu_x = INT4 ? x_dtype != MOE_DTYPE_F32 : nx == 1;
+    p.dense_gu = dense_gu_x && p.tiled && avg > min_avg &&
+                 (dmode == 1 || (dmode < 0 && dblocks >= MOE_DENSE_MIN_BLOCKS));
+    p.dense_dn = p.dense_gu || (INT4 && p.tiled && dmode != 0 && avg > dn_min_avg &&
+                                (dmode == 1 || dn_blocks >= MOE_DENSE_MIN_BLOCKS));
     // MXFP4 with bf16 x on the dense tiles: the block-scaled MFMA kernels instead (MOE_MXMFMA=0: the bf16-MFMA
     // dense tiles). x's terms go to the x-planes region, h's terms to the yp planes the split down would use; both
     // must fit there, with 32-bit record offsets
-    const size_t mx_xb = (size_t)a.T * ((w->d + 127) / 128) * mx_rec<2>();
+    const size_t mx_xb = (size_t)T * ((w->d + 127) / 128) * mx_rec<2>();
     const size_t mx_hb = (size_t)nslots * ((w->F + 127) / 128) * mx_rec<3>();
-    const bool mx_fit = !INT4 && a.nx == 1 && env_int("MOE_MXMFMA", 1) && a.xterm && mx_xb <= (size_t)6 * a.T * w->d &&
+    const bool mx_fit = !INT4 && nx == 1 && env_int("MOE_MXMFMA", 1) && mx_xb <= (size_t)6 * T * w->d &&
                         mx_hb <= (size_t)12 * nslots * w->d && mx_hb < (1ull << 32);
-    const bool mxd = mx_fit && dense_gu && w->F % (16 * mxd_rt<2>()) == 0 && w->d % (16 * mxd_rt<1>()) == 0;
-    const bool wave_gu = tiled && !dense_gu && (avg <= min_avg || dmode != 0);
-    const bool wave_dn = tiled && !dense_dn && (avg <= min_avg || dmode != 0);
+    p.mxd = mx_fit && p.dense_gu && w->F % (16 * mxd_rt<2>()) == 0 && w->d % (16 * mxd_rt<1>()) == 0;
+    p.wave_gu = p.tiled && !p.dense_gu && (avg <= min_avg || dmode != 0);
+    p.wave_dn = p.tiled && !p.dense_dn && (avg <= min_avg || dmode != 0);
     // the wave tiles of MXFP4 with bf16 x on the block-scaled MFMA too (terms as for the dense kernels)
-    const bool mxw = mx_fit && wave_gu && wave_dn;
-    const bool h16 = INT4 && dense_dn;   // h leaves the gate/up as h16 with per-32-row exponents
+    p.mxw = mx_fit && p.wave_gu && p.wave_dn;
+    p.h16 = INT4 && p.dense_dn;   // h leaves the gate/up as h16 with per-32-row exponents
     const int wnt = env_int("MOE_WAVE_NT", 0);
-    const int nt = a.nx > 1 ? 1
-                 : (wave_gu || wave_dn) ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2))
-                                        : tokens_per_pass_tiles(a.T, a.k, w->E);
+    p.nt = nx > 1 ? 1
+         : (p.wave_gu || p.wave_dn) ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2))
+                                    : tokens_per_pass_tiles(T, k, w->E);
     // pass lists: 16 nt tokens per pass for the wave tiles, DP_GU / DP_DN for the dense tiles; a second list
     // when the two stages take different kernels
-    const int P_gu = dense_gu ? DP_GU : 16 * nt, P_dn = dense_dn ? DP_DN : 16 * nt;
-    const bool two_lists = P_gu != P_dn;
+    p.P_gu = p.dense_gu ? DP_GU : 16 * p.nt;
+    p.P_dn = p.dense_dn ? DP_DN : 16 * p.nt;
+    p.two_lists = p.P_gu != p.P_dn;
+    // both stages on the wave tiles with few slots: each workgroup can find its pass from the raw ids itself (an LDS
+    // histogram and a wave scan, the grouping launch's order), so the call needs no grouping launch
+    p.ingroup = p.wave_gu && p.wave_dn && nslots <= 64 * GW_MAXJ && w->E <= 1024 && env_int("MOE_INGROUP", 1);
+    return p;
+}
+
+template <class FMT>
+int run_tiles_fmt(const ExpertsArgs& a) {
+    const moe_experts_t* w = a.w;
+    const int nslots = a.T * a.k;
+    const int max_active = nslots < w->E ? nslots : w->E;
+    TileArgs t{};
+    t.ksplit = 1;
+    t.counts = a.grp.counts;
+    t.offsets = a.grp.offsets;
+    t.sorted = a.grp.sorted;
+    t.active = a.grp.active;
+    t.meta = a.grp.meta;
+    t.E = w->E;
+    t.act = a.act;
+    t.kslots = a.k;
+    constexpr bool INT4 = FmtInt4::FMT == FMT::FMT;
+    constexpr int BN_DN = dense_bn<FMT, 1>(), DP_DN = 16 * dense_nt<FMT, 1>();
+    const Plan pl = make_plan<FMT>(w, a.T, a.k, a.x_dtype);
+    const bool dense_gu = pl.dense_gu, dense_dn = pl.dense_dn, mxd = pl.mxd && a.xterm, wave_gu = pl.wave_gu,
+               wave_dn = pl.wave_dn, mxw = pl.mxw && a.xterm, h16 = pl.h16, two_lists = pl.two_lists;
+    const int nt = pl.nt, P_gu = pl.P_gu, P_dn = pl.P_dn;
+    if ((pl.mxd || pl.mxw) && !a.xterm) return MOE_ERR_ARG;
     t.items = a.grp.items;
     t.nidx = 2;
-    // both stages on the wave tiles with few slots: each workgroup finds its pass from the raw ids itself (an LDS
-    // histogram and a wave scan, the grouping launch's order), so the call has no grouping launch
-    if (wave_gu && wave_dn && nslots <= 64 * GW_MAXJ && w->E <= 1024 && env_int("MOE_INGROUP", 1)) {
+    // in-kernel grouping unless the router already wrote the grouping and pass lists
+    if (pl.ingroup && !a.pregrouped) {
         t.gidx = a.idx;
         t.gn = nslots;
         // the compact pass list by default: its live passes come first in dispatch order whatever the skew. The
@@ -2003,8 +2023,9 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         if (t.eslot_off + (size_t)nslots * 4 > (size_t)nslots * w->F * 2) return MOE_ERR_ARG;
     }
     if (a.stages & 1) {
-        int rc = t.gidx ? 0
-                        : launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
+        int rc = t.gidx || a.pregrouped
+                     ? 0
+                     : launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
                                        a.grp.meta, a.st, P_gu, a.grp.items, two_lists ? P_dn : 0,
                                        two_lists ? a.grp.items2 : nullptr);
         if (rc) return rc;
@@ -2104,6 +2125,11 @@ int run_tiles_fmt(const ExpertsArgs& a) {
 
 int run_experts_tiles(const ExpertsArgs& a) {
     return a.w->fmt == MOE_FMT_INT4_G64 ? run_tiles_fmt<FmtInt4>(a) : run_tiles_fmt<FmtMxfp4>(a);
+}
+
+TilePasses tile_passes(const moe_experts_t* w, int T, int k, int x_dtype) {
+    const Plan p = w->fmt == MOE_FMT_INT4_G64 ? make_plan<FmtInt4>(w, T, k, x_dtype) : make_plan<FmtMxfp4>(w, T, k, x_dtype);
+    return TilePasses{p.P_gu, p.two_lists ? p.P_dn : 0, p.ingroup ? 1 : 0};
 }
 
 int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tiles, hipStream_t st) {

@@ -85,6 +85,34 @@ def test_router_argument_errors():
     assert L.moe_group(p, 4, 0, p, p, p, p, p, None) == -1                              # E < 1
 
 
+def test_router_group_and_layer_argument_errors():
+    """moe_router_group's in-launch grouping limit and the layer calls' counters / shared-expert checks, before any
+    launch."""
+    from moelab_amd import _lib
+    L = _lib.lib()
+    p = ctypes.c_void_p(4096)
+    assert L.moe_router_group_max_slots(128) == 4096 - 4 * 128
+    assert L.moe_router_group_max_slots(1000) == 2048 and L.moe_router_group_max_slots(0) == 0
+    args = (p, p, p, p, p, p, p, p, p)
+    assert L.moe_router_group(p, p, None, 449, 2048, 128, 8, 1, 1.0, *args, None) == -1   # 3592 slots > 3584
+    assert L.moe_router_group(p, p, None, 4, 2048, 128, 33, 1, 1.0, *args, None) == -1    # k > 32
+    assert L.moe_router_group(p, p, None, 4, 2048, 128, 8, 1, 1.0, p, p, p, None, p, p, p, p, p, None) == -1
+    assert L.moe_router_counter_count(1) == 2 and L.moe_router_counter_count(32) == 9
+    w = _desc(E=10, d=128, F=128)
+    ws = ctypes.c_void_p(8192)
+    # no counters
+    assert L.moe_layer_run(w, p, 0, p, None, 4, 2, 1, 1.0, 0, p, p, p, 0, None, None, ws, 1 << 30, None) == -1
+    # fp16 x: the router reads bf16
+    assert L.moe_layer_run(w, p, 1, p, None, 4, 2, 1, 1.0, 0, p, p, p, 0, None, p, ws, 1 << 30, None) == -2
+    # S = 0, S >= E, k + S > 64
+    for S, k in ((0, 2), (10, 2), (8, 60)):
+        assert L.moe_layer_run_shared(w, S, p, 0, p, None, None, 4, k, 1, 1.0, 0, p, p, p, 0, None, p, ws, 1 << 30,
+                                      None) == -1
+    assert L.moe_layer_shared_workspace_bytes(w, 2, 4, 2) > L.moe_layer_workspace_bytes(_desc(E=8), 4, 4) > 0
+    assert L.moe_layer_run_shared(w, 2, p, 0, p, None, None, 4, 2, 1, 1.0, 0, p, p, p, 0, None, p, ws, 100,
+                                  None) == -3
+
+
 def test_tile_bytes_and_pack_argument_errors():
     from moelab_amd import _lib
     L = _lib.lib()

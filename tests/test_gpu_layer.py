@@ -101,3 +101,89 @@ def test_layer_ties_across_logit_groups(E):
     print(f"case layer ties across groups E={E}", flush=True)
     idx = check_layer(s, x, wr, sh.k, what=("tiesJ", E))
     assert idx.cpu().numpy()[0, :3].tolist() == [9, 67, E - 50]
+
+
+@pytest.mark.parametrize("T,dist", [(32, "uniform"), (32, "zipf"), (64, "zipf"), (16, "uniform")])
+def test_layer_batched_router_builds_grouping(T, dist, monkeypatch):
+    """BASELINE config 3 through moe_layer_run: one router launch (logits, tail, slot grouping and pass lists), then
+    the wave tiles reading those lists; bit-identical to route + the experts call (which groups in-kernel), and the
+    same again with MOE_LAYER_INGROUP=1 (the router leaves the grouping to the wave tiles)."""
+    from moelab_amd.experts import run_routed
+    from moelab_amd.problem import baseline_int4_layer, baseline_x, zipf_bias
+    from moelab_amd.shapes import SHAPES
+    sh = SHAPES["qwen3-30b-a3b"]
+    s = baseline_int4_layer(sh, seed=90 + T, device=DEV)
+    x = baseline_x(T, sh.d, seed=T, device=DEV)
+    bias = torch.from_numpy(zipf_bias(sh.E, 1.1, seed=3)).to(DEV) if dist == "zipf" else None
+    print(f"case layer batched T={T} {dist}", flush=True)
+    check_layer(s, x, s["wr"], sh.k, bias=bias, what=("qwen3", T, dist))
+    y, _, _ = run_routed(s, x, s["wr"], sh.k, bias=bias, out_dtype=torch.float32)
+    monkeypatch.setenv("MOE_LAYER_INGROUP", "1")
+    y2, _, _ = run_routed(s, x, s["wr"], sh.k, bias=bias, out_dtype=torch.float32)
+    assert torch.equal(y, y2)
+
+
+def _shared_layer(fmt, d, F, E, k, S, seed, gated):
+    from moelab_amd import formats
+    from moelab_amd.experts import make_state, merge_shared
+    from moelab_amd.problem import baseline_int4_layer, baseline_mxfp4_layer
+    from moelab_amd.shapes import MoEShape
+    sh = MoEShape("m", d=d, f=F, E=E, k=k)
+    s = baseline_int4_layer(sh, seed, DEV) if fmt == "int4" else baseline_mxfp4_layer(sh, seed, DEV)
+    g = torch.Generator(device=DEV).manual_seed(seed + 1)
+    rnd = formats.random_int4 if fmt == "int4" else formats.random_mxfp4
+    s["shared"] = make_state(fmt, rnd(S, F, d, generator=g, device=DEV), rnd(S, F, d, generator=g, device=DEV),
+                             rnd(S, d, F, generator=g, device=DEV))
+    if gated:
+        s["shared_gate"] = (torch.randn(d, generator=g, device=DEV) * 0.05).to(torch.bfloat16)
+    return sh, s, merge_shared(s)
+
+
+SHARED_CASES = [
+    # (fmt, d, F, E, k, S, T, gated, norm, scale)
+    ("int4", 512, 256, 16, 4, 2, 1, False, True, 1.0),      # T = 1: per-slot GEMV over k + S slots
+    ("int4", 512, 256, 16, 4, 2, 7, True, True, 1.0),       # gated (Qwen-style), wave tiles
+    ("int4", 512, 384, 64, 6, 2, 256, False, False, 1.0),   # DeepSeek-V2 greedy: full softmax, dense down
+    ("int4", 256, 256, 16, 4, 1, 300, True, False, 2.5),    # 1500 slots, 300 on the shared expert: dense tiles
+    ("mxfp4", 512, 512, 8, 2, 2, 40, True, True, 1.0),      # MXFP4, block-scaled wave tiles
+]
+
+
+@pytest.mark.parametrize("case", SHARED_CASES, ids=lambda c: f"{c[0]}-E{c[3]}k{c[4]}S{c[5]}-T{c[6]}-{'g' if c[7] else 'u'}")
+def test_layer_shared_router_builds_grouping(case):
+    """moe_layer_run_shared: the router launch also computes the shared gate (one more logit row in the same fixed
+    order), writes the merged [T, k + S] slot lists and groups them; the experts follow as moe_experts_run_shared.
+    Bit-identical to route + run_experts_shared on the same ids, and within the gate of the oracle's routed +
+    shared sum."""
+    from moelab_amd import router
+    from moelab_amd.experts import run_experts_shared, run_routed
+    from moelab_amd.problem import baseline_x
+    fmt, d, F, E, k, S, T, gated, norm, scale = case
+    sh, s, m = _shared_layer(fmt, d, F, E, k, S, seed=100 + T, gated=gated)
+    x = baseline_x(T, d, seed=T + 5, device=DEV)
+    act = 0   # SwiGLU: the oracle's shared experts are SwiGLU MLPs (no model pairs gpt-oss's act with them)
+    print(f"case layer shared {case}", flush=True)
+    y, idx, wts = run_routed(m, x, s["wr"], k, norm=norm, scale=scale, act=act, out_dtype=torch.float32)
+    i2, w2 = router.route(x, s["wr"], k, norm=norm, scale=scale)
+    y2 = run_experts_shared(m, x, i2, w2, act=act, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    idx_ref, wts_ref = orc.topk(orc.router_logits(np_u16(x), np_u16(s["wr"])), k, norm=norm, scale=scale)
+    assert np.array_equal(idx.cpu().numpy(), idx_ref)
+    assert torch.equal(idx, i2) and torch.equal(wts, w2)
+    assert torch.equal(y, y2), float((y - y2).abs().max())
+    assert_close(y, oracle_y(s, x, idx, wts, act), what=case)
+    # the state with separate shared experts: router + routed experts in one call, the shared ones in a second
+    y3, _, _ = run_routed(s, x, s["wr"], k, norm=norm, scale=scale, act=act, out_dtype=torch.float32)
+    assert_close(y3, oracle_y(s, x, idx, wts, act), what=case)
+
+
+def test_layer_grouping_beyond_router_lds():
+    """4096 slots over 8 experts exceed what the router's last workgroup groups in LDS: the router runs the tail only
+    and the grouping runs as a launch of its own; results as the separate calls."""
+    from moelab_amd.problem import baseline_int4_layer, baseline_x
+    from moelab_amd.shapes import MoEShape
+    sh = MoEShape("big", d=128, f=128, E=8, k=2)
+    s = baseline_int4_layer(sh, seed=12, device=DEV)
+    x = baseline_x(2048, sh.d, seed=12, device=DEV)
+    print("case layer 4096 slots", flush=True)
+    check_layer(s, x, s["wr"], sh.k, what="big")

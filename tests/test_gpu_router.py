@@ -121,3 +121,55 @@ def test_group_rejects_out_of_range_ids():
     assert meta.cpu().numpy()[1] == 2
     assert counts.cpu().numpy().tolist() == [1, 0, 0, 2, 0, 1, 0, 0]
     assert srt.cpu().numpy()[:4].tolist() == [0, 2, 5, 1]
+
+
+@pytest.mark.parametrize("T,E,k,d,mode", [(1, 128, 8, 2048, "plain"), (32, 128, 8, 2048, "plain"),
+                                          (32, 128, 8, 2048, "zipf"), (64, 128, 8, 2048, "ties"),
+                                          (256, 64, 6, 2048, "plain"), (512, 8, 2, 4096, "plain"),
+                                          (448, 128, 8, 256, "zipf"), (7, 1000, 8, 256, "plain"),
+                                          (64, 1024, 32, 64, "ties"), (33, 16, 16, 128, "plain")])
+def test_route_group_bit_exact(T, E, k, d, mode):
+    """moe_router_group: the router launch also sorts the slots by expert (its last workgroup, a wave prefix sum of
+    the counts). Ids and logits bit-exact against the oracle, the grouping equal to the oracle's stable argsort
+    (reference triton_fused_moe.py:56-70) and to the separate route + group launches. (448, 128, 8): 3584 slots,
+    the largest the 4-wave form takes at E = 128; E = 1000 and 1024 take the one-wave form; "ties": every router row
+    equal, so every token picks experts 0..k-1 and all slots fall on k experts."""
+    from moelab_amd import router
+    x, wr, b = _router_inputs(T, d, E, seed=T * 3 + E + k, bias=mode == "zipf")
+    if mode == "ties":
+        wr = torch.full_like(wr, 0.0078125)
+    print(f"case route_group T={T} E={E} k={k} {mode}", flush=True)
+    idx, wts, logits, (counts, offsets, srt, active, meta) = router.route_group(x, wr, k, bias=b)
+    lg_ref = orc.router_logits(np_u16(x), np_u16(wr), None if b is None else b.cpu().numpy())
+    np.testing.assert_array_equal(logits.cpu().numpy().view(np.uint32), lg_ref.view(np.uint32))
+    idx_ref, wts_ref = orc.topk(lg_ref, k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), idx_ref)
+    np.testing.assert_allclose(wts.cpu().numpy(), wts_ref, rtol=1e-6, atol=1e-7)
+    c, o, s, a = orc.group(idx_ref, E)
+    np.testing.assert_array_equal(counts.cpu().numpy(), c)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), o)
+    np.testing.assert_array_equal(srt.cpu().numpy(), s)
+    m = meta.cpu().numpy()
+    assert m[0] == len(a) and m[1] == 0
+    np.testing.assert_array_equal(active.cpu().numpy()[:len(a)], a)
+    assert (active.cpu().numpy()[len(a):] == -1).all()
+    i2, w2 = router.route(x, wr, k, bias=b)
+    g2 = router.group(i2, E)
+    assert torch.equal(idx, i2) and torch.equal(wts, w2)
+    for u, v in zip((counts, offsets, srt, active), g2[:4]):
+        assert torch.equal(u, v)
+    if mode == "ties":
+        assert (idx.cpu().numpy() == np.arange(k)).all()
+
+
+def test_route_group_repeated_calls_and_limit():
+    """Both counter levels are left at zero (20 calls in a row agree), and a call past the in-launch limit raises."""
+    from moelab_amd import router
+    x, wr, _ = _router_inputs(40, 512, 64, seed=2)
+    first = router.route_group(x, wr, 6)
+    for _ in range(20):
+        again = router.route_group(x, wr, 6)
+        assert torch.equal(first[0], again[0]) and torch.equal(first[3][2], again[3][2])
+    x2, wr2, _ = _router_inputs(449, 64, 128, seed=3)
+    with pytest.raises(ValueError):
+        router.route_group(x2, wr2, 8)
