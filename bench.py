@@ -88,6 +88,9 @@ def main():
     ap.add_argument("--only-configs", default="", metavar="NAMES",
                     help="comma list of BASELINE config names (e.g. mixtral8x7b_int4_T512): run only those and print "
                          "their results (for profiling runs; not the bench line)")
+    ap.add_argument("--routed-only", action="store_true",
+                    help="with --only-configs: time only the chains with the router inside each layer call (for "
+                         "kernel traces of the routed layer)")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MIB",
                     help="finish with 3 device copies of MIB MiB (the plain-copy reference for --pmc traffic runs)")
     args = ap.parse_args()
@@ -173,16 +176,7 @@ def main():
     batched = {}
     routes_b = {}
     if not args.no_t32:
-        for T in (16, 32, 64):
-            for dist in ("uniform", "zipf"):
-                xT = baseline_x(T, sh.d, seed=T, device=dev)
-                bias = torch.from_numpy(zipf_bias(sh.E, 1.1, seed=3)).to(dev) if dist == "zipf" else None
-                routes = [router.route(xT, ly["wr"], sh.k, bias=bias) for ly in layers]
-                routes_b[(T, dist)] = (xT, routes)
-                batched.setdefault(f"T{T}", {})[dist] = r = time_batched(layers, xT, routes, T, sh, args)
-                log(f"T={T} {dist}: grouped {r['us_per_layer_grouped']:.1f} us/layer "
-                    f"({r['weight_GBps_grouped']:.0f} GB/s), per-slot {r['us_per_layer_per_slot']:.1f} us/layer, "
-                    f"speedup {r['speedup_per_token']:.2f}x, U={r['unique_experts_mean']:.1f}")
+        batched = run_batched(dev, layers, sh, args, routes_b=routes_b)
 
     # ------------------------------------------------------------------ BASELINE configs 4, 5a, 5b
     configs = {}
@@ -244,9 +238,67 @@ def main():
     copy_calibrate(dev, args.copy_calibrate)
 
 
-def time_batched(layers, x, routes, T, sh, args):
+def run_batched(dev, layers, sh, args, points=None, routes_b=None):
+    """BASELINE config 3 over the seeded Qwen3 layers: T = 16, 32, 64 with uniform and Zipf(1.1) routing (the Zipf
+    skew is a per-expert router bias); `points` limits it to some (T, dist) pairs."""
+    from moelab_amd import router
+    from moelab_amd.problem import baseline_x, zipf_bias
+    out = {}
+    for T in (16, 32, 64):
+        for dist in ("uniform", "zipf"):
+            if points is not None and (T, dist) not in points:
+                continue
+            xT = baseline_x(T, sh.d, seed=T, device=dev)
+            bias = torch.from_numpy(zipf_bias(sh.E, 1.1, seed=3)).to(dev) if dist == "zipf" else None
+            routes = [router.route(xT, ly["wr"], sh.k, bias=bias) for ly in layers]
+            if routes_b is not None:
+                routes_b[(T, dist)] = (xT, routes)
+            out.setdefault(f"T{T}", {})[dist] = r = time_batched(layers, xT, routes, T, sh, args, bias=bias)
+            log(f"T={T} {dist}: grouped {r['us_per_layer_grouped']:.1f} us/layer "
+                f"({r['weight_GBps_grouped']:.0f} GB/s), per-slot {r['us_per_layer_per_slot']:.1f} us/layer, "
+                f"speedup {r['speedup_per_token']:.2f}x, U={r['unique_experts_mean']:.1f}; with router "
+                f"{r['with_router']['us_per_layer']:.1f} us/layer (router then experts as two calls "
+                f"{r['with_router']['route_then_experts_us']:.1f})")
+    return out
+
+
+def routed_times(layers, x, k, args, bias=None, norm=True, scale=1.0, act=0):
+    """The residual chain with the router inside each layer call (moe_layer_run: the router's launches, which also
+    group the slots, then the expert launches), and the same layers as two calls each (router.route, then the experts
+    call on its ids, which groups the slots itself): seconds per layer of each. Every layer routes and computes from
+    the fixed x and adds to the running sum (y <- y + moe_l(x)), so the routing is the one the expert-only chains use
+    and the layers stay dependent."""
+    from moelab_amd import router
+    from moelab_amd.experts import run_layer, run_routed
+    steps, warm = max(5, args.steps // 5), max(2, args.warmup // 5)
+
+    def one_call():
+        y = x.clone()
+        for ly in layers:
+            y, _, _ = run_routed(ly, x, ly["wr"], k, bias=bias, norm=norm, scale=scale, act=act, residual=y)
+        return y
+
+    def two_calls():
+        y = x.clone()
+        for ly in layers:
+            idx, wts = router.route(x, ly["wr"], k, bias=bias, norm=norm, scale=scale)
+            y = run_layer(ly, x, idx, wts, act=act, residual=y)
+        return y
+    res = []
+    for fn in (one_call, two_calls):
+        if fn is two_calls and getattr(args, "routed_only", False):
+            res.append(float("nan"))
+            continue
+        g, _ = graph_of(fn)
+        res.append(time_graph(g, steps, warm) / len(layers))
+        del g
+    return res
+
+
+def time_batched(layers, x, routes, T, sh, args, bias=None):
     """One BASELINE config 3 point: the 48-layer residual chain on the grouped path and on the per-slot path
-    (graph replays), plus the grouped path's two stages timed alone (x fixed: timing only)."""
+    (graph replays), plus the grouped path's two stages timed alone (x fixed: timing only), and the chain with the
+    router inside each layer call."""
     from moelab_amd import _lib, roofline
     from moelab_amd.experts import run_experts
     L = len(layers)
@@ -270,9 +322,13 @@ def time_batched(layers, x, routes, T, sh, args):
     res = {}
     for name, fn in (("grouped", chain(_lib.PATH_GROUPED)), ("per_slot", chain(_lib.PATH_SLOTS)),
                      ("gate_up", stage(_lib.STAGE_GATE_UP)), ("down", stage(_lib.STAGE_DOWN))):
+        if getattr(args, "routed_only", False):
+            res[name] = float("nan")
+            continue
         g, _ = graph_of(fn)
         res[name] = time_graph(g, steps, warm)
         del g
+    t_one, t_two = routed_times(layers, x, sh.k, args, bias=bias)
     ub = sum(U) * per_expert
     return {
         "T": T,
@@ -288,6 +344,9 @@ def time_batched(layers, x, routes, T, sh, args):
         "down_stage_us": round(res["down"] * 1e6 / L, 2),
         "gate_up_stage_GBps": round(ub * 2 / 3 / res["gate_up"] / 1e9, 1),
         "down_stage_GBps": round(ub / 3 / res["down"] / 1e9, 1),
+        # router inside the layer call: one router launch (logits, tail, grouping), then the expert launches
+        "with_router": {"us_per_layer": round(t_one * 1e6, 2), "weight_GBps": round(ub / L / t_one / 1e9, 1),
+                        "route_then_experts_us": round(t_two * 1e6, 2)},
     }
 
 
@@ -327,11 +386,14 @@ def other_configs(dev, args, only=None, extra=None):
         del g
         return t
 
-    def report(name, sh, fmt, layers, T, act, shared_f=0, bias_bytes=0.0, into=None):
+    def report(name, sh, fmt, layers, T, act, shared_f=0, bias_bytes=0.0, into=None, with_router=True):
         x = baseline_x(T, sh.d, seed=T, device=dev)
         routes = [router.route(x, ly["wr"], sh.k) for ly in layers]
         U = [int(torch.unique(r[0]).numel()) for r in routes]
-        t = chain_time(layers, x, routes, act) / len(layers)
+        t = float("nan") if args.routed_only else chain_time(layers, x, routes, act) / len(layers)
+        t_one = t_two = None
+        if with_router:
+            t_one, t_two = routed_times(layers, x, sh.k, args, act=act)
         per_e = roofline.expert_bytes(sh.d, sh.f, fmt) + bias_bytes
         wb = np.mean(U) * per_e + (roofline.expert_bytes(sh.d, shared_f, fmt) if shared_f else 0.0)
         fl = 6.0 * sh.d * sh.f * T * sh.k + 6.0 * sh.d * shared_f * T
@@ -342,11 +404,26 @@ def other_configs(dev, args, only=None, extra=None):
              "weight_GBps": round(wb / t / 1e9, 1), "TFLOPs": round(fl / t / 1e12, 2),
              "bound": "mfma" if mfma_floor > hbm_floor else "hbm",
              "frac_of_roofline": round(max(hbm_floor, mfma_floor) / t, 4), "layers": len(layers)}
+        if with_router:   # one router launch (logits, tail, grouping) then the expert launches
+            r["with_router"] = {"us_per_layer": round(t_one * 1e6, 2), "route_then_experts_us": round(t_two * 1e6, 2)}
         (out if into is None else into)[name] = r
         log(f"{name}: {r}")
 
     def want(*names):
         return only is None or any(n in only for n in names)
+
+    # config 3 points by name, for profiling runs (`--only-configs qwen3_int4_T32_zipf`); the bench line runs them all
+    pts = {(T, dist) for T in (16, 32, 64) for dist in ("uniform", "zipf")
+           if only is not None and f"qwen3_int4_T{T}_{dist}" in only}
+    if pts:
+        sh = SHAPES["qwen3-30b-a3b"]
+        layers = [baseline_int4_layer(sh, seed=1000 + l, device=dev) for l in range(args.layers)]
+        from moelab_amd.experts import reserve
+        reserve(layers[0], 64, sh.k)
+        router.reserve(dev, 64)
+        out["batched"] = run_batched(dev, layers, sh, args, points=pts)
+        del layers
+        torch.cuda.empty_cache()
 
     # config 4: gpt-oss-20b MXFP4, biases, clamped SwiGLU (act 2), softmax over the top-4
     if want("gptoss20b_mxfp4_T1", "gptoss20b_mxfp4_T32"):
@@ -359,7 +436,8 @@ def other_configs(dev, args, only=None, extra=None):
         # beside the configs (not a BASELINE config): the same layers at a prefill size, where the MXFP4 tiles
         # run on the block-scaled MFMA (64 slots per expert: the dense tiles)
         if extra is not None:
-            report("gptoss20b_mxfp4_T512", sh, "mxfp4", layers, 512, 2, bias_bytes=bias_b, into=extra)
+            report("gptoss20b_mxfp4_T512", sh, "mxfp4", layers, 512, 2, bias_bytes=bias_b, into=extra,
+                   with_router=False)
         del layers
         torch.cuda.empty_cache()
     # config 5a: Mixtral-8x7B int4 T=512

@@ -120,30 +120,26 @@ typedef struct {
  *   idx [T, k] int32, wts [T, k] fp32 out; norm = 1: softmax over the top-k logits (= renormalised
  *   softmax), norm = 0: full-softmax probabilities (DeepSeek-V2 greedy); weights are multiplied by scale.
  *   Ties: lowest expert id. NaN logits count as -inf. Limits: E <= 1024, 1 <= k <= min(E, 32), d % 8 == 0.
- *   counters: int32 [moe_router_counter_count(T)], zero before the first call; every call leaves it zero (the same
- *   array serves moe_router_group and moe_layer_run; calls sharing it must be stream-ordered).
+ *   Two launches: the logits over many workgroups, then the tails, one wave per token. counters: unused (may be NULL; kept, with moe_router_counter_count, so existing callers link
+ *   unchanged).
  */
 int moe_router(const void* x, const void* wr, const float* bias, int T, int d, int E, int k, int norm, float scale,
                float* logits, int32_t* idx, float* wts, int32_t* counters, void* stream);
 int moe_router_counter_count(int T);
 
 /*
- * Fused router that also builds the slot grouping, in one launch: moe_router's logits and tail (the same ids and
- * weights), then the last workgroup to finish sorts the T*k slots p = t*k + j stably by expert, with the counts'
- * offsets from a wave prefix sum. Replaces the stock gate GEMV + router.topk_norm (as moe_router) followed by the
- * grouping prepass of the grouped kernels (reference metal_q4_tiles_v2.py:362-373 MAP kernel order, closed form of
- * reference triton_fused_moe.py:56-70 align()).
+ * Fused router that also builds the slot grouping: moe_router's logits launch, then one launch that runs every token's
+ * tail (one wave per token: the same ids and weights as moe_router), after which the last workgroup to finish sorts
+ * the T*k slots p = t*k + j stably by expert, with the counts' offsets from a wave prefix sum. Replaces the stock gate
+ * GEMV +
+ * router.topk_norm (as moe_router) followed by the grouping prepass of the grouped kernels (reference
+ * metal_q4_tiles_v2.py:362-373 MAP kernel order, closed form of reference triton_fused_moe.py:56-70 align()).
  *   x, wr, bias, T, d, E, k, norm, scale, logits, idx, wts: as moe_router;
  *   counts [E], offsets [E+1], sorted [T*k], active [E], meta [2] int32 out: as moe_group (meta[1] = 0).
- *   counters: int32 [moe_router_counter_count(T)], zero before the first call; every call leaves it zero.
- *   Limit: T*k <= moe_router_group_max_slots(E): what the last workgroup's 16 KB of LDS holds, the ids and one count
- *   array per wave (4096 - 4 E slots: 3584 at E = 128), or for larger E the counts and cursors alone with one wave
- *   placing up to 2048 slots; larger calls return MOE_ERR_ARG (use moe_router then moe_group).
  */
 int moe_router_group(const void* x, const void* wr, const float* bias, int T, int d, int E, int k, int norm,
                      float scale, float* logits, int32_t* idx, float* wts, int32_t* counts, int32_t* offsets,
-                     int32_t* sorted, int32_t* active, int32_t* meta, int32_t* counters, void* stream);
-int moe_router_group_max_slots(int E);
+                     int32_t* sorted, int32_t* active, int32_t* meta, void* stream);
 
 /*
  * Router tail on given logits: reference moelab/router.py:71-80 topk_norm(logits, k, norm).
@@ -228,18 +224,16 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
  *   T == 1: the router launch computes the logits only and every gate/up wave runs the tail over the 128..1024 logits
  *   itself for its own slot (no hand-off between workgroups inside a launch: measured at 1-2 us per round trip on this
  *   part); one wave writes idx / wts.
- *   T > 1: one router launch computes the logits, runs the tail (the last workgroup of each token group) and builds the
- *   slot grouping and the expert kernels' pass lists (the last token group to finish, as moe_router_group), so the
- *   expert launches follow with no top-k or grouping launch. Above moe_router_group_max_slots(E) slots the grouping
- *   runs as a launch of its own after the router.
+ *   T > 1: the router's two launches (as moe_router_group) compute the logits, run the tails and build the slot
+ *   grouping and the expert kernels' pass lists, so the expert launches follow with no top-k or grouping launch of
+ *   their own.
  *   x [T, d] bf16 (MOE_DTYPE_BF16 only: the gate GEMV reads bf16); wr [E, d] bf16, wr_bias [E] fp32 or NULL;
  *   norm, scale: as moe_router; idx [T, k] int32 and wts [T, k] fp32 out (as moe_router's); y, residual, act,
- *   y_dtype: as moe_experts_run. counters: as moe_router (zero before the first call, left zero).
- *   workspace: moe_layer_workspace_bytes(w, T, k) bytes (any contents).
+ *   y_dtype: as moe_experts_run. workspace: moe_layer_workspace_bytes(w, T, k) bytes (any contents).
  */
 int moe_layer_run(const moe_experts_t* w, const void* x, int x_dtype, const void* wr, const float* wr_bias, int T,
                   int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y, int y_dtype,
-                  const void* residual, int32_t* counters, void* workspace, size_t workspace_bytes, void* stream);
+                  const void* residual, void* workspace, size_t workspace_bytes, void* stream);
 size_t moe_layer_workspace_bytes(const moe_experts_t* w, int T, int k);
 
 /*
@@ -248,15 +242,15 @@ size_t moe_layer_workspace_bytes(const moe_experts_t* w, int T, int k);
  * as for moe_experts_run_shared (experts E_r .. E_r + S - 1 the shared ones), wr [E_r, d] routes over the first E_r.
  *   y[t] = residual[t] + sum_j wts[t,j] * expert_{idx[t,j]}(x_t) + g_t * sum_s expert_{E_r + s}(x_t),
  *   g_t = sigmoid(x_t . gate) (gate: bf16 [d], computed by the router launch as one more logit row, in the logits'
- *   fixed order) or 1 when gate is NULL. The router launch writes idx / wts [T, k] (the routed slots), the merged
+ *   fixed order) or 1 when gate is NULL. The router's launches write idx / wts [T, k] (the routed slots), the merged
  *   [T, k + S] slot lists and, at T > 1, their grouping; then the experts as moe_experts_run_shared.
  *   Limits: 1 <= S < E, E_r <= 1024, k <= min(E_r, 32), k + S <= 64.
- *   workspace: moe_layer_shared_workspace_bytes(w, S, T, k) bytes (any contents); counters as moe_layer_run.
+ *   workspace: moe_layer_shared_workspace_bytes(w, S, T, k) bytes (any contents).
  */
 int moe_layer_run_shared(const moe_experts_t* w, int S, const void* x, int x_dtype, const void* wr,
                          const float* wr_bias, const void* gate, int T, int k, int norm, float scale, int act,
-                         int32_t* idx, float* wts, void* y, int y_dtype, const void* residual, int32_t* counters,
-                         void* workspace, size_t workspace_bytes, void* stream);
+                         int32_t* idx, float* wts, void* y, int y_dtype, const void* residual, void* workspace,
+                         size_t workspace_bytes, void* stream);
 size_t moe_layer_shared_workspace_bytes(const moe_experts_t* w, int S, int T, int k);
 
 /*

@@ -24,8 +24,8 @@ EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "m
            "moe_experts_run_stages", "moe_experts_workspace_bytes", "moe_row_bytes", "moe_tile_bytes",
            "moe_tiles_pack", "moe_shared_experts_run", "moe_shared_experts_workspace_bytes", "moe_version",
            "moe_experts_run_static", "moe_layer_run", "moe_layer_workspace_bytes", "moe_experts_run_shared",
-           "moe_experts_shared_workspace_bytes", "moe_router_group", "moe_router_group_max_slots",
-           "moe_layer_run_shared", "moe_layer_shared_workspace_bytes")
+           "moe_experts_shared_workspace_bytes", "moe_router_group", "moe_layer_run_shared",
+           "moe_layer_shared_workspace_bytes")
 STATIC_SCRATCH_BYTES = 32 << 20   # MOE_STATIC_SCRATCH_BYTES: the workspace array of moe_experts_run_static
 STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 3
 
@@ -73,12 +73,11 @@ def lib():
         L.moe_experts_run_static.argtypes = [ctypes.POINTER(Experts), vp, i, vp, vp, i, i, i, i, i, vp, i, vp, vp]
         L.moe_experts_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i, i, i]
         L.moe_experts_workspace_bytes.restype = sz
-        L.moe_router_group.argtypes = [vp, vp, vp, i, i, i, i, i, f, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
-        L.moe_router_group_max_slots.argtypes = [i]
-        L.moe_layer_run.argtypes = [ctypes.POINTER(Experts), vp, i, vp, vp, i, i, i, f, i, vp, vp, vp, i, vp, vp, vp,
-                                    sz, vp]
+        L.moe_router_group.argtypes = [vp, vp, vp, i, i, i, i, i, f, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.moe_layer_run.argtypes = [ctypes.POINTER(Experts), vp, i, vp, vp, i, i, i, f, i, vp, vp, vp, i, vp, vp, sz,
+                                    vp]
         L.moe_layer_run_shared.argtypes = [ctypes.POINTER(Experts), i, vp, i, vp, vp, vp, i, i, i, f, i, vp, vp, vp, i,
-                                           vp, vp, vp, sz, vp]
+                                           vp, vp, sz, vp]
         L.moe_layer_shared_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i, i, i]
         L.moe_layer_shared_workspace_bytes.restype = sz
         L.moe_layer_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i, i]
@@ -98,8 +97,7 @@ def lib():
         L.moe_experts_shared_workspace_bytes.restype = sz
         for n in ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
                   "moe_experts_run_stages", "moe_tiles_pack", "moe_shared_experts_run", "moe_experts_run_static",
-                  "moe_layer_run", "moe_experts_run_shared", "moe_router_group", "moe_router_group_max_slots",
-                  "moe_layer_run_shared"):
+                  "moe_layer_run", "moe_experts_run_shared", "moe_router_group", "moe_layer_run_shared"):
             getattr(L, n).restype = ctypes.c_int
         _lib = L
     return _lib

@@ -124,35 +124,33 @@ int moe_tiles_pack(int fmt, int E, int N, int K, const void* rows, void* tiles, 
     return moe::launch_pack_tiles(fmt, E, N, K, rows, tiles, (hipStream_t)stream);
 }
 
-int moe_router_counter_count(int T) { return moe::router_counter_slots(T < 1 ? 1 : T); }
+// the router keeps no counters (its launches hand data over at kernel boundaries only): one int32, never read
+int moe_router_counter_count(int T) { return T < 0 ? 0 : 1; }
 
 int moe_router(const void* x, const void* wr, const float* bias, int T, int d, int E, int k, int norm, float scale,
                float* logits, int32_t* idx, float* wts, int32_t* counters, void* stream) {
     if (T < 0 || d < 8 || d % 8 || E < 1 || E > 1024 || k < 1 || k > E || k > 32) return MOE_ERR_ARG;
     if (T == 0) return MOE_OK;
-    if (!x || !wr || !logits || !idx || !wts || !counters) return MOE_ERR_ARG;
+    (void)counters;   // kept for ABI compatibility: the router hands data over at kernel boundaries only
+    if (!x || !wr || !logits || !idx || !wts) return MOE_ERR_ARG;
     if (!aligned16(x) || !aligned16(wr)) return MOE_ERR_ALIGN;
     return moe::launch_router((const uint16_t*)x, (const uint16_t*)wr, bias, T, d, E, k, norm, scale, logits, idx, wts,
-                              counters, (hipStream_t)stream);
+                              (hipStream_t)stream);
 }
 
 int moe_router_group(const void* x, const void* wr, const float* bias, int T, int d, int E, int k, int norm,
                      float scale, float* logits, int32_t* idx, float* wts, int32_t* counts, int32_t* offsets,
-                     int32_t* sorted, int32_t* active, int32_t* meta, int32_t* counters, void* stream) {
+                     int32_t* sorted, int32_t* active, int32_t* meta, void* stream) {
     if (T < 0 || d < 8 || d % 8 || E < 1 || E > 1024 || k < 1 || k > E || k > 32) return MOE_ERR_ARG;
     if (T == 0) return MOE_OK;
-    if (!x || !wr || !logits || !idx || !wts || !counters || !counts || !offsets || !sorted || !active || !meta)
-        return MOE_ERR_ARG;
+    if (!x || !wr || !logits || !idx || !wts || !counts || !offsets || !sorted || !active || !meta) return MOE_ERR_ARG;
     if (!aligned16(x) || !aligned16(wr)) return MOE_ERR_ALIGN;
-    if (!moe::route_groups_inline(T * k, E)) return MOE_ERR_ARG;
     moe::RouterArgs a{};
     a.x = (const uint16_t*)x, a.wr = (const uint16_t*)wr, a.bias = bias, a.T = T, a.d = d, a.E = E, a.k = k;
-    a.norm = norm, a.scale = scale, a.logits = logits, a.lstride = E, a.idx = idx, a.wts = wts, a.counters = counters;
+    a.norm = norm, a.scale = scale, a.logits = logits, a.lstride = E, a.idx = idx, a.wts = wts;
     a.grp = moe::GroupBufs{counts, offsets, sorted, active, meta, nullptr, nullptr};
     return moe::launch_route(a, true, (hipStream_t)stream);
 }
-
-int moe_router_group_max_slots(int E) { return E < 1 || E > 1024 ? 0 : moe::route_groups_max_slots(E); }
 
 int moe_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
              void* stream) {
@@ -260,8 +258,7 @@ int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32
                  float route_scale, int pregrouped = 0);
 int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const void* wr, const float* wr_bias,
                const void* gate, int T, int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y,
-               int y_dtype, const void* residual, int32_t* counters, void* workspace, size_t workspace_bytes,
-               void* stream);
+               int y_dtype, const void* residual, void* workspace, size_t workspace_bytes, void* stream);
 }  // namespace
 
 size_t moe_layer_workspace_bytes(const moe_experts_t* w, int T, int k) {
@@ -278,18 +275,18 @@ size_t moe_layer_shared_workspace_bytes(const moe_experts_t* w, int S, int T, in
 
 int moe_layer_run(const moe_experts_t* w, const void* x, int x_dtype, const void* wr, const float* wr_bias, int T,
                   int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y, int y_dtype,
-                  const void* residual, int32_t* counters, void* workspace, size_t workspace_bytes, void* stream) {
+                  const void* residual, void* workspace, size_t workspace_bytes, void* stream) {
     return layer_call(w, 0, x, x_dtype, wr, wr_bias, nullptr, T, k, norm, scale, act, idx, wts, y, y_dtype, residual,
-                      counters, workspace, workspace_bytes, stream);
+                      workspace, workspace_bytes, stream);
 }
 
 int moe_layer_run_shared(const moe_experts_t* w, int S, const void* x, int x_dtype, const void* wr,
                          const float* wr_bias, const void* gate, int T, int k, int norm, float scale, int act,
-                         int32_t* idx, float* wts, void* y, int y_dtype, const void* residual, int32_t* counters,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+                         int32_t* idx, float* wts, void* y, int y_dtype, const void* residual, void* workspace,
+                         size_t workspace_bytes, void* stream) {
     if (S < 1) return MOE_ERR_ARG;
     return layer_call(w, S, x, x_dtype, wr, wr_bias, gate, T, k, norm, scale, act, idx, wts, y, y_dtype, residual,
-                      counters, workspace, workspace_bytes, stream);
+                      workspace, workspace_bytes, stream);
 }
 
 int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,
@@ -379,8 +376,7 @@ int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32
 // leave it to them.)
 int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const void* wr, const float* wr_bias,
                const void* gate, int T, int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y,
-               int y_dtype, const void* residual, int32_t* counters, void* workspace, size_t workspace_bytes,
-               void* stream) {
+               int y_dtype, const void* residual, void* workspace, size_t workspace_bytes, void* stream) {
     int rc = check_experts(w);
     if (rc) return rc;
     const int Er = w->E - S;   // routed experts
@@ -390,7 +386,7 @@ int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const 
     if (x_dtype != MOE_DTYPE_BF16) return MOE_ERR_DTYPE;   // the router GEMV reads bf16 x
     if (y_dtype < MOE_DTYPE_BF16 || y_dtype > MOE_DTYPE_F32) return MOE_ERR_DTYPE;
     if (T == 0) return MOE_OK;
-    if (!x || !wr || !idx || !wts || !y || !counters) return MOE_ERR_ARG;
+    if (!x || !wr || !idx || !wts || !y) return MOE_ERR_ARG;
     if (!aligned16(x) || !aligned16(wr) || !aligned16(y) || (residual && !aligned16(residual)) ||
         (gate && !aligned16(gate)))
         return MOE_ERR_ALIGN;
@@ -405,7 +401,7 @@ int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const 
     ra.x = (const uint16_t*)x, ra.wr = (const uint16_t*)wr, ra.bias = wr_bias, ra.gate = (const uint16_t*)gate;
     ra.T = T, ra.d = w->d, ra.E = Er, ra.k = k, ra.norm = norm, ra.scale = scale;
     ra.logits = (float*)(ws + L.total), ra.lstride = Er + (gate ? 1 : 0);
-    ra.idx = idx, ra.wts = wts, ra.counters = counters, ra.S = S;
+    ra.idx = idx, ra.wts = wts, ra.S = S;
     const int32_t* eidx = idx;   // the slot lists the experts read
     const float* ewts = wts;
     if (S) {
@@ -420,7 +416,7 @@ int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const 
                             L.total, MOE_STAGE_ALL, stream, ra.logits, norm, scale);
     }
     int pregrouped = 0;
-    if (resolve_path(MOE_PATH_AUTO, T) == MOE_PATH_GROUPED && moe::route_groups_inline(T * ks, w->E)) {
+    if (resolve_path(MOE_PATH_AUTO, T) == MOE_PATH_GROUPED) {
         const moe::TilePasses tp = moe::tile_passes(w, T, ks, x_dtype);
         if (!(tp.ingroup && moe::env_int("MOE_LAYER_INGROUP", 0))) {
             ra.grp = moe::GroupBufs{(int32_t*)(ws + L.counts), (int32_t*)(ws + L.offsets), (int32_t*)(ws + L.sorted),

@@ -275,17 +275,13 @@ constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024
 // that needs only round r passes r + 1; the weights are then not computed). JM >= ceil(E / 64) logits per lane
 // (logit j * 64 + lane in v[j]); a round is one DPP max over the lanes' best values, then the lowest id holding it
 // from one ballot per j (the lowest j with a lane at the maximum, then the lowest such lane).
-template <int JM, typename F>
-__device__ __forceinline__ void topk_lanes(F lg, int E, int k, int norm, float scale, int rounds, uint32_t* id,
-                                           float* w) {
+template <int JM>
+__device__ __forceinline__ void topk_core(float (&v)[JM], int E, int k, int norm, float scale, int rounds, uint32_t* id,
+                                          float* w) {
     const int lane = threadIdx.x & 63;
-    float v[JM];
 #pragma unroll
-    for (int j = 0; j < JM; ++j) {
-        const int e = j * 64 + lane;
-        float l = e < E ? lg(e) : -INFINITY;
-        v[j] = __builtin_isnan(l) ? -INFINITY : l;
-    }
+    for (int j = 0; j < JM; ++j)
+        if (__builtin_isnan(v[j]) || j * 64 + lane >= E) v[j] = -INFINITY;
     const bool weights = rounds >= k;
     float m0 = -INFINITY;
 #pragma unroll
@@ -333,6 +329,19 @@ __device__ __forceinline__ void topk_lanes(F lg, int E, int k, int norm, float s
     else s = den;
     const float off = norm ? top0 : m0;
     *w = expf(myv - off) / s * scale;
+}
+// topk_core on logits read through lg(e) (logit j * 64 + lane into v[j]; e >= E is not read)
+template <int JM, typename F>
+__device__ __forceinline__ void topk_lanes(F lg, int E, int k, int norm, float scale, int rounds, uint32_t* id,
+                                           float* w) {
+    const int lane = threadIdx.x & 63;
+    float v[JM];
+#pragma unroll
+    for (int j = 0; j < JM; ++j) {
+        const int e = j * 64 + lane;
+        v[j] = e < E ? lg(e) : -INFINITY;
+    }
+    topk_core<JM>(v, E, k, norm, scale, rounds, id, w);
 }
 template <typename F>
 __device__ __forceinline__ void wave_topk_lanes(F lg, int E, int k, int norm, float scale, int rounds, uint32_t* id,

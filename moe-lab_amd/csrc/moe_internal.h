@@ -32,26 +32,25 @@ struct RouterArgs {
     int lstride;           // E, or E + 1 with the gate row
     int32_t* idx;          // [T, k] routed ids
     float* wts;            // [T, k] routed weights
-    int32_t* counters;     // [router_counter_slots(T)], zero on entry; the launch leaves them zero
     int S;                 // shared experts appended to every token's slots (0: none)
     int32_t* sidx;         // S > 0: [T, k + S] the k routed ids, then E .. E + S - 1
     float* swts;           // S > 0: [T, k + S] the routed weights, then sigmoid(gate logit) or 1
     GroupBufs grp;         // grp.counts null: no grouping; else the grouping of the slots (sidx when S > 0, else idx)
     int P, P2;             // pass sizes of grp.items / grp.items2 (unused when null)
     int mw;                // set by launch_route
+    int32_t* arrive;       // set by launch_route: the finishing workgroups' arrival counter, zeroed by the logits
 };
-// tail = false: logits only (no counters needed)
+// The router's launches: the logits over many workgroups, then (tail) route_finish: the tails, the merged lists and the
+// grouping (grp.counts) and pass lists. tail = false: logits only.
 int launch_route(RouterArgs a, bool tail, hipStream_t st);
-// whether launch_route can group n slots over E experts in its own launch (else: launch_group after it)
-bool route_groups_inline(int n, int E);
 int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
-                  float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st);
-int router_counter_slots(int T);
+                  float scale, float* logits, int32_t* idx, float* wts, hipStream_t st);
 // logits only (x . wr^T + bias in the router's fixed order), no tail
 int launch_router_logits(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, float* logits,
                          hipStream_t st);
+// lstride: elements between logit rows (0: E)
 int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
-                hipStream_t st);
+                hipStream_t st, int lstride = 0);
 // with items: also the grouped kernels' pass list for passes of P slots (items [3 * max_passes(n, E, P)], meta[2])
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
                  int32_t* active, int32_t* meta, hipStream_t st, int P = 0, int32_t* items = nullptr, int P2 = 0,
@@ -61,8 +60,6 @@ inline int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
     return v ? atoi(v) : dflt;
 }
-// how many slots launch_route can group over E experts in its own launch
-int route_groups_max_slots(int E);
 // upper bound of the pass count: sum over experts of ceil(count / P) <= n / P + (experts with a count)
 inline int max_passes(int n, int E, int P) { return (n + P - 1) / P + (n < E ? n : E); }
 int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int d, int S, int32_t* idx, float* wts,

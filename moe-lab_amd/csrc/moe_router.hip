@@ -197,16 +197,11 @@ __device__ void group_block(LD ld, int n, int E, const GroupBufs& o, int P, int 
     }
 }
 
-// grid (ceil(rows / (ROUTER_WAVES * EPW)), ceil(T / TPW)), block 64 * ROUTER_WAVES; rows = a.lstride (the E router
-// rows, plus the shared experts' gate row when a.gate is given).
-// TAIL: a.counters[ty] must be 0 on entry; the last block of token group ty runs the tail for its tokens and resets it
-// to 0. With a.grp.counts, the last token group to finish (counter a.counters[gridDim.y], reset to 0 likewise) groups
-// the slots in the same launch. Logits and ids pass between blocks through agent-scope atomic stores / loads (no L2
-// write-back or invalidation). !TAIL: logits only (plain stores, no counters), for callers that run the tail
-// elsewhere (moe_layer_run at T = 1: the gate/up waves).
-template <int TPW, int EPW, bool TAIL>
-__global__ void __launch_bounds__(64 * ROUTER_WAVES) router_kernel(RouterArgs a) {
-    const int nbx = gridDim.x;
+// Logits: grid (ceil(rows / (ROUTER_WAVES * EPW)), ceil(T / TPW)), block 64 * ROUTER_WAVES; rows = a.lstride (the E
+// router rows, plus the shared experts' gate row when a.gate is given). Each wave computes EPW rows for TPW tokens
+// (the Wr chunk it loads serves all TPW tokens), so the E*d router bytes spread over many CUs.
+template <int TPW, int EPW>
+__global__ void __launch_bounds__(64 * ROUTER_WAVES) router_logits(RouterArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int rows = a.lstride;
     const int e0 = (blockIdx.x * ROUTER_WAVES + wave) * EPW;
@@ -214,125 +209,132 @@ __global__ void __launch_bounds__(64 * ROUTER_WAVES) router_kernel(RouterArgs a)
     const int nt = min(TPW, a.T - t0);
     const int d = a.d;
     const int nchunk = d >> 3;
-    if (e0 < rows) {
-        const uint16_t* wrow[EPW];   // row e < E of Wr, row E the gate
+    if (a.arrive && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.arrive = 0;
+    if (e0 >= rows) return;
+    const uint16_t* wrow[EPW];   // row e < E of Wr, row E the gate
 #pragma unroll
-        for (int q = 0; q < EPW; ++q) {
-            const int e = min(e0 + q, rows - 1);
-            wrow[q] = e < a.E ? a.wr + (size_t)e * d : a.gate;
+    for (int q = 0; q < EPW; ++q) {
+        const int e = min(e0 + q, rows - 1);
+        wrow[q] = e < a.E ? a.wr + (size_t)e * d : a.gate;
+    }
+    float acc[EPW][TPW];
+#pragma unroll
+    for (int q = 0; q < EPW; ++q)
+#pragma unroll
+        for (int i = 0; i < TPW; ++i) acc[q][i] = 0.f;
+    for (int c0 = 0; c0 < nchunk; c0 += 64 * ROUTER_MAXC) {
+        // all loads of this pass first (chunks c0 + lane + 64m), then the fma chains in chunk order
+        uint4 w[EPW][ROUTER_MAXC], xv[TPW][ROUTER_MAXC];
+#pragma unroll
+        for (int m = 0; m < ROUTER_MAXC; ++m) {
+            const int c = min(c0 + lane + 64 * m, nchunk - 1);
+#pragma unroll
+            for (int q = 0; q < EPW; ++q) w[q][m] = reinterpret_cast<const uint4*>(wrow[q])[c];
+#pragma unroll
+            for (int i = 0; i < TPW; ++i)
+                xv[i][m] = reinterpret_cast<const uint4*>(a.x + (size_t)(t0 + min(i, nt - 1)) * d)[c];
         }
-        float acc[EPW][TPW];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int q = 0; q < EPW; ++q)
+        for (int m = 0; m < ROUTER_MAXC; ++m) {
+            if (c0 + lane + 64 * m < nchunk) {
 #pragma unroll
-            for (int i = 0; i < TPW; ++i) acc[q][i] = 0.f;
-        for (int c0 = 0; c0 < nchunk; c0 += 64 * ROUTER_MAXC) {
-            // all loads of this pass first (chunks c0 + lane + 64m), then the fma chains in chunk order
-            uint4 w[EPW][ROUTER_MAXC], xv[TPW][ROUTER_MAXC];
+                for (int q = 0; q < EPW; ++q) {
+                    const uint32_t ww[4] = {w[q][m].x, w[q][m].y, w[q][m].z, w[q][m].w};
 #pragma unroll
-            for (int m = 0; m < ROUTER_MAXC; ++m) {
-                const int c = min(c0 + lane + 64 * m, nchunk - 1);
+                    for (int i = 0; i < TPW; ++i) {
+                        const uint32_t xx[4] = {xv[i][m].x, xv[i][m].y, xv[i][m].z, xv[i][m].w};
+                        float s = acc[q][i];
 #pragma unroll
-                for (int q = 0; q < EPW; ++q) w[q][m] = reinterpret_cast<const uint4*>(wrow[q])[c];
-#pragma unroll
-                for (int i = 0; i < TPW; ++i)
-                    xv[i][m] = reinterpret_cast<const uint4*>(a.x + (size_t)(t0 + min(i, nt - 1)) * d)[c];
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int m = 0; m < ROUTER_MAXC; ++m) {
-                if (c0 + lane + 64 * m < nchunk) {
-#pragma unroll
-                    for (int q = 0; q < EPW; ++q) {
-                        const uint32_t ww[4] = {w[q][m].x, w[q][m].y, w[q][m].z, w[q][m].w};
-#pragma unroll
-                        for (int i = 0; i < TPW; ++i) {
-                            const uint32_t xx[4] = {xv[i][m].x, xv[i][m].y, xv[i][m].z, xv[i][m].w};
-                            float s = acc[q][i];
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                s = __builtin_fmaf(bf16lo(xx[r]), bf16lo(ww[r]), s);
-                                s = __builtin_fmaf(bf16hi(xx[r]), bf16hi(ww[r]), s);
-                            }
-                            acc[q][i] = s;
+                        for (int r = 0; r < 4; ++r) {
+                            s = __builtin_fmaf(bf16lo(xx[r]), bf16lo(ww[r]), s);
+                            s = __builtin_fmaf(bf16hi(xx[r]), bf16hi(ww[r]), s);
                         }
+                        acc[q][i] = s;
                     }
                 }
             }
         }
+    }
 #pragma unroll
-        for (int q = 0; q < EPW; ++q)
+    for (int q = 0; q < EPW; ++q)
 #pragma unroll
-            for (int i = 0; i < TPW; ++i) {
-                float s = sum_lanes<64>(acc[q][i]);   // lanes 48..63 hold the total
-                const int e = e0 + q;
-                if (lane == 63 && i < nt && e < rows) {
-                    if (a.bias && e < a.E) s = s + a.bias[e];
-                    if (TAIL) store_agent(&a.logits[(size_t)(t0 + i) * rows + e], s);
-                    else a.logits[(size_t)(t0 + i) * rows + e] = s;
-                }
+        for (int i = 0; i < TPW; ++i) {
+            float s = sum_lanes<64>(acc[q][i]);   // lanes 48..63 hold the total
+            const int e = e0 + q;
+            if (lane == 63 && i < nt && e < rows) {
+                if (a.bias && e < a.E) s = s + a.bias[e];
+                a.logits[(size_t)(t0 + i) * rows + e] = s;
             }
-    }
-    if (!TAIL) return;
-    // the last block of this token group runs the tail
+        }
+}
+
+// The rest of the router, on the logits of the previous launch (its kernel boundary makes them visible): one wave per
+// token, FIN_WAVES waves per workgroup, so the tails (a chain of DPP reductions, VALU-issue bound) run one wave per SIMD
+// on ceil(T / FIN_WAVES) CUs. A wave runs its token's tail, writes idx / wts and, with shared experts, the merged slot
+// list (the S shared experts last, weight sigmoid(gate logit) or 1). With a.grp.counts the slots are then grouped
+// (group_block: the counts' offsets from a wave prefix sum) and the pass lists written by the last workgroup to
+// finish: the ids pass from the other workgroups by agent-scope stores and loads, and the arrival counter is
+// a.grp.meta[0], zeroed by the logits launch and overwritten by the grouping's own meta[0]. a.mw: the ids and the
+// per-wave count arrays fit the LDS; otherwise wave 0 places every slot.
+constexpr int FIN_WAVES = 4;
+template <int JM>
+__global__ void __launch_bounds__(64 * FIN_WAVES) route_finish(RouterArgs a) {
+    extern __shared__ int32_t sm[];   // grouping: cnt[FIN_WAVES][E + S], ids[T (k + S)] (mw); else cnt, cursor
     __shared__ int s_last;
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(&a.counters[blockIdx.y], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == nbx - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int k = a.k, ws = a.k + a.S, Eg = a.E + a.S;
     const bool grouping = a.grp.counts != nullptr;
-    const int k = a.k, ws = a.k + a.S;
-    for (int i = wave; i < nt; i += ROUTER_WAVES) {
-        const int t = t0 + i;
-        const float* lrow = a.logits + (size_t)t * rows;
+    const bool single = gridDim.x == 1;
+    int32_t* ids = a.S ? a.sidx : a.idx;   // the list the grouping reads
+    const int t = blockIdx.x * FIN_WAVES + wave;
+    if (t < a.T) {
+        const float* lrow = a.logits + (size_t)t * a.lstride;
+        float v[JM];
+#pragma unroll
+        for (int j = 0; j < JM; ++j) v[j] = j * 64 + lane < a.E ? lrow[j * 64 + lane] : -INFINITY;
+        const float gl = a.gate ? lrow[a.E] : 0.f;
         uint32_t id;
         float w;
-        wave_topk_lanes([&](int ee) { return load_agent(lrow + ee); }, a.E, k, a.norm, a.scale, k, &id, &w);
+        topk_core<JM>(v, a.E, k, a.norm, a.scale, k, &id, &w);
+        int32_t sid = (int32_t)id;
+        if (a.S && lane >= k) sid = a.E + lane - k;
         if (lane < k) {
-            if (grouping && !a.S) store_agent(&a.idx[(size_t)t * k + lane], (int32_t)id);
-            else a.idx[(size_t)t * k + lane] = (int32_t)id;
+            if (a.S) a.idx[(size_t)t * k + lane] = sid;
             a.wts[(size_t)t * k + lane] = w;
         }
-        if (a.S) {   // merged slot list: the k routed slots, then the S shared experts E .. E + S - 1
-            const float g = a.gate ? 1.f / (1.f + expf(-load_agent(lrow + a.E))) : 1.f;
-            if (lane < ws) {
-                const int32_t sid = lane < k ? (int32_t)id : a.E + lane - k;
-                if (grouping) store_agent(&a.sidx[(size_t)t * ws + lane], sid);
-                else a.sidx[(size_t)t * ws + lane] = sid;
-                a.swts[(size_t)t * ws + lane] = lane < k ? w : g;
-            }
+        if (lane < ws) {
+            if (a.S) a.swts[(size_t)t * ws + lane] = lane < k ? w : (a.gate ? 1.f / (1.f + expf(-gl)) : 1.f);
+            if (grouping && !single) store_agent(&ids[(size_t)t * ws + lane], sid);
+            else ids[(size_t)t * ws + lane] = sid;
         }
     }
-    if (threadIdx.x == 0) a.counters[blockIdx.y] = 0;
     if (!grouping) return;
-    // the last token group to finish groups every slot (its ids pass by agent-scope stores and loads, as the logits)
+    const int n = a.T * ws;
+    if (single) {   // this workgroup wrote every id (the barrier orders its stores before the loads)
+        __syncthreads();
+        group_block([&](int p) { return ids[p]; }, n, Eg, a.grp, a.P, a.P2, sm, a.mw);
+        return;
+    }
     wait_stores();
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int ng = gridDim.y;
-        const int old = __hip_atomic_fetch_add(&a.counters[ng], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == ng - 1);
+        const int old = __hip_atomic_fetch_add(&a.grp.meta[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == (int)gridDim.x - 1);
     }
     __syncthreads();
     if (!s_last) return;
-    extern __shared__ int32_t sm[];
-    const int32_t* ids = a.S ? a.sidx : a.idx;
-    group_block([&](int p) { return load_agent(ids + p); }, a.T * ws, a.E + a.S, a.grp, a.P, a.P2, sm, a.mw);
-    if (threadIdx.x == 0) a.counters[gridDim.y] = 0;
+    group_block([&](int p) { return load_agent(ids + p); }, n, Eg, a.grp, a.P, a.P2, sm, a.mw);
 }
 
 // Router tail on given logits [T, E] (fp32, bf16 or fp16): one wave per token.
 template <typename LT>
 __global__ void __launch_bounds__(256)
-topk_kernel(const LT* __restrict__ logits, int T, int E, int k, int norm, float scale, int32_t* __restrict__ idx,
-            float* __restrict__ wts) {
+topk_kernel(const LT* __restrict__ logits, int T, int E, int lstride, int k, int norm, float scale,
+            int32_t* __restrict__ idx, float* __restrict__ wts) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
-    const LT* lrow = logits + (size_t)t * E;
+    const LT* lrow = logits + (size_t)t * lstride;
     wave_topk([&](int ee) { return to_f32<LT>(lrow[ee]); }, E, k, norm, scale, idx + (size_t)t * k,
               wts + (size_t)t * k);
 }
@@ -399,59 +401,44 @@ shared_route(const void* __restrict__ x, int xdt, const uint16_t* __restrict__ g
 }
 
 // ------------------------------------------------------------------------------------ host launchers
-// The router groups the slots in its own launch (its last block) when its LDS holds what the grouping needs; every
-// router block reserves that LDS, so more than ROUTER_GROUP_LDS would cost the logit blocks occupancy. Either the ids
-// and one count array per wave (the 4 waves place the slots in parallel), or, for many experts and up to
-// ROUTER_GROUP_WAVE0 slots, the counts and cursors only (wave 0 places every slot). Larger calls group in a launch
-// of their own (launch_group, up to 16 waves).
-constexpr size_t ROUTER_GROUP_LDS = 16 * 1024;
-constexpr int ROUTER_GROUP_WAVE0 = 2048;
+// route_finish's grouping LDS (every workgroup of the launch reserves it; only the last uses it): the ids and the
+// per-wave count arrays up to FIN_LDS, else the counts and cursors only, with wave 0 placing every slot.
+constexpr size_t FIN_LDS = 32 * 1024;
 
-size_t route_group_lds(int n, int E, int* mw) {
-    const size_t per_wave = ((size_t)ROUTER_WAVES * E + (size_t)n) * 4;
-    if (per_wave <= ROUTER_GROUP_LDS) {
-        *mw = 1;
-        return per_wave;
-    }
-    *mw = 0;
-    return n <= ROUTER_GROUP_WAVE0 && (size_t)E * 8 <= ROUTER_GROUP_LDS ? (size_t)E * 8 : 0;
-}
-
-bool route_groups_inline(int n, int E) {
-    int mw;
-    return route_group_lds(n, E, &mw) > 0;
-}
-
-int route_groups_max_slots(int E) {
-    const long n = (long)(ROUTER_GROUP_LDS / 4) - (long)ROUTER_WAVES * E;
-    const long w0 = (size_t)E * 8 <= ROUTER_GROUP_LDS ? ROUTER_GROUP_WAVE0 : 0;
-    return (int)(n > w0 ? n : w0);
+// logits (T > 1: ROUTER_TPW tokens per wave share each loaded Wr chunk; T == 1: one expert per wave, fewer larger
+// waves or one wave per workgroup spread over E CUs measured no faster)
+int launch_route_logits(const RouterArgs& a, hipStream_t st) {
+    const dim3 grid((a.lstride + ROUTER_WAVES - 1) / ROUTER_WAVES, a.T == 1 ? 1 : (a.T + ROUTER_TPW - 1) / ROUTER_TPW);
+    if (a.T == 1) router_logits<1, 1><<<grid, 64 * ROUTER_WAVES, 0, st>>>(a);
+    else router_logits<ROUTER_TPW, 1><<<grid, 64 * ROUTER_WAVES, 0, st>>>(a);
+    return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
 int launch_route(RouterArgs a, bool tail, hipStream_t st) {
+    const int nwg = (a.T + FIN_WAVES - 1) / FIN_WAVES;
+    a.arrive = tail && a.grp.counts && nwg > 1 ? a.grp.meta : nullptr;
+    int rc = launch_route_logits(a, st);
+    if (rc || !tail) return rc;
     size_t lds = 0;
-    if (tail && a.grp.counts) {
-        lds = route_group_lds(a.T * (a.k + a.S), a.E + a.S, &a.mw);
-        if (!lds) return MOE_ERR_ARG;
+    if (a.grp.counts) {
+        const int n = a.T * (a.k + a.S), Eg = a.E + a.S;
+        const size_t per_wave = ((size_t)FIN_WAVES * Eg + (size_t)n) * 4;
+        a.mw = per_wave <= FIN_LDS;
+        lds = a.mw ? per_wave : (size_t)Eg * 8;
     }
-    // T == 1: one expert per wave and token (fewer, larger waves, or one wave per workgroup spread over E CUs,
-    // measured no faster); T > 1: ROUTER_TPW tokens per wave share each loaded Wr chunk
-    const dim3 grid((a.lstride + ROUTER_WAVES - 1) / ROUTER_WAVES, a.T == 1 ? 1 : (a.T + ROUTER_TPW - 1) / ROUTER_TPW);
-    if (a.T == 1) {
-        if (tail) router_kernel<1, 1, true><<<grid, 64 * ROUTER_WAVES, lds, st>>>(a);
-        else router_kernel<1, 1, false><<<grid, 64 * ROUTER_WAVES, 0, st>>>(a);
-    } else {
-        if (tail) router_kernel<ROUTER_TPW, 1, true><<<grid, 64 * ROUTER_WAVES, lds, st>>>(a);
-        else router_kernel<ROUTER_TPW, 1, false><<<grid, 64 * ROUTER_WAVES, 0, st>>>(a);
-    }
+    const dim3 grid(nwg);
+    if (a.E <= 64) route_finish<1><<<grid, 64 * FIN_WAVES, lds, st>>>(a);
+    else if (a.E <= 128) route_finish<2><<<grid, 64 * FIN_WAVES, lds, st>>>(a);
+    else if (a.E <= 256) route_finish<4><<<grid, 64 * FIN_WAVES, lds, st>>>(a);
+    else route_finish<TOPK_MAX_J><<<grid, 64 * FIN_WAVES, lds, st>>>(a);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
 int launch_router(const uint16_t* x, const uint16_t* wr, const float* bias, int T, int d, int E, int k, int norm,
-                  float scale, float* logits, int32_t* idx, float* wts, int32_t* counters, hipStream_t st) {
+                  float scale, float* logits, int32_t* idx, float* wts, hipStream_t st) {
     RouterArgs a{};
     a.x = x, a.wr = wr, a.bias = bias, a.T = T, a.d = d, a.E = E, a.k = k, a.norm = norm, a.scale = scale;
-    a.logits = logits, a.lstride = E, a.idx = idx, a.wts = wts, a.counters = counters;
+    a.logits = logits, a.lstride = E, a.idx = idx, a.wts = wts;
     return launch_route(a, true, st);
 }
 
@@ -460,21 +447,19 @@ int launch_router_logits(const uint16_t* x, const uint16_t* wr, const float* bia
     RouterArgs a{};
     a.x = x, a.wr = wr, a.bias = bias, a.T = T, a.d = d, a.E = E, a.k = 1, a.norm = 1, a.scale = 1.f;
     a.logits = logits, a.lstride = E;
-    return launch_route(a, false, st);
+    return launch_route_logits(a, st);
 }
 
-// token groups + the grouping's counter
-int router_counter_slots(int T) { return (T + ROUTER_TPW - 1) / ROUTER_TPW + 1; }
-
 int launch_topk(const void* logits, int dtype, int T, int E, int k, int norm, float scale, int32_t* idx, float* wts,
-                hipStream_t st) {
+                hipStream_t st, int lstride) {
     dim3 grid((T + 3) / 4);
+    if (lstride < E) lstride = E;
     if (dtype == MOE_DTYPE_F32)
-        topk_kernel<float><<<grid, 256, 0, st>>>((const float*)logits, T, E, k, norm, scale, idx, wts);
+        topk_kernel<float><<<grid, 256, 0, st>>>((const float*)logits, T, E, lstride, k, norm, scale, idx, wts);
     else if (dtype == MOE_DTYPE_BF16)
-        topk_kernel<uint16_t><<<grid, 256, 0, st>>>((const uint16_t*)logits, T, E, k, norm, scale, idx, wts);
+        topk_kernel<uint16_t><<<grid, 256, 0, st>>>((const uint16_t*)logits, T, E, lstride, k, norm, scale, idx, wts);
     else if (dtype == MOE_DTYPE_F16)
-        topk_kernel<_Float16><<<grid, 256, 0, st>>>((const _Float16*)logits, T, E, k, norm, scale, idx, wts);
+        topk_kernel<_Float16><<<grid, 256, 0, st>>>((const _Float16*)logits, T, E, lstride, k, norm, scale, idx, wts);
     else
         return MOE_ERR_DTYPE;
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;

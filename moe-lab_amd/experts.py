@@ -157,11 +157,10 @@ def reserve(s, T, k, device=None):
 def run_routed(s, x, wr, k, bias=None, norm=True, scale=1.0, act=0, residual=None, out=None, out_dtype=None):
     """Router + experts in one call (moe_layer_run): the fused router's logits x . wr^T (+ bias) and tail (the same
     ids as router.route), then the experts on the default path; at T > 1 the router launch also builds the slot
-    grouping, so no top-k or grouping launch runs. x [T, d] bf16, wr [E, d] bf16 (E the routed experts).
+    grouping, so the experts run no grouping launch of their own. x [T, d] bf16, wr [E, d] bf16 (E the routed experts).
     A merge_shared state (s["n_shared"]) runs moe_layer_run_shared: its shared experts join every token, weighted by
     sigmoid(x . s["shared_gate"]) or 1. A state with separate shared experts (s["shared"]) adds them by a second call.
     Returns (y [T, d], idx [T, k] int32, wts [T, k] fp32), idx / wts the routed slots."""
-    from . import router
     _lib.require_device(x, "x")
     if x.dtype != torch.bfloat16 or wr.dtype != torch.bfloat16:
         raise TypeError("run_routed takes bf16 x and router weights (the gate GEMV reads bf16)")
@@ -174,7 +173,6 @@ def run_routed(s, x, wr, k, bias=None, norm=True, scale=1.0, act=0, residual=Non
     S = int(s.get("n_shared", 0))
     nbytes = L.moe_layer_shared_workspace_bytes(desc, S, T, k) if S else L.moe_layer_workspace_bytes(desc, T, k)
     ws = _lib.workspace(x.device, nbytes)
-    cnt = router.counters(x.device, T)
     final_dtype = x.dtype if out_dtype is None else out_dtype
     separate_shared = "shared" in s and not S
     user_out = out
@@ -190,14 +188,13 @@ def run_routed(s, x, wr, k, bias=None, norm=True, scale=1.0, act=0, residual=Non
         g = None if g is None else g.to(torch.bfloat16).contiguous()
         rc = L.moe_layer_run_shared(desc, S, _lib.ptr(x), _lib.DTYPE[x.dtype], _lib.ptr(wr), _lib.ptr(b), _lib.ptr(g),
                                     T, k, int(bool(norm)), float(scale), int(act), _lib.ptr(idx), _lib.ptr(wts),
-                                    _lib.ptr(out), _lib.DTYPE[out.dtype], _lib.ptr(res), _lib.ptr(cnt), _lib.ptr(ws),
-                                    ws.numel(), _lib.stream_of(x.device))
+                                    _lib.ptr(out), _lib.DTYPE[out.dtype], _lib.ptr(res), _lib.ptr(ws), ws.numel(),
+                                    _lib.stream_of(x.device))
         _lib.check("moe_layer_run_shared", rc)
     else:
         rc = L.moe_layer_run(desc, _lib.ptr(x), _lib.DTYPE[x.dtype], _lib.ptr(wr), _lib.ptr(b), T, k,
                              int(bool(norm)), float(scale), int(act), _lib.ptr(idx), _lib.ptr(wts), _lib.ptr(out),
-                             _lib.DTYPE[out.dtype], _lib.ptr(res), _lib.ptr(cnt), _lib.ptr(ws), ws.numel(),
-                             _lib.stream_of(x.device))
+                             _lib.DTYPE[out.dtype], _lib.ptr(res), _lib.ptr(ws), ws.numel(), _lib.stream_of(x.device))
         _lib.check("moe_layer_run", rc)
     if separate_shared:
         out = run_shared(s["shared"], x, gate=s.get("shared_gate"), act=act, residual=out, out=user_out,

@@ -32,21 +32,10 @@ def topk_norm(logits, k, norm=True, scale=1.0):
     return idx, wts
 
 
-_COUNTERS = {}
-
-
-def _counters(device, T):
-    """The router's per-device hand-off counters (zero on entry, left zero by every call); grown like the expert
-    workspace (_lib.grow: old buffers stay alive for graphs captured with them; no growth during capture)."""
-    device = torch.device(device)
-    n = max(int(_lib.lib().moe_router_counter_count(T)), 64)
-    return _lib.grow(_COUNTERS, device.index, n, lambda m: torch.zeros(m, dtype=torch.int32, device=device),
-                     "the router counters")
-
-
 def reserve(device, T):
-    """Size the router's counters for calls of up to T tokens (before capturing them in a HIP graph)."""
-    _counters(device, T)
+    """Nothing to size: the router's launches need no scratch of their own (kept for callers that size every buffer
+    before capturing a HIP graph)."""
+    return None
 
 
 def route(x, wr, k, bias=None, norm=True, scale=1.0, return_logits=False):
@@ -64,25 +53,22 @@ def route(x, wr, k, bias=None, norm=True, scale=1.0, return_logits=False):
     idx = torch.empty((T, k), dtype=torch.int32, device=x.device)
     wts = torch.empty((T, k), dtype=torch.float32, device=x.device)
     rc = _lib.lib().moe_router(_lib.ptr(x), _lib.ptr(wr), _lib.ptr(b), T, d, E, k, int(bool(norm)), float(scale),
-                               _lib.ptr(logits), _lib.ptr(idx), _lib.ptr(wts), _lib.ptr(_counters(x.device, T)),
-                               _lib.stream_of(x.device))
+                               _lib.ptr(logits), _lib.ptr(idx), _lib.ptr(wts), None, _lib.stream_of(x.device))
     _lib.check("moe_router", rc)
     return (idx, wts, logits) if return_logits else (idx, wts)
 
 
 def route_group(x, wr, k, bias=None, norm=True, scale=1.0):
-    """route() plus the stable slot grouping, built in the same launch (moe_router_group: the router's last workgroup
-    sorts the T*k slots by expert with a wave prefix sum of the counts). Returns (idx, wts, logits, (counts [E],
-    offsets [E+1], sorted [T*k], active [E], meta [2])), the grouping as group(idx, E) returns it."""
+    """route() plus the stable slot grouping, built by the router's own launches (moe_router_group: after the logits
+    launch, the launch that runs the tails sorts the T*k slots by expert with a wave prefix sum of the counts).
+    Returns (idx, wts, logits, (counts [E], offsets [E+1], sorted [T*k], active [E], meta [2])), the grouping as
+    group(idx, E) returns it."""
     _lib.require_device(x, "x")
     assert x.dtype == torch.bfloat16 and wr.dtype == torch.bfloat16, "router takes bf16 x and Wr"
     T, d = x.shape
     E = wr.shape[0]
     assert wr.shape[1] == d and E <= 1024 and 1 <= k <= min(E, 32), (x.shape, wr.shape, k)
     L = _lib.lib()
-    if T * k > L.moe_router_group_max_slots(E):
-        raise ValueError(f"{T * k} slots over {E} experts exceed the in-launch grouping's "
-                         f"{L.moe_router_group_max_slots(E)}: use route() then group()")
     x = x.contiguous()
     wr = wr.contiguous()
     b = None if bias is None else bias.to(torch.float32).contiguous()
@@ -97,15 +83,9 @@ def route_group(x, wr, k, bias=None, norm=True, scale=1.0):
     meta = torch.empty(2, dtype=torch.int32, device=dev)
     rc = L.moe_router_group(_lib.ptr(x), _lib.ptr(wr), _lib.ptr(b), T, d, E, k, int(bool(norm)), float(scale),
                             _lib.ptr(logits), _lib.ptr(idx), _lib.ptr(wts), _lib.ptr(counts), _lib.ptr(offsets),
-                            _lib.ptr(srt), _lib.ptr(active), _lib.ptr(meta), _lib.ptr(_counters(dev, T)),
-                            _lib.stream_of(dev))
+                            _lib.ptr(srt), _lib.ptr(active), _lib.ptr(meta), _lib.stream_of(dev))
     _lib.check("moe_router_group", rc)
     return idx, wts, logits, (counts, offsets, srt[:T * k], active, meta)
-
-
-def counters(device, T):
-    """The per-device router counters for calls of up to T tokens (moe_router, moe_router_group, moe_layer_run)."""
-    return _counters(device, T)
 
 
 def group(idx, E):

@@ -86,30 +86,24 @@ def test_router_argument_errors():
 
 
 def test_router_group_and_layer_argument_errors():
-    """moe_router_group's in-launch grouping limit and the layer calls' counters / shared-expert checks, before any
-    launch."""
+    """moe_router_group's and the layer calls' argument checks, before any launch."""
     from moelab_amd import _lib
     L = _lib.lib()
     p = ctypes.c_void_p(4096)
-    assert L.moe_router_group_max_slots(128) == 4096 - 4 * 128
-    assert L.moe_router_group_max_slots(1000) == 2048 and L.moe_router_group_max_slots(0) == 0
-    args = (p, p, p, p, p, p, p, p, p)
-    assert L.moe_router_group(p, p, None, 449, 2048, 128, 8, 1, 1.0, *args, None) == -1   # 3592 slots > 3584
+    args = (p, p, p, p, p, p, p, p)
     assert L.moe_router_group(p, p, None, 4, 2048, 128, 33, 1, 1.0, *args, None) == -1    # k > 32
-    assert L.moe_router_group(p, p, None, 4, 2048, 128, 8, 1, 1.0, p, p, p, None, p, p, p, p, p, None) == -1
-    assert L.moe_router_counter_count(1) == 2 and L.moe_router_counter_count(32) == 9
+    assert L.moe_router_group(p, p, None, 4, 2048, 128, 8, 1, 1.0, p, p, p, None, p, p, p, p, None) == -1
+    assert L.moe_router_group(p, p, None, 0, 2048, 128, 8, 1, 1.0, *args, None) == 0
     w = _desc(E=10, d=128, F=128)
     ws = ctypes.c_void_p(8192)
-    # no counters
-    assert L.moe_layer_run(w, p, 0, p, None, 4, 2, 1, 1.0, 0, p, p, p, 0, None, None, ws, 1 << 30, None) == -1
     # fp16 x: the router reads bf16
-    assert L.moe_layer_run(w, p, 1, p, None, 4, 2, 1, 1.0, 0, p, p, p, 0, None, p, ws, 1 << 30, None) == -2
+    assert L.moe_layer_run(w, p, 1, p, None, 4, 2, 1, 1.0, 0, p, p, p, 0, None, ws, 1 << 30, None) == -2
     # S = 0, S >= E, k + S > 64
     for S, k in ((0, 2), (10, 2), (8, 60)):
-        assert L.moe_layer_run_shared(w, S, p, 0, p, None, None, 4, k, 1, 1.0, 0, p, p, p, 0, None, p, ws, 1 << 30,
+        assert L.moe_layer_run_shared(w, S, p, 0, p, None, None, 4, k, 1, 1.0, 0, p, p, p, 0, None, ws, 1 << 30,
                                       None) == -1
     assert L.moe_layer_shared_workspace_bytes(w, 2, 4, 2) > L.moe_layer_workspace_bytes(_desc(E=8), 4, 4) > 0
-    assert L.moe_layer_run_shared(w, 2, p, 0, p, None, None, 4, 2, 1, 1.0, 0, p, p, p, 0, None, p, ws, 100,
+    assert L.moe_layer_run_shared(w, 2, p, 0, p, None, None, 4, 2, 1, 1.0, 0, p, p, p, 0, None, ws, 100,
                                   None) == -3
 
 
@@ -140,7 +134,7 @@ def test_misaligned_tiles_rejected_before_launch():
 
 
 def test_buffer_growth_keeps_old_buffers_and_refuses_growth_during_capture(monkeypatch):
-    """_lib.grow (the expert workspace and the router counters): a buffer that is large enough is returned as
+    """_lib.grow (the per-device expert workspace): a buffer that is large enough is returned as
     is; a smaller one is replaced by one of at least twice its size and kept alive (a HIP graph captured with it
     keeps its raw pointer); growing while the current stream captures raises (host-only: the capture state is
     stubbed)."""

@@ -177,9 +177,9 @@ def test_layer_shared_router_builds_grouping(case):
     assert_close(y3, oracle_y(s, x, idx, wts, act), what=case)
 
 
-def test_layer_grouping_beyond_router_lds():
-    """4096 slots over 8 experts exceed what the router's last workgroup groups in LDS: the router runs the tail only
-    and the grouping runs as a launch of its own; results as the separate calls."""
+def test_layer_grouping_beyond_one_workgroup():
+    """2048 tokens exceed what the router's one finishing workgroup takes: the tails run one wave per token and the
+    grouping runs as a launch of its own; results as the separate calls."""
     from moelab_amd.problem import baseline_int4_layer, baseline_x
     from moelab_amd.shapes import MoEShape
     sh = MoEShape("big", d=128, f=128, E=8, k=2)

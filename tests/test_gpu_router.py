@@ -49,8 +49,8 @@ def test_route_bias_zipf_and_full_softmax(T):
         np.testing.assert_allclose(wts.cpu().numpy(), wts_ref, rtol=1e-6, atol=1e-7)
 
 
-def test_route_repeated_calls_reset_counters():
-    """The last-block counters must be left at zero: many calls in a row give identical results."""
+def test_route_repeated_calls_agree():
+    """Many calls in a row give identical results (the router keeps no state between calls)."""
     from moelab_amd import router
     x, wr, _ = _router_inputs(5, 512, 64, seed=1)
     first = router.route(x, wr, 6)
@@ -125,8 +125,10 @@ def test_group_rejects_out_of_range_ids():
 
 @pytest.mark.parametrize("T,E,k,d,mode", [(1, 128, 8, 2048, "plain"), (32, 128, 8, 2048, "plain"),
                                           (32, 128, 8, 2048, "zipf"), (64, 128, 8, 2048, "ties"),
-                                          (256, 64, 6, 2048, "plain"), (512, 8, 2, 4096, "plain"),
-                                          (448, 128, 8, 256, "zipf"), (7, 1000, 8, 256, "plain"),
+                                          (65, 128, 8, 2048, "zipf"), (256, 64, 6, 2048, "plain"),
+                                          (512, 8, 2, 4096, "plain"), (448, 128, 8, 256, "zipf"),
+                                          (7, 1000, 8, 256, "plain"), (512, 128, 32, 128, "plain"),
+                                          (300, 1000, 32, 64, "plain"), (2000, 64, 6, 128, "zipf"),
                                           (64, 1024, 32, 64, "ties"), (33, 16, 16, 128, "plain")])
 def test_route_group_bit_exact(T, E, k, d, mode):
     """moe_router_group: the router launch also sorts the slots by expert (its last workgroup, a wave prefix sum of
@@ -162,14 +164,13 @@ def test_route_group_bit_exact(T, E, k, d, mode):
         assert (idx.cpu().numpy() == np.arange(k)).all()
 
 
-def test_route_group_repeated_calls_and_limit():
-    """Both counter levels are left at zero (20 calls in a row agree), and a call past the in-launch limit raises."""
+@pytest.mark.parametrize("T", [40, 200])
+def test_route_group_repeated_calls(T):
+    """20 calls in a row agree: one workgroup (T = 40) and the last-workgroup grouping, whose arrival counter the
+    logits launch zeroes on every call (T = 200)."""
     from moelab_amd import router
-    x, wr, _ = _router_inputs(40, 512, 64, seed=2)
+    x, wr, _ = _router_inputs(T, 512, 64, seed=2)
     first = router.route_group(x, wr, 6)
     for _ in range(20):
         again = router.route_group(x, wr, 6)
-        assert torch.equal(first[0], again[0]) and torch.equal(first[3][2], again[3][2])
-    x2, wr2, _ = _router_inputs(449, 64, 128, seed=3)
-    with pytest.raises(ValueError):
-        router.route_group(x2, wr2, 8)
+        assert torch.equal(first[0], again[0]) and all(torch.equal(u, v) for u, v in zip(first[3], again[3]))
