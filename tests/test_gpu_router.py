@@ -164,10 +164,10 @@ def test_route_group_bit_exact(T, E, k, d, mode):
         assert (idx.cpu().numpy() == np.arange(k)).all()
 
 
-@pytest.mark.parametrize("T", [40, 200])
+@pytest.mark.parametrize("T", [3, 200])
 def test_route_group_repeated_calls(T):
-    """20 calls in a row agree: one workgroup (T = 40) and the last-workgroup grouping, whose arrival counter the
-    logits launch zeroes on every call (T = 200)."""
+    """20 calls in a row agree: one finishing workgroup (T = 3) and the last-workgroup grouping, whose arrival counter
+    the logits launch zeroes on every call (T = 200)."""
     from moelab_amd import router
     x, wr, _ = _router_inputs(T, 512, 64, seed=2)
     first = router.route_group(x, wr, 6)
