@@ -289,6 +289,15 @@ int moe_experts_run_shared(const moe_experts_t* w, int S, const void* x, int x_d
                            const void* residual, void* workspace, size_t workspace_bytes, void* stream);
 size_t moe_experts_shared_workspace_bytes(const moe_experts_t* w, int S, int T, int k, int path);
 
+/*
+ * Read-bandwidth probe of the timing harness's contention guard (the reference's guard times a read-bound reduction,
+ * moelab/guard.py:31-45): MOE_PROBE_SINK workgroups stream src [nbytes] (16-byte aligned, nbytes % 16 == 0) with
+ * 16-byte loads, the expert kernels' weight-load pattern, and nothing else; workgroup b writes the XOR of the 32-bit
+ * words it read to sink[b] (so the XOR of sink [MOE_PROBE_SINK] uint32 is the XOR of the buffer's words).
+ */
+#define MOE_PROBE_SINK 1024
+int moe_probe_read(const void* src, size_t nbytes, uint32_t* sink, void* stream);
+
 /* Library version and build target, for logs. */
 const char* moe_version(void);
 

@@ -25,7 +25,8 @@ EXPORTS = ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "m
            "moe_tiles_pack", "moe_shared_experts_run", "moe_shared_experts_workspace_bytes", "moe_version",
            "moe_experts_run_static", "moe_layer_run", "moe_layer_workspace_bytes", "moe_experts_run_shared",
            "moe_experts_shared_workspace_bytes", "moe_router_group", "moe_layer_run_shared",
-           "moe_layer_shared_workspace_bytes")
+           "moe_layer_shared_workspace_bytes", "moe_probe_read")
+PROBE_SINK = 1024   # MOE_PROBE_SINK
 STATIC_SCRATCH_BYTES = 32 << 20   # MOE_STATIC_SCRATCH_BYTES: the workspace array of moe_experts_run_static
 STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 3
 
@@ -83,6 +84,7 @@ def lib():
         L.moe_layer_workspace_bytes.argtypes = [ctypes.POINTER(Experts), i, i]
         L.moe_layer_workspace_bytes.restype = sz
         L.moe_version.restype = ctypes.c_char_p
+        L.moe_probe_read.argtypes = [vp, sz, vp, vp]
         L.moe_row_bytes.argtypes = [i, i]
         L.moe_row_bytes.restype = sz
         L.moe_tile_bytes.argtypes = [i, i, i]
@@ -97,7 +99,8 @@ def lib():
         L.moe_experts_shared_workspace_bytes.restype = sz
         for n in ("moe_router", "moe_router_counter_count", "moe_topk", "moe_group", "moe_experts_run",
                   "moe_experts_run_stages", "moe_tiles_pack", "moe_shared_experts_run", "moe_experts_run_static",
-                  "moe_layer_run", "moe_experts_run_shared", "moe_router_group", "moe_layer_run_shared"):
+                  "moe_layer_run", "moe_experts_run_shared", "moe_router_group", "moe_layer_run_shared",
+                  "moe_probe_read"):
             getattr(L, n).restype = ctypes.c_int
         _lib = L
     return _lib

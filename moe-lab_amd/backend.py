@@ -10,8 +10,7 @@ build's own:
     gpt-oss biases built in;
   * ``errors`` reports the north-star gate (max |y - y_ref| / RMS(y_ref)) beside the relative Frobenius error;
   * timing captures the whole dependent chain x <- x + run(x) in one HIP graph and times its replays with HIP
-    events, with a device-wide synchronisation before each end event, so work a variant puts on another stream
-    is inside the measured interval (an eagerly launched chain is host-bound on ROCm).
+    events on the replaying stream (an eagerly launched chain is host-bound on ROCm).
 """
 import importlib
 import importlib.util
@@ -66,8 +65,9 @@ def make_weights(shape, dtype="bfloat16", seed=0):
 
 def make_inputs(shape, T, dtype="bfloat16", routing="uniform", seed=0):
     """(x [T, d], idx [T, k] int32, wts [T, k] fp32) on the device from one numpy stream: x ~ N(0, 1), then
-    the routing of problem.make_routing (uniform, zipf, one_hot) from the same stream."""
-    rng = np.random.default_rng(int(seed))
+    the routing of problem.make_routing (uniform, zipf, one_hot) from the same stream. seed: an int or a sequence
+    of ints (numpy's seed sequence)."""
+    rng = np.random.default_rng(seed if isinstance(seed, (list, tuple)) else int(seed))
     x = rng.standard_normal((T, shape.d), dtype=np.float32)
     idx, wts = make_routing(T, shape.E, shape.k, routing, rng)
     dev = lambda a: torch.as_tensor(a).to(DEVICE)  # noqa: E731
@@ -87,12 +87,16 @@ def reference(wg, wu, wd, x, idx, wts, act=0, bg=None, bu=None, bd=None):
     """fp32 layer on dense (dequantised) weights, the check every variant is held to (reference
     torch_backend.py:58-67; the gpt-oss biases and clamped SwiGLU of metal_mxfp4_gptoss.py:110-126).
     The T*k slots are sorted by expert once (stable), then each expert's contiguous segment of slots is
-    gathered, projected and scattered back with its routing weight."""
+    gathered, projected and scattered back with its routing weight. Slots with ids outside [0, E) contribute
+    nothing, as in the library."""
     x32 = x.float()
     T, k = idx.shape
+    E = wg.shape[0]
     flat = idx.reshape(-1).long()
-    order = torch.argsort(flat, stable=True)
-    counts = torch.bincount(flat, minlength=wg.shape[0]).tolist()
+    # slots with ids outside [0, E) add nothing (the library's contract): they sort after every expert's segment
+    key = torch.where((flat >= 0) & (flat < E), flat, torch.full_like(flat, E))
+    order = torch.argsort(key, stable=True)
+    counts = torch.bincount(key, minlength=E + 1)[:E].tolist()
     w_slot = wts.reshape(-1).float()[order]
     tok = order // k
     y = torch.zeros_like(x32)
@@ -147,24 +151,27 @@ def capture(fn):
 
 
 def replay_seconds(graph, reps, warmup=1):
-    """Seconds of each of `reps` replays of a captured graph: HIP events on the current stream, the end event
-    recorded after a device-wide synchronisation."""
+    """Seconds of each of `reps` replays of a captured graph: HIP events recorded on the current stream just before
+    and just after the replay (a replay is stream-ordered: every node of the graph, including work captured from
+    other streams, which capture joins back to this one, ends before the second event)."""
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
     out = np.empty(reps)
+    st = torch.cuda.current_stream()
     for i in range(reps):
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0.record()
+        t0.record(st)
         graph.replay()
-        torch.cuda.synchronize()
-        t1.record()
+        t1.record(st)
         t1.synchronize()
         out[i] = t0.elapsed_time(t1) * 1e-3
     return out
 
 
-def _chain(fn, inputs, chain):
+def chain_of(fn, inputs, chain):
+    """A function running `chain` dependent calls x <- x + fn(x, idx, wts) over the (x, idx, wts) windows
+    `inputs` (window i % len(inputs) for call i), returning the last x."""
     def run():
         x = inputs[0][0]
         for i in range(chain):
@@ -178,7 +185,7 @@ def time_chained(fn, inputs, reps, chain=10, eager=False):
     """Seconds per call of fn(x, idx, wts) in a chain of `chain` dependent calls x <- x + fn(x, idx, wts) over the
     (x, idx, wts) windows `inputs`, one value per repetition. The chain is one HIP graph replayed `reps` times
     (eager=True launches it from the host each time instead; on a CPU device always)."""
-    run = _chain(fn, inputs, chain)
+    run = chain_of(fn, inputs, chain)
     if DEVICE == "cuda" and not eager:
         g, _ = capture(run)
         per = replay_seconds(g, reps) / chain

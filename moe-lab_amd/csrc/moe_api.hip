@@ -101,7 +101,13 @@ int check_experts(const moe_experts_t* w) {
 
 extern "C" {
 
-const char* moe_version(void) { return "moe_mi355x 0.2 (gfx950, wave64)"; }
+const char* moe_version(void) { return "moe_mi355x 0.3 (gfx950, wave64)"; }
+
+int moe_probe_read(const void* src, size_t nbytes, uint32_t* sink, void* stream) {
+    if (!src || !sink || nbytes < 16 || nbytes % 16) return MOE_ERR_ARG;
+    if (!aligned16(src)) return MOE_ERR_ALIGN;
+    return moe::launch_probe_read(src, nbytes, sink, (hipStream_t)stream);
+}
 
 size_t moe_row_bytes(int fmt, int K) {
     if (K < 64 || K % 64) return 0;

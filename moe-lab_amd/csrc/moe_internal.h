@@ -114,6 +114,8 @@ int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tile
 // + bd[idx[t*k + j]])
 int launch_combine(const float* yp, int nplanes, size_t plane, const int32_t* idx, const float* wts, const float* bd, int E,
                    const void* residual, void* y, int T, int k, int d, int ydt, hipStream_t st);
+// guard probe (moe_probe.hip): XOR-fold a stream of 16-byte loads over nbytes into sink[MOE_PROBE_SINK]
+int launch_probe_read(const void* src, size_t nbytes, uint32_t* sink, hipStream_t st);
 // fp16 / fp32 activations x [T, d] -> bf16 planes [2 or 3][T, d] whose sum is x exactly (moe_experts.hip)
 int launch_x_planes(const void* x, int xdt, int T, int d, uint16_t* planes, hipStream_t st);
 

@@ -5,11 +5,13 @@ this machine's history:
     reference = 90th percentile of the last N_HISTORY probes recorded under the same device key,
     status    = "contended" if min(probes) < THRESH * reference, else "ok";
     fewer than MIN_HISTORY probes in the history -> "calibrating" (no verdict yet).
-The probe reads a 512 MiB fp16 buffer (twice the MI355X's 256 MB memory-side cache, so it measures HBM and
-not the cache) with a sum reduction, median of 9 calls timed by HIP events. The device key is the GPU's
+The probe streams a 512 MiB buffer (twice the MI355X's 256 MB memory-side cache, so it measures HBM and not the
+cache) with this library's read kernel (moe_probe_read: 16-byte loads, nothing else), median of 9 launches timed by
+HIP events. The device key is the GPU's
 name, gfx target and compute-unit count plus the host name (reference guard.py keys by chip and power source).
 The history is JSON at $MOELAB_AMD_PROBE_HISTORY, else ~/.cache/moelab_amd/hw_probe.json.
 """
+import ctypes
 import json
 import os
 import socket
@@ -33,20 +35,29 @@ def key():
 
 
 def probe(n_bytes=1 << 29, reps=9):
-    """GB/s of a read-bound fp16 sum over n_bytes on cuda:0 (median of `reps` timed calls)."""
+    """GB/s of this library's streaming-read probe (moe_probe_read: 16-byte loads, the expert kernels' weight-load
+    pattern) over n_bytes on cuda:0, median of `reps` launches timed by HIP events on the current stream."""
     import torch
-    a = torch.rand(n_bytes // 2, device="cuda", dtype=torch.float16)
-    a.sum()
+    from . import _lib
+    L = _lib.lib()
+    buf = torch.full((n_bytes,), 0x5A, dtype=torch.uint8, device="cuda")
+    sink = torch.empty(_lib.PROBE_SINK, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream()
+
+    def launch():
+        _lib.check("moe_probe_read", L.moe_probe_read(_lib.ptr(buf), n_bytes, _lib.ptr(sink),
+                                                      ctypes.c_void_p(st.cuda_stream)))
+    launch()
     torch.cuda.synchronize()
     ts = []
     for _ in range(reps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        a.sum()
-        e1.record()
+        e0.record(st)
+        launch()
+        e1.record(st)
         e1.synchronize()
         ts.append(e0.elapsed_time(e1) / 1e3)
-    del a
+    del buf, sink
     return float(n_bytes / np.median(ts) / 1e9)
 
 

@@ -13,6 +13,24 @@ from moelab_amd.shapes import MoEShape  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("nbytes", [16, 3 * (1 << 20) + 48, 1 << 24])
+def test_probe_read_folds_every_word(nbytes):
+    """moe_probe_read reads every 16-byte chunk once: the XOR of its sink equals the XOR of the buffer's words
+    (a length that is not a multiple of a workgroup's 16 KB block included)."""
+    import numpy as np
+    import torch
+    from moelab_amd import _lib
+    g = torch.Generator(device="cuda").manual_seed(nbytes)
+    buf = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device="cuda", generator=g)
+    sink = torch.full((_lib.PROBE_SINK,), 7, dtype=torch.int32, device="cuda")
+    _lib.check("moe_probe_read", _lib.lib().moe_probe_read(_lib.ptr(buf), nbytes, _lib.ptr(sink),
+                                                           _lib.stream_of(buf.device)))
+    want = np.bitwise_xor.reduce(buf.cpu().numpy().view(np.uint32))
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    assert got == want
+    assert _lib.lib().moe_probe_read(_lib.ptr(buf), 24, _lib.ptr(sink), None) == _lib.MOE_ERR_ARG
+
+
 def test_guard_probe_reads_hbm():
     gbs = guard.probe()
     print(f"probe {gbs:.0f} GB/s", flush=True)
@@ -21,23 +39,24 @@ def test_guard_probe_reads_hbm():
 
 def test_slope_of_a_chain():
     sh = MoEShape("slope", 256, 384, 8, 2)
-    mod = be.load_variant(__graft_entry__.PKG_DIR + "/variants/hip_q4_moe.py")
-    st = mod.prepare(*be.make_weights(sh, "bfloat16"))
-    inp = [be.make_inputs(sh, 1, "bfloat16", "uniform", seed=s) for s in range(16)]
-    per, fixed = slope.fit(lambda *z: mod.run(st, *z), inp, chains=(4, 8, 16))
-    print(f"per-call {per:.2f} us, fixed {fixed:.1f} us", flush=True)
-    assert 0.5 < per < 500.0
+    carry, (res,) = slope.run(sh, ["hip_q4_moe"], tokens=1, lengths=(4, 8, 16), windows=16)
+    print(f"carry {carry.per_call_us:.2f} us, per-call {res.per_call_us:.2f} us, own {res.own_us:.2f} us", flush=True)
+    assert 0.5 < res.per_call_us < 500.0 and res.own_us < res.per_call_us and res.floor_us > 0
 
 
-def test_compare_two_launches(tmp_path, monkeypatch):
+@pytest.mark.parametrize("in_process", [True, False])
+def test_compare_two_launches(tmp_path, monkeypatch, in_process):
+    """Two launches of the same variant as both arms: in this process, and as spawned launch processes."""
     monkeypatch.setenv("MOELAB_AMD_PROBE_HISTORY", str(tmp_path / "hist.json"))
     out = tmp_path / "cmp.json"
-    summary = compare.main(["hip_q4_moe", "hip_q4_moe", "--dims", "256,384,8,2", "--tokens", "1", "4",
-                            "--launches", "2", "--rounds", "2", "--windows", "2", "--out", str(out)])
-    assert [s["T"] for s in summary] == [1, 4]
-    for s in summary:
-        assert s["n"] == 4 and 0.5 < s["speedup_B_over_A"] < 2.0
-        assert 0.0 < s["ci95"][0] <= s["ci95"][1]
-        assert s["errA"] < 1e-2 and s["errB"] < 1e-2
+    args = ["hip_q4_moe", "hip_q4_moe", "--dims", "256,384,8,2", "--tokens", "1", "4", "--launches", "2",
+            "--rounds", "2", "--windows", "2", "--json", str(out)] + (["--in-process"] if in_process else [])
+    summaries = compare.main(args)
+    assert [s["tokens"] for s in summaries] == [1, 4]
+    for s in summaries:
+        assert s["replays"] == 4 and 0.5 < s["ratio"] < 2.0
+        assert 0.0 < s["interval95"][0] <= s["interval95"][1]
+        assert s["max_over_rms"]["A"] < 1e-2 and s["max_over_rms"]["B"] < 1e-2
     rec = json.load(open(out))
     assert len(rec["probes"]) == 4 and rec["guard"]["status"] == "calibrating"
+    assert {r["arm"] for r in rec["rows"]} == {"A", "B"} and len(rec["rows"]) == 2 * 2 * 2 * 2

@@ -1,5 +1,5 @@
 """A/B harness, slope fit and contention guard (host logic, CPU): moe-lab_amd/compare.py, slope.py, guard.py
-against closed forms and an exhaustive enumeration of the two-stage bootstrap on a tiny case."""
+against closed forms and an exhaustive enumeration of both bootstrap draws on a tiny case."""
 import itertools
 import json
 
@@ -12,39 +12,55 @@ __graft_entry__.load_package()
 from moelab_amd import compare, guard, slope  # noqa: E402
 
 
-def rows_of(per_launch):
-    return [{"launch": L, "A_us": a, "B_us": b} for L, rs in enumerate(per_launch) for a, b in rs]
+def rows_of(per_launch, tokens=1):
+    """Long-format rows from per-launch lists of (A us, B us) rounds."""
+    out = []
+    for L, rs in enumerate(per_launch):
+        for rd, (ua, ub) in enumerate(rs):
+            out += [{"launch": L, "tokens": tokens, "round": rd, "arm": "A", "us_per_call": ua},
+                    {"launch": L, "tokens": tokens, "round": rd, "arm": "B", "us_per_call": ub}]
+    return out
 
 
-def test_boot_ci_closed_forms():
-    a = np.linspace(90.0, 110.0, 12)
-    assert compare.boot_ci(a, a) == (1.0, 1.0, 1.0)
-    sp, lo, hi = compare.boot_ci(a, a / 2)
-    assert sp == 2.0 and abs(lo - 2.0) < 1e-12 and abs(hi - 2.0) < 1e-12
+def test_interval_closed_forms():
+    a = np.linspace(90.0, 110.0, 12).reshape(3, 4)
+    assert compare.Interval.of(a, a) == compare.Interval(1.0, 1.0, 1.0)
+    iv = compare.Interval.of(a, a / 2, by_launch=False)
+    assert iv.ratio == 2.0 and abs(iv.lo - 2.0) < 1e-12 and abs(iv.hi - 2.0) < 1e-12
 
 
-def test_boot_ci_interval_covers_and_is_seeded():
+def test_interval_covers_and_is_seeded():
     rng = np.random.default_rng(1)
-    a, b = rng.normal(100, 5, 40), rng.normal(50, 2.5, 40)
-    sp, lo, hi = compare.boot_ci(a, b, seed=3)
-    assert lo < sp < hi and hi - lo < 0.2
-    assert compare.boot_ci(a, b, seed=3) == (sp, lo, hi)
+    a, b = rng.normal(100, 5, (5, 8)), rng.normal(50, 2.5, (5, 8))
+    iv = compare.Interval.of(a, b, seed=3)
+    assert iv.lo < iv.ratio < iv.hi and iv.hi - iv.lo < 0.2
+    assert compare.Interval.of(a, b, seed=3) == iv
 
 
-def test_hier_bootstrap_matches_enumeration():
-    """2 launches x 2 rounds: every replicate is one of finitely many equally likely draws (launch picks, then
-    round picks inside each pick); the sampled frequencies match the enumerated probabilities."""
-    per = [[(10.0, 5.0), (12.0, 5.0)], [(30.0, 10.0), (20.0, 10.0)]]
-    rows = rows_of(per)
+def _enumerate(per, by_launch):
+    """Exact distribution of the replicate ratio for a tiny [launch, round] case: every launch pick (or the launches
+    as they are) times every round pick inside each, all equally likely."""
+    L, R = len(per), len(per[0])
+    picks = itertools.product(range(L), repeat=L) if by_launch else [tuple(range(L))]
+    picks = list(picks)
     exact = {}
-    for picks in itertools.product(range(2), repeat=2):
-        for r0 in itertools.product(range(2), repeat=2):
-            for r1 in itertools.product(range(2), repeat=2):
-                samp = [per[picks[0]][i] for i in r0] + [per[picks[1]][i] for i in r1]
-                a, b = zip(*samp)
-                v = round(float(np.median(a) / np.median(b)), 9)
-                exact[v] = exact.get(v, 0.0) + 1.0 / 64
-    got = compare.hier_samples(rows, n=40000, seed=5)
+    for pk in picks:
+        for rounds in itertools.product(itertools.product(range(R), repeat=R), repeat=L):
+            samp = [per[pk[i]][j] for i in range(L) for j in rounds[i]]
+            a, b = zip(*samp)
+            v = round(float(np.median(a) / np.median(b)), 9)
+            exact[v] = exact.get(v, 0.0) + 1.0 / (len(picks) * R ** (R * L))
+    return exact
+
+
+@pytest.mark.parametrize("by_launch", [True, False])
+def test_resample_matches_enumeration(by_launch):
+    """2 launches x 2 rounds: the sampled replicate frequencies match the enumerated probabilities of the two-stage
+    draw (launches, then rounds inside each drawn launch) and of the rounds-only draw (launches fixed)."""
+    per = [[(10.0, 5.0), (12.0, 5.0)], [(30.0, 10.0), (20.0, 10.0)]]
+    a, b = compare.paired_arrays(rows_of(per), 1)
+    exact = _enumerate(per, by_launch)
+    got = compare.resample(a, b, 40000, seed=5, by_launch=by_launch)
     vals, counts = np.unique(np.round(got, 9), return_counts=True)
     freq = dict(zip(vals.tolist(), (counts / got.size).tolist()))
     assert set(freq) <= set(exact)
@@ -52,27 +68,39 @@ def test_hier_bootstrap_matches_enumeration():
         assert abs(freq.get(v, 0.0) - p) < 0.01, (v, p, freq.get(v))
 
 
-def test_hier_interval_wider_than_rounds_when_launches_differ():
+def test_launch_interval_wider_than_rounds_when_launches_differ():
     rng = np.random.default_rng(2)
     per = [[(100.0 * f + rng.normal(0, 0.1), 50.0) for _ in range(6)] for f in (0.9, 1.0, 1.1, 0.95, 1.05)]
-    rows = rows_of(per)
-    lo, hi = compare.boot_ci_hier(rows)
-    _, rlo, rhi = compare.boot_ci([r["A_us"] for r in rows], [r["B_us"] for r in rows])
-    assert hi - lo > 1.5 * (rhi - rlo)
+    (s,) = [compare.summary_of(rows_of(per), 1)]
+    wide = s["interval95"][1] - s["interval95"][0]
+    narrow = s["interval95_rounds"][1] - s["interval95_rounds"][0]
+    assert wide > 1.5 * narrow
 
 
-def test_summarize_fields():
-    rows = [dict(r, T=1, errA=1e-3, errB=2e-3) for r in rows_of([[(10.0, 5.0), (11.0, 5.0)], [(9.0, 4.5)]])]
-    (s,) = compare.summarize(rows, [1])
-    assert s["n"] == 3 and s["per_launch"] == [2.1, 2.0] and s["speedup_B_over_A"] == 2.0
+def test_summary_fields_and_missing_rounds():
+    rows = rows_of([[(10.0, 5.0), (11.0, 5.0)], [(9.0, 4.5), (9.0, 4.5)]])
+    checks = [{1: {"A": 1e-3, "B": 2e-3}}, {1: {"A": 3e-3, "B": 1e-3}}]
+    s = compare.summary_of(rows, 1, checks)
+    assert s["replays"] == 4 and s["launch_ratios"] == [2.1, 2.0] and s["ratio"] == 9.5 / 4.75
+    assert s["max_over_rms"] == {"A": 3e-3, "B": 2e-3}
+    with pytest.raises(ValueError):
+        compare.paired_arrays(rows[:-1], 1)
 
 
-def test_slope_fit_recovers_line():
-    chains = (10, 20, 40, 80)
-    s, c = slope.fit_line(chains, [3e-6 + 2.5e-6 * ch for ch in chains])
+def test_slope_estimators():
+    xs = (8, 16, 32, 64)
+    s, c = slope.theil_sen(xs, [3e-6 + 2.5e-6 * n for n in xs])
     assert abs(s - 2.5e-6) < 1e-15 and abs(c - 3e-6) < 1e-15
-    per, fixed = slope.fit(None, None, chains, timer=lambda fn, inp, ch: 7e-6 + 1.25e-6 * ch)
-    assert abs(per - 1.25) < 1e-9 and abs(fixed - 7.0) < 1e-9
+    ys = [3e-6 + 2.5e-6 * n for n in xs]
+    ys[1] += 40e-6   # one disturbed length
+    s2, _ = slope.theil_sen(xs, ys)
+    l2, _ = slope.least_squares(xs, ys)
+    assert abs(s2 - 2.5e-6) < 0.5e-6 and abs(l2 - 2.5e-6) > abs(s2 - 2.5e-6)
+    line = slope.measure(None, None, xs, timer=lambda fn, w, n: 7e-6 + 1.25e-6 * n)
+    assert abs(line.per_call_us - 1.25) < 1e-9 and abs(line.fixed_us - 7.0) < 1e-9
+    assert abs(line.lsq_per_call_us - 1.25) < 1e-9 and sorted(line.points) == list(xs)
+    with pytest.raises(ValueError):
+        slope.theil_sen([4, 4], [1.0, 2.0])
 
 
 def test_guard_verdict_history(tmp_path):
@@ -107,3 +135,21 @@ def test_grid_crossover_and_fitted_policy():
         assert not hip_mxfp4_moe.grouped(t_slots, k, E, D, F) and hip_mxfp4_moe.grouped(t_grouped, k, E, D, F)
     assert hip_q4_moe.custom_wins(2, 2, 8, 4096, 14336) and hip_q4_moe.custom_wins(512, 2, 8, 4096, 14336)
     assert fallback.grouped_from_load(2048, 768) == 1.0 and fallback.grouped_from_load(4096, 14336) == 0.27
+
+
+def test_reference_skips_ids_outside_range():
+    """backend.reference follows the library's contract: a slot whose id is outside [0, E) adds nothing (the same
+    result as that slot pointing at expert 0 with weight 0)."""
+    import torch
+    from moelab_amd import backend as be
+    g = torch.Generator().manual_seed(3)
+    E, d, F = 4, 8, 16
+    wg, wu = torch.randn(E, F, d, generator=g), torch.randn(E, F, d, generator=g)
+    wd = torch.randn(E, d, F, generator=g)
+    x = torch.randn(3, d, generator=g)
+    idx = torch.tensor([[0, -1], [5, 2], [1, 1]], dtype=torch.int32)
+    wts = torch.rand(3, 2, generator=g)
+    keep = (idx >= 0) & (idx < E)
+    y = be.reference(wg, wu, wd, x, idx, wts)
+    y2 = be.reference(wg, wu, wd, x, torch.where(keep, idx, torch.zeros_like(idx)), wts * keep)
+    assert torch.allclose(y, y2, atol=1e-6) and y.abs().sum() > 0
