@@ -174,8 +174,10 @@ int moe_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offset
  *   grouped calls with more than 16 slots per expert on average (prefill-sized T, path MOE_PATH_GROUPED with
  *   the tile-major copies) run the down projection, and above 32 also the gate/up, on fp16 MFMA: weights
  *   rounded once to fp16 from the row-exponent-scaled metadata, x and h carried as fp16 with a power-of-two
- *   exponent per row (no overflow for large rows, no flush to zero for small ones; any scale range); ~1e-3 of
- *   the outputs' RMS in the worst case measured.
+ *   exponent per row (no overflow and no flush to zero whatever a row's absolute scale); within a row, weights
+ *   more than 2^13 below the row's largest |16 s|, |b| fall into fp16's subnormal range (absolute step 2^-19 of
+ *   the row's largest |s|, |b|); ~1e-3 of the outputs' RMS in the worst case measured, 1.4e-3 with one scale
+ *   group per row at 256x the others' (numpy emulation).
  *   Requirements: d % 64 == 0, F % 64 == 0, F <= 16384; x, y, rows 16-byte aligned.
  *   workspace: moe_experts_workspace_bytes(...) bytes (any contents; every call writes what it reads). Calls
  *   sharing a workspace must be stream-ordered.

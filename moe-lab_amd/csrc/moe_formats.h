@@ -37,10 +37,12 @@ __host__ __device__ __forceinline__ const int8_t* tile_row_exps(const uint8_t* t
     return reinterpret_cast<const int8_t*>(tiles + (size_t)E * tile_rec_bytes(MOE_FMT_INT4_G64, N, K));
 }
 // Row exponent of an int4 row from amax, the largest bf16 magnitude bits (sign cleared) over the row's scales and
-// biases: the records hold s 2^-E and b 2^-E (exact in bf16), which puts the row's largest at [2^10, 2^11), so
-// every w = s q + b of the row stays below 2^15 in magnitude and values down to 2^-24 of the row's largest stay
-// normal fp16 numbers where the dense tiles dequantise to fp16. E = (biased exponent of amax) - 127 - 10, clamped to
-// [-120, 120] (bf16 subnormals: -120); 0 for an all-zero row or one holding an inf or NaN.
+// biases: the records hold s 2^-E and b 2^-E (exact in bf16), which puts the row's largest at [2^10, 2^11) whatever
+// the row's absolute scale. The dense tiles dequantise to fp16 w' = (s q + b) 2^-E 2^-16, below 2^-1 in magnitude:
+// weights down to 2^-13 of that bound are normal fp16 numbers, smaller ones round to fp16's subnormal step 2^-24
+// (2^-19 of the row's largest |s|, |b| in the same units), so a row's within-row dynamic range, not its absolute
+// scale, is what limits their precision. E = (biased exponent of amax) - 127 - 10, clamped to [-120, 120] (bf16
+// subnormals: -120); 0 for an all-zero row or one holding an inf or NaN.
 __host__ __device__ __forceinline__ int int4_row_exponent(uint32_t amax) {
     const int ef = (int)(amax >> 7);
     if (amax == 0 || ef >= 0xFF) return 0;

@@ -308,6 +308,35 @@ def test_small_affine_scales_dense_tiles(case, T, monkeypatch):
     assert_close(y, ref, what=(case, T, "bf16 out"))
 
 
+@pytest.mark.parametrize("spread", [64, 256])
+@pytest.mark.parametrize("T", [50, 200])
+def test_dense_tiles_within_row_scale_spread(spread, T, monkeypatch):
+    """The dense tiles' fp16 weights carry one power-of-two scale per row (the largest |s|, |b| of the row), so a row
+    whose scale groups differ a lot keeps its small groups' weights near fp16's subnormal range. Here the first scale
+    group of every row of every projection has `spread` times the others' scale and the activations entering that
+    group are 100x smaller, so the output comes from the small groups: it must still meet the gate (the decode bounds
+    |w'| by 2^-1, so weights reach the subnormal range only 2^13 below the row's largest). T=200 runs the dense tiles
+    on both projections, T=50 the wave gate/up into the dense down."""
+    from moelab_amd.experts import make_state, unpack
+    monkeypatch.setenv("MOE_DENSE", "1")
+    sh = shape_("spread", 256, 384, 4, 2)
+    base = packed_state(sh, 21)
+    parts = {n: list(unpack(base, n)) for n in ("g", "u", "d")}
+    for n in parts:
+        sc = parts[n][1].float()
+        sc[..., 0] *= spread
+        parts[n][1] = sc.to(torch.bfloat16)
+        parts[n][2] = (parts[n][1].float() * -8.0).to(torch.bfloat16)
+    s = make_state("int4", parts["g"], parts["u"], parts["d"])
+    x, idx, wts = inputs(sh, T, "uniform", seed=T)
+    x = x.float()
+    x[:, :64] *= 0.01     # the large group's inputs of the gate/up
+    x = x.to(torch.bfloat16)
+    print(f"case dense scale spread {spread} T={T}", flush=True)
+    y32 = grouped(s, x, idx, wts, out_dtype=torch.float32)
+    assert_close(y32, oracle_y(s, x, idx, wts), what=("spread", spread, T))
+
+
 @pytest.mark.parametrize("fmt", ["int4", "mxfp4"])
 @pytest.mark.parametrize("N,K", [(16, 128), (48, 192), (32, 2048), (48, 2880)])
 def test_tiles_pack_matches_host_restatement(fmt, N, K):
