@@ -16,7 +16,8 @@
  *   - outputs and workspace are caller-allocated; sizes come from the *_workspace_bytes queries;
  *   - return 0 on success, a negative MOE_ERR_* code on invalid arguments (checked before any
  *     launch; mirrors the reference's shape asserts, e.g. metal_q4_moe.py:34) or launch failure;
- *   - reentrant: no global mutable state; calls that share a workspace must be stream-ordered.
+ *   - reentrant; calls that share a workspace must be stream-ordered. The library's only mutable state is the table
+ *     of moe_experts_run_static's array addresses, one per device, filled once under a lock (and that array).
  */
 #ifndef MOE_MI355X_H
 #define MOE_MI355X_H
@@ -196,8 +197,9 @@ size_t moe_experts_workspace_bytes(const moe_experts_t* w, int T, int k, int pat
  * to 110 tokens).
  * It allocates nothing. Every call on one GPU uses that GPU's one array, which keeps the last call's contents (no
  * call needs particular contents): calls that overlap on one GPU (other streams, other threads) race, and the
- * caller must order them. The first call on each device looks up the array's address (hipGetSymbolAddress);
- * make it outside graph capture: a call with T = 0 does only that.
+ * caller must order them. The first call on each device (the device of `stream`; the current device for the null
+ * stream) looks up the array's address (hipGetSymbolAddress); make it outside graph capture: a call with T = 0 does
+ * only that.
  */
 #define MOE_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
 int moe_experts_run_static(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts,

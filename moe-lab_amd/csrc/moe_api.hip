@@ -18,15 +18,21 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// the device address of `scratch` on the current device, looked up on the first call there
-int static_scratch(void** out) {
+// the device address of `scratch` on the device the stream belongs to (the current device for the null stream),
+// looked up on the first call there with that device current, then kept: the library's one table of mutable state
+int static_scratch(hipStream_t st, void** out) {
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess) return MOE_ERR_LAUNCH;
+    if (st ? hipStreamGetDevice(st, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) return MOE_ERR_LAUNCH;
     if (dev < 0 || dev >= kMaxDevices) return MOE_ERR_ARG;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess) return MOE_ERR_LAUNCH;
+        if (cur != dev && hipSetDevice(dev) != hipSuccess) return MOE_ERR_LAUNCH;
         void* p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MOE_ERR_LAUNCH;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev && hipSetDevice(cur) != hipSuccess) return MOE_ERR_LAUNCH;
+        if (e != hipSuccess || !p) return MOE_ERR_LAUNCH;
         g_scratch_ptr[dev] = p;
     }
     *out = g_scratch_ptr[dev];
@@ -248,7 +254,7 @@ int moe_experts_run_static(const moe_experts_t* w, const void* x, int x_dtype, c
                            int T, int k, int act, int path, int nored, void* y, int y_dtype, const void* residual,
                            void* stream) {
     void* ws = nullptr;
-    int rc = static_scratch(&ws);   // first call on a device: the lookup; later calls: a table read
+    int rc = static_scratch((hipStream_t)stream, &ws);   // first call on a device: the lookup; then a table read
     if (rc) return rc;
     if (T == 0) return MOE_OK;
     if (!w || T < 0 || k < 1) return MOE_ERR_ARG;

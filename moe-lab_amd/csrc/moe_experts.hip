@@ -773,15 +773,11 @@ int launch_dn_rows_k(const ExpertsArgs& a, int lgL) {
     const ProjPtrs P = ptrs(w);
     auto kern = k_down_rows<FMT, NC, RR, NW>;
     const int lds = down_rows_lds(a.k, w->F);
-    if (lds > 64 * 1024) {
-        static bool attr_set = false;   // per instantiation; setting it twice is harmless
-        if (!attr_set) {
-            if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, DR_LDS_MAX) !=
-                hipSuccess)
-                return MOE_ERR_LAUNCH;
-            attr_set = true;
-        }
-    }
+    // above 64 KB of LDS the kernel needs the attribute on the device it runs on: set on every such launch (a host
+    // call, no stream work) rather than remembered, so no state is kept and every device gets it
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, DR_LDS_MAX) != hipSuccess)
+        return MOE_ERR_LAUNCH;
     dim3 grid((w->d + NW * RR - 1) / (NW * RR), a.T);
     kern<<<grid, 64 * NW, lds, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.idx, a.wts, a.k, w->d, w->F, w->E, lgL,
                                    a.nored, a.ydt, a.residual, a.y);

@@ -1307,8 +1307,11 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
 // The words keep the records' nibble order (e0 e2 e4 e6 e1 e3 e5 e7); the activation terms are written in that
 // order instead. The activations enter as a sum of fp8 terms, each with an E8M0 byte per (token, 32 inputs): term t of a block
 // has scale 2^e, e = floor(log2 max |r|) - 7 (|r / 2^e| < 256, inside E4M3's range), q = E4M3(r / 2^e) and
-// r -= q 2^e (exact). Two terms hold bf16 x, three hold h = hi + lo; measured on this part, the instruction's own
-// accumulation keeps ~2e-5 of the outputs' RMS (two to four terms give the same result), against the 1e-2 RMS gate.
+// r -= q 2^e (exact). Two terms hold a bf16 x exactly for every input within ~2^12 of its 32-block's largest
+// magnitude (4 significant bits each); smaller inputs fall into E4M3's subnormal range in both terms and keep an
+// absolute error below the second term's step, 2^-20 of the block's largest. Three terms hold h = hi + lo to ~12
+// bits. Measured on this part, the instruction's own accumulation keeps ~2e-5 of the outputs' RMS (two to four terms
+// give the same result), against the 1e-2 RMS gate.
 
 // x rows (bf16) -> per (row, 128-input slice) records of REC = 16 (8 NTERM + 1) bytes: NTERM x 128 bytes of terms
 // at mx_pos (the records' code order, then the A operand's lane order), then the E8M0 byte of term t, block b at

@@ -115,6 +115,21 @@ def test_mxscale_wide_activation_range(monkeypatch):
     assert e1["max_abs"] <= 2e-3 * e1["rms_ref"], e1
 
 
+def test_mxscale_block_spanning_2_16(monkeypatch):
+    """One input of every 32-input block at 2^16 times the others: x's two fp8 terms (each with the block's own E8M0
+    scale from its largest residual) then keep the small inputs only to the second term's E4M3 subnormal step,
+    2^-20 of the block's largest, not exactly; the output still holds the gate, and the 2e-3 RMS bound."""
+    sh, s = state("span", 512, 512, 4, 2, seed=13)
+    x, idx, wts = inputs(sh, 96, "uniform", seed=13)
+    xs = x.float()
+    xs[:, 5::32] = 65536.0 * torch.sign(xs[:, 5::32])
+    x = xs.to(torch.bfloat16)
+    print("case mxscale block spanning 2^16", flush=True)
+    y1, _ = both(monkeypatch, s, x, idx, wts)
+    e1 = assert_close(y1, oracle_y(s, x, idx, wts), what="span 2^16")
+    assert e1["max_abs"] <= 2e-3 * e1["rms_ref"], e1
+
+
 def test_mxscale_stages_split(monkeypatch):
     """Gate/up and down as two calls (h kept in the workspace between them) equal the whole call bit for bit."""
     from moelab_amd import _lib
