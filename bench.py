@@ -20,7 +20,8 @@ duration.
 
 cpu_baseline: the reference's CPU torch path (torch_loop, reference variants/cuda/torch_loop.py:11-17)
 on dequantised fp32 weights of the selected experts, timed on this host for a bounded sample of layers.
-cpu_points: the same path at config 3's T=32 (one layer) and on 32-token samples of configs 5a and 5b.
+cpu_points: the same path at config 3's T=16, 32 and 64 (one layer each), config 4 at T=1 and T=32 (gpt-oss MXFP4 with
+biases and the clamped SwiGLU), and on 32-token samples of configs 5a and 5b.
 """
 import argparse
 import json
@@ -193,9 +194,11 @@ def main():
         cpu_layers = [baseline_int4_layer(sh, seed=1000 + l, device=dev) for l in range(args.cpu_layers)]
         cpu = cpu_baseline(cpu_layers, routes1[:args.cpu_layers], x1, sh)
         log(f"CPU baseline: {cpu['value']:.1f} us/layer on {cpu['cores']} threads")
-        if (32, "uniform") in routes_b:   # config 3 at T=32 (the first seeded layer of the GPU chain)
-            xT, routes = routes_b[(32, "uniform")]
-            cpu_points["qwen3_T32_uniform"] = cpu_point([cpu_layers[0]], [routes[0]], xT, sh, "T=32 uniform", 4.0)
+        for T in (16, 32, 64):   # config 3 (the first seeded layer of the GPU chain)
+            if (T, "uniform") in routes_b:
+                xT, routes = routes_b[(T, "uniform")]
+                cpu_points[f"qwen3_T{T}_uniform"] = cpu_point([cpu_layers[0]], [routes[0]], xT, sh, f"T={T} uniform",
+                                                             3.0)
         cpu_points.update(cpu_large_points(dev))
         for name, r in cpu_points.items():
             log(f"CPU {name}: {r['value']:.1f} {r['unit']} ({r['sample']})")
@@ -475,9 +478,10 @@ def cpu_baseline(layers, routes, x, sh):
     return r
 
 
-def cpu_point(layers, routes, x, sh, what, budget_s):
-    """torch_loop (the reference's CPU torch path) on fp32 dense copies of the selected experts of int4 SwiGLU
-    layers: a residual chain over `layers`, repeated for about budget_s seconds; microseconds per layer-call."""
+def cpu_point(layers, routes, x, sh, what, budget_s, fmt="int4", act=0):
+    """torch_loop (the reference's CPU torch path) on fp32 dense copies of the selected experts (int4 or MXFP4, with
+    the state's additive biases when it has them; act 2: gpt-oss's clamped SwiGLU): a residual chain over `layers`,
+    repeated for about budget_s seconds; microseconds per layer-call."""
     from moelab_amd import formats
     from moelab_amd.experts import unpack
     orc = __graft_entry__.load_oracle()
@@ -487,14 +491,18 @@ def cpu_point(layers, routes, x, sh, what, budget_s):
         sel = sorted(set(idx.flatten().tolist()))
         w = {}
         for n in ("g", "u", "d"):
-            codes, sc, bi = unpack(ly, n)
-            w[n] = {e: formats.dequant_int4(codes[e], sc[e], bi[e]).cpu() for e in sel}
-        dense.append((w, idx.cpu().long(), wts.cpu()))
+            p = unpack(ly, n)
+            deq = (lambda e: formats.dequant_int4(p[0][e], p[1][e], p[2][e])) if fmt == "int4" else \
+                (lambda e: formats.dequant_mxfp4(p[0][e], p[1][e]))
+            w[n] = {e: deq(e).float().cpu() for e in sel}
+        b = {n: {e: ly[n][e].float().cpu() for e in sel} for n in ("bg", "bu", "bd") if n in ly}
+        dense.append((w, b, idx.cpu().long(), wts.cpu()))
 
     def once():
         y = xs
-        for w, idx, wts in dense:
-            y = y + orc.torch_loop(w["g"], w["u"], w["d"], y, idx, wts)
+        for w, b, idx, wts in dense:
+            y = y + orc.torch_loop(w["g"], w["u"], w["d"], y, idx, wts, act=act, bg=b.get("bg"), bu=b.get("bu"),
+                                   bd=b.get("bd"))
         return y
     once()
     t0 = time.perf_counter()
@@ -506,19 +514,28 @@ def cpu_point(layers, routes, x, sh, what, budget_s):
     T = x.shape[0]
     return {"value": round(dt * 1e6, 1), "unit": "us/layer", "tokens_per_s": round(T / dt, 1),
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{len(dense)} {sh.name} int4 layer(s) at {what} (T={T}, k={sh.k}, selected experts "
-                      f"dequantised to fp32), {reps} reps, ~{budget_s:.0f} s"}
+            "sample": f"{len(dense)} {sh.name} {fmt} layer(s) at {what} (T={T}, k={sh.k}, selected experts "
+                      f"dequantised to fp32{', biases, clamped SwiGLU' if act == 2 else ''}), {reps} reps, "
+                      f"~{budget_s:.0f} s"}
 
 
 def cpu_large_points(dev):
-    """BASELINE configs 5a and 5b on the CPU torch path, on a bounded sample: the first 32 tokens of the T=512 /
-    T=256 batch (uniform router logits) through one seeded layer; 5b's routed experts only (the shared experts
-    are two dense SwiGLU MLPs on every token, left out of this sample). Reported as us per layer-call of 32
-    tokens and tokens/s."""
+    """BASELINE configs 4, 5a and 5b on the CPU torch path, on bounded samples: config 4 (gpt-oss-20b MXFP4, biases,
+    clamped SwiGLU) at T=1 and T=32 through one seeded layer; 5a and 5b on the first 32 tokens of the T=512 / T=256
+    batch (uniform router logits) through one seeded layer, 5b's routed experts only (the shared experts are two
+    dense SwiGLU MLPs on every token, left out of this sample). Reported per layer-call and tokens/s."""
     from moelab_amd import router
-    from moelab_amd.problem import baseline_int4_layer, baseline_x
+    from moelab_amd.problem import baseline_int4_layer, baseline_mxfp4_layer, baseline_x
     from moelab_amd.shapes import SHAPES
     out = {}
+    sh = SHAPES["gpt-oss-20b"]
+    ly = baseline_mxfp4_layer(sh, seed=2000, device=dev)
+    for T in (1, 32):
+        x = baseline_x(T, sh.d, seed=T, device=dev)
+        out[f"gptoss20b_mxfp4_T{T}"] = cpu_point([ly], [router.route(x, ly["wr"], sh.k)], x, sh, f"T={T}", 3.0,
+                                                 fmt="mxfp4", act=2)
+    del ly
+    torch.cuda.empty_cache()
     for key, name, T in (("mixtral8x7b_int4_T512_32tok", "mixtral-8x7b", 512),
                          ("dsv2lite_int4_T256_32tok_routed", "deepseek-v2-lite", 256)):
         sh = SHAPES[name]

@@ -242,14 +242,30 @@ def error_metrics(y, y_ref):
     }
 
 
-def torch_loop(wg, wu, wd, x, idx, wts):
+def torch_loop(wg, wu, wd, x, idx, wts, act=0, bg=None, bu=None, bd=None):
     """The reference's eager CPU torch path (variants/cuda/torch_loop.py:11-17) on dense weights:
-    per unique expert, gather its (token, slot) pairs, two matmuls, SiLU, down matmul, index_add."""
+    per unique expert, gather its (token, slot) pairs, two matmuls, the GLU, down matmul, index_add.
+    act 0 is the reference's SiLU GLU; act 2 with the optional biases bg, bu [E, F], bd [E, d] is the gpt-oss
+    expert of the reference's fp32 truth (metal_mxfp4_gptoss.py:110-126: biases added to the gate/up products,
+    g = min(g, 7), u = clip(u, -7, 7), g sigmoid(1.702 g) (u + 1), the down bias inside the routing weight);
+    act 1 is the tanh-GELU GLU. wg, wu, wd, bg, bu, bd may be dicts {expert: tensor}."""
     import torch
     y = torch.zeros_like(x)
     for e in idx.unique().tolist():
         t, j = (idx == e).nonzero(as_tuple=True)
         xe = x[t]
-        h = torch.nn.functional.silu(xe @ wg[e].T) * (xe @ wu[e].T)
-        y.index_add_(0, t, (h @ wd[e].T) * wts[t, j, None].to(x.dtype))
+        g, u = xe @ wg[e].T, xe @ wu[e].T
+        if bg is not None:
+            g, u = g + bg[e], u + bu[e]
+        if act == 0:
+            h = torch.nn.functional.silu(g) * u
+        elif act == 1:
+            h = torch.nn.functional.gelu(g, approximate="tanh") * u
+        else:
+            g, u = g.clamp(max=7.0), u.clamp(-7.0, 7.0)
+            h = g * torch.sigmoid(1.702 * g) * (u + 1.0)
+        o = h @ wd[e].T
+        if bd is not None:
+            o = o + bd[e]
+        y.index_add_(0, t, o * wts[t, j, None].to(x.dtype))
     return y

@@ -358,3 +358,14 @@ def test_torch_loop_matches_reference(orc):
     t = lambda a: torch.from_numpy(np.asarray(a, np.float64))  # noqa: E731
     y = orc.torch_loop(t(wg), t(wu), t(wd), t(x), torch.from_numpy(idx).long(), t(wts))
     np.testing.assert_allclose(y.numpy(), orc.moe_reference(x, wg, wu, wd, idx, wts), rtol=1e-10)
+    # gpt-oss: biases and the clamped SwiGLU (x scaled so that both clamps engage), and the tanh-GELU GLU
+    bg, bu, bd = rng.standard_normal((6, 32)), rng.standard_normal((6, 32)), rng.standard_normal((6, 64))
+    xs = 40.0 * x
+    y2 = orc.torch_loop(t(wg), t(wu), t(wd), t(xs), torch.from_numpy(idx).long(), t(wts), act=2, bg=t(bg), bu=t(bu),
+                        bd=t(bd))
+    ref2 = orc.moe_reference(xs, wg, wu, wd, idx, wts, act=2, bg=bg, bu=bu, bd=bd)
+    np.testing.assert_allclose(y2.numpy(), ref2, rtol=1e-10, atol=1e-10)
+    g = xs @ wg[idx[0, 0]].T
+    assert (g > 7).any() and (xs @ wu[idx[0, 0]].T < -7).any()   # the clamps engage
+    y1 = orc.torch_loop(t(wg), t(wu), t(wd), t(x), torch.from_numpy(idx).long(), t(wts), act=1)
+    np.testing.assert_allclose(y1.numpy(), orc.moe_reference(x, wg, wu, wd, idx, wts, act=1), rtol=1e-10)
