@@ -40,22 +40,32 @@ constexpr int ROUTER_MAXC = 4;   // 16-byte chunks per lane held in registers pe
 // ids outside [0, E) are left out of every group (they contribute nothing) and counted in meta[1].
 // Outputs (o): counts[E], offsets[E+1], sorted[n] (valid part: offsets[E] entries), active[E] (first meta[0]
 // entries: experts with count > 0, ascending), meta[0] = number of active experts, meta[1] = bad ids.
-// With o.items (the grouped kernels' work list, pass size P): items[3w .. 3w + 2] = (expert, pass index q within the
-// expert (first token q * P), the expert's pass count) of pass w; the passes of each active expert in ascending
-// order, expert by expert; meta[2] = number of passes. o.items2 (pass size P2), if given, is a second such list,
-// meta[3] its number of passes (the wave tiles' and the dense tiles' lists when a call uses both).
-// sm: dynamic LDS. mw (the ids and one count array per wave fit there): the ids are read once into LDS, and each
-// wave places one contiguous share of the slots with its own cursors (the expert's offset plus the counts of the
-// shares before it), so the order stays ascending within every expert. Otherwise wave 0 places all slots.
+// With o.items (the grouped kernels' work list, pass size P, a power of two): items[3w .. 3w + 2] = (expert, pass
+// index q within the expert (first token q * P), the expert's pass count) of pass w; the passes of each active expert
+// in ascending order, expert by expert; meta[2] = number of passes. o.items2 (pass size P2), if given, is a second
+// such list, meta[3] its number of passes (the wave tiles' and the dense tiles' lists when a call uses both).
+// sm: dynamic LDS of group_lds_ints(n, E, NW, mw) ints. mw (the ids and one count array per wave fit there): the ids
+// are read once into LDS, and each wave places one contiguous share of the slots with its own cursors (the expert's
+// offset plus the counts of the shares before it), so the order stays ascending within every expert. Otherwise wave 0
+// places all slots. The offsets come from a two-level prefix sum: chunk ch of 64 experts belongs to wave ch % NW,
+// which scans it in-wave (DPP) and leaves its totals in LDS; after a barrier every wave adds the earlier chunks'
+// totals to its own.
+__host__ __device__ inline int group_lds_ints(int n, int E, int nw, int mw) {
+    return (mw ? nw * E + n : 2 * E) + 4 * ((E + 63) / 64);
+}
+
 template <typename LD>
 __device__ void group_block(LD ld, int n, int E, const GroupBufs& o, int P, int P2, int32_t* sm, int mw) {
-    const int NT = (int)blockDim.x;
-    const int NW = mw ? NT >> 6 : 1;
-    int32_t* cnt = sm;            // mw: cnt[NW][E], ids[n]; else cnt[E], cursor[E]
+    const int NT = (int)blockDim.x, NWT = NT >> 6;
+    const int NW = mw ? NWT : 1;
+    int32_t* cnt = sm;            // mw: cnt[NW][E], ids[n]; else cnt[E], cursor[E]; then the chunk totals
     int32_t* cur1 = sm + E;
     int32_t* sidx = sm + NW * E;
+    int32_t* tot = sm + (mw ? NW * E + n : 2 * E);   // [nch][4]: slots, active experts, passes, passes of list 2
     __shared__ int32_t s_bad;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nch = (E + 63) >> 6;
+    const int lgP = o.items ? __builtin_ctz((unsigned)P) : 0, lgP2 = o.items2 ? __builtin_ctz((unsigned)P2) : 0;
     for (int i = tid; i < NW * E; i += NT) cnt[i] = 0;
     if (tid == 0) s_bad = 0;
     __syncthreads();
@@ -100,60 +110,80 @@ __device__ void group_block(LD ld, int n, int E, const GroupBufs& o, int P, int 
         }
     }
     __syncthreads();
-    if (tid < 64) {   // wave 0: exclusive scan of counts and the active list, in chunks of 64 experts
-        int run = 0, run_act = 0, run_p = 0, run_p2 = 0;
-        for (int base = 0; base < E; base += 64) {
-            const int e = base + lane;
-            int c = 0;
-            if (e < E)
-                for (int w = 0; w < NW; ++w) c += cnt[w * E + e];
-            const int np = o.items ? (c + P - 1) / P : 0;      // passes of expert e
-            const int np2 = o.items2 ? (c + P2 - 1) / P2 : 0;  // in the second list
-            // inclusive wave scans of c, of (c > 0) and of the pass counts
-            const int inc = wave_incl_scan(c), act = wave_incl_scan(c > 0 ? 1 : 0);
-            const int incp = wave_incl_scan(np), incp2 = wave_incl_scan(np2);
-            if (e < E) {
-                const int excl = run + inc - c;
-                o.offsets[e] = excl;
-                o.counts[e] = c;
-                if (mw) {   // per-wave cursors: the earlier waves' slots come first
-                    int cc = excl;
-                    for (int w = 0; w < NW; ++w) {
-                        const int cw = cnt[w * E + e];
-                        cnt[w * E + e] = cc;
-                        cc += cw;
-                    }
-                } else {
-                    cur1[e] = excl;
-                }
-                if (c > 0) o.active[run_act + act - 1] = e;
-                const int w0 = run_p + incp - np;
-                for (int q = 0; q < np; ++q) {
-                    o.items[3 * (w0 + q)] = e;
-                    o.items[3 * (w0 + q) + 1] = q;
-                    o.items[3 * (w0 + q) + 2] = np;
-                }
-                const int w2 = run_p2 + incp2 - np2;
-                for (int q = 0; q < np2; ++q) {
-                    o.items2[3 * (w2 + q)] = e;
-                    o.items2[3 * (w2 + q) + 1] = q;
-                    o.items2[3 * (w2 + q) + 2] = np2;
-                }
-            }
-            run += __builtin_amdgcn_readlane(inc, 63);
-            run_act += __builtin_amdgcn_readlane(act, 63);
-            run_p += __builtin_amdgcn_readlane(incp, 63);
-            run_p2 += __builtin_amdgcn_readlane(incp2, 63);
+    // chunk ch's counts: expert e = 64 ch + lane, summed over the per-wave count arrays
+    auto chunk = [&](int ch, int& c, int& np, int& np2) __attribute__((always_inline)) {
+        const int e = 64 * ch + lane;
+        c = 0;
+        if (e < E)
+            for (int w = 0; w < NW; ++w) c += cnt[w * E + e];
+        np = o.items ? (c + P - 1) >> lgP : 0;      // passes of expert e
+        np2 = o.items2 ? (c + P2 - 1) >> lgP2 : 0;  // in the second list
+    };
+    for (int ch = wave; ch < nch; ch += NWT) {   // level 1: each chunk's totals
+        int c, np, np2;
+        chunk(ch, c, np, np2);
+        const int t0 = wave_incl_scan(c), t1 = wave_incl_scan(c > 0 ? 1 : 0);
+        const int t2 = wave_incl_scan(np), t3 = wave_incl_scan(np2);
+        if (lane == 63) {
+            tot[4 * ch] = t0;
+            tot[4 * ch + 1] = t1;
+            tot[4 * ch + 2] = t2;
+            tot[4 * ch + 3] = t3;
         }
-        if (lane == 0) {
-            o.offsets[E] = run;
-            o.meta[0] = run_act;
-            o.meta[1] = s_bad;
-            if (o.items) o.meta[2] = run_p;
-            if (o.items2) o.meta[3] = run_p2;
-        }
-        for (int a = run_act + lane; a < E; a += 64) o.active[a] = -1;
     }
+    __syncthreads();
+    int all_act = 0;
+    for (int ch = 0; ch < nch; ++ch) all_act += tot[4 * ch + 1];
+    for (int ch = wave; ch < nch; ch += NWT) {   // level 2: the earlier chunks' totals, then this chunk's outputs
+        int run = 0, run_act = 0, run_p = 0, run_p2 = 0;
+        for (int c2 = 0; c2 < ch; ++c2) {
+            run += tot[4 * c2];
+            run_act += tot[4 * c2 + 1];
+            run_p += tot[4 * c2 + 2];
+            run_p2 += tot[4 * c2 + 3];
+        }
+        int c, np, np2;
+        chunk(ch, c, np, np2);
+        const int inc = wave_incl_scan(c), act = wave_incl_scan(c > 0 ? 1 : 0);
+        const int incp = wave_incl_scan(np), incp2 = wave_incl_scan(np2);
+        const int e = 64 * ch + lane;
+        if (e < E) {
+            const int excl = run + inc - c;
+            o.offsets[e] = excl;
+            o.counts[e] = c;
+            if (mw) {   // per-wave cursors: the earlier waves' slots come first
+                int cc = excl;
+                for (int w = 0; w < NW; ++w) {
+                    const int cw = cnt[w * E + e];
+                    cnt[w * E + e] = cc;
+                    cc += cw;
+                }
+            } else {
+                cur1[e] = excl;
+            }
+            if (c > 0) o.active[run_act + act - 1] = e;
+            const int w0 = run_p + incp - np;
+            for (int q = 0; q < np; ++q) {
+                o.items[3 * (w0 + q)] = e;
+                o.items[3 * (w0 + q) + 1] = q;
+                o.items[3 * (w0 + q) + 2] = np;
+            }
+            const int w2 = run_p2 + incp2 - np2;
+            for (int q = 0; q < np2; ++q) {
+                o.items2[3 * (w2 + q)] = e;
+                o.items2[3 * (w2 + q) + 1] = q;
+                o.items2[3 * (w2 + q) + 2] = np2;
+            }
+        }
+        if (ch == nch - 1 && lane == 63) {
+            o.offsets[E] = run + inc;
+            o.meta[0] = run_act + act;
+            o.meta[1] = s_bad;
+            if (o.items) o.meta[2] = run_p + incp;
+            if (o.items2) o.meta[3] = run_p2 + incp2;
+        }
+    }
+    for (int i = all_act + tid; i < E; i += NT) o.active[i] = -1;
     __syncthreads();
     if (mw || tid < 64) {   // stable placement, 64 slots per step in ascending order
         int32_t* cursor = mw ? cnt + wave * E : cur1;
@@ -270,14 +300,16 @@ __global__ void __launch_bounds__(64 * ROUTER_WAVES) router_logits(RouterArgs a)
 }
 
 // The rest of the router, on the logits of the previous launch (its kernel boundary makes them visible): one wave per
-// token, FIN_WAVES waves per workgroup, so the tails (a chain of DPP reductions, VALU-issue bound) run one wave per SIMD
-// on ceil(T / FIN_WAVES) CUs. A wave runs its token's tail, writes idx / wts and, with shared experts, the merged slot
-// list (the S shared experts last, weight sigmoid(gate logit) or 1). With a.grp.counts the slots are then grouped
-// (group_block: the counts' offsets from a wave prefix sum) and the pass lists written by the last workgroup to
-// finish: the ids pass from the other workgroups by agent-scope stores and loads, and the arrival counter is
-// a.grp.meta[0], zeroed by the logits launch and overwritten by the grouping's own meta[0]. a.mw: the ids and the
-// per-wave count arrays fit the LDS; otherwise wave 0 places every slot.
-constexpr int FIN_WAVES = 4;
+// token, FIN_TOK tokens per workgroup of FIN_WAVES waves, so the tails (a chain of DPP reductions, VALU-issue bound)
+// run one wave per SIMD on ceil(T / FIN_TOK) CUs, and the grouping has all FIN_WAVES waves of the last workgroup.
+// A wave runs its token's tail, writes idx / wts and, with shared experts, the merged slot list (the S shared experts
+// last, weight sigmoid(gate logit) or 1). With a.grp.counts the slots are then grouped (group_block: the counts'
+// offsets from a wave prefix sum) and the pass lists written by the last workgroup to finish: the ids pass from the
+// other workgroups by agent-scope stores and loads, and the arrival counter is a.grp.meta[0], zeroed by the logits
+// launch and overwritten by the grouping's own meta[0]. a.mw: the ids and the per-wave count arrays fit the LDS;
+// otherwise wave 0 places every slot.
+constexpr int FIN_WAVES = 16;   // waves per workgroup: all of them group the slots in the last workgroup
+constexpr int FIN_TOK = 4;      // tokens per workgroup: waves 0..3, one per SIMD, run the tails
 template <int JM>
 __global__ void __launch_bounds__(64 * FIN_WAVES) route_finish(RouterArgs a) {
     extern __shared__ int32_t sm[];   // grouping: cnt[FIN_WAVES][E + S], ids[T (k + S)] (mw); else cnt, cursor
@@ -287,8 +319,8 @@ __global__ void __launch_bounds__(64 * FIN_WAVES) route_finish(RouterArgs a) {
     const bool grouping = a.grp.counts != nullptr;
     const bool single = gridDim.x == 1;
     int32_t* ids = a.S ? a.sidx : a.idx;   // the list the grouping reads
-    const int t = blockIdx.x * FIN_WAVES + wave;
-    if (t < a.T) {
+    const int t = blockIdx.x * FIN_TOK + wave;
+    if (wave < FIN_TOK && t < a.T) {
         const float* lrow = a.logits + (size_t)t * a.lstride;
         float v[JM];
 #pragma unroll
@@ -415,16 +447,18 @@ int launch_route_logits(const RouterArgs& a, hipStream_t st) {
 }
 
 int launch_route(RouterArgs a, bool tail, hipStream_t st) {
-    const int nwg = (a.T + FIN_WAVES - 1) / FIN_WAVES;
+    const int nwg = (a.T + FIN_TOK - 1) / FIN_TOK;
     a.arrive = tail && a.grp.counts && nwg > 1 ? a.grp.meta : nullptr;
+    if (a.grp.counts && ((a.grp.items && (a.P < 1 || (a.P & (a.P - 1)))) ||
+                         (a.grp.items2 && (a.P2 < 1 || (a.P2 & (a.P2 - 1))))))
+        return MOE_ERR_ARG;   // pass sizes are powers of two
     int rc = launch_route_logits(a, st);
     if (rc || !tail) return rc;
     size_t lds = 0;
     if (a.grp.counts) {
         const int n = a.T * (a.k + a.S), Eg = a.E + a.S;
-        const size_t per_wave = ((size_t)FIN_WAVES * Eg + (size_t)n) * 4;
-        a.mw = per_wave <= FIN_LDS;
-        lds = a.mw ? per_wave : (size_t)Eg * 8;
+        a.mw = (size_t)group_lds_ints(n, Eg, FIN_WAVES, 1) * 4 <= FIN_LDS;
+        lds = (size_t)group_lds_ints(n, Eg, FIN_WAVES, a.mw) * 4;
     }
     const dim3 grid(nwg);
     if (a.E <= 64) route_finish<1><<<grid, 64 * FIN_WAVES, lds, st>>>(a);
@@ -475,16 +509,14 @@ int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int
 
 int launch_group(const int32_t* idx, int n, int E, int32_t* counts, int32_t* offsets, int32_t* sorted,
                  int32_t* active, int32_t* meta, hipStream_t st, int P, int32_t* items, int P2, int32_t* items2) {
-    if ((items && P < 1) || (items2 && P2 < 1)) return MOE_ERR_ARG;
+    if ((items && (P < 1 || (P & (P - 1)))) || (items2 && (P2 < 1 || (P2 & (P2 - 1))))) return MOE_ERR_ARG;
     // one block: 16 waves (1024 threads) each placing a sixteenth of the slots from 1024 slots, else 4 waves; the
     // per-wave counts and the ids in LDS (at most 64 KB), else wave 0 places all of them
     int nw = n >= 1024 ? 16 : 4;
-    if (((size_t)nw * E + (size_t)n) * sizeof(int32_t) > 64 * 1024) nw = 4;
-    const size_t mw_bytes = ((size_t)nw * E + (size_t)n) * sizeof(int32_t);
-    const int mw = mw_bytes <= 64 * 1024 ? 1 : 0;
-    if (!mw) nw = 4;
+    if ((size_t)group_lds_ints(n, E, nw, 1) * 4 > 64 * 1024) nw = 4;
+    const int mw = (size_t)group_lds_ints(n, E, nw, 1) * 4 <= 64 * 1024 ? 1 : 0;
     const GroupBufs o{counts, offsets, sorted, active, meta, items, items2};
-    group_slots<<<1, 64 * nw, mw ? mw_bytes : 2 * E * sizeof(int32_t), st>>>(idx, n, E, o, P, P2, mw);
+    group_slots<<<1, 64 * nw, (size_t)group_lds_ints(n, E, nw, mw) * 4, st>>>(idx, n, E, o, P, P2, mw);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
