@@ -230,7 +230,8 @@ int moe_experts_run_stages(const moe_experts_t* w, const void* x, int x_dtype, c
  *   part); one wave writes idx / wts.
  *   T > 1: the router's two launches (as moe_router_group) compute the logits, run the tails and build the slot
  *   grouping and the expert kernels' pass lists, so the expert launches follow with no top-k or grouping launch of
- *   their own.
+ *   their own; where the gate/up wave tiles group the slots in-kernel (a few slots per expert) they do it there
+ *   instead (one of their workgroups writes the lists for the down stage).
  *   x [T, d] bf16 (MOE_DTYPE_BF16 only: the gate GEMV reads bf16); wr [E, d] bf16, wr_bias [E] fp32 or NULL;
  *   norm, scale: as moe_router; idx [T, k] int32 and wts [T, k] fp32 out (as moe_router's); y, residual, act,
  *   y_dtype: as moe_experts_run. workspace: moe_layer_workspace_bytes(w, T, k) bytes (any contents).

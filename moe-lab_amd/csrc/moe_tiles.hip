@@ -26,6 +26,7 @@
 // The next slice's global loads are issued before the current slice's MFMAs (register double buffer).
 #include "moe_common.h"
 #include "moe_formats.h"
+#include "moe_group.h"
 #include "moe_internal.h"
 
 #include <math.h>
@@ -132,6 +133,10 @@ struct TileArgs {
     const int32_t* xexp;   // dense int4 gate/up: per-token exponents of x16 (actv) [T]
     const int32_t* gidx;   // wave tiles: when set, each workgroup finds its pass from these raw ids (gn = T k of them)
     int gn, gfirst;        // instead of the grouping kernel's pass list (gfirst: expert-major first passes)
+    // gate/up wave tiles grouping in-kernel: the workgroup in the grid's last row (x = 0) also writes the grouping and
+    // the pass lists of these ids (as the grouping launch would) for the down stage; emit_grp.counts null: none
+    GroupBufs emit_grp;
+    int emit_P, emit_P2;
     uint8_t* hterm;        // block-scaled MXFP4 gate/up: h leaves as 3-term records [T*k][ceil(N/128)] (no planes)
 };
 
@@ -503,6 +508,15 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     __shared__ int sCnt[1024];            // in-kernel grouping: counts per expert (E <= 1024)
     __shared__ int sSlot[16 * NT];        // and the pass's slots
     int e, tok0, n, beg = 0;
+    if constexpr (NPROJ == 2 && MXT == 0) {
+        // the lists for the down stage, by the workgroup of the last row (usually past the live passes), first: its
+        // own pass may be empty (not in the block-scaled variants: it would cost them occupancy)
+        __shared__ int sGrp[NPROJ == 2 ? 2 * 1024 + 4 * 16 : 1];
+        if (a.emit_grp.counts && blockIdx.x == 0 && blockIdx.y == gridDim.y - 1) {
+            const int32_t* ids = a.gidx;
+            group_block([&](int p) { return ids[p]; }, a.gn, a.E, a.emit_grp, a.emit_P, a.emit_P2, sGrp, 0);
+        }
+    }
     if (a.gidx) {
         if (!wave_find_pass(a.gidx, a.gn, a.E, 16 * NT, a.gfirst, (int)blockIdx.y, sCnt, sSlot, e, tok0, n))
             return;
@@ -2012,8 +2026,11 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     if ((pl.mxd || pl.mxw) && !a.xterm) return MOE_ERR_ARG;
     t.items = a.grp.items;
     t.nidx = 2;
-    // in-kernel grouping unless the router already wrote the grouping and pass lists
-    if (pl.ingroup && !a.pregrouped) {
+    // in-kernel grouping in the gate/up unless the router already wrote the grouping and pass lists; one gate/up
+    // workgroup then also writes the lists, and the down stage reads them
+    const bool ingroup = pl.ingroup && !a.pregrouped;
+    const bool emit = ingroup && !mxw;   // the block-scaled gate/up wave tiles do not write lists: their down groups too
+    if (ingroup) {
         t.gidx = a.idx;
         t.gn = nslots;
         // the compact pass list by default: its live passes come first in dispatch order whatever the skew. The
@@ -2028,13 +2045,19 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         if (t.eslot_off + (size_t)nslots * 4 > (size_t)nslots * w->F * 2) return MOE_ERR_ARG;
     }
     if (a.stages & 1) {
-        int rc = t.gidx || a.pregrouped
+        int rc = ingroup || a.pregrouped
                      ? 0
                      : launch_group(a.idx, nslots, w->E, a.grp.counts, a.grp.offsets, a.grp.sorted, a.grp.active,
                                        a.grp.meta, a.st, P_gu, a.grp.items, two_lists ? P_dn : 0,
                                        two_lists ? a.grp.items2 : nullptr);
         if (rc) return rc;
         TileArgs g = t;
+        if (emit) {
+            g.emit_grp = a.grp;
+            g.emit_grp.items2 = two_lists ? a.grp.items2 : nullptr;
+            g.emit_P = P_gu;
+            g.emit_P2 = two_lists ? P_dn : 0;
+        }
         g.actv = a.xb;
         g.act_plane = a.xplane;
         g.act_div = a.k;
@@ -2085,6 +2108,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     }
     if (a.stages & 2) {
         TileArgs d = t;
+        if (!ingroup || emit) d.gidx = nullptr;   // the pass lists: from the grouping launch, the router or the gate/up
         d.actv = a.hhi;
         d.actv2 = a.hlo;
         d.act_div = 1;

@@ -105,9 +105,9 @@ def test_layer_ties_across_logit_groups(E):
 
 @pytest.mark.parametrize("T,dist", [(32, "uniform"), (32, "zipf"), (64, "zipf"), (16, "uniform")])
 def test_layer_batched_router_builds_grouping(T, dist, monkeypatch):
-    """BASELINE config 3 through moe_layer_run: one router launch (logits, tail, slot grouping and pass lists), then
-    the wave tiles reading those lists; bit-identical to route + the experts call (which groups in-kernel), and the
-    same again with MOE_LAYER_INGROUP=1 (the router leaves the grouping to the wave tiles)."""
+    """BASELINE config 3 through moe_layer_run: the router's launches (logits, tails), the gate/up wave tiles grouping
+    the slots in-kernel and writing the lists the down stage reads; bit-identical to route + the experts call, and the
+    same again with MOE_LAYER_INGROUP=0 (the router's last workgroup builds the grouping and pass lists)."""
     from moelab_amd.experts import run_routed
     from moelab_amd.problem import baseline_int4_layer, baseline_x, zipf_bias
     from moelab_amd.shapes import SHAPES
@@ -118,7 +118,7 @@ def test_layer_batched_router_builds_grouping(T, dist, monkeypatch):
     print(f"case layer batched T={T} {dist}", flush=True)
     check_layer(s, x, s["wr"], sh.k, bias=bias, what=("qwen3", T, dist))
     y, _, _ = run_routed(s, x, s["wr"], sh.k, bias=bias, out_dtype=torch.float32)
-    monkeypatch.setenv("MOE_LAYER_INGROUP", "1")
+    monkeypatch.setenv("MOE_LAYER_INGROUP", "0")
     y2, _, _ = run_routed(s, x, s["wr"], sh.k, bias=bias, out_dtype=torch.float32)
     assert torch.equal(y, y2)
 
