@@ -912,6 +912,17 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
 // projection per wave: with 128 tokens and 16 rows each, every activation slice staged in LDS serves half as many
 // rows (K = d is long, the L2 -> LDS traffic doubles) and the kernel slowed 440 -> 509 us. MXFP4 (raw codes on
 // bf16 MFMA, fp32 fold per group): 64-token passes, 32 / 64 rows per wave.
+// The dense tiles' passes of one expert split its ceil(n / 16) token tiles evenly: pass p of np takes tiles
+// [p T / np, (p + 1) T / np), at most ceil(T / np) <= BM / 16 of them. Passes that share a weight tile then do
+// the same MFMA work and stream the tile side by side on one XCD (a short tail pass would run ahead of its
+// partner, and the partner's weight reads would miss the L2).
+__device__ __forceinline__ void pass_tokens(int n, int np, int p, int& tok0, int& nlive) {
+    const int nt = (n + 15) >> 4;
+    const int t0 = p * nt / np, t1 = (p + 1) * nt / np;
+    tok0 = 16 * t0;
+    nlive = (16 * t1 < n ? 16 * t1 : n) - tok0;
+}
+
 template <class FMT, int NPROJ>
 __host__ __device__ constexpr int dense_nt() { return FMT::XSUM && NPROJ == 1 ? 8 : 4; }
 template <class FMT, int NPROJ>
@@ -956,8 +967,10 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     const int e = a.items[3 * wq], np = a.items[3 * wq + 2];
     const int w0 = wq - a.items[3 * wq + 1];       // the expert's first pass
     const int local = bid - w0 * nrb;
-    const int rb = local / np, tok0 = (local - rb * np) * BM;
+    const int rb = local / np;
     const int n = a.counts[e], beg = a.offsets[e];
+    int tok0, nlive;
+    pass_tokens(n, np, local - rb * np, tok0, nlive);
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, N = a.N;
@@ -984,7 +997,6 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
     const bf16x8 ONES = as_bf16x8(ones, ones, ones, ones);
 
     {
-        const int nlive = n - tok0 < BM ? n - tok0 : BM;
         const int ntiles = (nlive + 15) >> 4;
         if (tid < BM) sSlot[tid] = a.sorted[beg + (tok0 + tid < n ? tok0 + tid : n - 1)];
         __syncthreads();
@@ -1429,8 +1441,10 @@ __global__ void __launch_bounds__(256, NPROJ == 2 ? MOE_MXD_MINB_GU : MOE_MXD_MI
     const int e = a.items[3 * wq], np = a.items[3 * wq + 2];
     const int w0 = wq - a.items[3 * wq + 1];
     const int local = item - w0 * nrb;
-    const int rb = local / np, tok0 = (local - rb * np) * BM;
+    const int rb = local / np;
     const int n = a.counts[e], beg = a.offsets[e];
+    int tok0, nlive;
+    pass_tokens(n, np, local - rb * np, tok0, nlive);
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, N = a.N;
@@ -1446,7 +1460,6 @@ __global__ void __launch_bounds__(256, NPROJ == 2 ? MOE_MXD_MINB_GU : MOE_MXD_MI
             tb[p][rt] = (p ? a.W1 : a.W0) + ((size_t)e * (N >> 4) + (wvalid ? (r0 >> 4) + rt : 0)) * (size_t)nsl * SB;
     const uint8_t* recs = reinterpret_cast<const uint8_t*>(a.actv);
 
-    const int nlive = n - tok0 < BM ? n - tok0 : BM;
     const int ntiles = (nlive + 15) >> 4;
     if (tid < BM) sSlot[tid] = a.sorted[beg + (tok0 + tid < n ? tok0 + tid : n - 1)];
     __syncthreads();
