@@ -156,8 +156,9 @@ def reserve(s, T, k, device=None):
 
 def run_routed(s, x, wr, k, bias=None, norm=True, scale=1.0, act=0, residual=None, out=None, out_dtype=None):
     """Router + experts in one call (moe_layer_run): the fused router's logits x . wr^T (+ bias) and tail (the same
-    ids as router.route), then the experts on the default path; at T > 1 the router launch also builds the slot
-    grouping, so the experts run no grouping launch of their own. x [T, d] bf16, wr [E, d] bf16 (E the routed experts).
+    ids as router.route), then the experts on the default path. At T > 1 no launch of its own groups the slots: the
+    gate/up wave tiles group them in-kernel (and write the down stage's pass lists) where they run, else the
+    router's last workgroup builds the grouping. x [T, d] bf16, wr [E, d] bf16 (E the routed experts).
     A merge_shared state (s["n_shared"]) runs moe_layer_run_shared: its shared experts join every token, weighted by
     sigmoid(x . s["shared_gate"]) or 1. A state with separate shared experts (s["shared"]) adds them by a second call.
     Returns (y [T, d], idx [T, k] int32, wts [T, k] fp32), idx / wts the routed slots."""

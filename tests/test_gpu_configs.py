@@ -58,6 +58,30 @@ def check_rows(y, state, x, idx, wts, rows, what, act=0):
     return assert_close(y[sel], ref, what=what)
 
 
+@pytest.mark.parametrize("norm", [True, False])
+def test_config1_tiny_routed_layer(norm):
+    """BASELINE config 1 as stated: d=512, F=256, E=8, top-1, T=4 tokens of bf16 x ~N(0,1), router weights
+    ~N(0,0.02), SwiGLU int4 g64 experts (uniform codes, scales U(0.005,0.02), biases -8 scale). The fused router runs
+    inside the layer call (moe_layer_run): softmax then top-1, with the one weight renormalised to 1 (norm) or the
+    full softmax probability. Ids and weights against the oracle's router (ids bit for bit), y at the gate."""
+    from moelab_amd.experts import run_routed
+    from moelab_amd.problem import baseline_int4_layer, baseline_x
+    from moelab_amd.shapes import MoEShape
+    print(f"case config1 norm={norm}", flush=True)
+    sh = MoEShape("config1", d=512, f=256, E=8, k=1)
+    ly = baseline_int4_layer(sh, seed=1, device=DEV)
+    x = baseline_x(4, sh.d, seed=1, device=DEV)
+    y, idx, wts = run_routed(ly, x, ly["wr"], 1, norm=norm, out_dtype=torch.float32)
+    lg_ref = orc.router_logits(np_u16(x), np_u16(ly["wr"]), None)
+    idx_ref, wts_ref = orc.topk(lg_ref, 1, norm=norm)
+    torch.cuda.synchronize()
+    assert np.array_equal(idx.cpu().numpy(), idx_ref), "router ids differ"
+    np.testing.assert_allclose(wts.cpu().numpy(), wts_ref, rtol=1e-6, atol=1e-7)
+    if norm:
+        assert np.all(wts.cpu().numpy() == 1.0)
+    check_rows(y, ly, x, idx, wts, np.arange(4), ("config1", norm))
+
+
 @pytest.mark.parametrize("routing", ["uniform", "zipf"])
 @pytest.mark.parametrize("T", [16, 32, 64])
 def test_config3_qwen3_full_size(T, routing):
