@@ -101,7 +101,7 @@ struct RouteArgs {
     int32_t* idx;          // outputs when routed
     float* wts;
 };
-template <class FMT, int R, int NCH, int HX>
+template <class FMT, int R, int NCH, int HX, bool ROUTED>
 __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x, size_t xplane,
                                                   const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
                                                   const float* __restrict__ bg, const float* __restrict__ bu,
@@ -126,7 +126,7 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
     };
     load_x(0);   // x does not depend on the expert: its first loads go out before the expert id or router tail
     int e;
-    if (rt.logits) {
+    if constexpr (ROUTED) {
         const int t = s / k, r = s - t * k;
         const bool writer = r == 0 && f0 == 0;
         const float* lrow = rt.logits + (size_t)t * E;
@@ -215,7 +215,7 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
     }
 }
 
-template <class FMT, int R, int NCH, int HX>
+template <class FMT, int R, int NCH, int HX, bool ROUTED>
 __global__ void __launch_bounds__(256)
 k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
                const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
@@ -225,7 +225,8 @@ k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __r
     const int q0 = (blockIdx.x * 4 + wave) * R;
     if (q0 >= Q) return;
     const int s = q0 / F, f0 = q0 - s * F;
-    gate_up_rows_wave<FMT, R, NCH, HX>(x, xplane, G, U, bg, bu, idx, k, d, F, E, act, hhi, hlo, s, f0, lane, rt);
+    gate_up_rows_wave<FMT, R, NCH, HX, ROUTED>(x, xplane, G, U, bg, bu, idx, k, d, F, E, act, hhi, hlo, s, f0, lane,
+                                               rt);
 }
 
 // ============================================================================ per-slot down, h staged in LDS
@@ -713,8 +714,16 @@ int launch_gu_rows_n(const ExpertsArgs& a, int R) {
     const int grid = (Q / R + 3) / 4;
     RouteArgs rt{a.route_logits, a.route_norm, a.route_scale, const_cast<int32_t*>(a.idx), const_cast<float*>(a.wts)};
 #define MOE_GUR(RR, H)                                                                                           \
-    k_gate_up_rows<FMT, RR, NCH, H><<<grid, 256, 0, a.st>>>(a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias,   \
-                                                           a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, a.hlo, rt)
+    do {                                                                                                         \
+        if (rt.logits)                                                                                           \
+            k_gate_up_rows<FMT, RR, NCH, H, true><<<grid, 256, 0, a.st>>>(                                       \
+                a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias, a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, \
+                a.hlo, rt);                                                                                      \
+        else                                                                                                     \
+            k_gate_up_rows<FMT, RR, NCH, H, false><<<grid, 256, 0, a.st>>>(                                      \
+                a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias, a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, \
+                a.hlo, rt);                                                                                      \
+    } while (0)
     if (a.nx > 1) {
         if (a.nx == 3) {
             if (R == 2) MOE_GUR(2, 3);
