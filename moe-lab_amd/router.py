@@ -39,7 +39,7 @@ def reserve(device, T):
 
 
 def route(x, wr, k, bias=None, norm=True, scale=1.0, return_logits=False):
-    """Gate GEMV + router tail in one launch. x [T, d] bf16, wr [E, d] bf16, bias [E] (any float) or None.
+    """Gate GEMV, then the router tails (two launches). x [T, d] bf16, wr [E, d] bf16, bias [E] (any float) or None.
     Returns (idx [T, k] int32, wts [T, k] fp32[, logits [T, E] fp32])."""
     _lib.require_device(x, "x")
     assert x.dtype == torch.bfloat16 and wr.dtype == torch.bfloat16, "router takes bf16 x and Wr"
