@@ -1,5 +1,6 @@
-"""The A/B harness, slope timing and contention guard on the GPU (moe-lab_amd/compare.py, slope.py, guard.py):
-one small run of each, checking that they measure and report, not any particular speed."""
+"""The A/B harness, slope timing, contention guard and random-shape sweep on the GPU (moe-lab_amd/compare.py,
+slope.py, guard.py, sweep.py): one small run of each, checking that they measure and report, not any particular
+speed (the sweep's correctness gates do hold)."""
 import json
 
 import pytest
@@ -7,7 +8,7 @@ import pytest
 import __graft_entry__
 
 __graft_entry__.load_package()
-from moelab_amd import backend as be, compare, guard, slope  # noqa: E402
+from moelab_amd import backend as be, compare, guard, slope, sweep  # noqa: E402
 from moelab_amd.shapes import MoEShape  # noqa: E402
 
 pytestmark = pytest.mark.gpu
@@ -60,3 +61,11 @@ def test_compare_two_launches(tmp_path, monkeypatch, in_process):
     rec = json.load(open(out))
     assert len(rec["probes"]) == 4 and rec["guard"]["status"] == "calibrating"
     assert {r["arm"] for r in rec["rows"]} == {"A", "B"} and len(rec["rows"]) == 2 * 2 * 2 * 2
+
+
+def test_sweep_small_run():
+    """Three small random cases (both formats): every default call passes its correctness gates and both arms time."""
+    rows, summ, g = sweep.run(3, seed=10, max_dense_bytes=3e8, probe=False, emit=lambda m: print(m, flush=True))
+    assert g is None and summ["cases"] == 3 and summ["all_correct"], rows
+    for r in rows:
+        assert r["ok"] and r["slots_us"] > 0 and r["default_us"] > 0 and r["max_over_rms"] <= 1e-2

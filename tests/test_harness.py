@@ -1,5 +1,6 @@
-"""A/B harness, slope fit and contention guard (host logic, CPU): moe-lab_amd/compare.py, slope.py, guard.py
-against closed forms and an exhaustive enumeration of both bootstrap draws on a tiny case."""
+"""A/B harness, slope fit, contention guard and random-shape sweep (host logic, CPU): moe-lab_amd/compare.py,
+slope.py, guard.py, sweep.py against closed forms, an exhaustive enumeration of both bootstrap draws on a tiny case,
+and the sweep's case generator against the library's shape requirements."""
 import itertools
 import json
 
@@ -9,7 +10,7 @@ import pytest
 import __graft_entry__
 
 __graft_entry__.load_package()
-from moelab_amd import compare, guard, slope  # noqa: E402
+from moelab_amd import compare, guard, slope, sweep  # noqa: E402
 
 
 def rows_of(per_launch, tokens=1):
@@ -153,3 +154,30 @@ def test_reference_skips_ids_outside_range():
     y = be.reference(wg, wu, wd, x, idx, wts)
     y2 = be.reference(wg, wu, wd, x, torch.where(keep, idx, torch.zeros_like(idx)), wts * keep)
     assert torch.allclose(y, y2, atol=1e-6) and y.abs().sum() > 0
+
+
+def test_sweep_cases_meet_the_library_requirements():
+    """Every drawn case is a shape the library takes (d, F multiples of 64, F <= 16384, 1 <= k <= E <= 1024) under
+    the weight cap; the generator is a function of its seed; 400 draws reach both formats, both dtypes, every
+    routing, T = 1 and T >= 64."""
+    cases = sweep.draw_cases(400, seed=11, max_dense_bytes=1.5e9)
+    assert cases == sweep.draw_cases(400, seed=11, max_dense_bytes=1.5e9)
+    assert cases != sweep.draw_cases(400, seed=12, max_dense_bytes=1.5e9)
+    for c in cases:
+        assert c.d % 64 == 0 and c.F % 64 == 0 and 256 <= c.F <= 16384 and 512 <= c.d <= 5120
+        assert 1 <= c.k <= c.E <= 1024 and c.E & (c.E - 1) == 0
+        assert c.dense_bytes() <= 1.5e9 and 1 <= c.T <= 128
+    assert {c.fmt for c in cases} == {"int4", "mxfp4"} and {c.dtype for c in cases} == {"bfloat16", "float16"}
+    assert {c.routing for c in cases} == {"uniform", "zipf", "one_hot"}
+    assert min(c.T for c in cases) == 1 and max(c.T for c in cases) >= 64
+    assert all(c.fmt == "int4" for c in sweep.draw_cases(50, seed=3, fmts=("int4",)))
+
+
+def test_sweep_summary_flags():
+    rows = [{"case": "a", "T": 1, "ok": True, "slots_over_default": 1.4, "max_over_rms": 1e-4},
+            {"case": "b", "T": 8, "ok": True, "slots_over_default": 0.8, "max_over_rms": 2e-4},
+            {"case": "c", "T": 32, "ok": False, "slots_over_default": 3.0, "max_over_rms": 5e-2}]
+    s = sweep.summary(rows, flag=0.95)
+    assert s["cases"] == 3 and not s["all_correct"] and s["worst_max_over_rms"] == 5e-2
+    assert s["flagged"] == ["b T=8", "c T=32"]
+    assert s["slots_over_default_min"] == 0.8 and s["slots_over_default_median"] == 1.4
