@@ -150,6 +150,22 @@ __device__ __forceinline__ uint32_t wave_min_dpp(uint32_t v) {
     v = dpp_min<0x143, 0xC>(v);
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
+// u32 max with the same DPP pattern; 0 (the max's identity) fills lanes a row mask leaves out, so each step can be
+// one v_max_u32 with a DPP source operand
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+    return o > v ? o : v;
+}
+__device__ __forceinline__ uint32_t wave_umax_dpp(uint32_t v) {
+    v = dpp_umax<0xB1>(v);
+    v = dpp_umax<0x4E>(v);
+    v = dpp_umax<0x141>(v);
+    v = dpp_umax<0x140>(v);
+    v = dpp_umax<0x142, 0xA>(v);
+    v = dpp_umax<0x143, 0xC>(v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     v = sum_lanes<64>(v);
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
@@ -273,15 +289,28 @@ constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024
 // id winning ties, fewer than k finite logits -> the lowest unused ids with weight 0; norm: softmax over the top-k
 // logits, !norm: full-softmax probabilities; weights times scale. rounds <= k stops after that many rounds (a caller
 // that needs only round r passes r + 1; the weights are then not computed). JM >= ceil(E / 64) logits per lane
-// (logit j * 64 + lane in v[j]); a round is one DPP max over the lanes' best values, then the lowest id holding it
-// from one ballot per j (the lowest j with a lane at the maximum, then the lowest such lane).
+// (logit j * 64 + lane in v[j]). The rounds run on order-preserving u32 keys of the logits (a larger logit has a
+// larger key; -0 keys as +0, since the two compare equal; a chosen logit's key becomes 0, below every logit's): a
+// round is one DPP max over the lanes' largest keys (one v_max_u32 per step), then the lowest id holding it from one
+// ballot per j (the lowest j with a lane at the maximum, then the lowest such lane).
+__device__ __forceinline__ uint32_t logit_key(float f) {
+    const uint32_t b = __float_as_uint(f == 0.f ? 0.f : f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_logit(uint32_t key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
 template <int JM>
 __device__ __forceinline__ void topk_core(float (&v)[JM], int E, int k, int norm, float scale, int rounds, uint32_t* id,
                                           float* w) {
     const int lane = threadIdx.x & 63;
+    uint32_t key[JM];
 #pragma unroll
-    for (int j = 0; j < JM; ++j)
+    for (int j = 0; j < JM; ++j) {
         if (__builtin_isnan(v[j]) || j * 64 + lane >= E) v[j] = -INFINITY;
+        key[j] = logit_key(v[j]);
+    }
+    const uint32_t KNEG = 0x007FFFFFu;   // logit_key(-inf): keys at or below it are no candidates
     const bool weights = rounds >= k;
     float m0 = -INFINITY;
 #pragma unroll
@@ -297,26 +326,29 @@ __device__ __forceinline__ void topk_core(float (&v)[JM], int E, int k, int norm
     uint32_t myi = 0;
     float top0 = -INFINITY;
     for (int r = 0; r < rounds; ++r) {
-        float b = -INFINITY;
-        int bj = -1;   // the lane's lowest j holding its maximum; -1: nothing above -inf
+        uint32_t b = key[0];
 #pragma unroll
-        for (int j = 0; j < JM; ++j)
-            if (v[j] > b) { b = v[j]; bj = j; }
-        float m = wave_max_dpp(b);
-        uint32_t sel = 0xFFFFFFFFu;
+        for (int j = 1; j < JM; ++j) b = key[j] > b ? key[j] : b;
+        const uint32_t mk = wave_umax_dpp(b);
+        uint32_t sel;
+        float m;
+        if (mk > KNEG) {   // wave-uniform: a finite (or +inf) logit is left
+            sel = 0xFFFFFFFFu;
 #pragma unroll
-        for (int j = 0; j < JM; ++j) {
-            const uint64_t hit = __ballot(bj == j && b == m);
-            if (sel == 0xFFFFFFFFu && hit) sel = (uint32_t)(j * 64 + __builtin_ctzll(hit));
-        }
-        if (sel == 0xFFFFFFFFu) {   // no finite candidate left: lowest id not chosen yet, weight 0
+            for (int j = 0; j < JM; ++j) {
+                const uint64_t hit = __ballot(key[j] == mk);
+                if (sel == 0xFFFFFFFFu && hit) sel = (uint32_t)(j * 64 + __builtin_ctzll(hit));
+            }
+            m = key_logit(mk);
+            if ((int)(sel & 63u) == lane) {
+#pragma unroll
+                for (int j = 0; j < JM; ++j)
+                    if (j == (int)(sel >> 6)) key[j] = 0u;
+            }
+        } else {   // no finite candidate left: lowest id not chosen yet, weight 0
             sel = 0;
             while (__ballot(lane < r && myi == sel) != 0ull) ++sel;
             m = -INFINITY;
-        } else if ((int)(sel & 63u) == lane) {
-#pragma unroll
-            for (int j = 0; j < JM; ++j)
-                if (j == (int)(sel >> 6)) v[j] = -INFINITY;
         }
         if (r == 0) top0 = m;
         if (lane == r) { myv = m; myi = sel; }
