@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 #include "moe_mi355x.h"
 
@@ -362,6 +363,63 @@ __device__ __forceinline__ void topk_core(float (&v)[JM], int E, int k, int norm
     const float off = norm ? top0 : m0;
     *w = expf(myv - off) / s * scale;
 }
+// One wave, one rank: the expert id of round q of topk_core's tail on the same logits (q < k), without the q earlier
+// rounds. Among the finite logits (nfin of them), round q's logit is the one of key Kq, the largest key with more than
+// q keys at or above it, found bit by bit from the top (32 steps of one ballot and popcount per j); round q takes the
+// (q - #keys above Kq)-th lowest id holding Kq. Past the finite logits (q >= nfin) round q takes the (q - nfin)-th
+// lowest id below E whose logit is not finite, as topk_core's fallback does. Wave-uniform result.
+template <int JM>
+__device__ __forceinline__ uint32_t topk_rank_id(float (&v)[JM], int E, int q) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t KNEG = 0x007FFFFFu;   // logit_key(-inf)
+    uint32_t key[JM];
+    int nfin = 0;
+#pragma unroll
+    for (int j = 0; j < JM; ++j) {
+        const bool in = j * 64 + lane < E;
+        key[j] = in && !__builtin_isnan(v[j]) ? logit_key(v[j]) : KNEG;
+        nfin += __builtin_popcountll(__ballot(key[j] > KNEG));
+    }
+    uint64_t pick[JM];   // the candidates of rank q's kind, in ascending id (j-major)
+    int skip;
+    if (q < nfin) {
+        uint32_t K = 0;
+        for (int bit = 31; bit >= 0; --bit) {
+            const uint32_t c = K | (1u << bit);
+            int n = 0;
+#pragma unroll
+            for (int j = 0; j < JM; ++j) n += __builtin_popcountll(__ballot(key[j] >= c));
+            K = n > q ? c : K;
+        }
+        int gt = 0;
+#pragma unroll
+        for (int j = 0; j < JM; ++j) {
+            gt += __builtin_popcountll(__ballot(key[j] > K));
+            pick[j] = __ballot(key[j] == K);
+        }
+        skip = q - gt;
+    } else {
+#pragma unroll
+        for (int j = 0; j < JM; ++j) pick[j] = __ballot(key[j] <= KNEG && j * 64 + lane < E);
+        skip = q - nfin;
+    }
+    uint32_t sel = 0;
+    bool found = false;
+#pragma unroll
+    for (int j = 0; j < JM; ++j) {
+        uint64_t m = pick[j];
+        const int c = __builtin_popcountll(m);
+        if (!found && skip < c) {
+            for (int i = 0; i < skip; ++i) m &= m - 1;
+            sel = (uint32_t)(j * 64 + __builtin_ctzll(m));
+            found = true;
+        } else if (!found) {
+            skip -= c;
+        }
+    }
+    return sel;
+}
+
 // topk_core on logits read through lg(e) (logit j * 64 + lane into v[j]; e >= E is not read)
 template <int JM, typename F>
 __device__ __forceinline__ void topk_lanes(F lg, int E, int k, int norm, float scale, int rounds, uint32_t* id,
@@ -382,6 +440,26 @@ __device__ __forceinline__ void wave_topk_lanes(F lg, int E, int k, int norm, fl
     else if (E <= 128) topk_lanes<2>(lg, E, k, norm, scale, rounds, id, w);
     else if (E <= 256) topk_lanes<4>(lg, E, k, norm, scale, rounds, id, w);
     else topk_lanes<TOPK_MAX_J>(lg, E, k, norm, scale, rounds, id, w);
+}
+
+// topk_rank_id on logits read through lg(e)
+template <typename F>
+__device__ __forceinline__ uint32_t wave_rank_id(F lg, int E, int q) {
+    auto run = [&](auto jm) __attribute__((always_inline)) {
+        constexpr int JM = decltype(jm)::value;
+        const int lane = threadIdx.x & 63;
+        float v[JM];
+#pragma unroll
+        for (int j = 0; j < JM; ++j) {
+            const int e = j * 64 + lane;
+            v[j] = e < E ? lg(e) : -INFINITY;
+        }
+        return topk_rank_id<JM>(v, E, q);
+    };
+    if (E <= 64) return run(std::integral_constant<int, 1>{});
+    if (E <= 128) return run(std::integral_constant<int, 2>{});
+    if (E <= 256) return run(std::integral_constant<int, 4>{});
+    return run(std::integral_constant<int, TOPK_MAX_J>{});
 }
 
 // One wave: router tail for one token, written to idx[k], wts[k].

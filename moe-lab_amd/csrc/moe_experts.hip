@@ -91,9 +91,10 @@ __global__ void __launch_bounds__(256) k_x_planes(const void* __restrict__ x, ui
 // HX activation planes (bf16 x: 1; fp16 / fp32 x: k_x_planes' 2 or 3 planes, xplane elements apart): every plane
 // is dotted with the same decoded chunk and the products add in fp32.
 // One wave: gate and up rows f0 .. f0 + R - 1 of slot s's expert; lanes 48..63 write h.
-// Routed (rt.logits != null): the expert is round s % k of the router tail over token s / k's logits, run by the
-// wave itself (as many rounds as it needs); the wave with s % k == 0 and f0 == 0 runs all k and writes the token's
-// idx / wts for the down kernel and the caller.
+// Routed (RJM > 0: RJM = ceil(E / 64) logits per lane): the expert is round s % k of the router tail over token
+// s / k's logits, which the wave selects itself (topk_rank_id: that round alone, no earlier rounds); the wave with
+// s % k == 0 and f0 == 0 also runs the whole tail (topk_core) once its weight loads are in flight, and writes the
+// token's idx / wts for the down kernel and the caller.
 struct RouteArgs {
     const float* logits;   // [T, E] fp32, or null: the expert ids come from idx
     int norm;
@@ -101,7 +102,7 @@ struct RouteArgs {
     int32_t* idx;          // outputs when routed
     float* wts;
 };
-template <class FMT, int R, int NCH, int HX, bool ROUTED>
+template <class FMT, int R, int NCH, int HX, int RJM>
 __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x, size_t xplane,
                                                   const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
                                                   const float* __restrict__ bg, const float* __restrict__ bu,
@@ -126,18 +127,15 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
     };
     load_x(0);   // x does not depend on the expert: its first loads go out before the expert id or router tail
     int e;
-    if constexpr (ROUTED) {
-        const int t = s / k, r = s - t * k;
-        const bool writer = r == 0 && f0 == 0;
-        const float* lrow = rt.logits + (size_t)t * E;
-        uint32_t id;
-        float w;
-        wave_topk_lanes([&](int ee) { return lrow[ee]; }, E, k, rt.norm, rt.scale, writer ? k : r + 1, &id, &w);
-        e = __builtin_amdgcn_readlane((int)id, r);
-        if (writer && lane < k) {
-            rt.idx[(size_t)t * k + lane] = (int32_t)id;
-            rt.wts[(size_t)t * k + lane] = w;
-        }
+    constexpr int LJ = RJM > 0 ? RJM : 1;
+    float lv[LJ];   // routed: the token's logits, logit j * 64 + lane in lv[j]
+    const int tok = s / k;
+    const bool writer = RJM > 0 && s - tok * k == 0 && f0 == 0;
+    if constexpr (RJM > 0) {
+        const float* lrow = rt.logits + (size_t)tok * E;
+#pragma unroll
+        for (int j = 0; j < LJ; ++j) lv[j] = j * 64 + lane < E ? lrow[j * 64 + lane] : -INFINITY;
+        e = __builtin_amdgcn_readfirstlane((int)topk_rank_id<LJ>(lv, E, s - tok * k));
     } else {
         e = idx[s];   // wave-uniform: a scalar load
     }
@@ -170,6 +168,19 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
                 mu[r][c] = FMT::meta(ub0 + r * rb, d, ch[c]);
             }
         __builtin_amdgcn_sched_barrier(0);   // every load of the pass is in flight before any use
+        if constexpr (RJM > 0) {
+            // the token's whole tail, for idx / wts, while the weights arrive (it reads only registers)
+            if (writer && c0 == 0) {
+                uint32_t id;
+                float w;
+                topk_core<LJ>(lv, E, k, rt.norm, rt.scale, k, &id, &w);
+                if (lane < k) {
+                    rt.idx[(size_t)tok * k + lane] = (int32_t)id;
+                    rt.wts[(size_t)tok * k + lane] = w;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
         uint32_t xp[HX][NCH][16];
         float xs[NCH];
 #pragma unroll
@@ -215,7 +226,7 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
     }
 }
 
-template <class FMT, int R, int NCH, int HX, bool ROUTED>
+template <class FMT, int R, int NCH, int HX, int RJM>
 __global__ void __launch_bounds__(256)
 k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
                const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
@@ -225,8 +236,7 @@ k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __r
     const int q0 = (blockIdx.x * 4 + wave) * R;
     if (q0 >= Q) return;
     const int s = q0 / F, f0 = q0 - s * F;
-    gate_up_rows_wave<FMT, R, NCH, HX, ROUTED>(x, xplane, G, U, bg, bu, idx, k, d, F, E, act, hhi, hlo, s, f0, lane,
-                                               rt);
+    gate_up_rows_wave<FMT, R, NCH, HX, RJM>(x, xplane, G, U, bg, bu, idx, k, d, F, E, act, hhi, hlo, s, f0, lane, rt);
 }
 
 // ============================================================================ per-slot down, h staged in LDS
@@ -710,19 +720,21 @@ int launch_gu_rows_n(const ExpertsArgs& a, int R) {
     const moe_experts_t* w = a.w;
     const ProjPtrs P = ptrs(w);
     const int Q = a.T * a.k * w->F;
+    if (a.route_logits && a.nx > 1) return MOE_ERR_DTYPE;   // the routed gate/up reads bf16 x (one plane)
     if (a.nx > 1) R = w->F % 2 == 0 && Q / 2 >= MOE_GU_MIN_WAVES ? 2 : 1;   // fp16 / fp32 planes: R <= 2
     const int grid = (Q / R + 3) / 4;
     RouteArgs rt{a.route_logits, a.route_norm, a.route_scale, const_cast<int32_t*>(a.idx), const_cast<float*>(a.wts)};
+#define MOE_GUR_J(RR, H, J)                                                                                       \
+    k_gate_up_rows<FMT, RR, NCH, H, J><<<grid, 256, 0, a.st>>>(a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias,   \
+                                                              a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, a.hlo, rt)
+// routed: the tail's logits per lane at compile time (E <= 64 J); the layer call routes bf16 x only (H == 1)
 #define MOE_GUR(RR, H)                                                                                           \
     do {                                                                                                         \
-        if (rt.logits)                                                                                           \
-            k_gate_up_rows<FMT, RR, NCH, H, true><<<grid, 256, 0, a.st>>>(                                       \
-                a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias, a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, \
-                a.hlo, rt);                                                                                      \
-        else                                                                                                     \
-            k_gate_up_rows<FMT, RR, NCH, H, false><<<grid, 256, 0, a.st>>>(                                      \
-                a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias, a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, \
-                a.hlo, rt);                                                                                      \
+        if (!rt.logits || H != 1) MOE_GUR_J(RR, H, 0);                                                           \
+        else if (w->E <= 64) MOE_GUR_J(RR, 1, 1);                                                                \
+        else if (w->E <= 128) MOE_GUR_J(RR, 1, 2);                                                               \
+        else if (w->E <= 256) MOE_GUR_J(RR, 1, 4);                                                               \
+        else MOE_GUR_J(RR, 1, TOPK_MAX_J);                                                                       \
     } while (0)
     if (a.nx > 1) {
         if (a.nx == 3) {
@@ -743,6 +755,7 @@ int launch_gu_rows_n(const ExpertsArgs& a, int R) {
         default: MOE_GUR(1, 1); break;
     }
 #undef MOE_GUR
+#undef MOE_GUR_J
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
