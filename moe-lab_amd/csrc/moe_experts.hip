@@ -561,15 +561,16 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
 // ============================================================================ combine
 // y[t, n] = residual[t, n] + sum_j wts[t, j] * (yp[t*k + j, n] (+ yp2[t*k + j, n], a second K part) +
 // bd[idx[t, j], n]); slots whose id is outside
-// [0, E) add nothing. 4 outputs per thread (D % 4 == 0). The slots are taken 8 at a time: their ids and
-// weights first, then every yp row (and bias row) load of the 8 at once (rows of skipped slots are read
-// too, then discarded by a select, so no load waits on an id), then the sums in slot order.
+// [0, E) add nothing. 4 outputs per thread (D % 4 == 0). The slots are taken KC at a time (KC: k rounded up to a
+// power of two, at most 8): their ids and weights first, then every yp row (and bias row) load of the KC at once
+// (rows of skipped slots are read too, then discarded by a select, so no load waits on an id), then the sums in slot
+// order.
+template <int KC>
 __global__ void __launch_bounds__(256)
 k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t* __restrict__ idx,
           const float* __restrict__ wts,
           const float* __restrict__ bd, int E, const void* __restrict__ resid, void* __restrict__ y, int T, int k,
           int D, int ydt) {
-    constexpr int KC = 8;
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total4 = (size_t)T * D / 4;
     if (i4 >= total4) return;
@@ -892,7 +893,10 @@ int launch_combine(const float* yp, int nplanes, size_t plane, const int32_t* id
     const size_t total4 = (size_t)T * d / 4;
     if (total4 == 0) return 0;
     dim3 grid((unsigned)((total4 + 255) / 256));
-    k_combine<<<grid, 256, 0, st>>>(yp, nplanes, plane, idx, wts, bd, E, residual, y, T, k, d, ydt);
+    if (k <= 1) k_combine<1><<<grid, 256, 0, st>>>(yp, nplanes, plane, idx, wts, bd, E, residual, y, T, k, d, ydt);
+    else if (k <= 2) k_combine<2><<<grid, 256, 0, st>>>(yp, nplanes, plane, idx, wts, bd, E, residual, y, T, k, d, ydt);
+    else if (k <= 4) k_combine<4><<<grid, 256, 0, st>>>(yp, nplanes, plane, idx, wts, bd, E, residual, y, T, k, d, ydt);
+    else k_combine<8><<<grid, 256, 0, st>>>(yp, nplanes, plane, idx, wts, bd, E, residual, y, T, k, d, ydt);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
 }
 
