@@ -906,9 +906,10 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
 #define MOE_BARRIER() asm volatile("s_barrier" ::: "memory")
 
 // Dense tile shapes (measured at the Mixtral T=512 shape). int4 down (operands decoded to fp16 with the scale
-// applied, no fold): 128-token passes and 32 rows per wave, so each decoded operand feeds 8 MFMAs (the decode's
-// 15 VALU instructions per code word come to ~2 per MFMA) and the 64 accumulators stay in VGPRs at 2 waves per
-// SIMD: 234 -> 214 us against 64-token passes. int4 gate/up keeps 64-token passes with 32 rows of each
+// applied, no fold): 32 rows per wave; dense_nt's 128-token passes (each decoded operand feeding 8 MFMAs, 64
+// accumulators, 2 waves per SIMD) measured 234 -> 214 us in the kernel alone against 64-token passes, but the call
+// runs 64-token passes (make_plan's dn_nt): 4 waves per SIMD and no K split, faster per layer. int4 gate/up keeps
+// 64-token passes with 32 rows of each
 // projection per wave: with 128 tokens and 16 rows each, every activation slice staged in LDS serves half as many
 // rows (K = d is long, the L2 -> LDS traffic doubles) and the kernel slowed 440 -> 509 us. MXFP4 (raw codes on
 // bf16 MFMA, fp32 fold per group): 64-token passes, 32 / 64 rows per wave.
@@ -1935,9 +1936,9 @@ int dense_ksplit(int N, int K, int nslots, int E, int BN, int P) {
     return (nsl + per - 1) / per;
 }
 
-template <class FMT, int NPROJ>
+template <class FMT, int NPROJ, int NT = dense_nt<FMT, NPROJ>()>
 int launch_dense(TileArgs t, int nslots, hipStream_t st) {
-    constexpr int BN = dense_bn<FMT, NPROJ>(), NT = dense_nt<FMT, NPROJ>();
+    constexpr int BN = dense_bn<FMT, NPROJ>();
     if (t.N % (16 * dense_rt<FMT, NPROJ>())) return MOE_ERR_ARG;   // whole row tiles per wave
     if (NPROJ == 2) t.ksplit = 1;
     // rounded up to a multiple of 8: every XCD slot then has a workgroup for each of its ceil(items / 8) items
@@ -1961,7 +1962,7 @@ int launch_dense(TileArgs t, int nslots, hipStream_t st) {
 // down, on two pass lists.
 struct Plan {
     bool tiled, dense_gu, dense_dn, mxd, wave_gu, wave_dn, mxw, h16, two_lists, ingroup;
-    int nt, P_gu, P_dn;
+    int nt, dn_nt, P_gu, P_dn;
 };
 
 template <class FMT>
@@ -2004,10 +2005,17 @@ Plan make_plan(const moe_experts_t* w, int T, int k, int x_dtype) {
     p.nt = nx > 1 ? 1
          : (p.wave_gu || p.wave_dn) ? (wnt == 1 || wnt == 2 ? wnt : (avg <= 16 ? 1 : 2))
                                     : tokens_per_pass_tiles(T, k, w->E);
-    // pass lists: 16 nt tokens per pass for the wave tiles, DP_GU / DP_DN for the dense tiles; a second list
+    // pass lists: 16 nt tokens per pass for the wave tiles, DP_GU / 16 dn_nt for the dense tiles; a second list
     // when the two stages take different kernels
+    // the int4 dense down's pass: 64 tokens (MOE_DENSE_DN_NT = 2, 4, 8 token tiles for A/B runs). Against 128-token
+    // passes (each decoded weight tile feeding 8 token tiles, 64 accumulators, 2 waves per SIMD) the 64-token pass
+    // runs 4 waves per SIMD (128 VGPRs) and, with twice the items, no K split: DeepSeek-V2-Lite T=256 (31 slots per
+    // expert, where a 128-token pass decodes its tiles for 2 live token tiles) 166-168 -> 148-149 us per layer,
+    // Mixtral T=512 655-672 -> 638-650 us (32-token passes: 147-153 and 682-696 us)
+    const int dnt = env_int("MOE_DENSE_DN_NT", 0);
+    p.dn_nt = !INT4 ? dense_nt<FMT, 1>() : (dnt == 2 || dnt == 4 || dnt == 8) ? dnt : 4;
     p.P_gu = p.dense_gu ? DP_GU : 16 * p.nt;
-    p.P_dn = p.dense_dn ? DP_DN : 16 * p.nt;
+    p.P_dn = p.dense_dn ? 16 * p.dn_nt : 16 * p.nt;
     p.two_lists = p.P_gu != p.P_dn;
     // both stages on the wave tiles with few slots: each workgroup can find its pass from the raw ids itself (an LDS
     // histogram and a wave scan, the grouping launch's order), so the call needs no grouping launch
@@ -2031,7 +2039,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
     t.act = a.act;
     t.kslots = a.k;
     constexpr bool INT4 = FmtInt4::FMT == FMT::FMT;
-    constexpr int BN_DN = dense_bn<FMT, 1>(), DP_DN = 16 * dense_nt<FMT, 1>();
+    constexpr int BN_DN = dense_bn<FMT, 1>();
     const Plan pl = make_plan<FMT>(w, a.T, a.k, a.x_dtype);
     const bool dense_gu = pl.dense_gu, dense_dn = pl.dense_dn, mxd = pl.mxd && a.xterm, wave_gu = pl.wave_gu,
                wave_dn = pl.wave_dn, mxw = pl.mxw && a.xterm, h16 = pl.h16, two_lists = pl.two_lists;
@@ -2129,7 +2137,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         d.N = w->d;
         d.W0 = (const uint8_t*)w->down.rows;
         d.yp = a.yp;
-        d.ksplit = dense_dn && !mxd ? dense_ksplit(d.N, d.K, nslots, w->E, BN_DN, DP_DN) : 1;
+        d.ksplit = dense_dn && !mxd ? dense_ksplit(d.N, d.K, nslots, w->E, BN_DN, P_dn) : 1;
         d.plane = (size_t)nslots * d.N;
         if (two_lists) {
             d.items = a.grp.items2;
@@ -2149,7 +2157,15 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         if (mxd) {
             d.W0 = (const uint8_t*)w->down.tiles;
             rc = launch_mxd<1, 3>(d, nslots, a.st);
-        } else if (dense_dn) rc = launch_dense<FMT, 1>(d, nslots, a.st);
+        } else if (dense_dn) {
+            if constexpr (INT4) {
+                if (pl.dn_nt == 2) rc = launch_dense<FMT, 1, 2>(d, nslots, a.st);
+                else if (pl.dn_nt == 4) rc = launch_dense<FMT, 1, 4>(d, nslots, a.st);
+                else rc = launch_dense<FMT, 1>(d, nslots, a.st);
+            } else {
+                rc = launch_dense<FMT, 1>(d, nslots, a.st);
+            }
+        }
         else if (wave_dn && wide_dn(MOE_WAVE_RT_DN_WIDE))
             rc = launch_wave_tile<FMT, 1, MOE_WAVE_RT_DN_WIDE, MOE_WAVE_D_DN>(d, nt, nslots, a.st, 1, mxt);
         else if (MOE_WAVE_RT_DN_MID && wave_dn && wide_dn(MOE_WAVE_RT_DN_MID))

@@ -42,7 +42,10 @@ def test_slope_of_a_chain():
     sh = MoEShape("slope", 256, 384, 8, 2)
     carry, (res,) = slope.run(sh, ["hip_q4_moe"], tokens=1, lengths=(4, 8, 16), windows=16)
     print(f"carry {carry.per_call_us:.2f} us, per-call {res.per_call_us:.2f} us, own {res.own_us:.2f} us", flush=True)
-    assert 0.5 < res.per_call_us < 500.0 and res.own_us < res.per_call_us and res.floor_us > 0
+    # the carry's slope (the chain's add alone, ~1-3 us per call) is a fit over three chain lengths: on a call this
+    # small its noise can exceed it, so only the report's consistency is asserted, not its sign
+    assert 0.5 < res.per_call_us < 500.0 and res.floor_us > 0
+    assert abs(res.own_us - (res.per_call_us - carry.per_call_us)) < 1e-9 and abs(carry.per_call_us) < 50.0
 
 
 @pytest.mark.parametrize("in_process", [True, False])
