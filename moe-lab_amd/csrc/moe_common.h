@@ -281,6 +281,18 @@ __device__ __forceinline__ float load_y(const void* y, size_t i, int ydt) {
     if (ydt == MOE_DTYPE_F16) return (float)reinterpret_cast<const _Float16*>(y)[i];
     return bf16_to_f32(reinterpret_cast<const uint16_t*>(y)[i]);
 }
+// the same value in two steps: the raw bits (a load with no use, so no wait on it follows), then the conversion
+// where the value is needed (a conversion inside the dtype branch would make the load's wait immediate, and the
+// in-order memory counter would then also wait for every load issued before it)
+__device__ __forceinline__ uint32_t load_y_bits(const void* y, size_t i, int ydt) {
+    if (ydt == MOE_DTYPE_F32) return reinterpret_cast<const uint32_t*>(y)[i];
+    return reinterpret_cast<const uint16_t*>(y)[i];
+}
+__device__ __forceinline__ float y_bits_f32(uint32_t b, int ydt) {
+    if (ydt == MOE_DTYPE_F32) return __uint_as_float(b);
+    if (ydt == MOE_DTYPE_F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+    return bf16_to_f32((uint16_t)b);
+}
 
 // ------------------------------------------------------------------------------------ router tail
 constexpr int TOPK_MAX_J = 16;    // E <= 64 * 16 = 1024

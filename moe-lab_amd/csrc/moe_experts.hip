@@ -147,27 +147,31 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
     const int ee = valid ? e : 0;
     const uint8_t* gb0 = G + ((size_t)ee * F + f0) * rb;
     const uint8_t* ub0 = U + ((size_t)ee * F + f0) * rb;
-    // the lane that writes row f0 + (lane - 48) fetches its additive biases now (gpt-oss), not after the sums
     const int rl = lane - 48;
     float bgl = 0.f, bul = 0.f;
-    if (valid && rl >= 0 && rl < R) {
-        if (bg) bgl = bg[(size_t)e * F + f0 + rl];
-        if (bu) bul = bu[(size_t)e * F + f0 + rl];
-    }
     for (int c0 = 0; c0 < nchunk; c0 += 64 * NCH) {
         if (c0) load_x(c0);
         uint4 wg[R][NCH], wu[R][NCH];
         uint32_t mg[R][NCH], mu[R][NCH];
+        // 32-bit byte offsets from the wave-uniform row bases (R <= 16 rows of one record each)
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
-                wg[r][c] = *reinterpret_cast<const uint4*>(gb0 + r * rb + 16 * ch[c]);
-                mg[r][c] = FMT::meta(gb0 + r * rb, d, ch[c]);
-                wu[r][c] = *reinterpret_cast<const uint4*>(ub0 + r * rb + 16 * ch[c]);
-                mu[r][c] = FMT::meta(ub0 + r * rb, d, ch[c]);
+                const uint32_t ro = (uint32_t)(r * rb);
+                wg[r][c] = *reinterpret_cast<const uint4*>(gb0 + (ro + 16u * (uint32_t)ch[c]));
+                mg[r][c] = FMT::meta_at(gb0, ro + FMT::meta_off(d, ch[c]));
+                wu[r][c] = *reinterpret_cast<const uint4*>(ub0 + (ro + 16u * (uint32_t)ch[c]));
+                mu[r][c] = FMT::meta_at(ub0, ro + FMT::meta_off(d, ch[c]));
             }
         __builtin_amdgcn_sched_barrier(0);   // every load of the pass is in flight before any use
+        // the lane that writes row f0 + (lane - 48) fetches its additive biases (gpt-oss) once the first pass's
+        // weight loads are out: their pointers' kernel-argument load and its wait stay off the weights' path
+        if (c0 == 0 && valid && rl >= 0 && rl < R) {
+            if (bg) bgl = bg[(size_t)e * F + f0 + rl];
+            if (bu) bul = bu[(size_t)e * F + f0 + rl];
+        }
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (RJM > 0) {
             // the token's whole tail, for idx / wts, while the weights arrive (it reads only registers)
             if (writer && c0 == 0) {
@@ -226,12 +230,21 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
     }
 }
 
+// Argument order: what the prologue needs before the first weight load (x, G, U, idx, k, d, F, Q, E) sits in the
+// first 64 bytes of the kernel arguments, so the wave's scalar loads of them are one scalar-cache line.
 template <class FMT, int R, int NCH, int HX, int RJM>
 __global__ void __launch_bounds__(256)
-k_gate_up_rows(const uint16_t* __restrict__ x, size_t xplane, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
-               const float* __restrict__ bg, const float* __restrict__ bu, const int32_t* __restrict__ idx, int k,
-               int d, int F, int E, int Q, int act, uint16_t* __restrict__ hhi, uint16_t* __restrict__ hlo,
-               RouteArgs rt) {
+k_gate_up_rows(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, const uint8_t* __restrict__ U,
+               const int32_t* __restrict__ idx, int k, int d, int F, int Q, int E, int act, size_t xplane,
+               const float* __restrict__ bg, const float* __restrict__ bu, uint16_t* __restrict__ hhi,
+               uint16_t* __restrict__ hlo, RouteArgs rt) {
+    // routed: every pointer argument is read into SGPRs at entry (one scalar-cache fill and one wait). Left to the
+    // compiler, some of these loads sink past the rank search, and their wait (which covers every scalar load then
+    // in flight) lands between the search and the first weight load. Not in the plain instance: an asm statement
+    // before the expert id's load turns that scalar load into a vector load with a full wait.
+    if constexpr (RJM > 0)
+        asm volatile("" ::"s"(x), "s"(G), "s"(U), "s"(bg), "s"(bu), "s"(hhi), "s"(hlo), "s"(rt.logits), "s"(rt.idx),
+                     "s"(rt.wts));
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int q0 = (blockIdx.x * 4 + wave) * R;
     if (q0 >= Q) return;
@@ -273,6 +286,9 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     const int slot = t * k + (jv ? j : k - 1);
     const int e = idx[slot];
     const float wraw = wts[slot];
+    // the id's load goes out first: the weight addresses wait on it, and the memory counter drains in issue order,
+    // so an h load issued ahead of it would be waited for as well
+    __builtin_amdgcn_sched_barrier(0);
     // ---- first staged words of this thread (L2): 16-byte word u of the token's hi and lo planes, u = thread +
     // m * block size, consecutive lanes on consecutive words (word u is quarter u & 3 of chunk u >> 2)
     constexpr int PF = 4;
@@ -294,9 +310,9 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     const int n0 = blockIdx.x * RB + wave * RR;
     // the residual of the wave's output rows (added by the storing lane at the end), loaded with the first
     // loads so that no memory round trip follows the reduction
-    float rres[RR];
+    uint32_t rres[RR];
 #pragma unroll
-    for (int i = 0; i < RR; ++i) rres[i] = resid ? load_y(resid, (size_t)t * D + min(n0 + i, D - 1), ydt) : 0.f;
+    for (int i = 0; i < RR; ++i) rres[i] = resid ? load_y_bits(resid, (size_t)t * D + min(n0 + i, D - 1), ydt) : 0u;
     const uint8_t* rows[RR];
 #pragma unroll
     for (int i = 0; i < RR; ++i) rows[i] = Dw + ((size_t)ee * D + min(n0 + i, D - 1)) * rb;
@@ -381,7 +397,7 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     for (int i = 0; i < RR; ++i) {
         const int n = n0 + i;
         const float v = sum_lanes<64>((acc[i] + bdv[i]) * wj);
-        if (lane == SL && n < D) store_y(y, (size_t)t * D + n, resid ? v + rres[i] : v, ydt);
+        if (lane == SL && n < D) store_y(y, (size_t)t * D + n, resid ? v + y_bits_f32(rres[i], ydt) : v, ydt);
     }
 }
 
@@ -494,7 +510,7 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
     const int cpr = F >> 5;
     // the residual of the output row wave 0's lane stores at the end, loaded before the slots' loads
     const int nr = blockIdx.x * RPW + lane;
-    const float rres = resid && !nored && wave == 0 && lane < RPW && nr < D ? load_y(resid, (size_t)t * D + nr, ydt) : 0.f;
+    const uint32_t rres = resid && !nored && wave == 0 && lane < RPW && nr < D ? load_y_bits(resid, (size_t)t * D + nr, ydt) : 0u;
     float yacc = 0.f;
     for (int j = wave; j < k; j += nw) {
         const int slot = t * k + j;
@@ -553,7 +569,7 @@ k_down_slots(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo,
         if (n2 < D) {
             float v = red[0][lane];
             for (int w = 1; w < nw; ++w) v += red[w][lane];
-            store_y(y, (size_t)t * D + n2, resid ? v + rres : v, ydt);
+            store_y(y, (size_t)t * D + n2, resid ? v + y_bits_f32(rres, ydt) : v, ydt);
         }
     }
 }
@@ -726,8 +742,8 @@ int launch_gu_rows_n(const ExpertsArgs& a, int R) {
     const int grid = (Q / R + 3) / 4;
     RouteArgs rt{a.route_logits, a.route_norm, a.route_scale, const_cast<int32_t*>(a.idx), const_cast<float*>(a.wts)};
 #define MOE_GUR_J(RR, H, J)                                                                                       \
-    k_gate_up_rows<FMT, RR, NCH, H, J><<<grid, 256, 0, a.st>>>(a.xb, a.xplane, P.G, P.U, w->gate.bias, w->up.bias,   \
-                                                              a.idx, a.k, w->d, w->F, w->E, Q, a.act, a.hhi, a.hlo, rt)
+    k_gate_up_rows<FMT, RR, NCH, H, J><<<grid, 256, 0, a.st>>>(a.xb, P.G, P.U, a.idx, a.k, w->d, w->F, Q, w->E, a.act, \
+                                                              a.xplane, w->gate.bias, w->up.bias, a.hhi, a.hlo, rt)
 // routed: the tail's logits per lane at compile time (E <= 64 J); the layer call routes bf16 x only (H == 1)
 #define MOE_GUR(RR, H)                                                                                           \
     do {                                                                                                         \

@@ -57,6 +57,12 @@ struct FmtInt4 {
     __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) {
         return *reinterpret_cast<const uint32_t*>(row + (K >> 1) + 4 * (c >> 1));
     }
+    // byte offset of chunk c's metadata word inside its row, and the load at a 32-bit offset from a wave-uniform
+    // base (the base in SGPRs, the offset in one VGPR: no 64-bit address arithmetic per load)
+    __device__ static __forceinline__ uint32_t meta_off(int K, int c) { return (uint32_t)(K >> 1) + 4u * (uint32_t)(c >> 1); }
+    __device__ static __forceinline__ uint32_t meta_at(const uint8_t* base, uint32_t off) {
+        return *reinterpret_cast<const uint32_t*>(base + off);
+    }
     // 7 VALU ops per word: t holds nibbles 0, 2, 4, 6 and u nibbles 1, 3, 5, 7 in the low halves of its
     // bytes; each v_perm_b32 picks two of those bytes and puts the bf16 exponent byte 0x43 above each.
     __device__ static __forceinline__ void decode_word(uint32_t w, uint32_t q[4]) {
@@ -82,6 +88,8 @@ struct FmtMxfp4 {
     static constexpr int FMT = MOE_FMT_MXFP4;
     static constexpr bool XSUM = false;
     __device__ static __forceinline__ uint32_t meta(const uint8_t* row, int K, int c) { return row[(K >> 1) + c]; }
+    __device__ static __forceinline__ uint32_t meta_off(int K, int c) { return (uint32_t)(K >> 1) + (uint32_t)c; }
+    __device__ static __forceinline__ uint32_t meta_at(const uint8_t* base, uint32_t off) { return base[off]; }
     // gfx950's v_cvt_scalef32_pk_bf16_fp4 turns the two E2M1 codes of one byte (low nibble first) into two bf16
     // (scale 1: exact), giving (e0, e1), (e2, e3), (e4, e5), (e6, e7); one v_perm_b32 per pair word regroups them
     // into the (n, n + 4) pairs the activations are laid out in. 8 VALU per code word, bit-identical to a
