@@ -587,23 +587,24 @@ k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t
           const float* __restrict__ wts,
           const float* __restrict__ bd, int E, const void* __restrict__ resid, void* __restrict__ y, int T, int k,
           int D, int ydt) {
+    // every pointer argument is read into SGPRs at entry (one scalar-cache fill, one wait); the kernel has no
+    // scalar loads from memory, which an asm statement ahead of them would turn into vector loads
+    asm volatile("" ::"s"(yp), "s"(idx), "s"(wts), "s"(bd), "s"(resid), "s"(y));
     const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total4 = (size_t)T * D / 4;
     if (i4 >= total4) return;
     const size_t i = i4 * 4;
     const int t = (int)(i / D), n = (int)(i % D);
-    // the residual first: its load goes out with the slots' loads (one memory round trip for the kernel)
-    float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
+    // the residual first, as raw bits: its load goes out with the slots' loads (one memory round trip for the
+    // kernel) and is converted at the end (a conversion here would wait for it, and for nothing else in flight)
+    uint4 rraw = make_uint4(0u, 0u, 0u, 0u);
     if (resid) {
         if (ydt == MOE_DTYPE_F32) {
-            rv = reinterpret_cast<const float4*>(resid)[i4];
-        } else if (ydt == MOE_DTYPE_F16) {
-            typedef _Float16 h4r __attribute__((ext_vector_type(4)));
-            const h4r r = reinterpret_cast<const h4r*>(resid)[i4];
-            rv = make_float4((float)r[0], (float)r[1], (float)r[2], (float)r[3]);
+            rraw = reinterpret_cast<const uint4*>(resid)[i4];
         } else {
             const uint2 r = reinterpret_cast<const uint2*>(resid)[i4];
-            rv = make_float4(bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y));
+            rraw.x = r.x;
+            rraw.y = r.y;
         }
     }
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -653,6 +654,16 @@ k_combine(const float* __restrict__ yp, int nplanes, size_t plane, const int32_t
         }
     }
     if (resid) {
+        float4 rv;
+        if (ydt == MOE_DTYPE_F32) {
+            rv = make_float4(__uint_as_float(rraw.x), __uint_as_float(rraw.y), __uint_as_float(rraw.z),
+                             __uint_as_float(rraw.w));
+        } else if (ydt == MOE_DTYPE_F16) {
+            rv = make_float4(y_bits_f32(rraw.x & 0xFFFFu, ydt), y_bits_f32(rraw.x >> 16, ydt),
+                             y_bits_f32(rraw.y & 0xFFFFu, ydt), y_bits_f32(rraw.y >> 16, ydt));
+        } else {
+            rv = make_float4(bf16lo(rraw.x), bf16hi(rraw.x), bf16lo(rraw.y), bf16hi(rraw.y));
+        }
         acc.x += rv.x;
         acc.y += rv.y;
         acc.z += rv.z;

@@ -21,15 +21,18 @@ struct GroupBufs {
 
 // One router launch (moe_router.hip): the logits, then (tail) the top-k tail per token, the merged slot lists with
 // shared experts, and the slot grouping.
+// The logits launch's fields come first: its prologue reads them from one 64-byte scalar-cache line.
 struct RouterArgs {
     const uint16_t* x;     // [T, d] bf16
     const uint16_t* wr;    // [E, d] bf16
-    const float* bias;     // [E] or null
     const uint16_t* gate;  // [d] bf16 or null: one more logit row (index E), the shared experts' gate
-    int T, d, E, k, norm;
-    float scale;
     float* logits;         // [T, lstride]
+    int32_t* arrive;       // set by launch_route: the finishing workgroups' arrival counter, zeroed by the logits
+    int T, d, E;
     int lstride;           // E, or E + 1 with the gate row
+    const float* bias;     // [E] or null
+    int k, norm;
+    float scale;
     int32_t* idx;          // [T, k] routed ids
     float* wts;            // [T, k] routed weights
     int S;                 // shared experts appended to every token's slots (0: none)
@@ -38,7 +41,6 @@ struct RouterArgs {
     GroupBufs grp;         // grp.counts null: no grouping; else the grouping of the slots (sidx when S > 0, else idx)
     int P, P2;             // pass sizes of grp.items / grp.items2 (unused when null)
     int mw;                // set by launch_route
-    int32_t* arrive;       // set by launch_route: the finishing workgroups' arrival counter, zeroed by the logits
 };
 // The router's launches: the logits over many workgroups, then (tail) route_finish: the tails, the merged lists and the
 // grouping (grp.counts) and pass lists. tail = false: logits only.

@@ -109,19 +109,33 @@ __device__ __forceinline__ void mx_h_block(float h0, float h1, bool write, uint8
     }
 }
 
+// Field order: what the tile kernels' prologues read (the in-kernel grouping's ids, the weight and activation
+// bases, the shapes, the pass lists) fills the first two 64-byte scalar-cache lines, so the prologue's scalar loads
+// miss once instead of once per line; epilogue-only fields follow.
 struct TileArgs {
+    const int32_t* gidx;   // wave tiles: when set, each workgroup finds its pass from these raw ids (gn = T k of them)
+    const uint8_t* W0;     // gate (or down) row records [E, N, rb]
+    const uint8_t* W1;     // up row records (gate/up only)
     const uint16_t* actv;  // gate/up: x [T, K] (bf16 plane 0); down: h [T*k, K] (bf16; the hi plane of h = hi + lo)
     const uint16_t* actv2; // down: the lo plane of h
     size_t act_plane;      // gate/up with fp16 / fp32 x: elements between x's bf16 planes (k_x_planes)
-    int act_div;           // activation row of slot p: p / act_div (k for gate/up, 1 for down)
-    const uint8_t* W0;     // gate (or down) row records [E, N, rb]
-    const uint8_t* W1;     // up row records (gate/up only)
+    int gn, gfirst;        // instead of the grouping kernel's pass list (gfirst: expert-major first passes)
+    int K, N;
+    int E, act_div;        // act_div: activation row of slot p is p / act_div (k for gate/up, 1 for down)
+    int nidx;              // 2 (first pass list) or 3 (second)
+    int act;               // GLU kind (gate/up)
+    const int32_t* meta;
+    const int32_t* items;  // wave and dense tiles: pass list (expert, pass, passes), meta[nidx] passes
+    const int32_t *counts, *offsets, *sorted;
+    // gate/up wave tiles grouping in-kernel: the workgroup (0, emit_y) (the grid's last row, set by the launch) also
+    // writes the grouping and the pass lists of these ids (as the grouping launch would) for the down stage;
+    // emit_grp.counts null: none
+    int emit_y;
+    GroupBufs emit_grp;
+    int emit_P, emit_P2;
+    const int32_t* active;
     const float* b0;       // additive row biases [E, N] (gpt-oss) or null
     const float* b1;
-    const int32_t *counts, *offsets, *sorted, *active, *meta;
-    const int32_t* items;  // wave and dense tiles: pass list (expert, pass, passes), meta[nidx] passes
-    int nidx;              // 2 (first pass list) or 3 (second)
-    int K, N, E, act;      // act: GLU kind (gate/up)
     int rpb;               // row tiles per block (k_tile_run)
     int kslots;            // k (slots per token)
     uint16_t* hout;        // gate/up: h = hi + lo as two bf16 planes [T*k, N]
@@ -131,12 +145,6 @@ struct TileArgs {
     size_t plane;
     size_t eslot_off;      // dense int4 down: per-slot exponents (int32 [slots]) at this byte offset from the exponent bytes
     const int32_t* xexp;   // dense int4 gate/up: per-token exponents of x16 (actv) [T]
-    const int32_t* gidx;   // wave tiles: when set, each workgroup finds its pass from these raw ids (gn = T k of them)
-    int gn, gfirst;        // instead of the grouping kernel's pass list (gfirst: expert-major first passes)
-    // gate/up wave tiles grouping in-kernel: the workgroup in the grid's last row (x = 0) also writes the grouping and
-    // the pass lists of these ids (as the grouping launch would) for the down stage; emit_grp.counts null: none
-    GroupBufs emit_grp;
-    int emit_P, emit_P2;
     uint8_t* hterm;        // block-scaled MXFP4 gate/up: h leaves as 3-term records [T*k][ceil(N/128)] (no planes)
 };
 
@@ -512,7 +520,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
         // the lists for the down stage, by the workgroup of the last row (usually past the live passes), first: its
         // own pass may be empty (not in the block-scaled variants: it would cost them occupancy)
         __shared__ int sGrp[NPROJ == 2 ? 2 * 1024 + 4 * 16 : 1];
-        if (a.emit_grp.counts && blockIdx.x == 0 && blockIdx.y == gridDim.y - 1) {
+        if (a.emit_grp.counts && blockIdx.x == 0 && (int)blockIdx.y == a.emit_y) {
             const int32_t* ids = a.gidx;
             group_block([&](int p) { return ids[p]; }, a.gn, a.E, a.emit_grp, a.emit_P, a.emit_P2, sGrp, 0);
         }
@@ -1890,13 +1898,15 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 #define MOE_WAVE_RT_DN 4   // 16-row tiles per wave, down (d % 64 == 0)
 #endif
 template <class FMT, int NPROJ, int RT, int D, bool H16O = false>
-int launch_wave_tile(const TileArgs& t, int nt, int nslots, hipStream_t st, int hx = 1, int mxt = 0) {
-    if (t.N % (16 * RT)) return MOE_ERR_ARG;
+int launch_wave_tile(const TileArgs& targs, int nt, int nslots, hipStream_t st, int hx = 1, int mxt = 0) {
+    if (targs.N % (16 * RT)) return MOE_ERR_ARG;
     // in-kernel grouping, expert-major: E first passes and at most ceil(n / P) further ones (an expert with c
     // slots has ceil(c / P) - 1 <= (c - 1) / P of them)
-    dim3 grid(t.N / (16 * RT), t.gidx && t.gfirst ? t.E + (nslots + 16 * nt - 1) / (16 * nt)
-                                                   : max_passes(nslots, t.E, 16 * nt));
+    dim3 grid(targs.N / (16 * RT), targs.gidx && targs.gfirst ? targs.E + (nslots + 16 * nt - 1) / (16 * nt)
+                                                           : max_passes(nslots, targs.E, 16 * nt));
     if (grid.y > 65535) return MOE_ERR_ARG;
+    TileArgs t = targs;
+    t.emit_y = (int)grid.y - 1;
     if constexpr (!FMT::XSUM && !H16O) {   // MXFP4 on the block-scaled MFMA: x 2 terms, h 3
         if (mxt) {
             constexpr int MT = NPROJ == 2 ? 2 : 3;
