@@ -21,7 +21,8 @@ struct GroupBufs {
 
 // One router launch (moe_router.hip): the logits, then (tail) the top-k tail per token, the merged slot lists with
 // shared experts, and the slot grouping.
-// The logits launch's fields come first: its prologue reads them from one 64-byte scalar-cache line.
+// Field order: the logits launch's prologue reads the first 64-byte scalar-cache line only; the tail launch's
+// (route_finish) reads the first two, then the grouping buffers in the third.
 struct RouterArgs {
     const uint16_t* x;     // [T, d] bf16
     const uint16_t* wr;    // [E, d] bf16
@@ -33,14 +34,15 @@ struct RouterArgs {
     const float* bias;     // [E] or null
     int k, norm;
     float scale;
+    int S;                 // shared experts appended to every token's slots (0: none)
     int32_t* idx;          // [T, k] routed ids
     float* wts;            // [T, k] routed weights
-    int S;                 // shared experts appended to every token's slots (0: none)
     int32_t* sidx;         // S > 0: [T, k + S] the k routed ids, then E .. E + S - 1
     float* swts;           // S > 0: [T, k + S] the routed weights, then sigmoid(gate logit) or 1
-    GroupBufs grp;         // grp.counts null: no grouping; else the grouping of the slots (sidx when S > 0, else idx)
-    int P, P2;             // pass sizes of grp.items / grp.items2 (unused when null)
     int mw;                // set by launch_route
+    int P;                 // pass size of grp.items (unused when null)
+    GroupBufs grp;         // grp.counts null: no grouping; else the grouping of the slots (sidx when S > 0, else idx)
+    int P2;                // pass size of grp.items2
 };
 // The router's launches: the logits over many workgroups, then (tail) route_finish: the tails, the merged lists and the
 // grouping (grp.counts) and pass lists. tail = false: logits only.

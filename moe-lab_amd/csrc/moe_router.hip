@@ -127,7 +127,8 @@ __global__ void __launch_bounds__(64 * FIN_WAVES) route_finish(RouterArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int k = a.k, ws = a.k + a.S, Eg = a.E + a.S;
     const bool grouping = a.grp.counts != nullptr;
-    const bool single = gridDim.x == 1;
+    const int nwg = (a.T + FIN_TOK - 1) / FIN_TOK;   // the grid (from T, not gridDim: no hidden-argument load)
+    const bool single = nwg == 1;
     int32_t* ids = a.S ? a.sidx : a.idx;   // the list the grouping reads
     const int t = blockIdx.x * FIN_TOK + wave;
     if (wave < FIN_TOK && t < a.T) {
@@ -162,7 +163,7 @@ __global__ void __launch_bounds__(64 * FIN_WAVES) route_finish(RouterArgs a) {
     __syncthreads();
     if (threadIdx.x == 0) {
         const int old = __hip_atomic_fetch_add(&a.grp.meta[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == (int)gridDim.x - 1);
+        s_last = (old == nwg - 1);
     }
     __syncthreads();
     if (!s_last) return;
