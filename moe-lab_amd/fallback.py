@@ -28,3 +28,30 @@ def grouped_from_load(D, F):
     fallback is a stock gather-matmul that wins at high load; here the fallback is this library's per-slot
     GEMV, which re-reads an expert for every slot and wins only where slots rarely share an expert."""
     return 1.0 if D * F < 5 << 19 else 0.27
+
+
+MIN_GROUPED_WAVES = 256   # gate/up wave tiles (32 rows each) the grouped path needs near its load threshold
+
+
+def grouped_waves(T, k, E, F):
+    """Expected live gate/up wave tiles of a grouped call: the expected number of distinct experts among T*k
+    uniformly routed slots, U = E (1 - (1 - 1/E)^(T k)), passes max(U, T k / 16), times F / 32 row blocks."""
+    n = T * k
+    U = E * (1.0 - (1.0 - 1.0 / E) ** n)
+    return max(U, n / 16) * F / 32
+
+
+def grouped_wins(T, k, E, D, F):
+    """The MI355X dispatch rule of the production dispatchers: grouped from the load grouped_from_load(D, F); near
+    that threshold (below twice the load) only when the grouped gate/up has MIN_GROUPED_WAVES live wave tiles.
+    With fewer, each wave walks its whole K with two slices in flight and the launch cannot fill the memory
+    pipe, while the per-slot GEMV spreads the same rows over many waves: random-shape sweeps found the per-slot
+    path 1.5-1.7x faster at d = 3328, F = 384, E = 16, k = 2, T = 8 (~124 such waves) and d = 896, F = 320, E = 32,
+    k = 2, T = 16 (~202), while every grouped win near the threshold had 447 or more (the fitted model shapes:
+    690-1950)."""
+    load = T * k / E
+    L0 = grouped_from_load(D, F)
+    if load < L0:
+        return False
+    return load >= 2 * L0 or grouped_waves(T, k, E, F) >= MIN_GROUPED_WAVES
+

@@ -12,7 +12,7 @@ import torch
 
 from .. import _lib, formats
 from ..experts import dims, make_state, reserve, run_experts, run_layer, unpack  # noqa: F401
-from ..fallback import gather_moe, grouped_from_load  # noqa: F401  (gather_moe: tests patch the attribute)
+from ..fallback import gather_moe, grouped_from_load, grouped_wins  # noqa: F401  (gather_moe: tests patch the attribute)
 
 META = {"name": "hip_mxfp4_moe", "description": "gfx950 HIP MXFP4: per-slot GEMV at T=1, grouped expert tiles at T>1"}
 MODE, GS, BITS = "mxfp4", 32, 4
@@ -29,11 +29,12 @@ def load_max(D, F):
 
 def grouped(T, k, E, D, F):
     """True: grouped tiles; False: the per-slot fallback. With LOAD_MAX set (tests, A/B runs) the reference's
-    rule, grouped up to LOAD_MAX; otherwise the MI355X fit, grouped from fallback.grouped_from_load."""
+    rule, grouped up to LOAD_MAX; otherwise the MI355X fit (fallback.grouped_wins): grouped from
+    fallback.grouped_from_load, near it only with enough live gate/up wave tiles."""
     load = T * k / E
     if LOAD_MAX is not None:
         return load <= LOAD_MAX
-    return load >= grouped_from_load(D, F)
+    return grouped_wins(T, k, E, D, F)
 
 
 def prepare(w_gate, w_up, w_down):

@@ -16,7 +16,7 @@ import torch
 
 from .. import _lib, formats
 from ..experts import dims, make_state, reserve, run_experts, run_layer, unpack  # noqa: F401
-from ..fallback import gather_moe, grouped_from_load  # noqa: F401  (gather_moe: tests patch the attribute)
+from ..fallback import gather_moe, grouped_from_load, grouped_wins  # noqa: F401  (gather_moe: tests patch the attribute)
 
 META = {"name": "hip_q4_moe", "description": "gfx950 HIP: per-slot GEMV at T=1, grouped expert tiles at T>1"}
 BITS, GS = 4, 64
@@ -42,10 +42,11 @@ def dequant(s):
 
 
 def custom_wins(T, k, E, D, F):
-    """Load policy, refitted on MI355X (fallback.grouped_from_load; the reference's name and meaning,
+    """Load policy, refitted on MI355X (fallback.grouped_wins; the reference's name and meaning,
     metal_q4_moe.py:42-46: True runs the grouped expert tiles, False the fallback): grouped from a load
-    T*k/E of 1.0 (experts below 2.5 Mi weights per projection) or 0.27, the per-slot GEMV below."""
-    return T * k / E >= grouped_from_load(D, F)
+    T*k/E of 1.0 (experts below 2.5 Mi weights per projection) or 0.27, the per-slot GEMV below, and near that
+    threshold only with enough live gate/up wave tiles to fill the chip."""
+    return grouped_wins(T, k, E, D, F)
 
 
 def run_slots(s, x, idx, act=0):

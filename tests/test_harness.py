@@ -136,6 +136,13 @@ def test_grid_crossover_and_fitted_policy():
         assert not hip_mxfp4_moe.grouped(t_slots, k, E, D, F) and hip_mxfp4_moe.grouped(t_grouped, k, E, D, F)
     assert hip_q4_moe.custom_wins(2, 2, 8, 4096, 14336) and hip_q4_moe.custom_wins(512, 2, 8, 4096, 14336)
     assert fallback.grouped_from_load(2048, 768) == 1.0 and fallback.grouped_from_load(4096, 14336) == 0.27
+    # near the threshold the grouped path also needs live gate/up wave tiles: the random-shape sweep's per-slot wins
+    # go per-slot, its grouped wins near the threshold stay grouped, and high loads are grouped whatever the count
+    assert abs(fallback.grouped_waves(16, 8, 128, 768) - 128 * (1 - (127 / 128) ** 128) * 24) < 1e-9
+    assert fallback.grouped_waves(128, 4, 16, 3264) == 32 * 102   # passes = T k / 16 when above U
+    assert not hip_q4_moe.custom_wins(8, 2, 16, 3328, 384) and not hip_mxfp4_moe.grouped(16, 2, 32, 896, 320)
+    assert hip_mxfp4_moe.grouped(3, 8, 32, 5120, 832) and hip_q4_moe.custom_wins(16, 1, 32, 3840, 1664)
+    assert hip_q4_moe.custom_wins(32, 2, 16, 3328, 384)   # load 4: no wave condition
 
 
 def test_reference_skips_ids_outside_range():
