@@ -307,7 +307,15 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     const bool ev = jv && (unsigned)e < (unsigned)E;
     const int ee = ev ? e : 0;
     const size_t rb = rbytes(FMT::FMT, F);
-    const int n0 = blockIdx.x * RB + wave * RR;
+    // row blocks XCD by XCD: blocks b = c (mod 8) run on one XCD, and XCD slot c takes a contiguous range of the
+    // nb = ceil(D / RB) row blocks, so the cache line two neighbouring blocks' records share (a record is not a
+    // whole number of lines) is fetched into one L2
+    int rbk;
+    {
+        const int nb = (D + RB - 1) / RB, q8 = nb >> 3, r8 = nb & 7, c = (int)(blockIdx.x & 7u), m = (int)(blockIdx.x >> 3);
+        rbk = (c < r8 ? c * (q8 + 1) : r8 * (q8 + 1) + (c - r8) * q8) + m;
+    }
+    const int n0 = rbk * RB + wave * RR;
     // the residual of the wave's output rows (added by the storing lane at the end), loaded with the first
     // loads so that no memory round trip follows the reduction
     uint32_t rres[RR];
