@@ -131,6 +131,9 @@ struct TileArgs {
     // writes the grouping and the pass lists of these ids (as the grouping launch would) for the down stage;
     // emit_grp.counts null: none
     int emit_y;
+    // down wave tiles from the emitted pass list: with at least this many live waves (passes x row blocks) a wave
+    // keeps one slice in flight instead of D (0: always D)
+    int shallow_min;
     GroupBufs emit_grp;
     int emit_P, emit_P2;
     const int32_t* active;
@@ -516,6 +519,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     __shared__ int sCnt[1024];            // in-kernel grouping: counts per expert (E <= 1024)
     __shared__ int sSlot[16 * NT];        // and the pass's slots
     int e, tok0, n, beg = 0;
+    bool shallow = false;   // see TileArgs::shallow_min
     if constexpr (NPROJ == 2 && MXT == 0) {
         // the lists for the down stage, by the workgroup of the last row (usually past the live passes), first: its
         // own pass may be empty (not in the block-scaled variants: it would cost them occupancy)
@@ -531,7 +535,9 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
         e = __builtin_amdgcn_readfirstlane(e);
         tok0 = __builtin_amdgcn_readfirstlane(tok0);
     } else {
-        if ((int)blockIdx.y >= a.meta[a.nidx]) return;   // one pass of the work list per workgroup row
+        const int npass = a.meta[a.nidx];
+        if ((int)blockIdx.y >= npass) return;   // one pass of the work list per workgroup row
+        shallow = a.shallow_min > 0 && npass * (a.N / (16 * RT)) >= a.shallow_min;
         e = a.items[3 * blockIdx.y];
         tok0 = a.items[3 * blockIdx.y + 1] * 16 * NT;
         n = a.counts[e];
@@ -795,6 +801,18 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
             for (int rt = 0; rt < RT; ++rt)
                 rex[p][rt] = INT4 ? tile_row_exps(p ? a.W1 : a.W0, a.E, N, K)[(size_t)e * N + r0 + 16 * rt + lr] : 0;
         __builtin_amdgcn_sched_barrier(0);
+        if (NPROJ == 1 && D > 1 && shallow) {
+            // many live waves: one slice in flight per wave. The launch's waves already request more than the
+            // memory system drains in a latency, and a deeper ring only lengthens its queues: Qwen3 down stage
+            // 24.6 -> 23.9, 27.7 -> 26.2, 31.2 -> 29.5 us at T = 16, 32, 64 uniform, while the Zipf(1.1) routings,
+            // with a few hundred live waves, keep the ring they need (a threshold of 1536 misses T = 16, 2560 all)
+            issue(0, rq[0], rm[0], rx[0]);
+            for (int s = 0; s < nsl; ++s) {
+                compute(true, rq[0], rm[0], rx[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                if (s + 1 < nsl) issue(s + 1, rq[0], rm[0], rx[0]);
+            }
+        } else {
         // ring: slices s0 .. s0 + D - 1 in flight at the top of each step. The walk is rounded up to a multiple
         // of D: slices past the last re-load the last one (cache hits) and fold with scale 0, so the loop body
         // has no branch. Issued slice by slice in the steady state's order, so the vmcnt waits at the loop top
@@ -813,6 +831,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
                 const int sn = s0 + i + D;
                 issue(sn < nsl ? sn : nsl - 1, rq[i], rm[i], rx[i]);
             }
+        }
         }
         if constexpr (INT4) {
 #pragma unroll
@@ -1930,6 +1949,9 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 #ifndef MOE_WAVE_RT_DN
 #define MOE_WAVE_RT_DN 4   // 16-row tiles per wave, down (d % 64 == 0)
 #endif
+#ifndef MOE_WAVE_DN_SHALLOW
+#define MOE_WAVE_DN_SHALLOW 1024   // live down waves from which a wave keeps one slice in flight (TileArgs::shallow_min)
+#endif
 template <class FMT, int NPROJ, int RT, int D, bool H16O = false>
 int launch_wave_tile(const TileArgs& targs, int nt, int nslots, hipStream_t st, int hx = 1, int mxt = 0) {
     if (targs.N % (16 * RT)) return MOE_ERR_ARG;
@@ -2187,6 +2209,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             d.nidx = 3;
         }
         if (wave_dn || dense_dn) d.W0 = (const uint8_t*)w->down.tiles;
+        d.shallow_min = env_int("MOE_WAVE_DN_SHALLOW", MOE_WAVE_DN_SHALLOW);
         // more row tiles per down wave (fewer activation loads per weight row) where d allows and the grid
         // keeps enough waves
         auto wide_dn = [&](int rt) {
