@@ -106,3 +106,27 @@ def test_ingroup_fp32_planes_and_stages(monkeypatch):
     y2 = run_experts(s, x, idx, wts, path=g, out_dtype=torch.float32, stages=_lib.STAGE_DOWN)
     torch.cuda.synchronize()
     assert torch.equal(y2, y1)
+
+
+@pytest.mark.parametrize("fmt,T,routing", [("int4", 32, "uniform"), ("int4", 64, "zipf"), ("mxfp4", 32, "uniform")])
+def test_down_ring_depth_bit_identical(monkeypatch, fmt, T, routing):
+    """The down wave tiles keep one slice in flight instead of two when the launch has many live waves (a choice
+    made on the device from the pass count; MOE_WAVE_DN_SHALLOW is its threshold). Both walks fold the same slices
+    in the same order, so forcing either one (threshold 1: always one slice; 0: always the ring) gives the same
+    outputs bit for bit, and the default call (uniform T=32 takes one slice, Zipf T=64 the ring) equals both."""
+    from moelab_amd import _lib
+    from moelab_amd.experts import run_experts
+    sh, s = state(fmt, 2048, 768, 128, 8, seed=11)
+    x, idx, wts = inputs(sh, T, routing, seed=T)
+    print(f"case ring depth {fmt} T={T} {routing}", flush=True)
+    ys = {}
+    for v in ("1", "0", None):
+        if v is None:
+            monkeypatch.delenv("MOE_WAVE_DN_SHALLOW", raising=False)
+        else:
+            monkeypatch.setenv("MOE_WAVE_DN_SHALLOW", v)
+        ys[v] = run_experts(s, x, idx, wts, out_dtype=torch.float32, path=_lib.PATH_GROUPED)
+    torch.cuda.synchronize()
+    assert torch.equal(ys["1"], ys["0"]), float((ys["1"] - ys["0"]).abs().max())
+    assert torch.equal(ys[None], ys["0"])
+    assert_close(ys[None], oracle_y(s, x, idx, wts), what=f"down ring depth {fmt} T={T} {routing}")
