@@ -253,6 +253,9 @@ k_gate_up_rows(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, co
 }
 
 // ============================================================================ per-slot down, h staged in LDS
+#ifndef MOE_DN_PF_MAX
+#define MOE_DN_PF_MAX 6   // h words per thread loaded ahead of the weights (k_down_rows)
+#endif
 // grid (ceil(D / RB), T), block 64 * NW (NW waves); every block computes RB = NW * RR rows of y[t] over all
 // k slots of token t. Lane l of a wave: chunk phase p = l % L, slot j = l / L (64 / L >= k slot lanes, L a
 // power of two), so one wave covers every (slot, chunk) pair of its RR rows, and the k-reduction is an
@@ -290,8 +293,10 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     // so an h load issued ahead of it would be waited for as well
     __builtin_amdgcn_sched_barrier(0);
     // ---- first staged words of this thread (L2): 16-byte word u of the token's hi and lo planes, u = thread +
-    // m * block size, consecutive lanes on consecutive words (word u is quarter u & 3 of chunk u >> 2)
-    constexpr int PF = 4;
+    // m * block size, consecutive lanes on consecutive words (word u is quarter u & 3 of chunk u >> 2). The
+    // token's k F / 8 words number at most 256 NC (k <= 64 / L slots of cpr <= NC L chunks, 4 words each), so
+    // ceil(4 NC / NW) words per thread take them all in the first round trip (up to MOE_DN_PF_MAX)
+    constexpr int PF = (4 * NC + NW - 1) / NW < MOE_DN_PF_MAX ? (4 * NC + NW - 1) / NW : MOE_DN_PF_MAX;
     const size_t hbase = (size_t)t * k * F;
     const uint4* h4 = reinterpret_cast<const uint4*>(hhi + hbase);
     const uint4* l4 = reinterpret_cast<const uint4*>(hlo + hbase);
