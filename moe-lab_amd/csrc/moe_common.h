@@ -270,6 +270,26 @@ __device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t bas
     hlo[i] = f32_to_bf16(v - bf16_to_f32(hi));
 }
 
+// The per-slot GEMV path (k_gate_up_rows -> k_down_rows) keeps h as one fp16 plane (in hhi, same pairing) when
+// its value is bounded above: MXFP4 weights with the gpt-oss GLU, whose clamps (g <= 7, |u| <= 7) give
+// |h| <= 7 * 1 * 8 = 56. The plane holds h 2^8 (<= 14336 < 65504), so h keeps fp16's 11 significant bits down to
+// |h| = 2^-22 and an absolute step of 2^-32 below that (the hi + lo bf16 planes: ~16 bits at any magnitude), with
+// half the bytes; the e2m1 codes decode to fp16 exactly and the down scales its sums back by 2^-8.
+__host__ __device__ constexpr bool h_is_f16(int fmt, int act) { return fmt == MOE_FMT_MXFP4 && act == MOE_ACT_GPTOSS; }
+#define MOE_H16_SCALE 256.0f
+__device__ __forceinline__ void store_h16(uint16_t* h16, size_t base, int n, float v) {
+    h16[base + paired_pos(n)] = __builtin_bit_cast(uint16_t, (_Float16)(v * MOE_H16_SCALE));
+}
+// a.x*b.x + a.y*b.y + c with fp16 pairs packed in 32-bit words (v_dot2_f32_f16)
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(moe_f16x2, a), __builtin_bit_cast(moe_f16x2, b), c, false);
+}
+__device__ __forceinline__ float dot16_f16(const uint32_t qp[16], const uint32_t hp[16], float acc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = dot2_f16(qp[i], hp[i], acc);
+    return acc;
+}
+
 // outputs and residuals: ydt = MOE_DTYPE_BF16, MOE_DTYPE_F16 or MOE_DTYPE_F32 (round to nearest even)
 __device__ __forceinline__ void store_y(void* y, size_t i, float v, int ydt) {
     if (ydt == MOE_DTYPE_F32) reinterpret_cast<float*>(y)[i] = v;

@@ -226,7 +226,8 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
         for (int q = 0; q < R; ++q)
             if (q == rl) { g = ag[q]; u = au[q]; }
         const float hv = valid ? glu_act(act, g + bgl, u + bul) : 0.f;
-        store_h(hhi, hlo, (size_t)s * F, f0 + rl, hv);
+        if (h_is_f16(FMT::FMT, act)) store_h16(hhi, (size_t)s * F, f0 + rl, hv);
+        else store_h(hhi, hlo, (size_t)s * F, f0 + rl, hv);
     }
 }
 
@@ -268,14 +269,19 @@ k_gate_up_rows(const uint16_t* __restrict__ x, const uint8_t* __restrict__ G, co
 // conflict). Order of memory operations: the lane's expert id and routing weight, the first staged h words
 // (L2), every weight chunk and metadata word of the lane (branch-free: chunk indices past the row are clamped
 // into it and masked out of the math), the LDS staging, then the math in load order.
-template <class FMT, int NC, int RR, int NW>
+// H16 (h_is_f16: MXFP4 with the gpt-oss GLU): h is one fp16 plane in hhi; a record is its 64 bytes plus one
+// 16-byte pad word (80 = 5 x 16, 5 odd: the same bank spread), the codes decode to fp16 and the dots run on
+// v_dot2_f32_f16, one per pair instead of two.
+template <class FMT, int NC, int RR, int NW, bool H16 = false>
 __global__ void __launch_bounds__(64 * NW)
 k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, const uint8_t* __restrict__ Dw,
             const float* __restrict__ bd, const int32_t* __restrict__ idx, const float* __restrict__ wts, int k,
             int D, int F, int E, int lgL, int nored, int ydt, const void* __restrict__ resid,
             void* __restrict__ y) {
+    static_assert(!H16 || !FMT::XSUM, "fp16 h: no chunk sums (MXFP4)");
     constexpr int SL = sum_lane<64>();
     constexpr int RB = NW * RR;
+    constexpr int REC = H16 ? 5 : 9;   // 16-byte words per staged chunk record
     extern __shared__ uint4 s_dyn[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int t = blockIdx.y;
@@ -283,7 +289,7 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     const int p = lane & (L - 1), j = lane >> lgL;
     const int cpr = F >> 5;
     const int nch = k * cpr;   // chunks of h to stage
-    uint4* s_h = s_dyn;   // [nch][9]: hi pairs x4, lo pairs x4, {chunk sum, pad}
+    uint4* s_h = s_dyn;   // [nch][REC]: hi pairs x4, lo pairs x4, {chunk sum, pad}; H16: fp16 pairs x4, pad
     // ---- expert id and routing weight of this lane's slot
     const bool jv = j < k;
     const int slot = t * k + (jv ? j : k - 1);
@@ -306,7 +312,7 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     for (int m = 0; m < PF; ++m) {
         const int u = min((int)threadIdx.x + m * 64 * NW, nu - 1);
         hv[2 * m] = h4[u];
-        hv[2 * m + 1] = l4[u];
+        if constexpr (!H16) hv[2 * m + 1] = l4[u];
     }
     // ---- weights of this lane
     const bool ev = jv && (unsigned)e < (unsigned)E;
@@ -348,9 +354,9 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
     // four lanes of a chunk are consecutive lanes of one wave and always active together (nu and the block size
     // are multiples of 4), so the chunk sum (int4 fold) is a quad reduction.
     auto put = [&](int u, const uint4& a, const uint4& b) __attribute__((always_inline)) {
-        uint4* r = s_h + (size_t)(u >> 2) * 9;
+        uint4* r = s_h + (size_t)(u >> 2) * REC;
         r[u & 3] = a;
-        r[4 + (u & 3)] = b;
+        if constexpr (!H16) r[4 + (u & 3)] = b;
         if (FMT::XSUM) {
             float sm = 0.f;
             sm = dot2_bf16(a.x, 0x3f803f80u, sm);
@@ -371,7 +377,10 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
         const int u = (int)threadIdx.x + m * 64 * NW;
         if (u < nu) put(u, hv[2 * m], hv[2 * m + 1]);
     }
-    for (int u = (int)threadIdx.x + PF * 64 * NW; u < nu; u += 64 * NW) put(u, h4[u], l4[u]);
+    for (int u = (int)threadIdx.x + PF * 64 * NW; u < nu; u += 64 * NW) {
+        if constexpr (H16) put(u, h4[u], uint4{});
+        else put(u, h4[u], l4[u]);
+    }
     __syncthreads();
     // ---- math
     float acc[RR];
@@ -383,16 +392,27 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
         const bool cv = ev && chk < cpr;
         const size_t hc = (size_t)(jv ? j : 0) * cpr + min(chk, cpr - 1);
         uint32_t wh[16], wl[16];
-        words16(&s_h[hc * 9], wh);
-        words16(&s_h[hc * 9 + 4], wl);
-        const float hs = FMT::XSUM ? reinterpret_cast<const float*>(s_h + hc * 9 + 8)[0] : 0.f;
+        words16(&s_h[hc * REC], wh);
+        if constexpr (!H16) words16(&s_h[hc * REC + 4], wl);
+        const float hs = FMT::XSUM ? reinterpret_cast<const float*>(s_h + hc * REC + 8)[0] : 0.f;
 #pragma unroll
         for (int i = 0; i < RR; ++i) {
             uint32_t qp[16];
-            FMT::decode(wv[c][i], qp);
-            const float v = FMT::fold(0.f, mv[c][i], dot16(qp, wl, dot16(qp, wh, 0.f)), hs);
+            float dd;
+            if constexpr (H16) {
+                FMT::decode_f16(wv[c][i], qp);
+                dd = dot16_f16(qp, wh, 0.f);
+            } else {
+                FMT::decode(wv[c][i], qp);
+                dd = dot16(qp, wl, dot16(qp, wh, 0.f));
+            }
+            const float v = FMT::fold(0.f, mv[c][i], dd, hs);
             acc[i] += cv ? v : 0.f;
         }
+    }
+    if constexpr (H16) {
+#pragma unroll
+        for (int i = 0; i < RR; ++i) acc[i] *= 1.0f / MOE_H16_SCALE;   // a power of two: exact
     }
     if (nored) {
 #pragma unroll
@@ -829,13 +849,13 @@ int down_rows_lds(int k, int F) { return k * (F >> 5) * 144; }   // 144-byte chu
 #ifndef MOE_DN_RR2_NC
 #define MOE_DN_RR2_NC 2   // two rows per lane while NC <= this (at NC = 3, Qwen3: twice the blocks, 4.95 -> 4.68 us)
 #endif
-template <class FMT, int NC, int RR>
-int launch_dn_rows_k(const ExpertsArgs& a, int lgL) {
+template <class FMT, int NC, int RR, bool H16>
+int launch_dn_rows_kh(const ExpertsArgs& a, int lgL) {
     constexpr int NW = MOE_DN_NW;
     const moe_experts_t* w = a.w;
     const ProjPtrs P = ptrs(w);
-    auto kern = k_down_rows<FMT, NC, RR, NW>;
-    const int lds = down_rows_lds(a.k, w->F);
+    auto kern = k_down_rows<FMT, NC, RR, NW, H16>;
+    const int lds = H16 ? a.k * (w->F >> 5) * 80 : down_rows_lds(a.k, w->F);
     // above 64 KB of LDS the kernel needs the attribute on the device it runs on: set on every such launch (a host
     // call, no stream work) rather than remembered, so no state is kept and every device gets it
     if (lds > 64 * 1024 &&
@@ -845,6 +865,13 @@ int launch_dn_rows_k(const ExpertsArgs& a, int lgL) {
     kern<<<grid, 64 * NW, lds, a.st>>>(a.hhi, a.hlo, P.Dn, w->down.bias, a.idx, a.wts, a.k, w->d, w->F, w->E, lgL,
                                    a.nored, a.ydt, a.residual, a.y);
     return hipGetLastError() == hipSuccess ? 0 : MOE_ERR_LAUNCH;
+}
+// h as the gate/up stage wrote it (h_is_f16: one fp16 plane)
+template <class FMT, int NC, int RR>
+int launch_dn_rows_k(const ExpertsArgs& a, int lgL) {
+    if constexpr (FMT::FMT == MOE_FMT_MXFP4)
+        if (h_is_f16(FMT::FMT, a.act)) return launch_dn_rows_kh<FMT, NC, RR, true>(a, lgL);
+    return launch_dn_rows_kh<FMT, NC, RR, false>(a, lgL);
 }
 
 // lanes per down row L = 64 / KP (KP = the power of two >= k); chunks per lane NC >= cpr / L, from a fixed

@@ -89,7 +89,7 @@ struct ExpertsArgs {
     void* y;              // [T, d] (or [T*k, d] when nored), of dtype ydt
     int ydt;              // MOE_DTYPE_BF16, MOE_DTYPE_F16 or MOE_DTYPE_F32
     const void* residual; // same dtype as y, or NULL
-    uint16_t* hhi;        // GLU output h = hi + lo, two bf16 planes [T*k, F]
+    uint16_t* hhi;        // GLU output h = hi + lo, two bf16 planes [T*k, F] (per-slot rows path with h_is_f16: one fp16 plane in hhi)
     uint16_t* hlo;
     float* yp;      // 4 x [T*k, d] fp32 scratch (grouped path; the further planes for a K-split down projection)
     uint16_t* x16;  // grouped path, dense int4: x as fp16 [T, d] with a power-of-two exponent per token

@@ -143,6 +143,20 @@ def test_gptoss_biases_and_clamped_glu(T, act):
     assert_close(gpt().reference(s, x.float(), idx, wts), ref, tol=2e-3)
 
 
+@pytest.mark.parametrize("T", [1, 5])
+def test_gptoss_small_h(T):
+    """The per-slot path keeps the gpt-oss GLU's h as one fp16 plane holding h 2^8 (|h| <= 56 by the clamps).
+    With activations 1e-6 of the usual size every |h| is near 2^-21, below fp16's smallest normal 2^-14: an
+    unscaled fp16 h would keep ~3 significant bits there (about 10% of the output RMS), the scaled one 11."""
+    sh = shape_("gs", 256, 256, 8, 4)
+    s = packed_state(sh, 7)
+    s["act"] = 1
+    x, idx, wts = inputs(sh, T, seed=7, scale=1e-6)
+    ref = oracle_y(s, x, idx, wts, act=2)
+    assert 0 < np.sqrt(np.mean(ref ** 2)) < 1e-5, "the case must keep h far below fp16's normal range"
+    assert_close(gpt().run(s, x, idx, wts, out_dtype=torch.float32), ref)
+
+
 def test_gptoss_large_scale_bytes():
     """gpt-oss checkpoints reach E8M0 bytes >= 133 (reference test_gptoss_patch.py:88-113)."""
     sh = shape_("gl", 256, 256, 8, 4)
