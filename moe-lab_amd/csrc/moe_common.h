@@ -263,9 +263,10 @@ __device__ __forceinline__ float sum16(const uint32_t w[16], float acc) {
 
 // h element n -> position inside its chunk so that 16-byte loads yield (n, n+4) pairs
 __device__ __forceinline__ int paired_pos(int n) { return (n & ~7) | ((n & 3) << 1) | ((n >> 2) & 1); }
-__device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t base, int n, float v) {
+// nat: element n at position n (the MXFP4 per-slot rows, FmtMxfp4::ROWS_NAT), else pre-paired
+__device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t base, int n, float v, bool nat = false) {
     const uint16_t hi = f32_to_bf16(v);
-    const size_t i = base + paired_pos(n);
+    const size_t i = base + (nat ? n : paired_pos(n));
     hhi[i] = hi;
     hlo[i] = f32_to_bf16(v - bf16_to_f32(hi));
 }
@@ -277,8 +278,8 @@ __device__ __forceinline__ void store_h(uint16_t* hhi, uint16_t* hlo, size_t bas
 // half the bytes; the e2m1 codes decode to fp16 exactly and the down scales its sums back by 2^-8.
 __host__ __device__ constexpr bool h_is_f16(int fmt, int act) { return fmt == MOE_FMT_MXFP4 && act == MOE_ACT_GPTOSS; }
 #define MOE_H16_SCALE 256.0f
-__device__ __forceinline__ void store_h16(uint16_t* h16, size_t base, int n, float v) {
-    h16[base + paired_pos(n)] = __builtin_bit_cast(uint16_t, (_Float16)(v * MOE_H16_SCALE));
+__device__ __forceinline__ void store_h16(uint16_t* h16, size_t base, int n, float v, bool nat) {
+    h16[base + (nat ? n : paired_pos(n))] = __builtin_bit_cast(uint16_t, (_Float16)(v * MOE_H16_SCALE));
 }
 // a.x*b.x + a.y*b.y + c with fp16 pairs packed in 32-bit words (v_dot2_f32_f16)
 __device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {

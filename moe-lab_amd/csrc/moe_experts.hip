@@ -14,11 +14,13 @@
 //          sum_k (s q_k + b) x_k = s * sum_k (128 + q_k) x_k + (b - 128 s) * sum_k x_k
 //   MXFP4: pairs hold e2m1(q) from two v_perm_b32 byte lookups, and the chunk's dot is scaled by
 //          2^(s-127) in fp32 (one E8M0 group = one chunk).
-// Pairs are (input 8j+i, input 8j+i+4): the activation side is paired the same way (pair_x32).
+// Pairs are (input 8j+i, input 8j+i+4): the activation side is paired the same way (pair_x32). The MXFP4
+// per-slot rows (k_gate_up_rows, k_down_rows) take the converts' natural pairs (2i, 2i+1) instead, against x
+// and h in natural order: no v_perm per code word and no pairing of x (FmtMxfp4::ROWS_NAT).
 //
 // The GLU output h (gate/up -> down) is kept at ~16 significant bits as two bf16 planes h = hi + lo,
 // stored pre-paired (element n of a chunk at (n & ~7) | (n & 3) << 1 | (n >> 2) & 1), so the down
-// projection loads ready-made pairs.
+// projection loads ready-made pairs (MXFP4 rows: natural order; with the gpt-oss GLU one fp16 plane, h_is_f16).
 //
 // Kernels:
 //   k_gate_up_slots / k_down_slots   per-slot GEMV (any T; the stock-style per-slot gather at T > 1)
@@ -192,7 +194,12 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
             xs[c] = 0.f;
 #pragma unroll
             for (int h = 0; h < HX; ++h) {
-                pair_x32(xw[h][c], xp[h][c]);
+                if constexpr (FMT::ROWS_NAT) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) xp[h][c][i] = xw[h][c][i];
+                } else {
+                    pair_x32(xw[h][c], xp[h][c]);
+                }
                 xs[c] = FMT::XSUM ? sum_x32(xw[h][c]) + xs[c] : 0.f;
             }
         }
@@ -207,9 +214,9 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 uint32_t qp[16];
-                FMT::decode(wg[r][c], qp);
+                FMT::decode_rows(wg[r][c], qp);
                 const float dg = FMT::fold(0.f, mg[r][c], dotx(qp, c), xs[c]);
-                FMT::decode(wu[r][c], qp);
+                FMT::decode_rows(wu[r][c], qp);
                 const float du = FMT::fold(0.f, mu[r][c], dotx(qp, c), xs[c]);
                 ag[r] += cv[c] ? dg : 0.f;
                 au[r] += cv[c] ? du : 0.f;
@@ -226,8 +233,8 @@ __device__ __forceinline__ void gate_up_rows_wave(const uint16_t* __restrict__ x
         for (int q = 0; q < R; ++q)
             if (q == rl) { g = ag[q]; u = au[q]; }
         const float hv = valid ? glu_act(act, g + bgl, u + bul) : 0.f;
-        if (h_is_f16(FMT::FMT, act)) store_h16(hhi, (size_t)s * F, f0 + rl, hv);
-        else store_h(hhi, hlo, (size_t)s * F, f0 + rl, hv);
+        if (h_is_f16(FMT::FMT, act)) store_h16(hhi, (size_t)s * F, f0 + rl, hv, FMT::ROWS_NAT);
+        else store_h(hhi, hlo, (size_t)s * F, f0 + rl, hv, FMT::ROWS_NAT);
     }
 }
 
@@ -400,10 +407,10 @@ k_down_rows(const uint16_t* __restrict__ hhi, const uint16_t* __restrict__ hlo, 
             uint32_t qp[16];
             float dd;
             if constexpr (H16) {
-                FMT::decode_f16(wv[c][i], qp);
+                FMT::decode_rows_f16(wv[c][i], qp);
                 dd = dot16_f16(qp, wh, 0.f);
             } else {
-                FMT::decode(wv[c][i], qp);
+                FMT::decode_rows(wv[c][i], qp);
                 dd = dot16(qp, wl, dot16(qp, wh, 0.f));
             }
             const float v = FMT::fold(0.f, mv[c][i], dd, hs);

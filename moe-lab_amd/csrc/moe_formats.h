@@ -78,6 +78,9 @@ struct FmtInt4 {
         decode_word(w.z, qp + 8);
         decode_word(w.w, qp + 12);
     }
+    // per-slot GEMV rows: the same (n, n + 4) pairs (one shift and mask per two codes), x and h paired to match
+    static constexpr bool ROWS_NAT = false;
+    __device__ static __forceinline__ void decode_rows(uint4 w, uint32_t qp[16]) { decode(w, qp); }
     __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float xsum) {
         const float s = bf16lo(m), b = bf16hi(m);
         return __builtin_fmaf(s, dot, __builtin_fmaf(__builtin_fmaf(-128.f, s, b), xsum, acc));
@@ -110,21 +113,29 @@ struct FmtMxfp4 {
         decode_word(w.z, qp + 8);
         decode_word(w.w, qp + 12);
     }
-    // the same pairs as fp16 (v_cvt_scalef32_pk_f16_fp4, scale 1: every e2m1 value is exact in fp16), for the
-    // per-slot down when h is one fp16 plane
-    __device__ static __forceinline__ void decode_f16(uint4 w, uint32_t qp[16]) {
+    // Per-slot GEMV rows (k_gate_up_rows, k_down_rows): the codes in natural pairs (e_2b, e_2b+1) of each byte, as
+    // the convert yields them (4 VALU per code word, no v_perm), against x and h in natural order too
+    static constexpr bool ROWS_NAT = true;
+    __device__ static __forceinline__ void decode_rows(uint4 w, uint32_t qp[16]) {
         const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t v = wd[i];
-            const uint32_t p0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 1.0f, 0));
-            const uint32_t p1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 1.0f, 1));
-            const uint32_t p2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 1.0f, 2));
-            const uint32_t p3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 1.0f, 3));
-            qp[4 * i + 0] = __builtin_amdgcn_perm(p2, p0, 0x05040100u);   // (e0, e4)
-            qp[4 * i + 1] = __builtin_amdgcn_perm(p2, p0, 0x07060302u);   // (e1, e5)
-            qp[4 * i + 2] = __builtin_amdgcn_perm(p3, p1, 0x05040100u);   // (e2, e6)
-            qp[4 * i + 3] = __builtin_amdgcn_perm(p3, p1, 0x07060302u);   // (e3, e7)
+            qp[4 * i + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[i], 1.0f, 0));
+            qp[4 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[i], 1.0f, 1));
+            qp[4 * i + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[i], 1.0f, 2));
+            qp[4 * i + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[i], 1.0f, 3));
+        }
+    }
+    // the same as fp16 (v_cvt_scalef32_pk_f16_fp4, scale 1: every e2m1 value is exact in fp16), for the per-slot
+    // down when h is one fp16 plane
+    __device__ static __forceinline__ void decode_rows_f16(uint4 w, uint32_t qp[16]) {
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qp[4 * i + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 0));
+            qp[4 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 1));
+            qp[4 * i + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 2));
+            qp[4 * i + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 3));
         }
     }
     __device__ static __forceinline__ float fold(float acc, uint32_t m, float dot, float) {
