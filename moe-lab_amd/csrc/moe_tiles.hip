@@ -516,8 +516,11 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     constexpr bool INT4 = FMT::XSUM;
     constexpr int HL = NPROJ == 2 ? HX : 2;   // activation planes: x's (1, or 2-3 for fp16 / fp32 x), h = hi + lo
     constexpr int SB = tile_slice_bytes<FMT>();
-    __shared__ int sCnt[1024];            // in-kernel grouping: counts per expert (E <= 1024)
-    __shared__ int sSlot[16 * NT];        // and the pass's slots
+    // in-kernel grouping from raw ids (a.gidx): the gate/up stage, and the block-scaled down that groups for itself;
+    // the other downs always read a pass list (the launch rejects a.gidx for them)
+    constexpr bool GIDX = NPROJ == 2 || MXT > 0;
+    __shared__ int sCnt[GIDX ? 1024 : 1];       // in-kernel grouping: counts per expert (E <= 1024)
+    __shared__ int sSlot[GIDX ? 16 * NT : 1];   // and the pass's slots
     int e, tok0, n, beg = 0;
     bool shallow = false;   // see TileArgs::shallow_min
     if constexpr (NPROJ == 2 && MXT == 0) {
@@ -529,19 +532,41 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
             group_block([&](int p) { return ids[p]; }, a.gn, a.E, a.emit_grp, a.emit_P, a.emit_P2, sGrp, 0);
         }
     }
-    if (a.gidx) {
+    // slot of the lane's activation row (A side: token tok0 + 16 t + lr), read in each branch from its own memory:
+    // a load through a pointer chosen between LDS and global memory is a flat load, which the compiler waits for
+    // with a full vmcnt(0), ahead of the first weight loads
+    int slotA[NT];
+    if (GIDX && a.gidx) {
         if (!wave_find_pass(a.gidx, a.gn, a.E, 16 * NT, a.gfirst, (int)blockIdx.y, sCnt, sSlot, e, tok0, n))
             return;
         e = __builtin_amdgcn_readfirstlane(e);
         tok0 = __builtin_amdgcn_readfirstlane(tok0);
+        const __attribute__((address_space(3))) int* ls = (const __attribute__((address_space(3))) int*)sSlot;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int m = tok0 + 16 * t + (int)(threadIdx.x & 15);
+            slotA[t] = ls[(m < n ? m : n - 1) - tok0];
+        }
     } else {
+        // the row's list entry is read with the pass count, in one round trip: the list has room for the grid's
+        // rows (max_passes of the launch's pass size), so the entry exists for rows past the live passes too, which
+        // return before using it; the exit test reads both, so neither load waits for the other, and keeps a bad
+        // entry's id off the weight addresses
         const int npass = a.meta[a.nidx];
-        if ((int)blockIdx.y >= npass) return;   // one pass of the work list per workgroup row
+        const int e_l = a.items[3 * blockIdx.y], p_l = a.items[3 * blockIdx.y + 1];
+        const bool past = (int)blockIdx.y >= npass, bad = ((unsigned)e_l >= (unsigned)a.E) | (p_l < 0);
+        if (past | bad) return;   // one pass of the work list per workgroup row
         shallow = a.shallow_min > 0 && npass * (a.N / (16 * RT)) >= a.shallow_min;
-        e = a.items[3 * blockIdx.y];
-        tok0 = a.items[3 * blockIdx.y + 1] * 16 * NT;
+        e = e_l;
+        tok0 = p_l * 16 * NT;
         n = a.counts[e];
         beg = a.offsets[e];
+        const __attribute__((address_space(1))) int* gs = (const __attribute__((address_space(1))) int*)a.sorted;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int m = tok0 + 16 * t + (int)(threadIdx.x & 15);
+            slotA[t] = gs[beg + (m < n ? m : n - 1)];
+        }
     }
     const int lane = threadIdx.x, lr = lane & 15, lg = lane >> 4;
     const int K = a.K, N = a.N;
@@ -561,13 +586,8 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
     {
         // byte offset of the lane's activation row (A side: token tok0 + 16 t + lr)
         uint32_t xo[NT];
-        int slotA[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int m = tok0 + 16 * t + lr;
-            slotA[t] = a.gidx ? sSlot[(m < n ? m : n - 1) - tok0] : a.sorted[beg + (m < n ? m : n - 1)];
-            xo[t] = (uint32_t)(slotA[t] / a.act_div) * (uint32_t)K * 2u;
-        }
+        for (int t = 0; t < NT; ++t) xo[t] = (uint32_t)(slotA[t] / a.act_div) * (uint32_t)K * 2u;
         f32x4 acc[NPROJ][RT][NT];
 #pragma unroll
         for (int p = 0; p < NPROJ; ++p)
@@ -793,13 +813,16 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
             }
         };
         // int4: the records hold each row's scales and biases times 2^-E (E per row, moe_tiles_pack), so the
-        // sums come back by 2^E in the epilogue; the lane's exponents are loaded before the ring starts
+        // sums come back by 2^E in the epilogue. Only the epilogue reads the lane's exponents: they are loaded after
+        // the ring's first slices, which then do not wait for them
         int rex[NPROJ][RT];
+        auto load_rex = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int p = 0; p < NPROJ; ++p)
+            for (int p = 0; p < NPROJ; ++p)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-                rex[p][rt] = INT4 ? tile_row_exps(p ? a.W1 : a.W0, a.E, N, K)[(size_t)e * N + r0 + 16 * rt + lr] : 0;
+                for (int rt = 0; rt < RT; ++rt)
+                    rex[p][rt] = INT4 ? tile_row_exps(p ? a.W1 : a.W0, a.E, N, K)[(size_t)e * N + r0 + 16 * rt + lr] : 0;
+        };
         __builtin_amdgcn_sched_barrier(0);
         if (NPROJ == 1 && D > 1 && shallow) {
             // many live waves: one slice in flight per wave. The launch's waves already request more than the
@@ -807,6 +830,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
             // 24.6 -> 23.9, 27.7 -> 26.2, 31.2 -> 29.5 us at T = 16, 32, 64 uniform, while the Zipf(1.1) routings,
             // with a few hundred live waves, keep the ring they need (a threshold of 1536 misses T = 16, 2560 all)
             issue(0, rq[0], rm[0], rx[0]);
+            load_rex();
             for (int s = 0; s < nsl; ++s) {
                 compute(true, rq[0], rm[0], rx[0]);
                 __builtin_amdgcn_sched_barrier(0);
@@ -822,6 +846,7 @@ __global__ void __launch_bounds__(64) k_wave_tile(TileArgs a) {
             issue(i < nsl ? i : nsl - 1, rq[i], rm[i], rx[i]);
             __builtin_amdgcn_sched_barrier(0);
         }
+        load_rex();
         for (int s0 = 0; s0 < nsl; s0 += D) {
 #pragma unroll
             for (int i = 0; i < D; ++i) {
@@ -1955,6 +1980,7 @@ int launch_tile(const TileArgs& t, int nt, int max_active, int T, hipStream_t st
 template <class FMT, int NPROJ, int RT, int D, bool H16O = false>
 int launch_wave_tile(const TileArgs& targs, int nt, int nslots, hipStream_t st, int hx = 1, int mxt = 0) {
     if (targs.N % (16 * RT)) return MOE_ERR_ARG;
+    if (NPROJ == 1 && !mxt && targs.gidx) return MOE_ERR_ARG;   // these downs read a pass list (no in-kernel grouping)
     // in-kernel grouping, expert-major: E first passes and at most ceil(n / P) further ones (an expert with c
     // slots has ceil(c / P) - 1 <= (c - 1) / P of them)
     dim3 grid(targs.N / (16 * RT), targs.gidx && targs.gfirst ? targs.E + (nslots + 16 * nt - 1) / (16 * nt)
