@@ -41,8 +41,8 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the T=1 gate/up kernel, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
 # `bench.py --layers 8 --steps 5 --warmup 2 --no-t32 --no-configs --cpu-layers 0 --copy-calibrate 256`, each
 # scaled by what the counter reads for the 256 MiB device copy of the same run (FETCH_SIZE x 2.0, WRITE_SIZE x
-# 1.0): 2 x 6969.5 KiB + 48.0 KiB (profiles/k_gate_up_rows_qwen3_t1_traffic.md)
-GU_T1_TRAFFIC_BYTES = int(round((2.0 * 6969.5 + 48.0) * 1024))
+# 1.0): 2 x 6981.0 KiB + 48.0 KiB (profiles/k_gate_up_rows_qwen3_t1_traffic.md)
+GU_T1_TRAFFIC_BYTES = int(round((2.0 * 6981.0 + 48.0) * 1024))
 
 
 def log(*a):
