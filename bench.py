@@ -97,7 +97,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one MI355X: the expert path is single-GPU (expert "
-                                   "parallel sharding is described in DESIGN.md, not launched); run with --gpus 1"}))
+                                   "parallel sharding is designed, not launched); run with --gpus 1"}))
         sys.exit(2)
 
     __graft_entry__.load_package()

@@ -6,7 +6,7 @@
  *     prepare(w_gate, w_up, w_down) -> state;  run(state, x, idx, wts, act) -> y;  dequant(state)
  * plus run_slots (moelab/variants/mlx/metal_q4_moe.py:49-51) and the fused router tail topk_norm
  * (moelab/router.py:71-80). Each entry point below replaces the GPU work behind one of those calls;
- * the Python variant modules in moe-lab_amd/variants/ bind them with ctypes.
+ * the Python variant modules in moe-lab_amd/variants/ bind them with ctypes (moe-lab_amd/_lib.py).
  *
  * Conventions (all entry points):
  *   - every pointer is a device pointer (HBM), except the moe_experts_t descriptor itself, which
