@@ -157,6 +157,21 @@ def test_gptoss_small_h(T):
     assert_close(gpt().run(s, x, idx, wts, out_dtype=torch.float32), ref)
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_gptoss_per_slot_outputs(T):
+    """Unweighted per-slot outputs (run_slots) with the gpt-oss GLU and biases: the per-slot path's fp16 h plane
+    (h 2^8) is scaled back before the down's bias and the per-slot store, as before the combine."""
+    sh = shape_("gp", 256, 256, 8, 4)
+    s = packed_state(sh, 8, biases=True)
+    x, idx, _ = inputs(sh, T, seed=8, scale=3.0)   # activations large enough to reach the clamps
+    ys = mx().run_slots(s, x, idx, act=2)
+    assert ys.shape == (T * 4, 256)
+    ones = torch.ones((T, 1), device=DEV)
+    for j in range(4):
+        ref = oracle_y(s, x, idx[:, j:j + 1], ones, act=2)
+        assert_close(ys.view(T, 4, 256)[:, j], ref, what=(T, j))
+
+
 def test_gptoss_large_scale_bytes():
     """gpt-oss checkpoints reach E8M0 bytes >= 133 (reference test_gptoss_patch.py:88-113)."""
     sh = shape_("gl", 256, 256, 8, 4)
