@@ -172,6 +172,23 @@ def test_gptoss_per_slot_outputs(T):
         assert_close(ys.view(T, 4, 256)[:, j], ref, what=(T, j))
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_gptoss_per_slot_stages_split(T):
+    """The per-slot path as two calls (gate/up, then down on the h the first left in the workspace) equals the whole
+    call bit for bit with the gpt-oss GLU, whose h travels as one fp16 plane between the stages."""
+    from moelab_amd import _lib
+    from moelab_amd.experts import run_experts
+    sh = shape_("gs2", 320, 448, 8, 4)
+    s = packed_state(sh, 9, biases=True)
+    x, idx, wts = inputs(sh, T, seed=9, scale=3.0)
+    sl = _lib.PATH_SLOTS
+    y = run_experts(s, x, idx, wts, act=2, path=sl, out_dtype=torch.float32)
+    run_experts(s, x, idx, wts, act=2, path=sl, out_dtype=torch.float32, stages=_lib.STAGE_GATE_UP)
+    y2 = run_experts(s, x, idx, wts, act=2, path=sl, out_dtype=torch.float32, stages=_lib.STAGE_DOWN)
+    assert torch.equal(y, y2)
+    assert_close(y, oracle_y(s, x, idx, wts, act=2))
+
+
 def test_gptoss_large_scale_bytes():
     """gpt-oss checkpoints reach E8M0 bytes >= 133 (reference test_gptoss_patch.py:88-113)."""
     sh = shape_("gl", 256, 256, 8, 4)
