@@ -267,7 +267,7 @@ namespace {
 int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T, int k,
                  int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                  size_t workspace_bytes, int stages, void* stream, const float* route_logits, int route_norm,
-                 float route_scale, int pregrouped = 0);
+                 float route_scale, int pregrouped = 0, int xterm_ready = 0);
 int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const void* wr, const float* wr_bias,
                const void* gate, int T, int k, int norm, float scale, int act, int32_t* idx, float* wts, void* y,
                int y_dtype, const void* residual, void* workspace, size_t workspace_bytes, void* stream);
@@ -314,7 +314,7 @@ namespace {
 int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32_t* idx, const float* wts, int T, int k,
                  int act, int path, int nored, void* y, int y_dtype, const void* residual, void* workspace,
                  size_t workspace_bytes, int stages, void* stream, const float* route_logits, int route_norm,
-                 float route_scale, int pregrouped) {
+                 float route_scale, int pregrouped, int xterm_ready) {
     if (stages < 1 || stages > MOE_STAGE_ALL) return MOE_ERR_ARG;
     int rc = check_experts(w);
     if (rc) return rc;
@@ -375,6 +375,7 @@ int experts_call(const moe_experts_t* w, const void* x, int x_dtype, const int32
         a.grp.items = (int32_t*)(ws + L.items);
         a.grp.items2 = (int32_t*)(ws + L.items2);
         a.pregrouped = pregrouped;
+        a.xterm_ready = a.xterm ? xterm_ready : 0;
     }
     return rpath == MOE_PATH_GROUPED ? moe::run_experts_tiles(a) : moe::run_experts_slots(a);
 }
@@ -428,9 +429,13 @@ int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const 
         return experts_call(w, x, x_dtype, idx, wts, T, k, act, MOE_PATH_AUTO, 0, y, y_dtype, residual, workspace,
                             L.total, MOE_STAGE_ALL, stream, ra.logits, norm, scale);
     }
-    int pregrouped = 0;
+    int pregrouped = 0, xterm_ready = 0;
     if (resolve_path(MOE_PATH_AUTO, T) == MOE_PATH_GROUPED) {
         const moe::TilePasses tp = moe::tile_passes(w, T, ks, x_dtype);
+        if (tp.mx) {   // the block-scaled MXFP4 tiles: the finishing launch also writes x's term records
+            ra.xterm = (uint8_t*)(ws + L.xp);
+            xterm_ready = 1;
+        }
         if (!(tp.ingroup && moe::env_int("MOE_LAYER_INGROUP", 1))) {
             ra.grp = moe::GroupBufs{(int32_t*)(ws + L.counts), (int32_t*)(ws + L.offsets), (int32_t*)(ws + L.sorted),
                                     (int32_t*)(ws + L.active), (int32_t*)(ws + L.meta), (int32_t*)(ws + L.items),
@@ -442,7 +447,7 @@ int layer_call(const moe_experts_t* w, int S, const void* x, int x_dtype, const 
     rc = moe::launch_route(ra, true, st);
     if (rc) return rc;
     return experts_call(w, x, x_dtype, eidx, ewts, T, ks, act, MOE_PATH_AUTO, 0, y, y_dtype, residual, workspace,
-                        L.total, MOE_STAGE_ALL, stream, nullptr, 1, 1.f, pregrouped);
+                        L.total, MOE_STAGE_ALL, stream, nullptr, 1, 1.f, pregrouped, xterm_ready);
 }
 
 }  // namespace

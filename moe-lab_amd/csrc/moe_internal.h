@@ -43,6 +43,8 @@ struct RouterArgs {
     int P;                 // pass size of grp.items (unused when null)
     GroupBufs grp;         // grp.counts null: no grouping; else the grouping of the slots (sidx when S > 0, else idx)
     int P2;                // pass size of grp.items2
+    uint8_t* xterm;        // or null: route_finish also writes x's 2-term fp8 records here (the block-scaled MXFP4
+                           // tiles' activations, as k_mx_terms would), so the experts call launches no k_mx_terms
 };
 // The router's launches: the logits over many workgroups, then (tail) route_finish: the tails, the merged lists and the
 // grouping (grp.counts) and pass lists. tail = false: logits only.
@@ -73,6 +75,7 @@ int launch_shared_route(const void* x, int xdt, const uint16_t* gate, int T, int
 // down list's when it differs (else 0); ingroup: the wave tiles group the slots in-kernel (no list needed).
 struct TilePasses {
     int P, P2, ingroup;
+    int mx;   // the call runs the block-scaled MXFP4 tiles, which read x as 2-term fp8 records (xterm)
 };
 TilePasses tile_passes(const moe_experts_t* w, int T, int k, int x_dtype);
 
@@ -97,6 +100,7 @@ struct ExpertsArgs {
     uint8_t* xterm; // grouped path, MXFP4 block-scaled MFMA: x's fp8 term records (the x-planes region when x is bf16)
     GroupBufs grp;  // grouped path
     int pregrouped; // grouped path: grp already holds the grouping and pass lists of idx (written by the router)
+    int xterm_ready; // grouped path: xterm already holds x's term records (written by the router)
     int stages;     // bit 0: grouping + gate/up (writes h), bit 1: down + combine (reads h)
     // moe_layer_run at T == 1: the gate/up waves take their experts from the top-k of these router logits [T, E] (and
     // write idx / wts, which the down kernel reads); null: idx / wts are inputs

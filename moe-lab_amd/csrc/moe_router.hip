@@ -19,6 +19,7 @@
 #include "moe_common.h"
 #include "moe_group.h"
 #include "moe_internal.h"
+#include "moe_mxterms.h"
 
 namespace moe {
 
@@ -151,6 +152,14 @@ __global__ void __launch_bounds__(64 * FIN_WAVES) route_finish(RouterArgs a) {
             if (grouping && !single) store_agent(&ids[(size_t)t * ws + lane], sid);
             else ids[(size_t)t * ws + lane] = sid;
         }
+    }
+    if (a.xterm) {
+        // x's 2-term fp8 records for the block-scaled MXFP4 tiles (what k_mx_terms writes), for this workgroup's
+        // tokens: one thread per 32-input block
+        const int nsl = (a.d + 127) >> 7, t0 = blockIdx.x * FIN_TOK;
+        const int rows = a.T - t0 < FIN_TOK ? a.T - t0 : FIN_TOK;
+        for (int i = threadIdx.x; i < rows * 4 * nsl; i += 64 * FIN_WAVES)
+            mx_terms_block<2>(a.x + (size_t)t0 * a.d, rows, a.d, a.xterm + (size_t)t0 * nsl * mx_rec<2>(), i);
     }
     if (!grouping) return;
     const int n = a.T * ws;

@@ -28,6 +28,7 @@
 #include "moe_formats.h"
 #include "moe_group.h"
 #include "moe_internal.h"
+#include "moe_mxterms.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -63,9 +64,6 @@ constexpr int TL_APAD = 4 * TL_KC + 4;   // words per staged row: [g 0..3][chunk
 constexpr int TL_BPAD = 4 * TL_KC + 1;   // 16-byte pieces per staged token (8 inputs each) + 1 of padding
 constexpr int TL_GMAX = TL_KC;           // scale groups per slice at most (MXFP4: one per chunk)
 
-// block-scaled MXFP4 tiles: bytes of one (activation row, 128-input slice) record of NTERM fp8 terms + scales
-template <int NTERM>
-__host__ __device__ constexpr int mx_rec() { return 16 * (8 * NTERM + 1); }
 
 // Byte of record-term position of input k (0..127) of a slice: the code order of the tile records within each
 // word (inputs 8 i + (0 2 4 6 1 3 5 7)), then the A operand's lane order (bytes 32 g .. 32 g + 15: logical inputs
@@ -1425,64 +1423,11 @@ __global__ void __launch_bounds__(256, 2) k_dense(TileArgs a) {
 // bits. Measured on this part, the instruction's own accumulation keeps ~2e-5 of the outputs' RMS (two to four terms
 // give the same result), against the 1e-2 RMS gate.
 
-// x rows (bf16) -> per (row, 128-input slice) records of REC = 16 (8 NTERM + 1) bytes: NTERM x 128 bytes of terms
-// at mx_pos (the records' code order, then the A operand's lane order), then the E8M0 byte of term t, block b at
-// 128 NTERM + 4 t + b. Inputs past K (K % 128 == 64) are zero codes with scale byte 127. One thread per 32-input
-// block. (h's records come from the gate/up epilogues, mx_h_block.)
+// x rows (bf16) -> their fp8 term records (mx_terms_block, moe_mxterms.h): one thread per 32-input block
 template <int NTERM>
 __global__ void __launch_bounds__(256) k_mx_terms(const uint16_t* __restrict__ src, int rows, int K,
                                                  uint8_t* __restrict__ out) {
-    constexpr int REC = mx_rec<NTERM>();
-    const int nsl = (K + 127) >> 7, nb = 4 * nsl;
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (long)rows * nb) return;
-    const int row = (int)(i / nb), blk = (int)(i - (long)row * nb);
-    const int s = blk >> 2, b = blk & 3;
-    uint8_t* rec = out + ((size_t)row * nsl + s) * REC;
-    float r[32];
-    if (32 * blk < K) {
-        const uint4* p = reinterpret_cast<const uint4*>(src + (size_t)row * K + 32 * blk);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint4 v = p[q];
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                r[8 * q + 2 * u] = bf16lo(w[u]);
-                r[8 * q + 2 * u + 1] = bf16hi(w[u]);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) r[j] = 0.f;
-    }
-#pragma unroll
-    for (int t = 0; t < NTERM; ++t) {
-        float am = 0.f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) am = fmaxf(am, fabsf(r[j]));
-        int e = am > 0.f ? (int)((__float_as_uint(am) >> 23) & 0xFFu) - 127 - 7 : -127;
-        e = e < -127 ? -127 : (e > 127 ? 127 : e);
-        const float inv = __builtin_ldexpf(1.f, -e);
-        // byte j of the block's 32 = input 8 (j / 8) + (0 2 4 6 1 3 5 7)[j % 8]: the order of the codes in the tile
-        // records' words (nibbles e0 e2 e4 e6 e1 e3 e5 e7)
-        uint32_t qw[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i0 = 8 * (j >> 1) + (j & 1);
-            uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(r[i0] * inv, r[i0 + 2] * inv, 0, false);
-            w = __builtin_amdgcn_cvt_pk_fp8_f32(r[i0 + 4] * inv, r[i0 + 6] * inv, (int)w, true);
-            qw[j] = w;
-            r[i0] -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 0), e);
-            r[i0 + 2] -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 1), e);
-            r[i0 + 4] -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 2), e);
-            r[i0 + 6] -= __builtin_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)w, 3), e);
-        }
-        uint8_t* tq = rec + 128 * t + 64 * (b & 1) + 16 * (b >> 1);
-        *reinterpret_cast<uint4*>(tq) = uint4{qw[0], qw[1], qw[2], qw[3]};        // code words 0, 1 of the block
-        *reinterpret_cast<uint4*>(tq + 32) = uint4{qw[4], qw[5], qw[6], qw[7]};   // code words 2, 3
-        rec[128 * NTERM + 4 * t + b] = (uint8_t)(32 * blk < K ? e + 127 : 127);
-    }
+    mx_terms_block<NTERM>(src, rows, K, out, (long)blockIdx.x * 256 + threadIdx.x);
 }
 
 // k_mxd: blocks of 4 waves own BN = 64 RT rows of one expert (per projection) and one pass of up to 64 of its slots
@@ -2189,7 +2134,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
         if (mxd) {
             g.W0 = (const uint8_t*)w->gate.tiles;
             g.W1 = (const uint8_t*)w->up.tiles;
-            rc = launch_mx_terms<2>(a.xb, a.T, w->d, a.xterm, a.st);
+            if (!a.xterm_ready) rc = launch_mx_terms<2>(a.xb, a.T, w->d, a.xterm, a.st);
             g.actv = reinterpret_cast<const uint16_t*>(a.xterm);
             if (!rc) rc = launch_mxd<2, 2>(g, nslots, a.st);
             if (rc) return rc;
@@ -2202,7 +2147,7 @@ int run_tiles_fmt(const ExpertsArgs& a) {
             g.xexp = a.xexp;
         }
         if (mxw) {
-            rc = launch_mx_terms<2>(a.xb, a.T, w->d, a.xterm, a.st);
+            if (!a.xterm_ready) rc = launch_mx_terms<2>(a.xb, a.T, w->d, a.xterm, a.st);
             g.actv = reinterpret_cast<const uint16_t*>(a.xterm);
             if (!rc) rc = launch_wave_tile<FMT, 2, MOE_WAVE_RT_GU, MOE_WAVE_D_GU>(g, nt, nslots, a.st, 1, 2);
         } else if (mxd) rc = 0;
@@ -2279,7 +2224,7 @@ int run_experts_tiles(const ExpertsArgs& a) {
 
 TilePasses tile_passes(const moe_experts_t* w, int T, int k, int x_dtype) {
     const Plan p = w->fmt == MOE_FMT_INT4_G64 ? make_plan<FmtInt4>(w, T, k, x_dtype) : make_plan<FmtMxfp4>(w, T, k, x_dtype);
-    return TilePasses{p.P_gu, p.two_lists ? p.P_dn : 0, p.ingroup ? 1 : 0};
+    return TilePasses{p.P_gu, p.two_lists ? p.P_dn : 0, p.ingroup ? 1 : 0, p.mxd || p.mxw ? 1 : 0};
 }
 
 int launch_pack_tiles(int fmt, int E, int N, int K, const void* rows, void* tiles, hipStream_t st) {
