@@ -1,8 +1,9 @@
 // Router and slot grouping kernels for gfx950.
 //
-// router_kernel: logits[t, e] = x[t] . Wr[e] (+ b[e]) in fp32, one wave per EPW experts x TPW tokens; then the last
-// block to finish a token group runs the router tail (top-k, softmax) for its tokens, and, when the call asks for the
-// grouping, the last token group to finish sorts all T*k slots by expert in the same launch (group_block).
+// router_logits: logits[t, e] = x[t] . Wr[e] (+ b[e]) in fp32, one wave per EPW experts x TPW tokens. route_finish,
+// the next launch: the router tail (top-k, softmax) of one token per wave and, when the call asks for the grouping,
+// the sort of all T*k slots by expert (group_block) in its last workgroup to finish. At T = 1 the layer call skips
+// route_finish: the gate/up waves rank the token's logits themselves (moe_experts.hip).
 // The logit reduction order is fixed, so a CPU restatement reproduces every logit bit for bit and top-k ids
 // match exactly: lane l takes the 8-element chunks l, l+64, ... in order with fused multiply-adds in
 // element order, starting from +0; the 64 lane partials a[0..63] are combined by the DPP tree of
