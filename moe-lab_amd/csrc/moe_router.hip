@@ -156,10 +156,12 @@ __global__ void __launch_bounds__(64 * FIN_WAVES) route_finish(RouterArgs a) {
     }
     if (a.xterm) {
         // x's 2-term fp8 records for the block-scaled MXFP4 tiles (what k_mx_terms writes), for this workgroup's
-        // tokens: one thread per 32-input block
+        // tokens: one thread per 32-input block, numbered from wave FIN_TOK on, so that the waves that ran the
+        // tails take blocks only when there are more blocks than the other waves' threads
         const int nsl = (a.d + 127) >> 7, t0 = blockIdx.x * FIN_TOK;
         const int rows = a.T - t0 < FIN_TOK ? a.T - t0 : FIN_TOK;
-        for (int i = threadIdx.x; i < rows * 4 * nsl; i += 64 * FIN_WAVES)
+        const int i0 = ((int)threadIdx.x + 64 * (FIN_WAVES - FIN_TOK)) % (64 * FIN_WAVES);
+        for (int i = i0; i < rows * 4 * nsl; i += 64 * FIN_WAVES)
             mx_terms_block<2>(a.x + (size_t)t0 * a.d, rows, a.d, a.xterm + (size_t)t0 * nsl * mx_rec<2>(), i);
     }
     if (!grouping) return;
